@@ -1,0 +1,219 @@
+/*
+ * mmr.h -- C ABI of the MiniMind gfx950 decode runtime (libmmr.so).
+ *
+ * Plain pointers and sizes only: device buffers are `void*`/typed pointers
+ * obtained from mmr_malloc (or any HIP allocation), streams are hipStream_t
+ * passed as `mmr_stream_t`.  Every function returns an MMR_* status; on
+ * failure mmr_last_error() (thread-local) holds the message.  Op-level entry
+ * points never allocate, never synchronise and may be recorded into a
+ * hipGraph; model-level entry points mirror the reference C++ API.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths under lvyufeng/minimind-orangepi, file:line).
+ */
+#ifndef MMR_H
+#define MMR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MMR_OK 0
+#define MMR_ERR_INVALID_ARGUMENT 1 /* reference: std::invalid_argument */
+#define MMR_ERR_OUT_OF_RANGE 2     /* reference: std::out_of_range (token id) */
+#define MMR_ERR_RUNTIME 3          /* reference: std::runtime_error (backend, IO) */
+#define MMR_ERR_LENGTH 4           /* KV cache capacity exhausted */
+
+#define MMR_KV_F16 0
+#define MMR_KV_F32 1
+
+typedef void* mmr_stream_t;
+typedef struct mmr_model mmr_model;
+typedef struct mmr_state mmr_state;
+typedef struct mmr_rope_table mmr_rope_table;
+typedef struct mmr_kv_cache mmr_kv_cache;
+
+/* Fields of MiniMindConfig (src/csrc/models/minimind/config.h:21-45) used by
+ * the dense path. */
+typedef struct mmr_config {
+  int64_t hidden_size;
+  int64_t num_hidden_layers;
+  int64_t vocab_size;
+  int64_t num_attention_heads;
+  int64_t num_key_value_heads;
+  int64_t head_dim;
+  int64_t intermediate_size;
+  int64_t max_position_embeddings;
+  int32_t bos_token_id;
+  int32_t eos_token_id;
+  int32_t use_moe;
+  int32_t tie_word_embeddings;
+  float rms_norm_eps;
+  float rope_theta;
+} mmr_config;
+
+const char* mmr_last_error(void);
+int mmr_version(void);
+
+/* ---- device plumbing: DeviceBuffer / upload_* / runtime()
+ *      (src/csrc/models/minimind/ascend_matmul.h:18-101) ------------------- */
+int mmr_device_count(int* count);
+int mmr_malloc(void** ptr, size_t bytes);
+int mmr_free(void* ptr);
+int mmr_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int mmr_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int mmr_memset(void* dst, int value, size_t bytes);
+int mmr_stream_create(mmr_stream_t* stream);
+int mmr_stream_destroy(mmr_stream_t stream);
+int mmr_stream_synchronize(mmr_stream_t stream);
+int mmr_device_synchronize(void);
+int mmr_event_create(void** event);
+int mmr_event_destroy(void* event);
+int mmr_event_record(void* event, mmr_stream_t stream);
+int mmr_event_elapsed_ms(void* start, void* stop, float* ms);
+/* float_to_half / half_to_float (ascend_matmul.h:14-15), but IEEE
+ * round-to-nearest-even instead of the reference's ties-away rounding. */
+int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n);
+int mmr_f16_to_f32(const uint16_t* src, float* dst, size_t n);
+
+/* ---- projection matvec: device_matmul batch 1 (ascend_matmul.h:102,
+ *      ascend_matmul.cpp:385-410) and device_matmul_add (ascend_matmul.h:103-107).
+ * y[r] = sum_c W[r*cols + c] * x[c] (+ residual[r] when residual != NULL).
+ * W fp16 row-major [rows][cols] (the reference stores W^T; row-major keeps each
+ * output row one contiguous HBM stream), x/y/residual fp32 on the device.
+ * cols % 8 == 0, cols <= 4096.  residual may alias y. */
+int mmr_matvec_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* residual, float* y,
+                   mmr_stream_t stream);
+
+#define MMR_PRO_PLAIN 0
+#define MMR_PRO_RMSNORM 1       /* x := x * (scale * norm_w), decoder_layer.cpp:32-42 */
+#define MMR_PRO_RMSNORM_FINAL 2 /* x := (x * scale) * norm_w, language_model.cpp:24-38 */
+#define MMR_EPI_STORE 0
+#define MMR_EPI_RESIDUAL 1
+#define MMR_EPI_SWIGLU 2 /* rows interleaved gate_0, up_0, ...: y[i] = silu(g_i) * u_i, decoder_layer.cpp:175-182 */
+/* Fused variant used by the decode step: RMSNorm prologue (K1 folded in) and
+ * residual / SwiGLU epilogue (K5 / K4 folded in).  lanes_per_row (16/32/64)
+ * and rows_per_group (1/2/4) select the launch shape; 0 = automatic. */
+int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
+                      int prologue, int epilogue, const float* residual, float* y, int lanes_per_row,
+                      int rows_per_group, mmr_stream_t stream);
+
+/* ---- lm_head matvec + argmax: device_matmul_argmax (ascend_matmul.h:108-109,
+ *      ascend_matmul.cpp:467-502) / cube_matvec_argmax (ascend_matmul.h:127-130).
+ * token_out (device int32) receives the first index of the maximum logit
+ * (std::max_element, language_model.cpp:408-413); logits (device fp32,
+ * nullable) receives all logits.  norm_w != NULL fuses the final RMSNorm
+ * (language_model.cpp:325).  The workspace (device, see _workspace_size)
+ * must be zero-filled once before its first use; the kernel re-arms it. */
+size_t mmr_matvec_argmax_workspace_size(int64_t rows, int64_t cols);
+int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
+                          float* logits, int32_t* token_out, void* workspace, size_t workspace_bytes,
+                          mmr_stream_t stream);
+
+/* ---- RoPE table: cached_rope_table (ascend_custom_ops.cpp:93-123), kept in
+ * fp32 (the reference uploads fp16) with the CPU formula of
+ * decoder_layer.cpp:109-119. */
+int mmr_rope_table_create(int64_t max_positions, int64_t head_dim, float theta, mmr_rope_table** out);
+int mmr_rope_table_destroy(mmr_rope_table* table);
+
+/* ---- resident KV cache of one layer: CustomAttentionCache /
+ * ensure_attention_cache (ascend_custom_ops.cpp:59-65,126-139).  Layout
+ * [kv_head][capacity][head_dim]; capacity fixed at creation, never
+ * reallocated (the reference regrows and discards contents). */
+int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, int kv_dtype, mmr_kv_cache** out);
+int mmr_kv_cache_destroy(mmr_kv_cache* cache);
+int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values);
+
+/* ---- QKV post-process + KV append: device_decode_qkv_postprocess
+ * (ascend_custom_ops.h:132-143, ascend_custom_ops.cpp:825-884).
+ * qkv fp32 [Hq*d | Hkv*d | Hkv*d]; per-head RMSNorm with eps (honoured; the
+ * AscendC kernel hardcodes 1e-5) then RoPE at `position`; q -> query
+ * [Hq*d]; k, v appended at cache index tokens - 1. */
+int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const float* k_norm, mmr_kv_cache* cache,
+                               int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t position,
+                               const mmr_rope_table* rope, float eps, float* query, mmr_stream_t stream);
+
+/* ---- decode attention: device_attention_from_cache (ascend_custom_ops.h:145-151,
+ * ascend_custom_ops.cpp:886-916).  Attends `query` [Hq*d] over the first
+ * `tokens` cached keys: softmax(q.k / sqrt(d)) v per head, GQA mapping
+ * kv = h / (Hq/Hkv) (decoder_layer.cpp:184-234).  Split along the context in
+ * `splits` ranges (0 = automatic) with a log-sum-exp combine.  The workspace
+ * must be zero-filled once before its first use. */
+size_t mmr_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_t head_dim, int splits);
+int mmr_attention_from_cache(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
+                             int64_t kv_heads, int64_t head_dim, float* out, void* workspace, size_t workspace_bytes,
+                             int splits, mmr_stream_t stream);
+
+/* ---- fused post-process + append + attend (the decode-step form of
+ * device_decode_attention, ascend_custom_ops.h:153-161): position read from
+ * device memory (*position), k/v appended at that index, attention over
+ * *position + 1 keys.  *error (device int32) is set to 1 when the position is
+ * out of range. */
+int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const float* k_norm, float eps,
+                               const mmr_rope_table* rope, const int32_t* position, mmr_kv_cache* cache,
+                               int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, void* workspace,
+                               size_t workspace_bytes, int splits, int32_t* error, mmr_stream_t stream);
+
+/* ---- support ops (ascend_custom_ops.h:70-79,109-120) ----------------------- */
+int mmr_rms_norm_rows(const float* in, const float* w, float eps, int64_t rows, int64_t cols, float* out,
+                      mmr_stream_t stream);
+int mmr_add(const float* a, const float* b, int64_t n, float* out, mmr_stream_t stream);
+int mmr_swiglu_rows(const float* gate_up, int64_t rows, int64_t cols, float* out, mmr_stream_t stream);
+int mmr_embedding_gather(const uint16_t* table, const int32_t* ids, int64_t tokens, int64_t vocab, int64_t hidden,
+                         float* out, int32_t* error, mmr_stream_t stream);
+
+/* ---- model API: LanguageModel / DecoderState (language_model.h:22-49),
+ *      load_runtime_language_model / has_runtime_language_model
+ *      (runtime_loader.h:9-10) ---------------------------------------------- */
+int mmr_default_config(mmr_config* out);
+int mmr_load_config(const char* path, mmr_config* out);
+int mmr_has_runtime_model(const char* model_dir, int* out);
+int mmr_model_load(const char* model_dir, mmr_model** out);
+int mmr_model_create_synthetic(const mmr_config* config, uint64_t seed, double std, int round_fp16,
+                               mmr_model** out);
+int mmr_model_free(mmr_model* model);
+int mmr_model_config(const mmr_model* model, mmr_config* out);
+int mmr_model_weight_bytes(const mmr_model* model, uint64_t* bytes);
+
+/* Writes minimind_runtime_config.txt + weights.bin (MMRTW001,
+ * runtime_loader.cpp:121-167) with seeded synthetic weights. */
+int mmr_write_synthetic_model(const char* model_dir, const mmr_config* config, uint64_t seed, double std,
+                              int round_fp16);
+int mmr_synthesize_normals(uint64_t seed, uint64_t first, uint64_t count, double std, int round_fp16, float* out);
+int mmr_synthesize_prompt(uint64_t seed, int64_t count, int64_t vocab, int32_t* out);
+
+/* capacity 0 = max_position_embeddings */
+int mmr_state_create(const mmr_model* model, int64_t capacity, int kv_dtype, mmr_state** out);
+int mmr_state_free(mmr_state* state);
+int mmr_state_position(const mmr_state* state, int64_t* position);
+int mmr_state_stream(const mmr_state* state, mmr_stream_t* stream);
+int mmr_state_reset(const mmr_model* model, mmr_state* state);
+
+/* language_model.cpp:297-308 / :310-333 / :335-366 / :368-406 */
+int mmr_forward_token(const mmr_model* model, mmr_state* state, int32_t token, float* logits);
+int mmr_forward_next_token(const mmr_model* model, mmr_state* state, int32_t token, int32_t* next);
+int mmr_prefill_next_token(const mmr_model* model, mmr_state* state, const int32_t* prompt, int64_t n,
+                           int32_t* next);
+int mmr_generate(const mmr_model* model, const int32_t* prompt, int64_t n, int64_t max_new_tokens, int32_t* out,
+                 int64_t* out_count);
+
+/* Device-resident loop (no host round trip per token). */
+int mmr_enqueue_prefill(const mmr_model* model, mmr_state* state, const int32_t* prompt, int64_t n);
+int mmr_enqueue_decode(const mmr_model* model, mmr_state* state, int64_t steps, int32_t first_token);
+int mmr_state_synchronize(const mmr_model* model, mmr_state* state);
+int mmr_read_sequence(const mmr_model* model, mmr_state* state, int64_t first, int64_t count, int32_t* out);
+int mmr_read_logits(const mmr_model* model, mmr_state* state, float* logits);
+
+/* Enqueue `count` launches of one kernel of the decode step on the state's
+ * stream, cycling over layers from `layer` (kernel: 0 qkv, 1 attention,
+ * 2 o, 3 gate_up, 4 down, 5 lm_head without step bookkeeping).  For timing
+ * with events recorded on the state's stream; overwrites scratch buffers. */
+int mmr_launch_step_kernel(const mmr_model* model, mmr_state* state, int kernel, int64_t layer, int64_t count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MMR_H */

@@ -1,0 +1,708 @@
+// capi.cpp -- extern "C" boundary of libmmr.so (declared in include/mmr.h).
+//
+// Thin: argument checks, exception -> status translation, then a kernel
+// launcher (op-level) or the LanguageModel (model-level).
+#include "../../include/mmr.h"
+
+#include "kernels/kernels.h"
+#include "runtime/device.h"
+#include "runtime/language_model.h"
+
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+using namespace minimind::model;
+
+struct mmr_model {
+  std::unique_ptr<LanguageModel> lm;
+};
+struct mmr_state {
+  DecoderState st;
+};
+struct mmr_rope_table {
+  DeviceBuffer cos_sin;  // [max_pos][d/2] cos, then [max_pos][d/2] sin
+  int64_t max_positions = 0;
+  int64_t head_dim = 0;
+  const float* cos() const { return static_cast<const float*>(cos_sin.data()); }
+  const float* sin() const { return cos() + max_positions * (head_dim / 2); }
+};
+struct mmr_kv_cache {
+  DeviceBuffer keys, values;
+  int64_t kv_heads = 0, head_dim = 0, capacity = 0;
+  int dtype = MMR_KV_F32;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return MMR_OK;
+  } catch (const std::invalid_argument& e) {
+    return fail(MMR_ERR_INVALID_ARGUMENT, e.what());
+  } catch (const std::out_of_range& e) {
+    return fail(MMR_ERR_OUT_OF_RANGE, e.what());
+  } catch (const std::length_error& e) {
+    return fail(MMR_ERR_LENGTH, e.what());
+  } catch (const std::exception& e) {
+    return fail(MMR_ERR_RUNTIME, e.what());
+  } catch (...) {
+    return fail(MMR_ERR_RUNTIME, "unknown error");
+  }
+}
+
+void require(bool ok, const char* msg) {
+  if (!ok) throw std::invalid_argument(msg);
+}
+
+hipStream_t as_stream(mmr_stream_t s) { return static_cast<hipStream_t>(s); }
+
+void hip(hipError_t st, const char* what) { check_hip(st, what); }
+
+MiniMindConfig to_cpp(const mmr_config& c) {
+  MiniMindConfig m = default_minimind_config();
+  m.hidden_size = c.hidden_size;
+  m.num_hidden_layers = c.num_hidden_layers;
+  m.vocab_size = c.vocab_size;
+  m.num_attention_heads = c.num_attention_heads;
+  m.num_key_value_heads = c.num_key_value_heads;
+  m.head_dim = c.head_dim;
+  m.intermediate_size = c.intermediate_size;
+  m.max_position_embeddings = c.max_position_embeddings;
+  m.bos_token_id = c.bos_token_id;
+  m.eos_token_id = c.eos_token_id;
+  m.use_moe = c.use_moe != 0;
+  m.tie_word_embeddings = c.tie_word_embeddings != 0;
+  m.rms_norm_eps = c.rms_norm_eps;
+  m.rope_theta = c.rope_theta;
+  m.moe_intermediate_size = c.intermediate_size;
+  return m;
+}
+
+mmr_config to_c(const MiniMindConfig& m) {
+  mmr_config c;
+  c.hidden_size = m.hidden_size;
+  c.num_hidden_layers = m.num_hidden_layers;
+  c.vocab_size = m.vocab_size;
+  c.num_attention_heads = m.num_attention_heads;
+  c.num_key_value_heads = m.num_key_value_heads;
+  c.head_dim = m.head_dim;
+  c.intermediate_size = m.intermediate_size;
+  c.max_position_embeddings = m.max_position_embeddings;
+  c.bos_token_id = m.bos_token_id;
+  c.eos_token_id = m.eos_token_id;
+  c.use_moe = m.use_moe ? 1 : 0;
+  c.tie_word_embeddings = m.tie_word_embeddings ? 1 : 0;
+  c.rms_norm_eps = m.rms_norm_eps;
+  c.rope_theta = m.rope_theta;
+  return c;
+}
+
+void check_matvec_shape(int64_t rows, int64_t cols) {
+  require(rows > 0 && cols > 0, "rows and cols must be positive");
+  require(cols % 8 == 0 && cols <= 4096, "cols must be a multiple of 8 and <= 4096");
+  require(rows < (int64_t{1} << 30), "rows too large");
+}
+
+// Argmax workspace: [u32 ticket counter][pad][u64 packed best key]
+constexpr size_t kArgmaxWorkspaceBytes = 256;
+
+int auto_splits(int64_t tokens, int64_t head_dim) {
+  const int tile = mmr::attention_tile_tokens(static_cast<int>(head_dim));
+  const int64_t tiles = (tokens + tile - 1) / tile;
+  return static_cast<int>(tiles < 1 ? 1 : (tiles > 512 ? 512 : tiles));
+}
+
+// Attention workspace: [counters: 256 B][partials]
+size_t attention_ws_bytes(int64_t hq, int64_t hkv, int64_t d, int splits) {
+  return 256 + mmr::attention_partial_floats(static_cast<int>(hq), static_cast<int>(hkv), static_cast<int>(d), splits) * 4;
+}
+
+void check_attention_shape(int64_t hq, int64_t hkv, int64_t d) {
+  require(mmr::attention_supported(static_cast<int>(hq), static_cast<int>(hkv), static_cast<int>(d)),
+          "unsupported heads/head_dim: need Hq % Hkv == 0, Hq/Hkv <= 8, head_dim in {16,32,64,96,128}");
+  require(hkv <= 64, "kv_heads must be <= 64");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mmr_last_error(void) { return g_last_error.c_str(); }
+int mmr_version(void) { return 1; }
+
+int mmr_device_count(int* count) {
+  return guarded([&] {
+    require(count, "null count");
+    *count = 0;
+    const hipError_t st = hipGetDeviceCount(count);
+    if (st != hipSuccess) *count = 0;
+  });
+}
+
+int mmr_malloc(void** ptr, size_t bytes) {
+  return guarded([&] {
+    require(ptr, "null ptr");
+    hip(hipMalloc(ptr, bytes), "hipMalloc");
+  });
+}
+int mmr_free(void* ptr) {
+  return guarded([&] { hip(hipFree(ptr), "hipFree"); });
+}
+int mmr_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return guarded([&] { hip(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy H2D"); });
+}
+int mmr_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return guarded([&] { hip(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H"); });
+}
+int mmr_memset(void* dst, int value, size_t bytes) {
+  return guarded([&] { hip(hipMemset(dst, value, bytes), "hipMemset"); });
+}
+int mmr_stream_create(mmr_stream_t* stream) {
+  return guarded([&] {
+    require(stream, "null stream");
+    hipStream_t s = nullptr;
+    hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    *stream = s;
+  });
+}
+int mmr_stream_destroy(mmr_stream_t stream) {
+  return guarded([&] { hip(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy"); });
+}
+int mmr_stream_synchronize(mmr_stream_t stream) {
+  return guarded([&] { hip(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize"); });
+}
+int mmr_device_synchronize(void) {
+  return guarded([&] { hip(hipDeviceSynchronize(), "hipDeviceSynchronize"); });
+}
+int mmr_event_create(void** event) {
+  return guarded([&] {
+    require(event, "null event");
+    hipEvent_t e = nullptr;
+    hip(hipEventCreate(&e), "hipEventCreate");
+    *event = e;
+  });
+}
+int mmr_event_destroy(void* event) {
+  return guarded([&] { hip(hipEventDestroy(static_cast<hipEvent_t>(event)), "hipEventDestroy"); });
+}
+int mmr_event_record(void* event, mmr_stream_t stream) {
+  return guarded([&] { hip(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)), "hipEventRecord"); });
+}
+int mmr_event_elapsed_ms(void* start, void* stop, float* ms) {
+  return guarded([&] {
+    require(ms, "null ms");
+    hip(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "hipEventSynchronize");
+    hip(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+        "hipEventElapsedTime");
+  });
+}
+int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n) {
+  return guarded([&] {
+    require(src && dst, "null buffer");
+    for (size_t i = 0; i < n; ++i) dst[i] = float_to_half(src[i]);
+  });
+}
+int mmr_f16_to_f32(const uint16_t* src, float* dst, size_t n) {
+  return guarded([&] {
+    require(src && dst, "null buffer");
+    for (size_t i = 0; i < n; ++i) dst[i] = half_to_float(src[i]);
+  });
+}
+
+// ------------------------------------------------------------------ ops --
+
+int mmr_matvec_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* residual, float* y,
+                   mmr_stream_t stream) {
+  return mmr_matvec_f16_ex(w, rows, cols, x, nullptr, 0.0f, MMR_PRO_PLAIN,
+                           residual ? MMR_EPI_RESIDUAL : MMR_EPI_STORE, residual, y, 0, 0, stream);
+}
+
+int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
+                      int prologue, int epilogue, const float* residual, float* y, int lanes_per_row,
+                      int rows_per_group, mmr_stream_t stream) {
+  return guarded([&] {
+    check_matvec_shape(rows, cols);
+    require(w && x && y, "null buffer");
+    require(prologue >= MMR_PRO_PLAIN && prologue <= MMR_PRO_RMSNORM_FINAL, "unknown prologue");
+    require(epilogue >= MMR_EPI_STORE && epilogue <= MMR_EPI_SWIGLU, "unknown epilogue");
+    require(prologue == MMR_PRO_PLAIN || norm_w, "RMSNorm prologue needs norm_w");
+    require(epilogue != MMR_EPI_RESIDUAL || residual, "residual epilogue needs residual");
+    require(prologue != MMR_PRO_RMSNORM_FINAL, "the final-norm prologue is fused with argmax only");
+    mmr::GemvPlan plan;
+    require(mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), static_cast<mmr::GemvEpilogue>(epilogue),
+                           lanes_per_row, rows_per_group, &plan),
+            "unsupported launch shape (lanes_per_row 16/32/64, rows_per_group 1/2/4, even for SwiGLU)");
+    mmr::GemvArgs a;
+    a.w = reinterpret_cast<const __half*>(w);
+    a.rows = static_cast<int>(rows);
+    a.k = static_cast<int>(cols);
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.y = y;
+    a.residual = residual;
+    hip(mmr::launch_gemv(a, static_cast<mmr::GemvPrologue>(prologue), static_cast<mmr::GemvEpilogue>(epilogue), plan,
+                         as_stream(stream)),
+        "matvec launch");
+  });
+}
+
+size_t mmr_matvec_argmax_workspace_size(int64_t rows, int64_t cols) {
+  mmr::GemvPlan plan;
+  if (rows <= 0 || rows >= (int64_t{1} << 30) ||
+      !mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), mmr::kEpiArgmax, 0, 0, &plan))
+    return 0;
+  return kArgmaxWorkspaceBytes;
+}
+
+int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
+                          float* logits, int32_t* token_out, void* workspace, size_t workspace_bytes,
+                          mmr_stream_t stream) {
+  return guarded([&] {
+    check_matvec_shape(rows, cols);
+    require(w && x && token_out && workspace, "null buffer");
+    mmr::GemvPlan plan;
+    require(mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), mmr::kEpiArgmax, 0, 0, &plan),
+            "unsupported shape");
+    require(workspace_bytes >= kArgmaxWorkspaceBytes, "workspace too small");
+    char* ws = static_cast<char*>(workspace);
+    mmr::GemvArgs a;
+    a.w = reinterpret_cast<const __half*>(w);
+    a.rows = static_cast<int>(rows);
+    a.k = static_cast<int>(cols);
+    a.x = x;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.y = logits;
+    a.counter = reinterpret_cast<unsigned int*>(ws);
+    a.best = reinterpret_cast<unsigned long long*>(ws + 8);
+    a.token_out = token_out;
+    hip(mmr::launch_gemv(a, norm_w ? mmr::kProRmsNormFinal : mmr::kProPlain, mmr::kEpiArgmax, plan,
+                         as_stream(stream)),
+        "matvec argmax launch");
+  });
+}
+
+int mmr_rope_table_create(int64_t max_positions, int64_t head_dim, float theta, mmr_rope_table** out) {
+  return guarded([&] {
+    require(out, "null out");
+    require(max_positions > 0 && max_positions <= (int64_t{1} << 24), "max_positions out of range");
+    require(head_dim > 0 && head_dim % 2 == 0 && head_dim <= 128, "head_dim must be even and <= 128");
+    require(theta > 0.0f, "theta must be positive");
+    auto t = std::make_unique<mmr_rope_table>();
+    const int64_t half = head_dim / 2;
+    std::vector<float> inv(static_cast<size_t>(half));
+    for (int64_t i = 0; i < half; ++i)
+      inv[static_cast<size_t>(i)] =
+          1.0F / std::pow(theta, static_cast<float>(i * 2) / static_cast<float>(head_dim));
+    std::vector<float> host(static_cast<size_t>(2 * max_positions * half));
+    for (int64_t p = 0; p < max_positions; ++p)
+      for (int64_t i = 0; i < half; ++i) {
+        const float angle = static_cast<float>(p) * inv[static_cast<size_t>(i)];
+        host[static_cast<size_t>(p * half + i)] = std::cos(angle);
+        host[static_cast<size_t>(max_positions * half + p * half + i)] = std::sin(angle);
+      }
+    t->cos_sin.reset(host.size() * sizeof(float));
+    hip(hipMemcpy(t->cos_sin.data(), host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+    t->max_positions = max_positions;
+    t->head_dim = head_dim;
+    *out = t.release();
+  });
+}
+
+int mmr_rope_table_destroy(mmr_rope_table* table) {
+  return guarded([&] { delete table; });
+}
+
+int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, int kv_dtype, mmr_kv_cache** out) {
+  return guarded([&] {
+    require(out, "null out");
+    require(kv_heads > 0 && head_dim > 0 && capacity > 0, "dimensions must be positive");
+    require(kv_dtype == MMR_KV_F16 || kv_dtype == MMR_KV_F32, "unknown kv dtype");
+    require(capacity < (int64_t{1} << 28), "capacity too large");
+    auto c = std::make_unique<mmr_kv_cache>();
+    const size_t bytes = static_cast<size_t>(kv_heads * head_dim * capacity) * (kv_dtype == MMR_KV_F16 ? 2 : 4);
+    c->keys.reset(bytes);
+    c->values.reset(bytes);
+    hip(hipMemset(c->keys.data(), 0, bytes), "hipMemset");
+    hip(hipMemset(c->values.data(), 0, bytes), "hipMemset");
+    c->kv_heads = kv_heads;
+    c->head_dim = head_dim;
+    c->capacity = capacity;
+    c->dtype = kv_dtype;
+    *out = c.release();
+  });
+}
+
+int mmr_kv_cache_destroy(mmr_kv_cache* cache) {
+  return guarded([&] { delete cache; });
+}
+
+int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values) {
+  return guarded([&] {
+    require(cache && keys && values, "null argument");
+    *keys = cache->keys.data();
+    *values = cache->values.data();
+  });
+}
+
+int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const float* k_norm, mmr_kv_cache* cache,
+                               int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t position,
+                               const mmr_rope_table* rope, float eps, float* query, mmr_stream_t stream) {
+  return guarded([&] {
+    require(qkv && q_norm && k_norm && cache && rope && query, "null argument");
+    check_attention_shape(q_heads, kv_heads, head_dim);
+    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(rope->head_dim == head_dim, "rope table head_dim mismatch");
+    require(tokens >= 1 && tokens <= cache->capacity, "tokens must be in [1, capacity]");
+    require(position >= 0 && position < rope->max_positions, "position outside the rope table");
+    mmr::QkvPostArgs a;
+    a.qkv = qkv;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.eps = eps;
+    a.rope_cos = rope->cos();
+    a.rope_sin = rope->sin();
+    a.position = static_cast<int>(position);
+    a.index = static_cast<int>(tokens - 1);
+    a.kcache = cache->keys.data();
+    a.vcache = cache->values.data();
+    a.capacity = static_cast<int>(cache->capacity);
+    a.hq = static_cast<int>(q_heads);
+    a.hkv = static_cast<int>(kv_heads);
+    a.d = static_cast<int>(head_dim);
+    a.query_out = query;
+    hip(mmr::launch_qkv_postprocess(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32, as_stream(stream)),
+        "qkv postprocess launch");
+  });
+}
+
+size_t mmr_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_t head_dim, int splits) {
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || head_dim <= 0) return 0;
+  if (splits <= 0) splits = 512;
+  return attention_ws_bytes(q_heads, kv_heads, head_dim, splits);
+}
+
+int mmr_attention_from_cache(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
+                             int64_t kv_heads, int64_t head_dim, float* out, void* workspace, size_t workspace_bytes,
+                             int splits, mmr_stream_t stream) {
+  return guarded([&] {
+    require(query && cache && out && workspace, "null argument");
+    check_attention_shape(q_heads, kv_heads, head_dim);
+    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(tokens >= 1 && tokens <= cache->capacity, "tokens must be in [1, capacity]");
+    if (splits <= 0) splits = auto_splits(tokens, head_dim);
+    require(splits <= 4096, "splits too large");
+    require(workspace_bytes >= attention_ws_bytes(q_heads, kv_heads, head_dim, splits), "workspace too small");
+    char* ws = static_cast<char*>(workspace);
+    mmr::AttnArgs a;
+    a.q = query;
+    a.tokens = static_cast<int>(tokens);
+    a.kcache = cache->keys.data();
+    a.vcache = cache->values.data();
+    a.capacity = static_cast<int>(cache->capacity);
+    a.hq = static_cast<int>(q_heads);
+    a.hkv = static_cast<int>(kv_heads);
+    a.d = static_cast<int>(head_dim);
+    a.splits = splits;
+    a.counters = reinterpret_cast<unsigned int*>(ws);
+    a.part = reinterpret_cast<float*>(ws + 256);
+    a.out = out;
+    hip(mmr::launch_attention(a, mmr::kAttnFromCache, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
+                              as_stream(stream)),
+        "attention launch");
+  });
+}
+
+int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const float* k_norm, float eps,
+                               const mmr_rope_table* rope, const int32_t* position, mmr_kv_cache* cache,
+                               int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, void* workspace,
+                               size_t workspace_bytes, int splits, int32_t* error, mmr_stream_t stream) {
+  return guarded([&] {
+    require(qkv && q_norm && k_norm && rope && position && cache && out && workspace && error, "null argument");
+    check_attention_shape(q_heads, kv_heads, head_dim);
+    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(rope->head_dim == head_dim, "rope table head_dim mismatch");
+    if (splits <= 0) splits = auto_splits(cache->capacity, head_dim);
+    require(splits <= 4096, "splits too large");
+    require(workspace_bytes >= attention_ws_bytes(q_heads, kv_heads, head_dim, splits), "workspace too small");
+    char* ws = static_cast<char*>(workspace);
+    mmr::AttnArgs a;
+    a.qkv = qkv;
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.eps = eps;
+    a.rope_cos = rope->cos();
+    a.rope_sin = rope->sin();
+    a.pos = position;
+    a.kcache = cache->keys.data();
+    a.vcache = cache->values.data();
+    a.capacity = static_cast<int>(cache->capacity);
+    a.max_pos = static_cast<int>(rope->max_positions);
+    a.hq = static_cast<int>(q_heads);
+    a.hkv = static_cast<int>(kv_heads);
+    a.d = static_cast<int>(head_dim);
+    a.splits = splits;
+    a.counters = reinterpret_cast<unsigned int*>(ws);
+    a.part = reinterpret_cast<float*>(ws + 256);
+    a.out = out;
+    a.err = error;
+    hip(mmr::launch_attention(a, mmr::kAttnFused, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
+                              as_stream(stream)),
+        "fused attention launch");
+  });
+}
+
+int mmr_rms_norm_rows(const float* in, const float* w, float eps, int64_t rows, int64_t cols, float* out,
+                      mmr_stream_t stream) {
+  return guarded([&] {
+    require(in && w && out, "null buffer");
+    require(rows >= 0 && cols > 0 && rows < (int64_t{1} << 31), "invalid shape");
+    hip(mmr::launch_rms_norm_rows(in, w, eps, static_cast<int>(rows), static_cast<int>(cols), out, as_stream(stream)),
+        "rms_norm_rows launch");
+  });
+}
+
+int mmr_add(const float* a, const float* b, int64_t n, float* out, mmr_stream_t stream) {
+  return guarded([&] {
+    require(a && b && out, "null buffer");
+    hip(mmr::launch_add(a, b, n, out, as_stream(stream)), "add launch");
+  });
+}
+
+int mmr_swiglu_rows(const float* gate_up, int64_t rows, int64_t cols, float* out, mmr_stream_t stream) {
+  return guarded([&] {
+    require(gate_up && out, "null buffer");
+    require(rows >= 0 && cols > 0, "invalid shape");
+    hip(mmr::launch_swiglu_rows(gate_up, static_cast<int>(rows), static_cast<int>(cols), out, as_stream(stream)),
+        "swiglu_rows launch");
+  });
+}
+
+int mmr_embedding_gather(const uint16_t* table, const int32_t* ids, int64_t tokens, int64_t vocab, int64_t hidden,
+                         float* out, int32_t* error, mmr_stream_t stream) {
+  return guarded([&] {
+    require(table && ids && out, "null buffer");
+    require(tokens >= 0 && tokens < 65536 && vocab > 0 && hidden > 0, "invalid shape");
+    hip(mmr::launch_embedding_gather(reinterpret_cast<const __half*>(table), ids, static_cast<int>(tokens),
+                                     static_cast<int>(vocab), static_cast<int>(hidden), out, error, as_stream(stream)),
+        "embedding_gather launch");
+  });
+}
+
+// ---------------------------------------------------------------- model --
+
+int mmr_default_config(mmr_config* out) {
+  return guarded([&] {
+    require(out, "null out");
+    *out = to_c(default_minimind_config());
+  });
+}
+
+int mmr_load_config(const char* path, mmr_config* out) {
+  return guarded([&] {
+    require(path && out, "null argument");
+    *out = to_c(config_from_file(path));
+  });
+}
+
+int mmr_has_runtime_model(const char* model_dir, int* out) {
+  return guarded([&] {
+    require(model_dir && out, "null argument");
+    *out = has_runtime_language_model(model_dir) ? 1 : 0;
+  });
+}
+
+int mmr_model_load(const char* model_dir, mmr_model** out) {
+  return guarded([&] {
+    require(model_dir && out, "null argument");
+    auto m = std::make_unique<mmr_model>();
+    m->lm = std::make_unique<LanguageModel>(load_runtime_language_model(model_dir));
+    *out = m.release();
+  });
+}
+
+int mmr_model_create_synthetic(const mmr_config* config, uint64_t seed, double std, int round_fp16,
+                               mmr_model** out) {
+  return guarded([&] {
+    require(config && out, "null argument");
+    const MiniMindConfig c = to_cpp(*config);
+    const auto errors = validate_config(c);
+    if (!errors.empty()) throw std::invalid_argument("invalid MiniMind config: " + errors.front());
+    auto m = std::make_unique<mmr_model>();
+    m->lm = std::make_unique<LanguageModel>(c, synthesize_weights(c, seed, std, round_fp16 != 0));
+    *out = m.release();
+  });
+}
+
+int mmr_model_free(mmr_model* model) {
+  return guarded([&] { delete model; });
+}
+
+int mmr_model_config(const mmr_model* model, mmr_config* out) {
+  return guarded([&] {
+    require(model && out, "null argument");
+    *out = to_c(model->lm->config());
+  });
+}
+
+int mmr_model_weight_bytes(const mmr_model* model, uint64_t* bytes) {
+  return guarded([&] {
+    require(model && bytes, "null argument");
+    *bytes = model->lm->device_weight_bytes();
+  });
+}
+
+int mmr_write_synthetic_model(const char* model_dir, const mmr_config* config, uint64_t seed, double std,
+                              int round_fp16) {
+  return guarded([&] {
+    require(model_dir && config, "null argument");
+    const MiniMindConfig c = to_cpp(*config);
+    const auto errors = validate_config(c);
+    if (!errors.empty()) throw std::invalid_argument("invalid MiniMind config: " + errors.front());
+    write_synthetic_model(model_dir, c, seed, std, round_fp16 != 0);
+  });
+}
+
+int mmr_synthesize_normals(uint64_t seed, uint64_t first, uint64_t count, double std, int round_fp16, float* out) {
+  return guarded([&] {
+    require(out || count == 0, "null out");
+    synthesize_normals(seed, first, count, std, round_fp16 != 0, out);
+  });
+}
+
+int mmr_synthesize_prompt(uint64_t seed, int64_t count, int64_t vocab, int32_t* out) {
+  return guarded([&] {
+    require((out || count == 0) && count >= 0 && vocab > 0, "invalid argument");
+    const auto ids = synthesize_prompt(seed, count, vocab);
+    std::memcpy(out, ids.data(), ids.size() * sizeof(int32_t));
+  });
+}
+
+int mmr_state_create(const mmr_model* model, int64_t capacity, int kv_dtype, mmr_state** out) {
+  return guarded([&] {
+    require(model && out, "null argument");
+    require(kv_dtype == MMR_KV_F16 || kv_dtype == MMR_KV_F32, "unknown kv dtype");
+    auto s = std::make_unique<mmr_state>();
+    s->st = model->lm->make_state(capacity, kv_dtype == MMR_KV_F16 ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32);
+    *out = s.release();
+  });
+}
+
+int mmr_state_free(mmr_state* state) {
+  return guarded([&] { delete state; });
+}
+
+int mmr_state_position(const mmr_state* state, int64_t* position) {
+  return guarded([&] {
+    require(state && position, "null argument");
+    *position = state->st.position;
+  });
+}
+
+int mmr_state_stream(const mmr_state* state, mmr_stream_t* stream) {
+  return guarded([&] {
+    require(state && stream, "null argument");
+    *stream = state->st.stream();
+  });
+}
+
+int mmr_state_reset(const mmr_model* model, mmr_state* state) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->reset_state(state->st);
+  });
+}
+
+int mmr_forward_token(const mmr_model* model, mmr_state* state, int32_t token, float* logits) {
+  return guarded([&] {
+    require(model && state && logits, "null argument");
+    const auto v = model->lm->forward_token(token, state->st);
+    std::memcpy(logits, v.data(), v.size() * sizeof(float));
+  });
+}
+
+int mmr_forward_next_token(const mmr_model* model, mmr_state* state, int32_t token, int32_t* next) {
+  return guarded([&] {
+    require(model && state && next, "null argument");
+    *next = model->lm->forward_next_token(token, state->st);
+  });
+}
+
+int mmr_prefill_next_token(const mmr_model* model, mmr_state* state, const int32_t* prompt, int64_t n,
+                           int32_t* next) {
+  return guarded([&] {
+    require(model && state && next && (prompt || n == 0) && n >= 0, "null argument");
+    *next = model->lm->prefill_next_token(std::vector<int32_t>(prompt, prompt + n), state->st);
+  });
+}
+
+int mmr_generate(const mmr_model* model, const int32_t* prompt, int64_t n, int64_t max_new_tokens, int32_t* out,
+                 int64_t* out_count) {
+  return guarded([&] {
+    require(model && out_count && (prompt || n == 0) && n >= 0, "null argument");
+    require(out || max_new_tokens <= 0, "null out");
+    const auto ids = model->lm->generate(std::vector<int32_t>(prompt, prompt + n), max_new_tokens);
+    std::memcpy(out, ids.data(), ids.size() * sizeof(int32_t));
+    *out_count = static_cast<int64_t>(ids.size());
+  });
+}
+
+int mmr_enqueue_prefill(const mmr_model* model, mmr_state* state, const int32_t* prompt, int64_t n) {
+  return guarded([&] {
+    require(model && state && (prompt || n == 0) && n >= 0, "null argument");
+    model->lm->enqueue_prefill(state->st, std::vector<int32_t>(prompt, prompt + n));
+  });
+}
+
+int mmr_enqueue_decode(const mmr_model* model, mmr_state* state, int64_t steps, int32_t first_token) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->enqueue_decode(state->st, steps, first_token);
+  });
+}
+
+int mmr_state_synchronize(const mmr_model* model, mmr_state* state) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->synchronize(state->st);
+  });
+}
+
+int mmr_read_sequence(const mmr_model* model, mmr_state* state, int64_t first, int64_t count, int32_t* out) {
+  return guarded([&] {
+    require(model && state && (out || count == 0), "null argument");
+    const auto ids = model->lm->read_sequence(state->st, first, count);
+    std::memcpy(out, ids.data(), ids.size() * sizeof(int32_t));
+  });
+}
+
+int mmr_read_logits(const mmr_model* model, mmr_state* state, float* logits) {
+  return guarded([&] {
+    require(model && state && logits, "null argument");
+    const auto v = model->lm->read_logits(state->st);
+    std::memcpy(logits, v.data(), v.size() * sizeof(float));
+  });
+}
+
+int mmr_launch_step_kernel(const mmr_model* model, mmr_state* state, int kernel, int64_t layer, int64_t count) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->enqueue_kernel(state->st, kernel, layer, count);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,250 @@
+// gemv_impl.h -- batch-1 fp16-weight GEMV family for gfx950.
+//
+// Replaces the reference's projection matvec (decoder_layer.cpp:65-90 on the
+// CPU, aclnnMm through device_matmul at ascend_matmul.cpp:385-410) and the
+// lm_head matvec + argmax (language_model.cpp:326-332, device_matmul_argmax at
+// ascend_matmul.cpp:467-497).
+//
+// Design: the op is HBM-bound (about 1 FLOP per weight byte), so the kernel is
+// built around getting every weight byte in flight at once.
+//  * W is row-major [rows][k] fp16.  A group of G lanes (16/32/64) owns RPG
+//    consecutive rows; lane j reads 16-byte chunks j, j+G, ... of each row, so
+//    every load instruction of a group covers G*16 contiguous bytes.
+//  * All RPG*CPL weight loads of a lane are issued before any arithmetic, so
+//    one memory latency covers the whole tile.
+//  * x (fp32) lives in registers: each lane only needs the chunks it multiplies.
+//  * Fused prologues (RMSNorm / embedding gather) and epilogues (residual add,
+//    SwiGLU over interleaved gate/up rows, first-index argmax with a
+//    last-block-done reduction) remove the separate elementwise launches of
+//    the reference (K1, K4, K5, L2, L3).
+#pragma once
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace mmr {
+namespace gemv_detail {
+
+template <int G, int RPG, int CPL, int PRO, int EPI>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
+  constexpr int kGroups = kGemvBlock / G;
+  const int lane = threadIdx.x % G;
+  const int group = threadIdx.x / G;
+  const int k = a.k;
+  const int kchunks = k >> 3;
+  const int row0 = (blockIdx.x * kGroups + group) * RPG;
+
+  // 1. Weight loads, issued first: they do not depend on x.
+  uint4 wv[RPG][CPL];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    const int row = row0 + r;
+    const uint4* wrow = reinterpret_cast<const uint4*>(a.w + static_cast<int64_t>(row) * k);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + G * i;
+      if (row < a.rows && c < kchunks) {
+        wv[r][i] = wrow[c];
+      } else {
+        wv[r][i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+
+  // 2. x chunks owned by this lane (+ fused prologue).
+  float xv[CPL][8];
+  if constexpr (PRO == kProEmbedRmsNorm) {
+    int token = a.seq[*a.pos];
+    token = token < 0 ? 0 : (token >= a.vocab ? a.vocab - 1 : token);
+    const uint4* erow = reinterpret_cast<const uint4*>(a.embed + static_cast<int64_t>(token) * k);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + G * i;
+      if (c < kchunks) {
+        half8_to_float8(erow[c], xv[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
+      }
+    }
+    if (blockIdx.x == 0 && group == 0) {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = lane + G * i;
+        if (c < kchunks) {
+          float4* dst = reinterpret_cast<float4*>(a.h_out + c * 8);
+          dst[0] = make_float4(xv[i][0], xv[i][1], xv[i][2], xv[i][3]);
+          dst[1] = make_float4(xv[i][4], xv[i][5], xv[i][6], xv[i][7]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + G * i;
+      if (c < kchunks) {
+        const float4* src = reinterpret_cast<const float4*>(a.x + c * 8);
+        const float4 lo = src[0];
+        const float4 hi = src[1];
+        xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
+        xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
+      }
+    }
+  }
+
+  if constexpr (PRO != kProPlain) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += xv[i][e] * xv[i][e];
+    ss = group_sum<G>(ss);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(k) + a.eps);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + G * i;
+      if (c < kchunks) {
+        const float4* nw = reinterpret_cast<const float4*>(a.norm_w + c * 8);
+        const float4 lo = nw[0];
+        const float4 hi = nw[1];
+        const float w8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (PRO == kProRmsNormFinal) {
+            xv[i][e] = (xv[i][e] * scale) * w8[e];
+          } else {
+            xv[i][e] = xv[i][e] * (scale * w8[e]);
+          }
+        }
+      }
+    }
+  }
+
+  // 3. Dot products, fp32 accumulation, butterfly reduce over the group.
+  float acc[RPG];
+#pragma unroll
+  for (int r = 0; r < RPG; ++r) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      float wf[8];
+      half8_to_float8(wv[r][i], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s = fmaf(wf[e], xv[i][e], s);
+    }
+    acc[r] = group_sum<G>(s);
+  }
+
+  // 4. Epilogue.
+  if constexpr (EPI == kEpiStore || EPI == kEpiResidual) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RPG; ++r) {
+        const int row = row0 + r;
+        if (row < a.rows) {
+          if constexpr (EPI == kEpiResidual) {
+            a.y[row] = a.residual[row] + acc[r];
+          } else {
+            a.y[row] = acc[r];
+          }
+        }
+      }
+    }
+  } else if constexpr (EPI == kEpiSwiGlu) {
+    static_assert(RPG % 2 == 0, "SwiGLU needs (gate, up) row pairs");
+    if (lane == 0) {
+#pragma unroll
+      for (int p = 0; p < RPG / 2; ++p) {
+        const int row = row0 + 2 * p;
+        if (row + 1 < a.rows) {
+          const float g = acc[2 * p];
+          const float u = acc[2 * p + 1];
+          a.y[row / 2] = (g / (1.0f + expf(-g))) * u;
+        }
+      }
+    }
+  } else {  // kEpiArgmax
+    constexpr int kRowsPerBlock = kGroups * RPG;
+    __shared__ float s_val[kRowsPerBlock];
+    __shared__ int s_idx[kRowsPerBlock];
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RPG; ++r) {
+        const int row = row0 + r;
+        const bool ok = row < a.rows;
+        if (ok && a.y) a.y[row] = acc[r];
+        s_val[group * RPG + r] = ok ? acc[r] : -INFINITY;
+        s_idx[group * RPG + r] = ok ? row : 0x7fffffff;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = s_val[0];
+      int bi = s_idx[0];
+      for (int j = 1; j < kRowsPerBlock; ++j)
+        if (argmax_better(s_val[j], s_idx[j], bv, bi)) {
+          bv = s_val[j];
+          bi = s_idx[j];
+        }
+      if (bi != 0x7fffffff) atomicMax(a.best, argmax_key(bv, bi));
+    }
+    if (last_block_ticket(a.counter, gridDim.x)) {
+      if (threadIdx.x == 0) {
+        const int32_t next = argmax_key_index(atomicExch(a.best, 0ull));
+        if (a.token_out) *a.token_out = next;
+        if (a.step_pos) {
+          const int32_t p = *a.step_pos;
+          if (p + 1 < a.seq_len && p + 1 >= *a.step_prompt_len) a.step_seq[p + 1] = next;
+          *a.step_pos = p + 1;
+        }
+      }
+    }
+  }
+}
+
+template <int G, int RPG, int CPL>
+hipError_t launch_shape(const GemvArgs& a, GemvPrologue pro, GemvEpilogue epi, int blocks, hipStream_t s) {
+  const dim3 grid(blocks), block(kGemvBlock);
+#define MMR_GEMV_CASE(P, E)                                                           \
+  if (pro == P && epi == E) {                                                         \
+    gemv_kernel<G, RPG, CPL, P, E><<<grid, block, 0, s>>>(a);                         \
+    return hipGetLastError();                                                         \
+  }
+  MMR_GEMV_CASE(kProPlain, kEpiStore)
+  MMR_GEMV_CASE(kProPlain, kEpiResidual)
+  MMR_GEMV_CASE(kProRmsNorm, kEpiStore)
+  MMR_GEMV_CASE(kProEmbedRmsNorm, kEpiStore)
+  MMR_GEMV_CASE(kProRmsNormFinal, kEpiArgmax)
+  MMR_GEMV_CASE(kProPlain, kEpiArgmax)
+  if constexpr (RPG % 2 == 0) {
+    MMR_GEMV_CASE(kProRmsNorm, kEpiSwiGlu)
+    MMR_GEMV_CASE(kProPlain, kEpiSwiGlu)
+  }
+#undef MMR_GEMV_CASE
+  return hipErrorInvalidValue;
+}
+
+template <int G, int RPG>
+hipError_t launch_cpl_impl(const GemvArgs& a, GemvPrologue pro, GemvEpilogue epi, int cpl, int blocks,
+                      hipStream_t s) {
+  switch (cpl) {
+    case 1: return launch_shape<G, RPG, 1>(a, pro, epi, blocks, s);
+    case 2: return launch_shape<G, RPG, 2>(a, pro, epi, blocks, s);
+    case 3: return launch_shape<G, RPG, 3>(a, pro, epi, blocks, s);
+    case 4: return launch_shape<G, RPG, 4>(a, pro, epi, blocks, s);
+    case 6: return launch_shape<G, RPG, 6>(a, pro, epi, blocks, s);
+    case 8: return launch_shape<G, RPG, 8>(a, pro, epi, blocks, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace gemv_detail
+
+// Defined in gemv_g16.hip / gemv_g32.hip / gemv_g64.hip (one TU per lane width).
+template <int G, int RPG>
+hipError_t launch_cpl(const GemvArgs& a, GemvPrologue pro, GemvEpilogue epi, int cpl, int blocks, hipStream_t s);
+
+}  // namespace mmr

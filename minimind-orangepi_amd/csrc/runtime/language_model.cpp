@@ -1,0 +1,644 @@
+// language_model.cpp -- device-resident decode step and the reference-shaped
+// model API on top of it.
+//
+// One decode step (language_model.cpp:310-333 + decoder_layer.cpp:312-407 of
+// the reference) is 5 kernels per layer plus one for the head:
+//   qkv   GEMV  RMSNorm prologue (layer 0: embedding gather of seq[pos])
+//   attn        q/k RMSNorm + RoPE, K/V append at pos, split-context GQA
+//               attention with log-sum-exp combine
+//   o     GEMV  residual epilogue  (h += W_o attn)
+//   gu    GEMV  RMSNorm prologue, SwiGLU epilogue over interleaved gate/up rows
+//   down  GEMV  residual epilogue  (h += W_down act)
+//   head  GEMV  final RMSNorm prologue, first-index argmax epilogue; writes
+//               seq[pos + 1] and advances pos on the device
+// Every kernel reads the position from device memory, so the step is captured
+// once into a hipGraph (per attention split count) and replayed per token.
+#include "language_model.h"
+
+#include "device.h"
+#include "../kernels/kernels.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <filesystem>
+#include <map>
+#include <stdexcept>
+
+namespace minimind::model {
+
+struct LayerDev {
+  const float* input_norm = nullptr;
+  const float* post_norm = nullptr;
+  const float* q_norm = nullptr;
+  const float* k_norm = nullptr;
+  const __half* qkv = nullptr;      // [(Hq + 2 Hkv) d][H]  rows q | k | v
+  const __half* o = nullptr;        // [H][Hq d]
+  const __half* gate_up = nullptr;  // [2F][H]  rows gate_0, up_0, gate_1, up_1, ...
+  const __half* down = nullptr;     // [H][F]
+};
+
+struct DeviceModel {
+  MiniMindConfig cfg;
+  Arena arena;
+  const __half* embed = nullptr;    // [V][H]
+  const __half* lm_head = nullptr;  // [V][H] (aliases embed when identical)
+  const float* final_norm = nullptr;
+  std::vector<LayerDev> layers;
+  const float* rope_cos = nullptr;  // [max_pos][d/2], same formula as decoder_layer.cpp:109-119
+  const float* rope_sin = nullptr;
+  mmr::GemvPlan plan_qkv, plan_o, plan_gu, plan_down, plan_lm;
+  std::size_t weight_bytes = 0;
+};
+
+struct DeviceState {
+  std::shared_ptr<const DeviceModel> model;
+  mmr::KvDtype kv = mmr::kKvF32;
+  int64_t capacity = 0;
+  Arena arena;
+  std::vector<void*> kcache, vcache;
+  int32_t* seq = nullptr;  // [capacity + 1]
+  int32_t* pos = nullptr;
+  int32_t* prompt_len = nullptr;
+  int32_t* err = nullptr;
+  int32_t* token_out = nullptr;
+  float* h = nullptr;
+  float* qkv = nullptr;
+  float* attn = nullptr;
+  float* act = nullptr;
+  float* logits = nullptr;
+  float* attn_part = nullptr;
+  unsigned long long* lm_best = nullptr;  // packed argmax key of the head GEMV
+  unsigned int* counters = nullptr;       // [Hkv] attention, [1] head
+  int32_t* staging = nullptr;        // pinned host [capacity + 8]
+  hipStream_t stream = nullptr;
+  std::map<int, hipGraphExec_t> graphs;
+  bool use_graphs = true;
+
+  ~DeviceState() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    if (stream) (void)hipStreamDestroy(stream);
+    if (staging) (void)hipHostFree(staging);
+  }
+};
+
+namespace {
+
+constexpr int kSplitBuckets[] = {8, 32, 128, 512};
+constexpr int kMaxSplits = 512;
+
+void require_size(const std::vector<float>& v, int64_t expected, const std::string& name) {
+  if (static_cast<int64_t>(v.size()) != expected) throw std::invalid_argument(name + " has invalid size");
+}
+
+int choose_splits(int64_t n_keys, int tile) {
+  const int64_t n_tiles = (n_keys + tile - 1) / tile;
+  for (int s : kSplitBuckets)
+    if (s >= n_tiles) return s;
+  return kMaxSplits;
+}
+
+std::vector<uint16_t> to_half(const std::vector<float>& v) {
+  std::vector<uint16_t> out(v.size());
+  for (size_t i = 0; i < v.size(); ++i) out[i] = float_to_half(v[i]);
+  return out;
+}
+
+template <typename T>
+T* upload(Arena& arena, const void* host, std::size_t count) {
+  T* dst = arena.take<T>(count);
+  check_hip(hipMemcpy(dst, host, count * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy weights");
+  return dst;
+}
+
+mmr::GemvPlan plan_or_throw(int rows, int k, mmr::GemvEpilogue epi, const char* name) {
+  mmr::GemvPlan p;
+  if (!mmr::gemv_plan(rows, k, epi, 0, 0, &p))
+    throw std::invalid_argument(std::string("unsupported GEMV shape for ") + name);
+  return p;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ state --
+
+DecoderState::DecoderState() = default;
+DecoderState::~DecoderState() = default;
+DecoderState::DecoderState(DecoderState&&) noexcept = default;
+DecoderState& DecoderState::operator=(DecoderState&&) noexcept = default;
+int64_t DecoderState::capacity() const { return device ? device->capacity : 0; }
+KvCacheDtype DecoderState::kv_dtype() const {
+  return device && device->kv == mmr::kKvF16 ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32;
+}
+void* DecoderState::stream() const { return device ? static_cast<void*>(device->stream) : nullptr; }
+
+// ------------------------------------------------------------------ model --
+
+LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) : config_(std::move(config)) {
+  const auto errors = validate_config(config_);
+  if (!errors.empty()) throw std::invalid_argument("invalid MiniMind config: " + errors.front());
+  const auto dev_errors = validate_device_config(config_);
+  if (!dev_errors.empty()) throw std::invalid_argument("unsupported by the gfx950 runtime: " + dev_errors.front());
+  const auto& c = config_;
+  const int64_t H = c.hidden_size, V = c.vocab_size, D = c.head_dim, F = c.intermediate_size;
+  const int64_t qs = c.num_attention_heads * D, kvs = c.num_key_value_heads * D;
+  require_size(weights.embed_tokens, V * H, "embed_tokens");
+  require_size(weights.final_norm, H, "final_norm");
+  require_size(weights.lm_head, V * H, "lm_head");
+  if (static_cast<int64_t>(weights.layers.size()) != c.num_hidden_layers)
+    throw std::invalid_argument("layer weight count does not match config");
+  for (const auto& L : weights.layers) {
+    require_size(L.input_norm, H, "input_norm");
+    require_size(L.post_attention_norm, H, "post_attention_norm");
+    require_size(L.q_norm, D, "q_norm");
+    require_size(L.k_norm, D, "k_norm");
+    require_size(L.q_proj, qs * H, "q_proj");
+    require_size(L.k_proj, kvs * H, "k_proj");
+    require_size(L.v_proj, kvs * H, "v_proj");
+    require_size(L.o_proj, H * qs, "o_proj");
+    require_size(L.gate_proj, F * H, "gate_proj");
+    require_size(L.up_proj, F * H, "up_proj");
+    require_size(L.down_proj, H * F, "down_proj");
+  }
+
+  auto dm = std::make_shared<DeviceModel>();
+  dm->cfg = c;
+  const bool share_head = weights.lm_head == weights.embed_tokens;
+  const int64_t half_d = D / 2;
+  const int64_t max_pos = c.max_position_embeddings;
+  Arena& ar = dm->arena;
+  ar.plan(V * H * 2);
+  if (!share_head) ar.plan(V * H * 2);
+  ar.plan(H * 4);
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+    ar.plan(H * 4);
+    ar.plan(H * 4);
+    ar.plan(D * 4);
+    ar.plan(D * 4);
+    ar.plan((qs + 2 * kvs) * H * 2);
+    ar.plan(H * qs * 2);
+    ar.plan(2 * F * H * 2);
+    ar.plan(H * F * 2);
+  }
+  ar.plan(max_pos * half_d * 4);
+  ar.plan(max_pos * half_d * 4);
+  ar.allocate();
+
+  dm->embed = upload<__half>(ar, to_half(weights.embed_tokens).data(), V * H);
+  dm->lm_head = share_head ? dm->embed : upload<__half>(ar, to_half(weights.lm_head).data(), V * H);
+  dm->final_norm = upload<float>(ar, weights.final_norm.data(), H);
+  std::size_t wbytes = V * H * 2 * (share_head ? 1 : 2) + H * 4;
+  for (const auto& L : weights.layers) {
+    LayerDev d;
+    d.input_norm = upload<float>(ar, L.input_norm.data(), H);
+    d.post_norm = upload<float>(ar, L.post_attention_norm.data(), H);
+    d.q_norm = upload<float>(ar, L.q_norm.data(), D);
+    d.k_norm = upload<float>(ar, L.k_norm.data(), D);
+    std::vector<float> qkv;
+    qkv.reserve((qs + 2 * kvs) * H);
+    qkv.insert(qkv.end(), L.q_proj.begin(), L.q_proj.end());
+    qkv.insert(qkv.end(), L.k_proj.begin(), L.k_proj.end());
+    qkv.insert(qkv.end(), L.v_proj.begin(), L.v_proj.end());
+    d.qkv = upload<__half>(ar, to_half(qkv).data(), qkv.size());
+    d.o = upload<__half>(ar, to_half(L.o_proj).data(), L.o_proj.size());
+    std::vector<uint16_t> gu(static_cast<size_t>(2 * F * H));
+    for (int64_t r = 0; r < F; ++r)
+      for (int64_t k = 0; k < H; ++k) {
+        gu[static_cast<size_t>((2 * r) * H + k)] = float_to_half(L.gate_proj[static_cast<size_t>(r * H + k)]);
+        gu[static_cast<size_t>((2 * r + 1) * H + k)] = float_to_half(L.up_proj[static_cast<size_t>(r * H + k)]);
+      }
+    d.gate_up = upload<__half>(ar, gu.data(), gu.size());
+    d.down = upload<__half>(ar, to_half(L.down_proj).data(), L.down_proj.size());
+    dm->layers.push_back(d);
+    wbytes += 2 * H * 4 + 2 * D * 4 + ((qs + 2 * kvs) * H + H * qs + 2 * F * H + H * F) * 2;
+  }
+  // RoPE tables with the reference formula (decoder_layer.cpp:109-119):
+  // inv_freq = 1 / powf(theta, 2i / d), angle = float(pos) * inv_freq.
+  {
+    std::vector<float> inv(static_cast<size_t>(half_d));
+    for (int64_t i = 0; i < half_d; ++i)
+      inv[static_cast<size_t>(i)] =
+          1.0F / std::pow(c.rope_theta, static_cast<float>(i * 2) / static_cast<float>(D));
+    std::vector<float> cs(static_cast<size_t>(max_pos * half_d)), sn(cs.size());
+    for (int64_t p = 0; p < max_pos; ++p)
+      for (int64_t i = 0; i < half_d; ++i) {
+        const float angle = static_cast<float>(p) * inv[static_cast<size_t>(i)];
+        cs[static_cast<size_t>(p * half_d + i)] = std::cos(angle);
+        sn[static_cast<size_t>(p * half_d + i)] = std::sin(angle);
+      }
+    dm->rope_cos = upload<float>(ar, cs.data(), cs.size());
+    dm->rope_sin = upload<float>(ar, sn.data(), sn.size());
+  }
+  dm->weight_bytes = wbytes;
+  dm->plan_qkv = plan_or_throw(static_cast<int>(qs + 2 * kvs), static_cast<int>(H), mmr::kEpiStore, "qkv_proj");
+  dm->plan_o = plan_or_throw(static_cast<int>(H), static_cast<int>(qs), mmr::kEpiResidual, "o_proj");
+  dm->plan_gu = plan_or_throw(static_cast<int>(2 * F), static_cast<int>(H), mmr::kEpiSwiGlu, "gate_up_proj");
+  dm->plan_down = plan_or_throw(static_cast<int>(H), static_cast<int>(F), mmr::kEpiResidual, "down_proj");
+  dm->plan_lm = plan_or_throw(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, "lm_head");
+  check_hip(hipDeviceSynchronize(), "weight upload");
+  device_ = std::move(dm);
+}
+
+LanguageModel::~LanguageModel() = default;
+LanguageModel::LanguageModel(LanguageModel&&) noexcept = default;
+LanguageModel& LanguageModel::operator=(LanguageModel&&) noexcept = default;
+
+std::size_t LanguageModel::device_weight_bytes() const { return device_->weight_bytes; }
+
+DecoderState LanguageModel::make_state() const { return make_state(0, KvCacheDtype::kFloat32); }
+
+DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const {
+  const auto& c = config_;
+  if (capacity <= 0) capacity = c.max_position_embeddings;
+  if (capacity > c.max_position_embeddings)
+    throw std::invalid_argument("state capacity exceeds max_position_embeddings");
+  auto s = std::make_unique<DeviceState>();
+  s->model = device_;
+  s->kv = kv == KvCacheDtype::kFloat16 ? mmr::kKvF16 : mmr::kKvF32;
+  s->capacity = capacity;
+  const char* nog = std::getenv("MMR_NO_GRAPH");
+  s->use_graphs = !(nog && nog[0] == '1');
+  const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
+  const int64_t F = c.intermediate_size, V = c.vocab_size;
+  const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
+  const std::size_t cache_bytes = static_cast<std::size_t>(Hkv * capacity * D) * kv_elem;
+  Arena& ar = s->arena;
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+    ar.plan(cache_bytes);
+    ar.plan(cache_bytes);
+  }
+  const std::size_t part_floats =
+      mmr::attention_partial_floats(static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(D), kMaxSplits);
+  ar.plan((capacity + 1) * 4);
+  ar.plan(4 * 4);  // pos, prompt_len, err, token_out
+  ar.plan(H * 4);
+  ar.plan((Hq * D + 2 * Hkv * D) * 4);
+  ar.plan(Hq * D * 4);
+  ar.plan(F * 4);
+  ar.plan(V * 4);
+  ar.plan(part_floats * 4);
+  ar.plan(8);
+  ar.plan((Hkv + 1) * 4);
+  ar.allocate();
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+    s->kcache.push_back(ar.take<char>(cache_bytes));
+    s->vcache.push_back(ar.take<char>(cache_bytes));
+  }
+  s->seq = ar.take<int32_t>(capacity + 1);
+  int32_t* scalars = ar.take<int32_t>(4);
+  s->pos = scalars;
+  s->prompt_len = scalars + 1;
+  s->err = scalars + 2;
+  s->token_out = scalars + 3;
+  s->h = ar.take<float>(H);
+  s->qkv = ar.take<float>(Hq * D + 2 * Hkv * D);
+  s->attn = ar.take<float>(Hq * D);
+  s->act = ar.take<float>(F);
+  s->logits = ar.take<float>(V);
+  s->attn_part = ar.take<float>(part_floats);
+  s->lm_best = ar.take<unsigned long long>(1);
+  s->counters = ar.take<unsigned int>(Hkv + 1);
+  check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
+                          hipHostMallocDefault),
+            "hipHostMalloc staging");
+  check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+  check_hip(hipMemsetAsync(scalars, 0, 4 * sizeof(int32_t), s->stream), "hipMemsetAsync");
+  check_hip(hipMemsetAsync(s->counters, 0, (Hkv + 1) * sizeof(unsigned int), s->stream), "hipMemsetAsync");
+  check_hip(hipMemsetAsync(s->lm_best, 0, sizeof(unsigned long long), s->stream), "hipMemsetAsync");
+  check_hip(hipMemsetAsync(s->seq, 0, (capacity + 1) * sizeof(int32_t), s->stream), "hipMemsetAsync");
+  check_hip(hipStreamSynchronize(s->stream), "state init");
+  DecoderState state;
+  state.device = std::move(s);
+  state.position = 0;
+  return state;
+}
+
+namespace {
+
+enum StepKernel : int { kQkv = 0, kAttention = 1, kOProj = 2, kGateUp = 3, kDown = 4, kHead = 5 };
+
+// One kernel of the decode step; `bookkeeping` (head only) lets the argmax
+// write seq[pos + 1] and advance the device position.
+void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool bookkeeping) {
+  const DeviceModel& m = *s.model;
+  const auto& c = m.cfg;
+  const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
+  const int Hq = static_cast<int>(c.num_attention_heads), Hkv = static_cast<int>(c.num_key_value_heads);
+  const int F = static_cast<int>(c.intermediate_size), V = static_cast<int>(c.vocab_size);
+  const int qkv_rows = (Hq + 2 * Hkv) * D;
+  const LayerDev& L = m.layers[l];
+  switch (kernel) {
+    case kQkv: {
+      mmr::GemvArgs a;
+      a.w = L.qkv;
+      a.rows = qkv_rows;
+      a.k = H;
+      a.x = s.h;
+      a.norm_w = L.input_norm;
+      a.eps = c.rms_norm_eps;
+      a.y = s.qkv;
+      mmr::GemvPrologue pro = mmr::kProRmsNorm;
+      if (l == 0) {
+        pro = mmr::kProEmbedRmsNorm;
+        a.embed = m.embed;
+        a.seq = s.seq;
+        a.pos = s.pos;
+        a.vocab = V;
+        a.h_out = s.h;
+      }
+      check_hip(mmr::launch_gemv(a, pro, mmr::kEpiStore, m.plan_qkv, s.stream), "qkv gemv");
+      return;
+    }
+    case kAttention: {
+      mmr::AttnArgs t;
+      t.qkv = s.qkv;
+      t.q_norm = L.q_norm;
+      t.k_norm = L.k_norm;
+      t.eps = c.rms_norm_eps;
+      t.rope_cos = m.rope_cos;
+      t.rope_sin = m.rope_sin;
+      t.pos = s.pos;
+      t.kcache = s.kcache[l];
+      t.vcache = s.vcache[l];
+      t.capacity = static_cast<int>(s.capacity);
+      t.max_pos = static_cast<int>(c.max_position_embeddings);
+      t.hq = Hq;
+      t.hkv = Hkv;
+      t.d = D;
+      t.splits = splits;
+      t.part = s.attn_part;
+      t.counters = s.counters;
+      t.out = s.attn;
+      t.err = s.err;
+      check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "attention");
+      return;
+    }
+    case kOProj: {
+      mmr::GemvArgs a;
+      a.w = L.o;
+      a.rows = H;
+      a.k = Hq * D;
+      a.x = s.attn;
+      a.y = s.h;
+      a.residual = s.h;
+      check_hip(mmr::launch_gemv(a, mmr::kProPlain, mmr::kEpiResidual, m.plan_o, s.stream), "o gemv");
+      return;
+    }
+    case kGateUp: {
+      mmr::GemvArgs a;
+      a.w = L.gate_up;
+      a.rows = 2 * F;
+      a.k = H;
+      a.x = s.h;
+      a.norm_w = L.post_norm;
+      a.eps = c.rms_norm_eps;
+      a.y = s.act;
+      check_hip(mmr::launch_gemv(a, mmr::kProRmsNorm, mmr::kEpiSwiGlu, m.plan_gu, s.stream), "gate_up gemv");
+      return;
+    }
+    case kDown: {
+      mmr::GemvArgs a;
+      a.w = L.down;
+      a.rows = H;
+      a.k = F;
+      a.x = s.act;
+      a.y = s.h;
+      a.residual = s.h;
+      check_hip(mmr::launch_gemv(a, mmr::kProPlain, mmr::kEpiResidual, m.plan_down, s.stream), "down gemv");
+      return;
+    }
+    case kHead: {
+      mmr::GemvArgs a;
+      a.w = m.lm_head;
+      a.rows = V;
+      a.k = H;
+      a.x = s.h;
+      a.norm_w = m.final_norm;
+      a.eps = c.rms_norm_eps;
+      a.y = s.logits;
+      a.best = s.lm_best;
+      a.counter = s.counters + Hkv;
+      a.token_out = s.token_out;
+      if (bookkeeping) {
+        a.step_seq = s.seq;
+        a.step_pos = s.pos;
+        a.step_prompt_len = s.prompt_len;
+        a.seq_len = static_cast<int>(s.capacity + 1);
+      }
+      check_hip(mmr::launch_gemv(a, mmr::kProRmsNormFinal, mmr::kEpiArgmax, m.plan_lm, s.stream), "lm_head gemv");
+      return;
+    }
+    default:
+      throw std::invalid_argument("unknown step kernel");
+  }
+}
+
+void enqueue_step_kernels(const DeviceState& s, int splits) {
+  for (size_t l = 0; l < s.model->layers.size(); ++l)
+    for (int k = kQkv; k <= kDown; ++k) enqueue_kernel(s, k, l, splits, false);
+  enqueue_kernel(s, kHead, 0, splits, true);
+}
+
+hipGraphExec_t capture_step(DeviceState& s, int splits) {
+  hipGraph_t graph = nullptr;
+  check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    enqueue_step_kernels(s, splits);
+  } catch (...) {
+    (void)hipStreamEndCapture(s.stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+    throw;
+  }
+  check_hip(hipStreamEndCapture(s.stream, &graph), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  check_hip(st, "hipGraphInstantiate");
+  return exec;
+}
+
+void check_token(const MiniMindConfig& c, int32_t token) {
+  if (token < 0 || token >= c.vocab_size) throw std::out_of_range("token id out of vocabulary range");
+}
+
+}  // namespace
+
+void LanguageModel::launch_step(DecoderState& state) const {
+  DeviceState& s = *state.device;
+  if (state.position >= s.capacity) throw std::length_error("KV cache capacity exhausted");
+  const int splits = choose_splits(state.position + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  if (s.use_graphs) {
+    auto it = s.graphs.find(splits);
+    if (it == s.graphs.end()) it = s.graphs.emplace(splits, capture_step(s, splits)).first;
+    check_hip(hipGraphLaunch(it->second, s.stream), "hipGraphLaunch");
+  } else {
+    enqueue_step_kernels(s, splits);
+  }
+  state.position += 1;
+}
+
+void LanguageModel::synchronize(DecoderState& state) const {
+  DeviceState& s = *state.device;
+  check_hip(hipMemcpyAsync(s.staging + s.capacity + 4, s.err, sizeof(int32_t), hipMemcpyDeviceToHost, s.stream),
+            "hipMemcpyAsync err");
+  check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+  if (s.staging[s.capacity + 4] != 0) throw std::runtime_error("device kernel reported an out-of-range position");
+}
+
+void LanguageModel::enqueue_decode(DecoderState& state, int64_t n, int32_t first_token) const {
+  DeviceState& s = *state.device;
+  if (n < 0) throw std::invalid_argument("step count cannot be negative");
+  if (state.position + n > s.capacity) throw std::length_error("KV cache capacity exhausted");
+  if (first_token >= 0) {
+    check_token(config_, first_token);
+    check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    s.staging[0] = first_token;
+    check_hip(hipMemcpyAsync(s.seq + state.position, s.staging, sizeof(int32_t), hipMemcpyHostToDevice, s.stream),
+              "hipMemcpyAsync token");
+  }
+  for (int64_t i = 0; i < n; ++i) launch_step(state);
+}
+
+void LanguageModel::enqueue_prefill(DecoderState& state, const std::vector<int32_t>& prompt) const {
+  DeviceState& s = *state.device;
+  if (prompt.empty()) throw std::invalid_argument("prompt_tokens cannot be empty");
+  for (int32_t t : prompt) check_token(config_, t);
+  const int64_t n = static_cast<int64_t>(prompt.size());
+  if (state.position + n > s.capacity) throw std::length_error("KV cache capacity exhausted");
+  check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+  std::memcpy(s.staging, prompt.data(), prompt.size() * sizeof(int32_t));
+  s.staging[s.capacity + 1] = static_cast<int32_t>(state.position + n);
+  check_hip(hipMemcpyAsync(s.seq + state.position, s.staging, prompt.size() * sizeof(int32_t),
+                           hipMemcpyHostToDevice, s.stream),
+            "hipMemcpyAsync prompt");
+  check_hip(hipMemcpyAsync(s.prompt_len, s.staging + s.capacity + 1, sizeof(int32_t), hipMemcpyHostToDevice,
+                           s.stream),
+            "hipMemcpyAsync prompt_len");
+  for (int64_t i = 0; i < n; ++i) launch_step(state);
+}
+
+void LanguageModel::enqueue_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const {
+  DeviceState& s = *state.device;
+  const int64_t L = config_.num_hidden_layers;
+  if (kernel < kQkv || kernel > kHead) throw std::invalid_argument("unknown step kernel");
+  if (layer < 0 || layer >= L || count < 0) throw std::invalid_argument("layer / count out of range");
+  if (kernel == kAttention && state.position >= s.capacity) throw std::length_error("KV cache capacity exhausted");
+  const int splits = choose_splits(state.position + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  for (int64_t i = 0; i < count; ++i)
+    ::minimind::model::enqueue_kernel(s, kernel, static_cast<size_t>((layer + i) % L), splits, false);
+}
+
+std::vector<int32_t> LanguageModel::read_sequence(DecoderState& state, int64_t first, int64_t count) const {
+  DeviceState& s = *state.device;
+  if (first < 0 || count < 0 || first + count > s.capacity + 1) throw std::out_of_range("sequence range");
+  std::vector<int32_t> out(static_cast<size_t>(count));
+  check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+  if (count > 0) {
+    check_hip(hipMemcpyAsync(s.staging, s.seq + first, count * sizeof(int32_t), hipMemcpyDeviceToHost, s.stream),
+              "hipMemcpyAsync seq");
+    synchronize(state);
+    std::memcpy(out.data(), s.staging, count * sizeof(int32_t));
+  }
+  return out;
+}
+
+std::vector<float> LanguageModel::read_logits(DecoderState& state) const {
+  DeviceState& s = *state.device;
+  std::vector<float> out(static_cast<size_t>(config_.vocab_size));
+  check_hip(hipMemcpyAsync(out.data(), s.logits, out.size() * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+            "hipMemcpyAsync logits");
+  synchronize(state);
+  return out;
+}
+
+void LanguageModel::reset_state(DecoderState& state) const {
+  DeviceState& s = *state.device;
+  check_hip(hipMemsetAsync(s.pos, 0, 2 * sizeof(int32_t), s.stream), "hipMemsetAsync");
+  check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+  state.position = 0;
+}
+
+std::vector<float> LanguageModel::forward_token(int32_t token, DecoderState& state) const {
+  check_token(config_, token);
+  enqueue_decode(state, 1, token);
+  return read_logits(state);
+}
+
+int32_t LanguageModel::forward_next_token(int32_t token, DecoderState& state) const {
+  check_token(config_, token);
+  const int64_t p = state.position;
+  enqueue_decode(state, 1, token);
+  DeviceState& s = *state.device;
+  check_hip(hipMemcpyAsync(s.staging, s.seq + p + 1, sizeof(int32_t), hipMemcpyDeviceToHost, s.stream),
+            "hipMemcpyAsync next");
+  synchronize(state);
+  return s.staging[0];
+}
+
+int32_t LanguageModel::prefill_next_token(const std::vector<int32_t>& prompt_tokens, DecoderState& state) const {
+  if (prompt_tokens.empty()) throw std::invalid_argument("prompt_tokens cannot be empty");
+  if (state.position != 0) throw std::invalid_argument("prefill layer requires an empty KV cache");
+  enqueue_prefill(state, prompt_tokens);
+  DeviceState& s = *state.device;
+  check_hip(hipMemcpyAsync(s.staging, s.seq + state.position, sizeof(int32_t), hipMemcpyDeviceToHost, s.stream),
+            "hipMemcpyAsync next");
+  synchronize(state);
+  return s.staging[0];
+}
+
+void LanguageModel::generate_stream(const std::vector<int32_t>& prompt_tokens, int64_t max_new_tokens,
+                                    const std::function<void(int32_t)>& on_token) const {
+  if (prompt_tokens.empty()) throw std::invalid_argument("prompt_tokens cannot be empty");
+  if (max_new_tokens < 0) throw std::invalid_argument("max_new_tokens cannot be negative");
+  const int64_t prompt_len = static_cast<int64_t>(prompt_tokens.size());
+  const int64_t needed = prompt_len + std::max<int64_t>(max_new_tokens, 1) - 1;
+  if (needed > config_.max_position_embeddings) throw std::length_error("sequence exceeds max_position_embeddings");
+  DecoderState state = make_state(std::max<int64_t>(needed, 1), KvCacheDtype::kFloat32);
+  enqueue_prefill(state, prompt_tokens);
+  // The prompt's last step predicts generated token 0 at seq[prompt_len].
+  // Further steps run ahead in small chunks; tokens after an EOS are computed
+  // but never emitted (language_model.cpp:389-395 stops after emitting EOS).
+  constexpr int64_t kChunk = 8;
+  int64_t emitted = 0;
+  while (emitted < max_new_tokens) {
+    const int64_t have = state.position - prompt_len + 1;  // generated ids present in seq
+    const int64_t want = std::min(max_new_tokens, have);
+    const auto ids = read_sequence(state, prompt_len + emitted, want - emitted);
+    for (int32_t id : ids) {
+      on_token(id);
+      ++emitted;
+      if (id == config_.eos_token_id) return;
+    }
+    if (emitted >= max_new_tokens) return;
+    const int64_t steps = std::min<int64_t>(kChunk, max_new_tokens - emitted);
+    enqueue_decode(state, steps);
+  }
+}
+
+std::vector<int32_t> LanguageModel::generate(const std::vector<int32_t>& prompt_tokens, int64_t max_new_tokens) const {
+  std::vector<int32_t> generated;
+  generated.reserve(static_cast<size_t>(std::max<int64_t>(max_new_tokens, 0)));
+  generate_stream(prompt_tokens, max_new_tokens, [&generated](int32_t t) { generated.push_back(t); });
+  return generated;
+}
+
+int32_t argmax_token(const std::vector<float>& logits) {
+  if (logits.empty()) throw std::invalid_argument("logits cannot be empty");
+  return static_cast<int32_t>(std::distance(logits.begin(), std::max_element(logits.begin(), logits.end())));
+}
+
+bool has_runtime_language_model(const std::string& model_dir) {
+  const std::filesystem::path dir(model_dir);
+  return std::filesystem::exists(dir / "minimind_runtime_config.txt") && std::filesystem::exists(dir / "weights.bin");
+}
+
+LanguageModel load_runtime_language_model(const std::string& model_dir) {
+  const std::filesystem::path dir(model_dir);
+  MiniMindConfig config = config_from_file((dir / "minimind_runtime_config.txt").string());
+  DenseModelWeights weights = read_weights(config, (dir / "weights.bin").string());
+  return LanguageModel(std::move(config), std::move(weights));
+}
+
+}  // namespace minimind::model

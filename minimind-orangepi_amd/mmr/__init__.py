@@ -1,0 +1,572 @@
+"""ctypes binding of libmmr.so, the MiniMind gfx950 decode runtime.
+
+Everything here is a thin wrapper over the C ABI declared in include/mmr.h.
+Device memory is plain HIP memory owned by DeviceArray objects (no torch):
+numpy arrays go in and out through explicit copies.
+
+The library must have been built (python minimind-orangepi_amd/build.py);
+importing this module without it raises ImportError instead of falling back to
+any CPU implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG / "lib" / "libmmr.so"
+
+if not LIB_PATH.exists():
+    raise ImportError(f"libmmr.so not built: run python {PKG / 'build.py'} (expected {LIB_PATH})")
+
+_lib = C.CDLL(str(LIB_PATH))
+
+OK, ERR_INVALID_ARGUMENT, ERR_OUT_OF_RANGE, ERR_RUNTIME, ERR_LENGTH = 0, 1, 2, 3, 4
+KV_F16, KV_F32 = 0, 1
+PRO_PLAIN, PRO_RMSNORM, PRO_RMSNORM_FINAL = 0, 1, 2
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
+KERNEL_QKV, KERNEL_ATTENTION, KERNEL_O, KERNEL_GATE_UP, KERNEL_DOWN, KERNEL_LM_HEAD = range(6)
+
+
+class MmrError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"mmr error {code}: {message}")
+        self.code = code
+
+
+class InvalidArgument(MmrError, ValueError):
+    pass
+
+
+class OutOfRange(MmrError, IndexError):
+    pass
+
+
+class LengthError(MmrError):
+    pass
+
+
+_ERRORS = {ERR_INVALID_ARGUMENT: InvalidArgument, ERR_OUT_OF_RANGE: OutOfRange, ERR_LENGTH: LengthError}
+
+
+class Config(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_int64),
+        ("num_hidden_layers", C.c_int64),
+        ("vocab_size", C.c_int64),
+        ("num_attention_heads", C.c_int64),
+        ("num_key_value_heads", C.c_int64),
+        ("head_dim", C.c_int64),
+        ("intermediate_size", C.c_int64),
+        ("max_position_embeddings", C.c_int64),
+        ("bos_token_id", C.c_int32),
+        ("eos_token_id", C.c_int32),
+        ("use_moe", C.c_int32),
+        ("tie_word_embeddings", C.c_int32),
+        ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_float),
+    ]
+
+    def as_dict(self) -> dict:
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+
+VP, I64, I32, U64, F32, SZ = C.c_void_p, C.c_int64, C.c_int32, C.c_uint64, C.c_float, C.c_size_t
+P_I32 = C.POINTER(C.c_int32)
+P_F32 = C.POINTER(C.c_float)
+
+_SIGS = {
+    "mmr_last_error": ([], C.c_char_p),
+    "mmr_version": ([], C.c_int),
+    "mmr_device_count": ([C.POINTER(C.c_int)], C.c_int),
+    "mmr_malloc": ([C.POINTER(VP), SZ], C.c_int),
+    "mmr_free": ([VP], C.c_int),
+    "mmr_memcpy_h2d": ([VP, VP, SZ], C.c_int),
+    "mmr_memcpy_d2h": ([VP, VP, SZ], C.c_int),
+    "mmr_memset": ([VP, C.c_int, SZ], C.c_int),
+    "mmr_stream_create": ([C.POINTER(VP)], C.c_int),
+    "mmr_stream_destroy": ([VP], C.c_int),
+    "mmr_stream_synchronize": ([VP], C.c_int),
+    "mmr_device_synchronize": ([], C.c_int),
+    "mmr_event_create": ([C.POINTER(VP)], C.c_int),
+    "mmr_event_destroy": ([VP], C.c_int),
+    "mmr_event_record": ([VP, VP], C.c_int),
+    "mmr_event_elapsed_ms": ([VP, VP, P_F32], C.c_int),
+    "mmr_f32_to_f16": ([VP, VP, SZ], C.c_int),
+    "mmr_f16_to_f32": ([VP, VP, SZ], C.c_int),
+    "mmr_matvec_f16": ([VP, I64, I64, VP, VP, VP, VP], C.c_int),
+    "mmr_matvec_f16_ex": ([VP, I64, I64, VP, VP, F32, C.c_int, C.c_int, VP, VP, C.c_int, C.c_int, VP], C.c_int),
+    "mmr_matvec_argmax_workspace_size": ([I64, I64], SZ),
+    "mmr_matvec_argmax_f16": ([VP, I64, I64, VP, VP, F32, VP, VP, VP, SZ, VP], C.c_int),
+    "mmr_rope_table_create": ([I64, I64, F32, C.POINTER(VP)], C.c_int),
+    "mmr_rope_table_destroy": ([VP], C.c_int),
+    "mmr_kv_cache_create": ([I64, I64, I64, C.c_int, C.POINTER(VP)], C.c_int),
+    "mmr_kv_cache_destroy": ([VP], C.c_int),
+    "mmr_kv_cache_data": ([VP, C.POINTER(VP), C.POINTER(VP)], C.c_int),
+    "mmr_decode_qkv_postprocess": ([VP, VP, VP, VP, I64, I64, I64, I64, I64, VP, F32, VP, VP], C.c_int),
+    "mmr_attention_workspace_size": ([I64, I64, I64, C.c_int], SZ),
+    "mmr_attention_from_cache": ([VP, VP, I64, I64, I64, I64, VP, VP, SZ, C.c_int, VP], C.c_int),
+    "mmr_decode_attention_fused": ([VP, VP, VP, F32, VP, VP, VP, I64, I64, I64, VP, VP, SZ, C.c_int, VP, VP],
+                                   C.c_int),
+    "mmr_rms_norm_rows": ([VP, VP, F32, I64, I64, VP, VP], C.c_int),
+    "mmr_add": ([VP, VP, I64, VP, VP], C.c_int),
+    "mmr_swiglu_rows": ([VP, I64, I64, VP, VP], C.c_int),
+    "mmr_embedding_gather": ([VP, VP, I64, I64, I64, VP, VP, VP], C.c_int),
+    "mmr_default_config": ([C.POINTER(Config)], C.c_int),
+    "mmr_load_config": ([C.c_char_p, C.POINTER(Config)], C.c_int),
+    "mmr_has_runtime_model": ([C.c_char_p, C.POINTER(C.c_int)], C.c_int),
+    "mmr_model_load": ([C.c_char_p, C.POINTER(VP)], C.c_int),
+    "mmr_model_create_synthetic": ([C.POINTER(Config), U64, C.c_double, C.c_int, C.POINTER(VP)], C.c_int),
+    "mmr_model_free": ([VP], C.c_int),
+    "mmr_model_config": ([VP, C.POINTER(Config)], C.c_int),
+    "mmr_model_weight_bytes": ([VP, C.POINTER(U64)], C.c_int),
+    "mmr_write_synthetic_model": ([C.c_char_p, C.POINTER(Config), U64, C.c_double, C.c_int], C.c_int),
+    "mmr_synthesize_normals": ([U64, U64, U64, C.c_double, C.c_int, VP], C.c_int),
+    "mmr_synthesize_prompt": ([U64, I64, I64, VP], C.c_int),
+    "mmr_state_create": ([VP, I64, C.c_int, C.POINTER(VP)], C.c_int),
+    "mmr_state_free": ([VP], C.c_int),
+    "mmr_state_position": ([VP, C.POINTER(I64)], C.c_int),
+    "mmr_state_stream": ([VP, C.POINTER(VP)], C.c_int),
+    "mmr_state_reset": ([VP, VP], C.c_int),
+    "mmr_forward_token": ([VP, VP, I32, VP], C.c_int),
+    "mmr_forward_next_token": ([VP, VP, I32, P_I32], C.c_int),
+    "mmr_prefill_next_token": ([VP, VP, VP, I64, P_I32], C.c_int),
+    "mmr_generate": ([VP, VP, I64, I64, VP, C.POINTER(I64)], C.c_int),
+    "mmr_enqueue_prefill": ([VP, VP, VP, I64], C.c_int),
+    "mmr_enqueue_decode": ([VP, VP, I64, I32], C.c_int),
+    "mmr_state_synchronize": ([VP, VP], C.c_int),
+    "mmr_read_sequence": ([VP, VP, I64, I64, VP], C.c_int),
+    "mmr_read_logits": ([VP, VP, VP], C.c_int),
+    "mmr_launch_step_kernel": ([VP, VP, C.c_int, I64, I64], C.c_int),
+}
+
+EXPORTED = sorted(_SIGS)
+
+for _name, (_args, _res) in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _res
+
+
+def lib() -> C.CDLL:
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != OK:
+        msg = _lib.mmr_last_error().decode(errors="replace")
+        raise _ERRORS.get(code, MmrError)(code, msg)
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(_lib.mmr_device_count(C.byref(n)))
+    return n.value
+
+
+# ------------------------------------------------------------- plumbing ----
+
+class DeviceArray:
+    """A HIP allocation with a numpy dtype/shape for copies in and out."""
+
+    def __init__(self, shape, dtype, zero: bool = False):
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = VP()
+        check(_lib.mmr_malloc(C.byref(p), max(self.nbytes, 1)))
+        self.ptr = p.value
+        if zero:
+            self.zero()
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        if a.nbytes:
+            check(_lib.mmr_memcpy_h2d(d.ptr, _ptr(a), a.nbytes))
+        return d
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            check(_lib.mmr_memcpy_d2h(_ptr(out), self.ptr, self.nbytes))
+        return out
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes
+        check(_lib.mmr_memcpy_h2d(self.ptr, _ptr(a), a.nbytes))
+
+    def zero(self) -> None:
+        check(_lib.mmr_memset(self.ptr, 0, max(self.nbytes, 1)))
+
+    def free(self) -> None:
+        if self.ptr:
+            _lib.mmr_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    def __init__(self, handle: int | None = None):
+        self.owned = handle is None
+        if handle is None:
+            h = VP()
+            check(_lib.mmr_stream_create(C.byref(h)))
+            handle = h.value
+        self.handle = handle
+
+    def synchronize(self) -> None:
+        check(_lib.mmr_stream_synchronize(self.handle))
+
+    def __del__(self):
+        if getattr(self, "owned", False) and self.handle:
+            try:
+                _lib.mmr_stream_destroy(self.handle)
+            except Exception:
+                pass
+
+
+class Event:
+    def __init__(self):
+        h = VP()
+        check(_lib.mmr_event_create(C.byref(h)))
+        self.handle = h.value
+
+    def record(self, stream) -> None:
+        check(_lib.mmr_event_record(self.handle, stream.handle if isinstance(stream, Stream) else stream))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float(0.0)
+        check(_lib.mmr_event_elapsed_ms(self.handle, end.handle, C.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            _lib.mmr_event_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def synchronize() -> None:
+    check(_lib.mmr_device_synchronize())
+
+
+def f32_to_f16(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, np.uint16)
+    check(_lib.mmr_f32_to_f16(_ptr(a), _ptr(out), a.size))
+    return out
+
+
+def f16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, np.float32)
+    check(_lib.mmr_f16_to_f32(_ptr(a), _ptr(out), a.size))
+    return out
+
+
+def _s(stream) -> int | None:
+    if stream is None:
+        return None
+    return stream.handle if isinstance(stream, Stream) else stream
+
+
+# ------------------------------------------------------------------ ops ----
+
+def matvec_f16(w: DeviceArray, rows: int, cols: int, x: DeviceArray, y: DeviceArray, residual: DeviceArray | None = None,
+               stream=None) -> None:
+    check(_lib.mmr_matvec_f16(w.ptr, rows, cols, x.ptr, residual.ptr if residual else None, y.ptr, _s(stream)))
+
+
+def matvec_f16_ex(w, rows, cols, x, y, *, norm_w=None, eps=0.0, prologue=PRO_PLAIN, epilogue=EPI_STORE,
+                  residual=None, lanes_per_row=0, rows_per_group=0, stream=None) -> None:
+    check(_lib.mmr_matvec_f16_ex(w.ptr, rows, cols, x.ptr, norm_w.ptr if norm_w else None, eps, prologue, epilogue,
+                                 residual.ptr if residual else None, y.ptr, lanes_per_row, rows_per_group, _s(stream)))
+
+
+def matvec_argmax_workspace_size(rows: int, cols: int) -> int:
+    return int(_lib.mmr_matvec_argmax_workspace_size(rows, cols))
+
+
+def matvec_argmax_f16(w, rows, cols, x, token_out, workspace, *, logits=None, norm_w=None, eps=0.0,
+                      stream=None) -> None:
+    check(_lib.mmr_matvec_argmax_f16(w.ptr, rows, cols, x.ptr, norm_w.ptr if norm_w else None, eps,
+                                     logits.ptr if logits else None, token_out.ptr, workspace.ptr, workspace.nbytes,
+                                     _s(stream)))
+
+
+class RopeTable:
+    def __init__(self, max_positions: int, head_dim: int, theta: float):
+        h = VP()
+        check(_lib.mmr_rope_table_create(max_positions, head_dim, theta, C.byref(h)))
+        self.handle = h.value
+
+    def __del__(self):
+        try:
+            _lib.mmr_rope_table_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class KvCache:
+    def __init__(self, kv_heads: int, head_dim: int, capacity: int, kv_dtype: int = KV_F32):
+        h = VP()
+        check(_lib.mmr_kv_cache_create(kv_heads, head_dim, capacity, kv_dtype, C.byref(h)))
+        self.handle = h.value
+        self.kv_heads, self.head_dim, self.capacity, self.kv_dtype = kv_heads, head_dim, capacity, kv_dtype
+        self.np_dtype = np.float16 if kv_dtype == KV_F16 else np.float32
+
+    def pointers(self) -> tuple[int, int]:
+        k, v = VP(), VP()
+        check(_lib.mmr_kv_cache_data(self.handle, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+    def _nbytes(self) -> int:
+        return self.kv_heads * self.capacity * self.head_dim * np.dtype(self.np_dtype).itemsize
+
+    def upload(self, keys: np.ndarray, values: np.ndarray) -> None:
+        """keys/values shaped [kv_heads, capacity, head_dim] (cache layout)."""
+        kp, vp = self.pointers()
+        for ptr, a in ((kp, keys), (vp, values)):
+            a = np.ascontiguousarray(a, dtype=self.np_dtype)
+            assert a.nbytes == self._nbytes()
+            check(_lib.mmr_memcpy_h2d(ptr, _ptr(a), a.nbytes))
+
+    def download(self) -> tuple[np.ndarray, np.ndarray]:
+        kp, vp = self.pointers()
+        out = []
+        for ptr in (kp, vp):
+            a = np.empty((self.kv_heads, self.capacity, self.head_dim), self.np_dtype)
+            check(_lib.mmr_memcpy_d2h(_ptr(a), ptr, a.nbytes))
+            out.append(a)
+        return out[0], out[1]
+
+    def __del__(self):
+        try:
+            _lib.mmr_kv_cache_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def attention_workspace_size(q_heads, kv_heads, head_dim, splits=0) -> int:
+    return int(_lib.mmr_attention_workspace_size(q_heads, kv_heads, head_dim, splits))
+
+
+def decode_qkv_postprocess(qkv, q_norm, k_norm, cache: KvCache, tokens, q_heads, kv_heads, head_dim, position,
+                           rope: RopeTable, eps, query, stream=None) -> None:
+    check(_lib.mmr_decode_qkv_postprocess(qkv.ptr, q_norm.ptr, k_norm.ptr, cache.handle, tokens, q_heads, kv_heads,
+                                          head_dim, position, rope.handle, eps, query.ptr, _s(stream)))
+
+
+def attention_from_cache(query, cache: KvCache, tokens, q_heads, kv_heads, head_dim, out, workspace, splits=0,
+                         stream=None) -> None:
+    check(_lib.mmr_attention_from_cache(query.ptr, cache.handle, tokens, q_heads, kv_heads, head_dim, out.ptr,
+                                        workspace.ptr, workspace.nbytes, splits, _s(stream)))
+
+
+def decode_attention_fused(qkv, q_norm, k_norm, eps, rope: RopeTable, position, cache: KvCache, q_heads, kv_heads,
+                           head_dim, out, workspace, splits, error, stream=None) -> None:
+    check(_lib.mmr_decode_attention_fused(qkv.ptr, q_norm.ptr, k_norm.ptr, eps, rope.handle, position.ptr,
+                                          cache.handle, q_heads, kv_heads, head_dim, out.ptr, workspace.ptr,
+                                          workspace.nbytes, splits, error.ptr, _s(stream)))
+
+
+def rms_norm_rows(x, w, eps, rows, cols, out, stream=None) -> None:
+    check(_lib.mmr_rms_norm_rows(x.ptr, w.ptr, eps, rows, cols, out.ptr, _s(stream)))
+
+
+def add(a, b, n, out, stream=None) -> None:
+    check(_lib.mmr_add(a.ptr, b.ptr, n, out.ptr, _s(stream)))
+
+
+def swiglu_rows(gate_up, rows, cols, out, stream=None) -> None:
+    check(_lib.mmr_swiglu_rows(gate_up.ptr, rows, cols, out.ptr, _s(stream)))
+
+
+def embedding_gather(table, ids, tokens, vocab, hidden, out, error=None, stream=None) -> None:
+    check(_lib.mmr_embedding_gather(table.ptr, ids.ptr, tokens, vocab, hidden, out.ptr,
+                                    error.ptr if error else None, _s(stream)))
+
+
+# ---------------------------------------------------------------- model ----
+
+def default_config() -> Config:
+    c = Config()
+    check(_lib.mmr_default_config(C.byref(c)))
+    return c
+
+
+def make_config(**kw) -> Config:
+    c = default_config()
+    for k, v in kw.items():
+        if not hasattr(c, k):
+            raise KeyError(k)
+        setattr(c, k, v)
+    return c
+
+
+def load_config(path) -> Config:
+    c = Config()
+    check(_lib.mmr_load_config(str(path).encode(), C.byref(c)))
+    return c
+
+
+def has_runtime_model(model_dir) -> bool:
+    out = C.c_int(0)
+    check(_lib.mmr_has_runtime_model(str(model_dir).encode(), C.byref(out)))
+    return bool(out.value)
+
+
+def write_synthetic_model(model_dir, config: Config, seed: int, std: float = 0.02, round_fp16: bool = True) -> None:
+    check(_lib.mmr_write_synthetic_model(str(model_dir).encode(), C.byref(config), seed, std, int(round_fp16)))
+
+
+def synthesize_normals(seed: int, first: int, count: int, std: float = 0.02, round_fp16: bool = False) -> np.ndarray:
+    out = np.empty(count, np.float32)
+    check(_lib.mmr_synthesize_normals(seed, first, count, std, int(round_fp16), _ptr(out)))
+    return out
+
+
+def synthesize_prompt(seed: int, count: int, vocab: int) -> np.ndarray:
+    out = np.empty(count, np.int32)
+    check(_lib.mmr_synthesize_prompt(seed, count, vocab, _ptr(out)))
+    return out
+
+
+class Model:
+    """LanguageModel (reference language_model.h:27-49) on the GPU."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+        c = Config()
+        check(_lib.mmr_model_config(self.handle, C.byref(c)))
+        self.config = c
+
+    @classmethod
+    def load(cls, model_dir) -> "Model":
+        h = VP()
+        check(_lib.mmr_model_load(str(model_dir).encode(), C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def synthetic(cls, config: Config, seed: int, std: float = 0.02, round_fp16: bool = True) -> "Model":
+        h = VP()
+        check(_lib.mmr_model_create_synthetic(C.byref(config), seed, std, int(round_fp16), C.byref(h)))
+        return cls(h.value)
+
+    def weight_bytes(self) -> int:
+        b = C.c_uint64(0)
+        check(_lib.mmr_model_weight_bytes(self.handle, C.byref(b)))
+        return int(b.value)
+
+    def make_state(self, capacity: int = 0, kv_dtype: int = KV_F32) -> "State":
+        h = VP()
+        check(_lib.mmr_state_create(self.handle, capacity, kv_dtype, C.byref(h)))
+        return State(self, h.value)
+
+    def generate(self, prompt, max_new_tokens: int) -> list[int]:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(max(int(max_new_tokens), 1), np.int32)
+        n = C.c_int64(0)
+        check(_lib.mmr_generate(self.handle, _ptr(p) if p.size else None, p.size, max_new_tokens, _ptr(out),
+                                C.byref(n)))
+        return out[: n.value].tolist()
+
+    def free(self) -> None:
+        if self.handle:
+            _lib.mmr_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class State:
+    """DecoderState (reference language_model.h:22-25) with a device KV cache."""
+
+    def __init__(self, model: Model, handle: int):
+        self.model = model
+        self.handle = handle
+
+    @property
+    def position(self) -> int:
+        p = C.c_int64(0)
+        check(_lib.mmr_state_position(self.handle, C.byref(p)))
+        return int(p.value)
+
+    @property
+    def stream(self) -> int:
+        s = VP()
+        check(_lib.mmr_state_stream(self.handle, C.byref(s)))
+        return s.value
+
+    def reset(self) -> None:
+        check(_lib.mmr_state_reset(self.model.handle, self.handle))
+
+    def forward_token(self, token: int) -> np.ndarray:
+        out = np.empty(self.model.config.vocab_size, np.float32)
+        check(_lib.mmr_forward_token(self.model.handle, self.handle, token, _ptr(out)))
+        return out
+
+    def forward_next_token(self, token: int) -> int:
+        n = C.c_int32(0)
+        check(_lib.mmr_forward_next_token(self.model.handle, self.handle, token, C.byref(n)))
+        return int(n.value)
+
+    def prefill_next_token(self, prompt) -> int:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        n = C.c_int32(0)
+        check(_lib.mmr_prefill_next_token(self.model.handle, self.handle, _ptr(p) if p.size else None, p.size,
+                                          C.byref(n)))
+        return int(n.value)
+
+    def enqueue_prefill(self, prompt) -> None:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        check(_lib.mmr_enqueue_prefill(self.model.handle, self.handle, _ptr(p) if p.size else None, p.size))
+
+    def enqueue_decode(self, steps: int, first_token: int = -1) -> None:
+        check(_lib.mmr_enqueue_decode(self.model.handle, self.handle, steps, first_token))
+
+    def synchronize(self) -> None:
+        check(_lib.mmr_state_synchronize(self.model.handle, self.handle))
+
+    def read_sequence(self, first: int, count: int) -> np.ndarray:
+        out = np.empty(count, np.int32)
+        check(_lib.mmr_read_sequence(self.model.handle, self.handle, first, count, _ptr(out) if count else None))
+        return out
+
+    def read_logits(self) -> np.ndarray:
+        out = np.empty(self.model.config.vocab_size, np.float32)
+        check(_lib.mmr_read_logits(self.model.handle, self.handle, _ptr(out)))
+        return out
+
+    def launch_step_kernel(self, kernel: int, layer: int, count: int) -> None:
+        check(_lib.mmr_launch_step_kernel(self.model.handle, self.handle, kernel, layer, count))
+
+    def free(self) -> None:
+        if self.handle:
+            _lib.mmr_state_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

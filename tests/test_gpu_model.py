@@ -1,0 +1,175 @@
+"""End-to-end parity of the device-resident decode step (C ABI model API)
+against the golden fixtures of the reference's CPU path.
+
+Greedy token ids must be identical; logits within max|d| / max|ref| <= 2e-3.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from conftest import load_golden, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def synth_model(mmr, g, **overrides):
+    cfg = mmr.make_config(**{**g["config"], **overrides})
+    return mmr.Model.synthetic(cfg, g["seed"], g["std"], g["round_fp16"])
+
+
+def step_logits(state, prompt, generated, steps):
+    """Logits of the steps that produced generated[i] for i in steps (forward_token API)."""
+    rows, lg = [], None
+    for t in prompt:
+        lg = state.forward_token(t)
+    for i, tok in enumerate(generated):
+        if i in steps:
+            rows.append(lg)
+        if i + 1 < len(generated):
+            lg = state.forward_token(tok)
+    return np.array(rows)
+
+
+@pytest.mark.parametrize("case", ["mini", "cfg3_short"])
+def test_generate_and_logits_match_reference(gpu, case):
+    mmr = gpu
+    print(f"[case] model {case}", flush=True)
+    g = load_golden(case)
+    m = synth_model(mmr, g)
+    assert m.generate(g["prompt"], g["max_new"]) == g["generated"]
+    st = m.make_state(len(g["prompt"]) + g["max_new"])
+    rows = step_logits(st, g["prompt"], g["generated"], g["logit_steps"])
+    for i, (got, ref) in enumerate(zip(rows, g["logits"])):
+        assert rel_err(got, ref) < TOL, (case, g["logit_steps"][i], rel_err(got, ref))
+    assert st.position == len(g["prompt"]) + len(g["generated"]) - 1
+
+
+def test_minimind2_512_prompt_256_steps_device_loop(gpu):
+    # BASELINE configs[3] at full size: 512-token prompt, 256 greedy steps in the hipGraph loop
+    mmr = gpu
+    g = load_golden("cfg3")
+    m = synth_model(mmr, g)
+    st = m.make_state(len(g["prompt"]) + g["max_new"])
+    st.enqueue_prefill(g["prompt"])
+    st.enqueue_decode(g["max_new"] - 1)
+    st.synchronize()
+    got = st.read_sequence(len(g["prompt"]), g["max_new"]).tolist()
+    assert got == g["generated"]
+    np.testing.assert_array_equal(st.read_sequence(0, len(g["prompt"])), g["prompt"])
+    assert rel_err(st.read_logits(), g["logits"][-1]) < TOL
+
+
+def test_minimind2_fp16_kv_cache(gpu):
+    # fp16 KV (north-star layout): same tokens on the short MiniMind2 case, logits within bound
+    mmr = gpu
+    g = load_golden("cfg3_short")
+    m = synth_model(mmr, g)
+    st = m.make_state(len(g["prompt"]) + g["max_new"], mmr.KV_F16)
+    rows = step_logits(st, g["prompt"], g["generated"], g["logit_steps"])
+    for got, ref in zip(rows, g["logits"]):
+        assert rel_err(got, ref) < TOL
+    st2 = m.make_state(len(g["prompt"]) + g["max_new"], mmr.KV_F16)
+    st2.enqueue_prefill(g["prompt"])
+    st2.enqueue_decode(g["max_new"] - 1)
+    st2.synchronize()
+    assert st2.read_sequence(len(g["prompt"]), g["max_new"]).tolist() == g["generated"]
+
+
+def test_loader_roundtrip_matches_reference_loader(gpu, tmp_path):
+    # files without rms_norm_eps / rope_theta -> reference defaults (runtime_loader.cpp:71-88)
+    mmr = gpu
+    g = load_golden("mini_loader")
+    mmr.write_synthetic_model(tmp_path, mmr.make_config(**g["config"]), g["seed"], g["std"], g["round_fp16"])
+    p = tmp_path / "minimind_runtime_config.txt"
+    p.write_text("\n".join(l for l in p.read_text().splitlines() if l.split("=")[0] not in g["strip_keys"]) + "\n")
+    m = mmr.Model.load(tmp_path)
+    assert m.config.rms_norm_eps == pytest.approx(1e-6)
+    assert m.generate(g["prompt"], g["max_new"]) == g["generated"]
+
+
+def test_prefill_consistency(gpu):
+    # check_prefill_consistency.cpp:29-53: prefill vs token-by-token decode, then 4 follow-ups
+    mmr = gpu
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    prompt = [(i % 500) + 1 for i in range(40)]
+    a, b = m.make_state(64), m.make_state(64)
+    nxt_a = 0
+    for t in prompt:
+        nxt_a = a.forward_next_token(t)
+    nxt_b = b.prefill_next_token(prompt)
+    assert nxt_a == nxt_b and a.position == b.position == len(prompt)
+    for _ in range(4):
+        nxt_a, nxt_b = a.forward_next_token(nxt_a), b.forward_next_token(nxt_b)
+        assert nxt_a == nxt_b and a.position == b.position
+    with pytest.raises(mmr.InvalidArgument, match="empty KV cache"):
+        b.prefill_next_token(prompt)
+
+
+def test_generate_stops_after_eos(gpu):
+    # language_model.cpp:389-395: EOS is emitted, then generation stops
+    mmr = gpu
+    g = load_golden("mini")
+    eos = g["generated"][5]
+    m = synth_model(mmr, g, eos_token_id=eos)
+    expect = g["generated"][: g["generated"].index(eos) + 1]
+    assert m.generate(g["prompt"], g["max_new"]) == expect
+    assert m.generate(g["prompt"], 0) == []
+    assert m.generate(g["prompt"], 1) == g["generated"][:1]
+
+
+def test_error_behaviour(gpu):
+    mmr = gpu
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    V = g["config"]["vocab_size"]
+    with pytest.raises(mmr.InvalidArgument, match="cannot be empty"):
+        m.generate([], 4)
+    with pytest.raises(mmr.InvalidArgument, match="negative"):
+        m.generate([1], -1)
+    st = m.make_state(4)
+    with pytest.raises(mmr.OutOfRange):
+        st.forward_next_token(V)
+    with pytest.raises(mmr.OutOfRange):
+        st.forward_next_token(-1)
+    assert st.position == 0  # rejected before any device work
+    for t in range(4):
+        st.forward_next_token(t)
+    with pytest.raises(mmr.LengthError):
+        st.forward_next_token(1)
+    with pytest.raises(mmr.InvalidArgument):
+        m.make_state(g["config"]["max_position_embeddings"] + 1)
+
+
+def test_graph_replays_match_eager_launches(gpu, monkeypatch):
+    # Every graph replay (one per step, with host syncs and copies between
+    # replays) equals the same kernels launched eagerly.
+    mmr = gpu
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    graph_state = m.make_state(80)
+    monkeypatch.setenv("MMR_NO_GRAPH", "1")
+    eager_state = m.make_state(80)
+    monkeypatch.delenv("MMR_NO_GRAPH")
+    tok_g = tok_e = g["prompt"][0]
+    for step in range(70):
+        lg = graph_state.forward_token(tok_g)
+        le = eager_state.forward_token(tok_e)
+        np.testing.assert_array_equal(lg, le)
+        tok_g = tok_e = int(np.argmax(lg))
+
+
+def test_state_reset_and_reuse(gpu):
+    mmr = gpu
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    st = m.make_state(64)
+    first = [st.forward_next_token(t) for t in g["prompt"]]
+    st.reset()
+    assert st.position == 0
+    assert [st.forward_next_token(t) for t in g["prompt"]] == first
+    assert first[-1] == g["generated"][0]
