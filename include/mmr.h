@@ -107,15 +107,16 @@ int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float
  * (std::max_element, language_model.cpp:408-413); logits (device fp32,
  * nullable) receives all logits.  norm_w != NULL fuses the final RMSNorm
  * (language_model.cpp:325).  The workspace (device, see _workspace_size)
- * must be zero-filled once before its first use; the kernel re-arms it. */
+ * holds per-block partials reduced by a second, one-block launch. */
 size_t mmr_matvec_argmax_workspace_size(int64_t rows, int64_t cols);
 int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
                           float* logits, int32_t* token_out, void* workspace, size_t workspace_bytes,
                           mmr_stream_t stream);
 
-/* ---- RoPE table: cached_rope_table (ascend_custom_ops.cpp:93-123), kept in
- * fp32 (the reference uploads fp16) with the CPU formula of
- * decoder_layer.cpp:109-119. */
+/* ---- RoPE table: cached_rope_table (ascend_custom_ops.cpp:93-123).  Holds
+ * the fp32 frequencies inv_freq[i] = 1 / powf(theta, 2i / d) of the CPU
+ * formula (decoder_layer.cpp:114); kernels evaluate cos/sin(float(pos) *
+ * inv_freq[i]) in fp32 (the reference uploads an fp16 table). */
 int mmr_rope_table_create(int64_t max_positions, int64_t head_dim, float theta, mmr_rope_table** out);
 int mmr_rope_table_destroy(mmr_rope_table* table);
 
@@ -126,6 +127,9 @@ int mmr_rope_table_destroy(mmr_rope_table* table);
 int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, int kv_dtype, mmr_kv_cache** out);
 int mmr_kv_cache_destroy(mmr_kv_cache* cache);
 int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values);
+/* Rows allocated per KV head: capacity rounded up to the attention tile
+ * (64 tokens, 32 for head_dim 128); keys/values are [kv_head][rows][head_dim]. */
+int mmr_kv_cache_rows(const mmr_kv_cache* cache, int64_t* rows);
 
 /* ---- QKV post-process + KV append: device_decode_qkv_postprocess
  * (ascend_custom_ops.h:132-143, ascend_custom_ops.cpp:825-884).
@@ -140,8 +144,8 @@ int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const floa
  * ascend_custom_ops.cpp:886-916).  Attends `query` [Hq*d] over the first
  * `tokens` cached keys: softmax(q.k / sqrt(d)) v per head, GQA mapping
  * kv = h / (Hq/Hkv) (decoder_layer.cpp:184-234).  Split along the context in
- * `splits` ranges (0 = automatic) with a log-sum-exp combine.  The workspace
- * must be zero-filled once before its first use. */
+ * `splits` tile sets (0 = automatic), merged by a log-sum-exp combine (a
+ * second launch on the same stream).  The workspace holds the split partials. */
 size_t mmr_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_t head_dim, int splits);
 int mmr_attention_from_cache(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, float* out, void* workspace, size_t workspace_bytes,

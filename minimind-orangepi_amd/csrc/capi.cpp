@@ -8,6 +8,7 @@
 #include "runtime/device.h"
 #include "runtime/language_model.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -24,15 +25,14 @@ struct mmr_state {
   DecoderState st;
 };
 struct mmr_rope_table {
-  DeviceBuffer cos_sin;  // [max_pos][d/2] cos, then [max_pos][d/2] sin
+  DeviceBuffer inv_freq;  // [d/2]: 1 / powf(theta, 2i / d); cos/sin(pos * inv_freq) on the device
   int64_t max_positions = 0;
   int64_t head_dim = 0;
-  const float* cos() const { return static_cast<const float*>(cos_sin.data()); }
-  const float* sin() const { return cos() + max_positions * (head_dim / 2); }
+  const float* data() const { return static_cast<const float*>(inv_freq.data()); }
 };
 struct mmr_kv_cache {
   DeviceBuffer keys, values;
-  int64_t kv_heads = 0, head_dim = 0, capacity = 0;
+  int64_t kv_heads = 0, head_dim = 0, capacity = 0, rows = 0;
   int dtype = MMR_KV_F32;
 };
 
@@ -116,8 +116,8 @@ void check_matvec_shape(int64_t rows, int64_t cols) {
   require(rows < (int64_t{1} << 30), "rows too large");
 }
 
-// Argmax workspace: [u32 ticket counter][pad][u64 packed best key]
-constexpr size_t kArgmaxWorkspaceBytes = 256;
+// Argmax workspace: per-block partial values, then per-block indices.
+size_t argmax_ws_bytes(const mmr::GemvPlan& p) { return static_cast<size_t>(p.blocks) * 8; }
 
 int auto_splits(int64_t tokens, int64_t head_dim) {
   const int tile = mmr::attention_tile_tokens(static_cast<int>(head_dim));
@@ -125,9 +125,9 @@ int auto_splits(int64_t tokens, int64_t head_dim) {
   return static_cast<int>(tiles < 1 ? 1 : (tiles > 512 ? 512 : tiles));
 }
 
-// Attention workspace: [counters: 256 B][partials]
+// Attention workspace: the split partials [Hkv][splits][R][d + 2] (fp32).
 size_t attention_ws_bytes(int64_t hq, int64_t hkv, int64_t d, int splits) {
-  return 256 + mmr::attention_partial_floats(static_cast<int>(hq), static_cast<int>(hkv), static_cast<int>(d), splits) * 4;
+  return mmr::attention_partial_floats(static_cast<int>(hq), static_cast<int>(hkv), static_cast<int>(d), splits) * 4;
 }
 
 void check_attention_shape(int64_t hq, int64_t hkv, int64_t d) {
@@ -265,7 +265,7 @@ size_t mmr_matvec_argmax_workspace_size(int64_t rows, int64_t cols) {
   if (rows <= 0 || rows >= (int64_t{1} << 30) ||
       !mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), mmr::kEpiArgmax, 0, 0, &plan))
     return 0;
-  return kArgmaxWorkspaceBytes;
+  return argmax_ws_bytes(plan);
 }
 
 int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
@@ -277,7 +277,7 @@ int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const f
     mmr::GemvPlan plan;
     require(mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), mmr::kEpiArgmax, 0, 0, &plan),
             "unsupported shape");
-    require(workspace_bytes >= kArgmaxWorkspaceBytes, "workspace too small");
+    require(workspace_bytes >= argmax_ws_bytes(plan), "workspace too small");
     char* ws = static_cast<char*>(workspace);
     mmr::GemvArgs a;
     a.w = reinterpret_cast<const __half*>(w);
@@ -287,12 +287,17 @@ int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const f
     a.norm_w = norm_w;
     a.eps = eps;
     a.y = logits;
-    a.counter = reinterpret_cast<unsigned int*>(ws);
-    a.best = reinterpret_cast<unsigned long long*>(ws + 8);
-    a.token_out = token_out;
+    a.part_val = reinterpret_cast<float*>(ws);
+    a.part_idx = reinterpret_cast<int*>(ws + static_cast<size_t>(plan.blocks) * 4);
     hip(mmr::launch_gemv(a, norm_w ? mmr::kProRmsNormFinal : mmr::kProPlain, mmr::kEpiArgmax, plan,
                          as_stream(stream)),
         "matvec argmax launch");
+    mmr::ArgmaxFinalizeArgs f;
+    f.part_val = a.part_val;
+    f.part_idx = a.part_idx;
+    f.parts = plan.blocks;
+    f.token_out = token_out;
+    hip(mmr::launch_argmax_finalize(f, as_stream(stream)), "argmax finalize launch");
   });
 }
 
@@ -308,15 +313,8 @@ int mmr_rope_table_create(int64_t max_positions, int64_t head_dim, float theta, 
     for (int64_t i = 0; i < half; ++i)
       inv[static_cast<size_t>(i)] =
           1.0F / std::pow(theta, static_cast<float>(i * 2) / static_cast<float>(head_dim));
-    std::vector<float> host(static_cast<size_t>(2 * max_positions * half));
-    for (int64_t p = 0; p < max_positions; ++p)
-      for (int64_t i = 0; i < half; ++i) {
-        const float angle = static_cast<float>(p) * inv[static_cast<size_t>(i)];
-        host[static_cast<size_t>(p * half + i)] = std::cos(angle);
-        host[static_cast<size_t>(max_positions * half + p * half + i)] = std::sin(angle);
-      }
-    t->cos_sin.reset(host.size() * sizeof(float));
-    hip(hipMemcpy(t->cos_sin.data(), host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+    t->inv_freq.reset(inv.size() * sizeof(float));
+    hip(hipMemcpy(t->inv_freq.data(), inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
     t->max_positions = max_positions;
     t->head_dim = head_dim;
     *out = t.release();
@@ -333,8 +331,10 @@ int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, in
     require(kv_heads > 0 && head_dim > 0 && capacity > 0, "dimensions must be positive");
     require(kv_dtype == MMR_KV_F16 || kv_dtype == MMR_KV_F32, "unknown kv dtype");
     require(capacity < (int64_t{1} << 28), "capacity too large");
+    require(head_dim <= 128, "head_dim must be <= 128");
     auto c = std::make_unique<mmr_kv_cache>();
-    const size_t bytes = static_cast<size_t>(kv_heads * head_dim * capacity) * (kv_dtype == MMR_KV_F16 ? 2 : 4);
+    c->rows = mmr::attention_cache_rows(capacity, static_cast<int>(head_dim));
+    const size_t bytes = static_cast<size_t>(kv_heads * head_dim * c->rows) * (kv_dtype == MMR_KV_F16 ? 2 : 4);
     c->keys.reset(bytes);
     c->values.reset(bytes);
     hip(hipMemset(c->keys.data(), 0, bytes), "hipMemset");
@@ -359,6 +359,13 @@ int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values) {
   });
 }
 
+int mmr_kv_cache_rows(const mmr_kv_cache* cache, int64_t* rows) {
+  return guarded([&] {
+    require(cache && rows, "null argument");
+    *rows = cache->rows;
+  });
+}
+
 int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const float* k_norm, mmr_kv_cache* cache,
                                int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t position,
                                const mmr_rope_table* rope, float eps, float* query, mmr_stream_t stream) {
@@ -374,13 +381,12 @@ int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const floa
     a.q_norm = q_norm;
     a.k_norm = k_norm;
     a.eps = eps;
-    a.rope_cos = rope->cos();
-    a.rope_sin = rope->sin();
+    a.inv_freq = rope->data();
     a.position = static_cast<int>(position);
     a.index = static_cast<int>(tokens - 1);
     a.kcache = cache->keys.data();
     a.vcache = cache->values.data();
-    a.capacity = static_cast<int>(cache->capacity);
+    a.rows = static_cast<int>(cache->rows);
     a.hq = static_cast<int>(q_heads);
     a.hkv = static_cast<int>(kv_heads);
     a.d = static_cast<int>(head_dim);
@@ -407,23 +413,23 @@ int mmr_attention_from_cache(const float* query, const mmr_kv_cache* cache, int6
     if (splits <= 0) splits = auto_splits(tokens, head_dim);
     require(splits <= 4096, "splits too large");
     require(workspace_bytes >= attention_ws_bytes(q_heads, kv_heads, head_dim, splits), "workspace too small");
-    char* ws = static_cast<char*>(workspace);
     mmr::AttnArgs a;
     a.q = query;
     a.tokens = static_cast<int>(tokens);
     a.kcache = cache->keys.data();
     a.vcache = cache->values.data();
     a.capacity = static_cast<int>(cache->capacity);
+    a.rows = static_cast<int>(cache->rows);
     a.hq = static_cast<int>(q_heads);
     a.hkv = static_cast<int>(kv_heads);
     a.d = static_cast<int>(head_dim);
     a.splits = splits;
-    a.counters = reinterpret_cast<unsigned int*>(ws);
-    a.part = reinterpret_cast<float*>(ws + 256);
-    a.out = out;
+    a.part = static_cast<float*>(workspace);
     hip(mmr::launch_attention(a, mmr::kAttnFromCache, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
                               as_stream(stream)),
         "attention launch");
+    hip(mmr::launch_attention_combine(a.part, a.hq, a.hkv, a.d, splits, out, as_stream(stream)),
+        "attention combine launch");
   });
 }
 
@@ -439,30 +445,28 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
     if (splits <= 0) splits = auto_splits(cache->capacity, head_dim);
     require(splits <= 4096, "splits too large");
     require(workspace_bytes >= attention_ws_bytes(q_heads, kv_heads, head_dim, splits), "workspace too small");
-    char* ws = static_cast<char*>(workspace);
     mmr::AttnArgs a;
     a.qkv = qkv;
     a.q_norm = q_norm;
     a.k_norm = k_norm;
     a.eps = eps;
-    a.rope_cos = rope->cos();
-    a.rope_sin = rope->sin();
+    a.inv_freq = rope->data();
     a.pos = position;
     a.kcache = cache->keys.data();
     a.vcache = cache->values.data();
-    a.capacity = static_cast<int>(cache->capacity);
-    a.max_pos = static_cast<int>(rope->max_positions);
+    a.capacity = static_cast<int>(std::min(cache->capacity, rope->max_positions));
+    a.rows = static_cast<int>(cache->rows);
     a.hq = static_cast<int>(q_heads);
     a.hkv = static_cast<int>(kv_heads);
     a.d = static_cast<int>(head_dim);
     a.splits = splits;
-    a.counters = reinterpret_cast<unsigned int*>(ws);
-    a.part = reinterpret_cast<float*>(ws + 256);
-    a.out = out;
+    a.part = static_cast<float*>(workspace);
     a.err = error;
     hip(mmr::launch_attention(a, mmr::kAttnFused, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
                               as_stream(stream)),
         "fused attention launch");
+    hip(mmr::launch_attention_combine(a.part, a.hq, a.hkv, a.d, splits, out, as_stream(stream)),
+        "attention combine launch");
   });
 }
 

@@ -7,21 +7,27 @@
 //  * the decode attention (reference K3 via device_attention_from_cache,
 //    ascend_custom_ops.cpp:886-916; CPU semantics decoder_layer.cpp:184-234).
 //
-// Layout: per layer the cache holds K and V as [kv_head][capacity][head_dim]
-// (fp16 or fp32), so one KV head's context is one contiguous stream.
+// Layout: per layer the cache holds K and V as [kv_head][rows][head_dim]
+// (fp16 or fp32, rows = capacity rounded up to the tile size), so one KV
+// head's context is one contiguous stream.
 //
-// Grid (splits, kv_heads), 256 threads.  A block owns one KV head and a range
-// of 64-token tiles (32 for d = 128) and serves all Hq/Hkv query heads of the
-// group from that single read of K/V:
-//   1. prologue: per-head q RMSNorm + RoPE (fp32 cos/sin table) into LDS; the
-//      block whose range holds the new token also normalises/rotates its k,
-//      rounds k and v to the cache dtype and appends them to the cache;
-//   2. per tile: K/V staged through LDS with 16-byte coalesced loads, one lane
-//      per token computes q.k / sqrt(d), online softmax per head (one wave per
-//      head), P.V with one lane per dimension pair;
-//   3. the last block of each KV head (ticket counter) merges the per-split
-//      (max, sum, o) partials with a log-sum-exp combine in fixed split order,
-//      so results are deterministic.
+// attention_split_kernel, grid (splits, kv_heads), 256 threads.  Block
+// (s, g) owns KV head g and the 64-token tiles s, s + splits, ... (32-token
+// tiles for d = 128), and serves all Hq/Hkv query heads of the group from one
+// read of K/V.  Latency is the cost, so the first tile's K/V loads, the raw
+// q/k/v and the RoPE frequencies are all issued before the device position
+// arrives; RoPE angles are float(pos) * inv_freq with inv_freq from the host
+// (the reference formula) and cos/sin evaluated on the device.
+//   1. q RMSNorm + RoPE into LDS; the block holding the new token also
+//      normalises/rotates its k, rounds k and v to the cache dtype and appends
+//      them (fused mode);
+//   2. per tile: scores q.k / sqrt(d) with one lane per token, online softmax
+//      with one wave per query head, P.V with one lane per dimension pair;
+//   3. the block writes its (max, sum, o[d]) partial per head; splits with no
+//      tile write the neutral partial (-inf, 0, 0).
+// No block waits for another: the log-sum-exp combine runs in the consumer
+// (the O-projection GEMV prologue, or attention_combine_kernel).
+#include "attention_common.h"
 #include "device_common.h"
 #include "kernels.h"
 
@@ -31,62 +37,61 @@ namespace {
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
 
-template <int D>
-constexpr int tile_tokens() {
-  return D <= 96 ? 64 : 32;
-}
-
 template <typename KV>
-__device__ __forceinline__ void load_chunk(const KV* src, float* dst);
+__device__ __forceinline__ void chunk_to_float(const uint4& c, float* dst);
 template <>
-__device__ __forceinline__ void load_chunk<__half>(const __half* src, float* dst) {
-  half8_to_float8(*reinterpret_cast<const uint4*>(src), dst);
+__device__ __forceinline__ void chunk_to_float<__half>(const uint4& c, float* dst) {
+  half8_to_float8(c, dst);
 }
 template <>
-__device__ __forceinline__ void load_chunk<float>(const float* src, float* dst) {
-  const float4 v = *reinterpret_cast<const float4*>(src);
-  dst[0] = v.x;
-  dst[1] = v.y;
-  dst[2] = v.z;
-  dst[3] = v.w;
+__device__ __forceinline__ void chunk_to_float<float>(const uint4& c, float* dst) {
+  dst[0] = __uint_as_float(c.x);
+  dst[1] = __uint_as_float(c.y);
+  dst[2] = __uint_as_float(c.z);
+  dst[3] = __uint_as_float(c.w);
 }
 
-// Per-head RMSNorm of `src` (decoder_layer.cpp:32-42, x * (scale * w)) into
-// dst, executed by one wave; d <= 128 so a lane owns dims lane and lane + 64.
+// Per-head RMSNorm (decoder_layer.cpp:32-42, x * (scale * w)) of values held
+// as (x0 at dim lane, x1 at dim lane + 64; zero outside d) with gains
+// (w0, w1) at the same dims, into dst; executed by one wave.
 template <int D>
-__device__ __forceinline__ void wave_rms_norm(const float* src, const float* w, float eps, float* dst, int lane) {
-  const float x0 = lane < D ? src[lane] : 0.0f;
-  const float x1 = lane + kWave < D ? src[lane + kWave] : 0.0f;
+__device__ __forceinline__ void wave_rms_norm_regs(float x0, float x1, float w0, float w1, float eps, float* dst,
+                                                   int lane) {
   const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
   const float scale = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-  if (lane < D) dst[lane] = x0 * (scale * w[lane]);
-  if (lane + kWave < D) dst[lane + kWave] = x1 * (scale * w[lane + kWave]);
+  if (lane < D) dst[lane] = x0 * (scale * w0);
+  if (lane + kWave < D) dst[lane + kWave] = x1 * (scale * w1);
 }
 
-// Rotate-half RoPE in place on one head held in LDS (decoder_layer.cpp:139-152).
+// Rotate-half RoPE in place on one head in LDS (decoder_layer.cpp:139-152);
+// lane i < d/2 holds (cos, sin) of pair i.
 template <int D>
-__device__ __forceinline__ void wave_rope(float* x, const float* cos_row, const float* sin_row, int lane) {
+__device__ __forceinline__ void wave_rope(float* x, float c, float s, int lane) {
   constexpr int kHalf = D / 2;
-  for (int i = lane; i < kHalf; i += kWave) {
-    const float first = x[i];
-    const float second = x[i + kHalf];
-    const float c = cos_row[i];
-    const float s = sin_row[i];
-    x[i] = first * c - second * s;
-    x[i + kHalf] = second * c + first * s;
+  if (lane < kHalf) {
+    const float first = x[lane];
+    const float second = x[lane + kHalf];
+    x[lane] = first * c - second * s;
+    x[lane + kHalf] = second * c + first * s;
   }
 }
 
 template <typename KV, int D, int MODE>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
-  constexpr int TT = tile_tokens<D>();
+__global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs a) {
+  constexpr int TT = attn_tile_tokens<D>();
   constexpr int LD = D + 4;  // padded row: conflict-free 16-byte LDS reads
   constexpr int CH = 16 / static_cast<int>(sizeof(KV));
-  constexpr int kHalf = D / 2;
+  constexpr int kChunks = TT * D / CH;  // 16-byte chunks per K (or V) tile
+  constexpr int kPerThread = (kChunks + kAttnThreads - 1) / kAttnThreads;
   __shared__ __align__(16) float q_s[kAttnMaxGroup][D];
   __shared__ __align__(16) float k_s[TT][LD];
   __shared__ __align__(16) float v_s[TT][LD];
-  __shared__ float p_s[kAttnMaxGroup][TT];
+  __shared__ __align__(16) float p_s[TT][kAttnMaxGroup];  // token-major: one 16-byte read per 4 heads
+  __shared__ float alpha_s[kAttnMaxGroup];
+  // P.V token groups: 256 threads cover d dims x kPvGroups groups of tokens.
+  constexpr int kPvGroups = (D <= 64) ? ((kAttnThreads / D) < 8 ? (kAttnThreads / D) : 8) : 2;
+  constexpr int kPvTokens = TT / kPvGroups;
+  static_assert(kPvGroups * kAttnMaxGroup * D <= TT * LD, "P.V reduction must fit in k_s");
   __shared__ float knew_s[D];
   __shared__ float vnew_s[D];
 
@@ -96,61 +101,123 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
   const int lane = threadIdx.x % kWave;
   const int R = a.hq / a.hkv;
   const int S = a.splits;
+  const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.rows * D;
+  const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
 
-  int n_keys = 0;
+  // ---- 1. independent loads, issued before the position is known ----
   int p = -1;
+  if constexpr (MODE == kAttnFused) p = *a.pos;
+  uint4 kc[kPerThread], vc[kPerThread];
+  const int t_spec = split * TT;
+  const bool spec = t_spec + TT <= a.rows;
+  const int t_load = spec ? t_spec : 0;  // always in range; unused unless spec
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+    const int64_t off = static_cast<int64_t>(t_load) * D + c * CH;
+    kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
+    vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+  }
+  // Loads are unconditional (indices clamped into range, values masked
+  // afterwards): a predicated load makes the compiler wait for it before the
+  // branch joins, which would serialise these round trips.
+  const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
+  const bool in0 = lane < D, in1 = lane + kWave < D;
+  float qx0[2], qx1[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int h = min(wave + j * kAttnWaves, R - 1);
+    const float* src = (MODE == kAttnFused ? a.qkv : a.q) + (g * R + h) * D;
+    qx0[j] = src[d0];
+    qx1[j] = src[d1];
+  }
+  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
+  float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
   if constexpr (MODE == kAttnFused) {
-    p = *a.pos;
-    if (p < 0 || p >= a.capacity || p >= a.max_pos) {
-      if (threadIdx.x == 0 && split == 0 && g == 0) *a.err = 1;
-    } else {
-      n_keys = p + 1;
-    }
+    const float* kraw = a.qkv + a.hq * D + g * D;
+    const float* vraw = kraw + a.hkv * D;
+    kx0 = kraw[d0];
+    vx0 = vraw[d0];
+    kx1 = kraw[d1];
+    vx1 = vraw[d1];
+    inv_freq = a.inv_freq[min(lane, D / 2 - 1)];
+    qw0 = a.q_norm[d0];
+    qw1 = a.q_norm[d1];
+    kw0 = a.k_norm[d0];
+    kw1 = a.k_norm[d1];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    qx0[j] = in0 ? qx0[j] : 0.0f;
+    qx1[j] = in1 ? qx1[j] : 0.0f;
+  }
+  kx0 = in0 ? kx0 : 0.0f;
+  vx0 = in0 ? vx0 : 0.0f;
+  kx1 = in1 ? kx1 : 0.0f;
+  vx1 = in1 ? vx1 : 0.0f;
+
+  // ---- 2. extent of the context ----
+  int n_keys;
+  if constexpr (MODE == kAttnFused) {
+    const bool ok = p >= 0 && p < a.capacity;
+    if (!ok && threadIdx.x == 0 && split == 0 && g == 0) *a.err = 1;
+    n_keys = ok ? p + 1 : 0;
   } else {
     n_keys = a.tokens < a.capacity ? a.tokens : a.capacity;
   }
   const int n_tiles = (n_keys + TT - 1) / TT;
-  const int tps = n_tiles > 0 ? (n_tiles + S - 1) / S : 1;
-  const int active = n_tiles > 0 ? (n_tiles + tps - 1) / tps : 0;
-  const int tile_begin = split * tps;
-  const int tile_end = min(n_tiles, tile_begin + tps);
 
-  if (tile_begin < tile_end) {
-    const bool owns_new = (MODE == kAttnFused) && p >= tile_begin * TT && p < tile_end * TT;
-    const float* cos_row = nullptr;
-    const float* sin_row = nullptr;
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.0f, 0.0f};
+  // P.V ownership: thread = (dimension pv_dim, token group pv_group).
+  const int pv_dim = threadIdx.x % D;
+  const int pv_group = threadIdx.x / D;
+  const bool pv_active = static_cast<int>(threadIdx.x) < kPvGroups * D;
+  float pacc[kAttnMaxGroup];
+#pragma unroll
+  for (int h = 0; h < kAttnMaxGroup; ++h) pacc[h] = 0.0f;
+
+  if (split < n_tiles) {
+    // ---- 3. queries (and the new key/value), RoPE angle from the position ----
+    float rc = 1.0f, rs = 0.0f;
     if constexpr (MODE == kAttnFused) {
-      cos_row = a.rope_cos + static_cast<int64_t>(p) * kHalf;
-      sin_row = a.rope_sin + static_cast<int64_t>(p) * kHalf;
+      if (lane < D / 2) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
     }
-
-    // ---- prologue: queries (and the new key/value) ----
-    for (int h = wave; h < R; h += kAttnWaves) {
-      const int qh = g * R + h;
-      if constexpr (MODE == kAttnFused) {
-        wave_rms_norm<D>(a.qkv + qh * D, a.q_norm, a.eps, q_s[h], lane);
-      } else {
-        if (lane < D) q_s[h][lane] = a.q[qh * D + lane];
-        if (lane + kWave < D) q_s[h][lane + kWave] = a.q[qh * D + lane + kWave];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = wave + j * kAttnWaves;
+      if (h < R) {
+        if constexpr (MODE == kAttnFused) {
+          wave_rms_norm_regs<D>(qx0[j], qx1[j], qw0, qw1, a.eps, q_s[h], lane);
+        } else {
+          if (lane < D) q_s[h][lane] = qx0[j];
+          if (lane + kWave < D) q_s[h][lane + kWave] = qx1[j];
+        }
       }
     }
+    // The new token sits in tile p / TT; only the block owning that tile
+    // appends it.
+    const bool owns_new = (MODE == kAttnFused) && ((p / TT) % S == split);
     if (owns_new && wave == kAttnWaves - 1) {
-      const float* kraw = a.qkv + a.hq * D + g * D;
-      const float* vraw = a.qkv + a.hq * D + a.hkv * D + g * D;
-      wave_rms_norm<D>(kraw, a.k_norm, a.eps, knew_s, lane);
-      if (lane < D) vnew_s[lane] = vraw[lane];
-      if (lane + kWave < D) vnew_s[lane + kWave] = vraw[lane + kWave];
+      wave_rms_norm_regs<D>(kx0, kx1, kw0, kw1, a.eps, knew_s, lane);
+      if (lane < D) vnew_s[lane] = vx0;
+      if (lane + kWave < D) vnew_s[lane + kWave] = vx1;
     }
     __syncthreads();
     if constexpr (MODE == kAttnFused) {
-      for (int h = wave; h < R; h += kAttnWaves) wave_rope<D>(q_s[h], cos_row, sin_row, lane);
-      if (owns_new && wave == kAttnWaves - 1) wave_rope<D>(knew_s, cos_row, sin_row, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int h = wave + j * kAttnWaves;
+        if (h < R) wave_rope<D>(q_s[h], rc, rs, lane);
+      }
+      if (owns_new && wave == kAttnWaves - 1) wave_rope<D>(knew_s, rc, rs, lane);
+      // The rounding below reads elements other lanes rotated: barrier first.
       __syncthreads();
       if (owns_new && wave == kAttnWaves - 1) {
-        // Round to the cache dtype once; this step and later steps then see
-        // the same key/value.
-        KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(g) * a.capacity + p) * D;
-        KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(g) * a.capacity + p) * D;
+        // Round to the cache dtype once, so this step and later steps see the
+        // same key/value.
+        KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(g) * a.rows + p) * D;
+        KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(g) * a.rows + p) * D;
         for (int i = lane; i < D; i += kWave) {
           const KV kq = from_float<KV>(knew_s[i]);
           const KV vq = from_float<KV>(vnew_s[i]);
@@ -163,26 +230,32 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
       __syncthreads();
     }
 
-    float m_run[2] = {-INFINITY, -INFINITY};
-    float l_run[2] = {0.0f, 0.0f};
-    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};
     const float sqrt_d = sqrtf(static_cast<float>(D));
-
-    const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.capacity * D;
-    const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.capacity * D;
-
-    for (int tile = tile_begin; tile < tile_end; ++tile) {
+    for (int tile = split; tile < n_tiles; tile += S) {
       const int t0 = tile * TT;
       const int rows = min(TT, n_keys - t0);
-      // ---- stage K/V tile through LDS ----
-      const int nchunks = rows * D / CH;
-      for (int c = threadIdx.x; c < nchunks; c += kAttnThreads) {
+      // ---- stage K/V through LDS (first tile: the speculative registers) ----
+      if (!(tile == split && spec)) {
+        // Later tiles (or an unaligned capacity): fetch the tile into the same
+        // registers, all loads issued before any is consumed.
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+          const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+          const int r = min((c * CH) / D, rows - 1);
+          const int64_t off = static_cast<int64_t>(t0 + r) * D + (c * CH) % D;
+          kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
+          vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kPerThread; ++i) {
+        const int c = threadIdx.x + i * kAttnThreads;
         const int r = (c * CH) / D;
         const int col = (c * CH) % D;
-        if (MODE == kAttnFused && t0 + r == p) continue;
-        const int64_t off = static_cast<int64_t>(t0 + r) * D + col;
-        load_chunk<KV>(kbase + off, &k_s[r][col]);
-        load_chunk<KV>(vbase + off, &v_s[r][col]);
+        if (c < kChunks && r < rows && !(MODE == kAttnFused && t0 + r == p)) {
+          chunk_to_float<KV>(kc[i], &k_s[r][col]);
+          chunk_to_float<KV>(vc[i], &v_s[r][col]);
+        }
       }
       if (MODE == kAttnFused && p >= t0 && p < t0 + rows) {
         const int r = p - t0;
@@ -217,67 +290,86 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         const float alpha = expf(m_run[j] - m_new);
         const float pv = lane < rows ? expf(s - m_new) : 0.0f;
         l_run[j] = l_run[j] * alpha + group_sum<kWave>(pv);
-        if (lane < TT) p_s[h][lane] = pv;
-        acc[j][0] *= alpha;
-        acc[j][1] *= alpha;
+        if (lane < TT) p_s[lane][h] = pv;
+        if (lane == 0) alpha_s[h] = alpha;
         m_run[j] = m_new;
       }
       __syncthreads();
 
-      // ---- P.V ----
+      // ---- P.V: thread = (dimension, token group), every head at once; the
+      // probabilities of one token for all heads are one 16-byte LDS read ----
+      if (pv_active) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int h = wave + j * kAttnWaves;
-        if (h >= R) break;
-        float a0 = acc[j][0];
-        float a1 = acc[j][1];
-        for (int t = 0; t < rows; ++t) {
-          const float pt = p_s[h][t];
-          if (lane < D) a0 = fmaf(pt, v_s[t][lane], a0);
-          if (lane + kWave < D) a1 = fmaf(pt, v_s[t][lane + kWave], a1);
+        for (int h = 0; h < kAttnMaxGroup; ++h)
+          if (h < R) pacc[h] *= alpha_s[h];
+        const int tb = pv_group * kPvTokens;
+        const int n = min(kPvTokens, rows - tb);
+        for (int i = 0; i < n; ++i) {
+          const int t = tb + i;
+          const float v = v_s[t][pv_dim];
+          const float4 p0 = *reinterpret_cast<const float4*>(&p_s[t][0]);
+          pacc[0] = fmaf(p0.x, v, pacc[0]);
+          pacc[1] = fmaf(p0.y, v, pacc[1]);
+          pacc[2] = fmaf(p0.z, v, pacc[2]);
+          pacc[3] = fmaf(p0.w, v, pacc[3]);
+          if (R > 4) {
+            const float4 p1 = *reinterpret_cast<const float4*>(&p_s[t][4]);
+            pacc[4] = fmaf(p1.x, v, pacc[4]);
+            pacc[5] = fmaf(p1.y, v, pacc[5]);
+            pacc[6] = fmaf(p1.z, v, pacc[6]);
+            pacc[7] = fmaf(p1.w, v, pacc[7]);
+          }
         }
-        acc[j][0] = a0;
-        acc[j][1] = a1;
       }
       __syncthreads();
     }
+  }
 
-    // ---- per-split partial (m, l, o[D]) ----
+  // ---- partial (m, l, o[d]) per head; neutral when the split had no tile ----
+  // The token groups' P.V sums meet in LDS (k_s is free after the last tile).
+  float* red = &k_s[0][0];  // [kPvGroups][kAttnMaxGroup][D]
+  if (pv_active) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int h = wave + j * kAttnWaves;
-      if (h >= R) break;
-      float* dst = a.part + ((static_cast<int64_t>(g) * S + split) * R + h) * (D + 2);
-      if (lane == 0) {
-        store_coherent(&dst[0], m_run[j]);
-        store_coherent(&dst[1], l_run[j]);
-      }
-      if (lane < D) store_coherent(&dst[2 + lane], acc[j][0]);
-      if (lane + kWave < D) store_coherent(&dst[2 + lane + kWave], acc[j][1]);
+    for (int h = 0; h < kAttnMaxGroup; ++h)
+      if (h < R) red[(pv_group * kAttnMaxGroup + h) * D + pv_dim] = pacc[h];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int h = wave + j * kAttnWaves;
+    if (h < R && lane == 0) {
+      float* dst = a.part + attn_partial_offset(g, split, h, S, R, D);
+      dst[0] = m_run[j];
+      dst[1] = l_run[j];
     }
   }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * D; idx += kAttnThreads) {
+    const int h = idx / D, dim = idx - (idx / D) * D;
+    float o = 0.0f;
+#pragma unroll
+    for (int gidx = 0; gidx < kPvGroups; ++gidx) o += red[(gidx * kAttnMaxGroup + h) * D + dim];
+    a.part[attn_partial_offset(g, split, h, S, R, D) + 2 + dim] = o;
+  }
+}
 
-  // ---- last block of this KV head: log-sum-exp combine ----
-  if (last_block_ticket(&a.counters[g], static_cast<unsigned int>(S))) {
-    for (int h = wave; h < R; h += kAttnWaves) {
-      const float* base = a.part + (static_cast<int64_t>(g) * S * R + h) * (D + 2);
-      const int64_t stride = static_cast<int64_t>(R) * (D + 2);
-      float M = -INFINITY;
-      for (int s = 0; s < active; ++s) M = fmaxf(M, load_coherent(&base[s * stride]));
-      float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-      for (int s = 0; s < active; ++s) {
-        const float* part = base + s * stride;
-        const float w = expf(load_coherent(&part[0]) - M);
-        L = fmaf(load_coherent(&part[1]), w, L);
-        if (lane < D) o0 = fmaf(load_coherent(&part[2 + lane]), w, o0);
-        if (lane + kWave < D) o1 = fmaf(load_coherent(&part[2 + lane + kWave]), w, o1);
-      }
-      const float inv = active > 0 ? 1.0f / L : 0.0f;
-      float* out = a.out + (g * R + h) * D;
-      if (lane < D) out[lane] = o0 * inv;
-      if (lane + kWave < D) out[lane + kWave] = o1 * inv;
-    }
+// Log-sum-exp combine of the split partials: one block of 128 threads per
+// query head, thread = dimension; fixed split order, so deterministic.
+__global__ __launch_bounds__(128) void attention_combine_kernel(const float* part, int hq, int hkv, int d, int splits,
+                                                                 float* out) {
+  const int qh = blockIdx.x;
+  const int R = hq / hkv;
+  const int g = qh / R, h = qh % R;
+  float M = -INFINITY;
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, part[attn_partial_offset(g, s, h, splits, R, d)]);
+  float L = 0.0f, o = 0.0f;
+  const int dim = threadIdx.x;
+  for (int s = 0; s < splits; ++s) {
+    const float* pp = part + attn_partial_offset(g, s, h, splits, R, d);
+    const float w = expf(pp[0] - M);
+    L = fmaf(pp[1], w, L);
+    if (dim < d) o = fmaf(pp[2 + dim], w, o);
   }
+  if (dim < d) out[qh * d + dim] = o * (1.0f / L);
 }
 
 // Standalone post-process (reference K2): one wave per head.
@@ -289,17 +381,22 @@ __global__ __launch_bounds__(kWave) void qkv_postprocess_kernel(QkvPostArgs a) {
   const bool is_q = b < a.hq;
   const int head = is_q ? b : b - a.hq;
   const float* src = a.qkv + (is_q ? head * D : a.hq * D + head * D);
-  wave_rms_norm<D>(src, is_q ? a.q_norm : a.k_norm, a.eps, x_s, lane);
+  const float* w = is_q ? a.q_norm : a.k_norm;
+  const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
+  const float x0 = lane < D ? src[d0] : 0.0f;
+  const float x1 = lane + kWave < D ? src[d1] : 0.0f;
+  wave_rms_norm_regs<D>(x0, x1, w[d0], w[d1], a.eps, x_s, lane);
+  float rc = 1.0f, rs = 0.0f;
+  if (lane < D / 2) sincosf(static_cast<float>(a.position) * a.inv_freq[lane], &rs, &rc);
   __syncthreads();
-  wave_rope<D>(x_s, a.rope_cos + static_cast<int64_t>(a.position) * (D / 2),
-               a.rope_sin + static_cast<int64_t>(a.position) * (D / 2), lane);
+  wave_rope<D>(x_s, rc, rs, lane);
   __syncthreads();
   if (is_q) {
     for (int i = lane; i < D; i += kWave) a.query_out[head * D + i] = x_s[i];
   } else {
     const float* vsrc = a.qkv + a.hq * D + a.hkv * D + head * D;
-    KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.capacity + a.index) * D;
-    KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.capacity + a.index) * D;
+    KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.rows + a.index) * D;
+    KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + a.index) * D;
     for (int i = lane; i < D; i += kWave) {
       kdst[i] = from_float<KV>(x_s[i]);
       vdst[i] = from_float<KV>(vsrc[i]);
@@ -311,9 +408,9 @@ template <typename KV, int D>
 hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
   const dim3 grid(a.splits, a.hkv), block(kAttnThreads);
   if (mode == kAttnFused) {
-    attention_kernel<KV, D, kAttnFused><<<grid, block, 0, s>>>(a);
+    attention_split_kernel<KV, D, kAttnFused><<<grid, block, 0, s>>>(a);
   } else {
-    attention_kernel<KV, D, kAttnFromCache><<<grid, block, 0, s>>>(a);
+    attention_split_kernel<KV, D, kAttnFromCache><<<grid, block, 0, s>>>(a);
   }
   return hipGetLastError();
 }
@@ -353,6 +450,11 @@ bool attention_supported(int hq, int hkv, int d) {
 
 int attention_tile_tokens(int d) { return d <= 96 ? 64 : 32; }
 
+int64_t attention_cache_rows(int64_t capacity, int d) {
+  const int tile = attention_tile_tokens(d);
+  return (capacity + tile - 1) / tile * tile;
+}
+
 size_t attention_partial_floats(int hq, int hkv, int d, int splits) {
   return static_cast<size_t>(hkv) * splits * (hq / hkv) * (d + 2);
 }
@@ -360,6 +462,13 @@ size_t attention_partial_floats(int hq, int hkv, int d, int splits) {
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream) {
   if (!attention_supported(a.hq, a.hkv, a.d) || a.splits <= 0) return hipErrorInvalidValue;
   return kv == kKvF16 ? launch_attn_kv<__half>(a, mode, stream) : launch_attn_kv<float>(a, mode, stream);
+}
+
+hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
+                                    hipStream_t stream) {
+  if (!attention_supported(hq, hkv, d) || splits <= 0) return hipErrorInvalidValue;
+  attention_combine_kernel<<<hq, 128, 0, stream>>>(part, hq, hkv, d, splits, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_qkv_postprocess(const QkvPostArgs& a, KvDtype kv, hipStream_t stream) {

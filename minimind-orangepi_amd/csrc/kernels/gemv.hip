@@ -14,6 +14,53 @@ int round_cpl(int needed) {
 
 }  // namespace
 
+namespace {
+
+// One block reduces the per-block argmax partials; thread 0 does the step
+// bookkeeping.
+__global__ __launch_bounds__(kGemvBlock) void argmax_finalize_kernel(ArgmaxFinalizeArgs a) {
+  __shared__ float r_val[kGemvBlock];
+  __shared__ int r_idx[kGemvBlock];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int b = threadIdx.x; b < a.parts; b += kGemvBlock) {
+    const float v = a.part_val[b];
+    const int i = a.part_idx[b];
+    if (argmax_better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+  r_val[threadIdx.x] = bv;
+  r_idx[threadIdx.x] = bi;
+  __syncthreads();
+  for (int off = kGemvBlock / 2; off > 0; off >>= 1) {
+    if (threadIdx.x < off && argmax_better(r_val[threadIdx.x + off], r_idx[threadIdx.x + off], r_val[threadIdx.x],
+                                           r_idx[threadIdx.x])) {
+      r_val[threadIdx.x] = r_val[threadIdx.x + off];
+      r_idx[threadIdx.x] = r_idx[threadIdx.x + off];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int32_t next = r_idx[0];
+    if (a.token_out) *a.token_out = next;
+    if (a.pos) {
+      const int32_t p = *a.pos;
+      if (p + 1 < a.seq_len && p + 1 >= *a.prompt_len) a.seq[p + 1] = next;
+      *a.pos = p + 1;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_argmax_finalize(const ArgmaxFinalizeArgs& a, hipStream_t stream) {
+  if (a.parts <= 0) return hipErrorInvalidValue;
+  argmax_finalize_kernel<<<1, kGemvBlock, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 bool gemv_plan(int rows, int k, GemvEpilogue epi, int lanes_per_row, int rows_per_group, GemvPlan* plan) {
   if (rows <= 0 || k <= 0 || k % 8 != 0) return false;
   const int kchunks = k / 8;

@@ -13,12 +13,13 @@
 //  * All RPG*CPL weight loads of a lane are issued before any arithmetic, so
 //    one memory latency covers the whole tile.
 //  * x (fp32) lives in registers: each lane only needs the chunks it multiplies.
-//  * Fused prologues (RMSNorm / embedding gather) and epilogues (residual add,
-//    SwiGLU over interleaved gate/up rows, first-index argmax with a
-//    last-block-done reduction) remove the separate elementwise launches of
-//    the reference (K1, K4, K5, L2, L3).
+//  * Fused prologues (RMSNorm, embedding gather, attention split combine) and
+//    epilogues (residual add, SwiGLU over interleaved gate/up rows, per-block
+//    first-index argmax) remove the separate elementwise launches of the
+//    reference (K1, K4, K5, L2, L3).  No block ever waits for another.
 #pragma once
 
+#include "attention_common.h"
 #include "device_common.h"
 #include "kernels.h"
 
@@ -34,7 +35,8 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
   const int kchunks = k >> 3;
   const int row0 = (blockIdx.x * kGroups + group) * RPG;
 
-  // 1. Weight loads, issued first: they do not depend on x.
+  // 1. Every load that does not depend on another is issued first: weights,
+  //    then residual / norm gain / x, so one memory latency covers them all.
   uint4 wv[RPG][CPL];
 #pragma unroll
   for (int r = 0; r < RPG; ++r) {
@@ -47,6 +49,25 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
         wv[r][i] = wrow[c];
       } else {
         wv[r][i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+  float res[RPG];
+  if constexpr (EPI == kEpiResidual) {
+#pragma unroll
+    for (int r = 0; r < RPG; ++r) res[r] = (lane == 0 && row0 + r < a.rows) ? a.residual[row0 + r] : 0.0f;
+  }
+  float nw[CPL][8];
+  if constexpr (PRO == kProRmsNorm || PRO == kProRmsNormFinal || PRO == kProEmbedRmsNorm) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + G * i;
+      if (c < kchunks) {
+        const float4* src = reinterpret_cast<const float4*>(a.norm_w + c * 8);
+        const float4 lo = src[0];
+        const float4 hi = src[1];
+        nw[i][0] = lo.x; nw[i][1] = lo.y; nw[i][2] = lo.z; nw[i][3] = lo.w;
+        nw[i][4] = hi.x; nw[i][5] = hi.y; nw[i][6] = hi.z; nw[i][7] = hi.w;
       }
     }
   }
@@ -78,6 +99,68 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
         }
       }
     }
+  } else if constexpr (PRO == kProAttnCombine) {
+    // Log-sum-exp merge of the attention split partials, done by the whole
+    // block into LDS (k = hq * head_dim <= 1024, splits <= 16):
+    //   w[h][s] = exp(m[h][s] - M_h) / sum_s l[h][s] exp(m[h][s] - M_h),
+    //   x[h*d + i] = sum_s o[h][s][i] * w[h][s]   (fixed split order).
+    __shared__ __align__(16) float s_x[1024];
+    __shared__ float s_m[kGemvBlock];  // normalised split weights w[head][split]
+    // All partial loads are unconditional (clamped indices) so that they
+    // issue back to back; out-of-range values are never consumed.
+    const int S = a.splits, D = a.head_dim, R = a.hq / a.hkv;
+    float ov[4][kCombineMaxSplits];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = min(static_cast<int>(threadIdx.x) + i * kGemvBlock, k - 1);
+      const int head = kk / D, dim = kk - head * D;
+#pragma unroll
+      for (int s = 0; s < kCombineMaxSplits; ++s)
+        ov[i][s] = a.part[attn_partial_offset(head / R, min(s, S - 1), head % R, S, R, D) + 2 + dim];
+    }
+    {
+      // One lane per (head, split): S is a power of two <= 16 and hq * S <= 256
+      // (host-checked), so each head's splits are S adjacent lanes of one wave
+      // and M_h, L_h are butterfly reductions over those lanes.
+      const int t = min(static_cast<int>(threadIdx.x), a.hq * S - 1);
+      const int head = t / S, s = t - (t / S) * S;
+      const float* pp = a.part + attn_partial_offset(head / R, s, head % R, S, R, D);
+      const float m = pp[0];
+      const float l = pp[1];
+      float M = m;
+      for (int off = S / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, S));
+      const float e = expf(m - M);
+      float L = l * e;
+      for (int off = S / 2; off > 0; off >>= 1) L += __shfl_xor(L, off, S);
+      if (static_cast<int>(threadIdx.x) < a.hq * S) s_m[threadIdx.x] = e * (1.0f / L);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = threadIdx.x + i * kGemvBlock;
+      if (kk < k) {
+        const int head = kk / D;
+        float x = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kCombineMaxSplits; ++s)
+          if (s < S) x = fmaf(ov[i][s], s_m[head * S + s], x);
+        s_x[kk] = x;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = lane + G * i;
+      if (c < kchunks) {
+        const float4 lo = *reinterpret_cast<const float4*>(&s_x[c * 8]);
+        const float4 hi = *reinterpret_cast<const float4*>(&s_x[c * 8 + 4]);
+        xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
+        xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
+      }
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
@@ -95,7 +178,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  if constexpr (PRO != kProPlain) {
+  if constexpr (PRO == kProRmsNorm || PRO == kProRmsNormFinal || PRO == kProEmbedRmsNorm) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i)
@@ -107,16 +190,12 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     for (int i = 0; i < CPL; ++i) {
       const int c = lane + G * i;
       if (c < kchunks) {
-        const float4* nw = reinterpret_cast<const float4*>(a.norm_w + c * 8);
-        const float4 lo = nw[0];
-        const float4 hi = nw[1];
-        const float w8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           if constexpr (PRO == kProRmsNormFinal) {
-            xv[i][e] = (xv[i][e] * scale) * w8[e];
+            xv[i][e] = (xv[i][e] * scale) * nw[i][e];
           } else {
-            xv[i][e] = xv[i][e] * (scale * w8[e]);
+            xv[i][e] = xv[i][e] * (scale * nw[i][e]);
           }
         }
       }
@@ -146,7 +225,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
         const int row = row0 + r;
         if (row < a.rows) {
           if constexpr (EPI == kEpiResidual) {
-            a.y[row] = a.residual[row] + acc[r];
+            a.y[row] = res[r] + acc[r];
           } else {
             a.y[row] = acc[r];
           }
@@ -166,7 +245,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
         }
       }
     }
-  } else {  // kEpiArgmax
+  } else {  // kEpiArgmax: per-block (max, first index) partial
     constexpr int kRowsPerBlock = kGroups * RPG;
     __shared__ float s_val[kRowsPerBlock];
     __shared__ int s_idx[kRowsPerBlock];
@@ -189,18 +268,8 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
           bv = s_val[j];
           bi = s_idx[j];
         }
-      if (bi != 0x7fffffff) atomicMax(a.best, argmax_key(bv, bi));
-    }
-    if (last_block_ticket(a.counter, gridDim.x)) {
-      if (threadIdx.x == 0) {
-        const int32_t next = argmax_key_index(atomicExch(a.best, 0ull));
-        if (a.token_out) *a.token_out = next;
-        if (a.step_pos) {
-          const int32_t p = *a.step_pos;
-          if (p + 1 < a.seq_len && p + 1 >= *a.step_prompt_len) a.step_seq[p + 1] = next;
-          *a.step_pos = p + 1;
-        }
-      }
+      a.part_val[blockIdx.x] = bv;
+      a.part_idx[blockIdx.x] = bi;
     }
   }
 }
@@ -215,6 +284,7 @@ hipError_t launch_shape(const GemvArgs& a, GemvPrologue pro, GemvEpilogue epi, i
   }
   MMR_GEMV_CASE(kProPlain, kEpiStore)
   MMR_GEMV_CASE(kProPlain, kEpiResidual)
+  MMR_GEMV_CASE(kProAttnCombine, kEpiResidual)
   MMR_GEMV_CASE(kProRmsNorm, kEpiStore)
   MMR_GEMV_CASE(kProEmbedRmsNorm, kEpiStore)
   MMR_GEMV_CASE(kProRmsNormFinal, kEpiArgmax)

@@ -20,16 +20,20 @@ enum GemvPrologue : int {
   kProPlain = 0,       // x used as given
   kProRmsNorm = 1,     // x := x * (scale * norm_w)      decoder_layer.cpp:32-42
   kProRmsNormFinal = 2,// x := (x * scale) * norm_w      language_model.cpp:24-38
-  kProEmbedRmsNorm = 3 // x := embed[seq[*pos]] (fp16 -> fp32), then kProRmsNorm;
+  kProEmbedRmsNorm = 3,// x := embed[seq[*pos]] (fp16 -> fp32), then kProRmsNorm;
                        //      block 0 also stores the raw row to h_out
+  kProAttnCombine = 4  // x := log-sum-exp combine of the attention split partials
+                       //      (part, splits, hq, hkv, head_dim; k = hq * head_dim)
 };
+constexpr int kCombineMaxSplits = 16;  // kProAttnCombine supports splits <= 16, k <= 1024
 
 enum GemvEpilogue : int {
   kEpiStore = 0,     // y[r] = dot
   kEpiResidual = 1,  // y[r] = residual[r] + dot
   kEpiSwiGlu = 2,    // rows interleaved (gate_0, up_0, gate_1, up_1, ...):
                      //   y[i] = silu(gate_i) * up_i      decoder_layer.cpp:175-182
-  kEpiArgmax = 3     // y[r] = dot (optional), token = first argmax over r
+  kEpiArgmax = 3     // y[r] = dot (optional); per-block (max, first index) partials,
+                     //   reduced by launch_argmax_finalize
 };
 
 struct GemvArgs {
@@ -48,18 +52,29 @@ struct GemvArgs {
   // outputs
   float* y = nullptr;
   const float* residual = nullptr;
-  // kEpiArgmax
-  unsigned long long* best = nullptr;  // packed (value, ~index) key, zero before first use
-  unsigned int* counter = nullptr;      // zero before first use
+  // kProAttnCombine
+  const float* part = nullptr;
+  int splits = 0, hq = 0, hkv = 0, head_dim = 0;
+  // kEpiArgmax: one (value, index) pair per block
+  float* part_val = nullptr;
+  int* part_idx = nullptr;
+};
+
+// Reduces the per-block argmax partials (first index among equal maxima),
+// writes the token, and optionally does the decode-step bookkeeping: the step
+// at position p = *pos writes its prediction to seq[p + 1] when
+// p + 1 >= *prompt_len, then advances *pos.  One block.
+struct ArgmaxFinalizeArgs {
+  const float* part_val = nullptr;
+  const int* part_idx = nullptr;
+  int parts = 0;
   int32_t* token_out = nullptr;
-  // optional decode-step bookkeeping with kEpiArgmax: the step at position
-  // p = *step_pos writes its prediction to step_seq[p + 1] when
-  // p + 1 >= *step_prompt_len, then advances *step_pos.
-  int32_t* step_seq = nullptr;
-  int32_t* step_pos = nullptr;
-  const int32_t* step_prompt_len = nullptr;
+  int32_t* seq = nullptr;
+  int32_t* pos = nullptr;
+  const int32_t* prompt_len = nullptr;
   int seq_len = 0;
 };
+hipError_t launch_argmax_finalize(const ArgmaxFinalizeArgs& a, hipStream_t stream);
 
 struct GemvPlan {
   int lanes_per_row = 32;  // 16, 32 or 64
@@ -77,8 +92,8 @@ constexpr int kGemvBlock = 256;
 
 // ----------------------------------------------------------- attention ----
 // GQA decode attention for one query token over a resident KV cache laid out
-// [kv_head][capacity][head_dim], split along the context into `splits` ranges
-// per KV head and merged with a log-sum-exp combine by the last block.
+// [kv_head][rows][head_dim], split along the context into `splits` tile sets
+// per KV head; the partials are merged by a log-sum-exp combine in the consumer.
 enum AttnMode : int {
   kAttnFused = 0,     // q/k RMSNorm + RoPE from the raw projection, append k/v at
                       // index *pos, attend over *pos + 1 keys
@@ -88,32 +103,33 @@ enum AttnMode : int {
 enum KvDtype : int { kKvF16 = 0, kKvF32 = 1 };
 
 struct AttnArgs {
-  const float* qkv = nullptr;  // fused: [Hq*D + 2*Hkv*D]
+  const float* qkv = nullptr;       // fused: raw projection [Hq*D + 2*Hkv*D]
   const float* q_norm = nullptr;
   const float* k_norm = nullptr;
   float eps = 0.0f;
-  const float* rope_cos = nullptr;  // [max_pos][D/2]
-  const float* rope_sin = nullptr;
-  const int32_t* pos = nullptr;     // fused: index of the new token
+  const float* inv_freq = nullptr;  // fused: [D/2] RoPE frequencies
+  const int32_t* pos = nullptr;     // fused: index of the new token (device)
   const float* q = nullptr;         // from-cache: [Hq*D]
   int tokens = 0;                   // from-cache: cached keys
-  void* kcache = nullptr;
+  void* kcache = nullptr;           // [Hkv][rows][D]
   void* vcache = nullptr;
-  int capacity = 0;
-  int max_pos = 0;
+  int capacity = 0;                 // usable positions
+  int rows = 0;                     // allocated rows per head (capacity rounded up to the tile)
   int hq = 0, hkv = 0, d = 0;
   int splits = 1;
   float* part = nullptr;            // [Hkv][splits][R][D+2]
-  unsigned int* counters = nullptr; // [Hkv], zero on first use, re-armed by the kernel
-  float* out = nullptr;             // [Hq*D]
   int32_t* err = nullptr;           // set to 1 when *pos is out of range
 };
 
 constexpr int kAttnMaxGroup = 8;  // Hq / Hkv supported
 size_t attention_partial_floats(int hq, int hkv, int d, int splits);
 int attention_tile_tokens(int d);
+int64_t attention_cache_rows(int64_t capacity, int d);
 bool attention_supported(int hq, int hkv, int d);
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream);
+// Merge the split partials into out [Hq*D] (one block per query head).
+hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
+                                    hipStream_t stream);
 
 // qkv post-process as a standalone op (reference K2): per-head q/k RMSNorm +
 // RoPE at `position`, q -> query_out, k/v appended at cache index `index`.
@@ -122,13 +138,12 @@ struct QkvPostArgs {
   const float* q_norm = nullptr;
   const float* k_norm = nullptr;
   float eps = 0.0f;
-  const float* rope_cos = nullptr;
-  const float* rope_sin = nullptr;
+  const float* inv_freq = nullptr;  // [D/2]
   int position = 0;
   int index = 0;
   void* kcache = nullptr;
   void* vcache = nullptr;
-  int capacity = 0;
+  int rows = 0;
   int hq = 0, hkv = 0, d = 0;
   float* query_out = nullptr;
 };

@@ -46,8 +46,7 @@ struct DeviceModel {
   const __half* lm_head = nullptr;  // [V][H] (aliases embed when identical)
   const float* final_norm = nullptr;
   std::vector<LayerDev> layers;
-  const float* rope_cos = nullptr;  // [max_pos][d/2], same formula as decoder_layer.cpp:109-119
-  const float* rope_sin = nullptr;
+  const float* inv_freq = nullptr;  // [d/2] RoPE frequencies, formula of decoder_layer.cpp:114
   mmr::GemvPlan plan_qkv, plan_o, plan_gu, plan_down, plan_lm;
   std::size_t weight_bytes = 0;
 };
@@ -68,13 +67,15 @@ struct DeviceState {
   float* attn = nullptr;
   float* act = nullptr;
   float* logits = nullptr;
-  float* attn_part = nullptr;
-  unsigned long long* lm_best = nullptr;  // packed argmax key of the head GEMV
-  unsigned int* counters = nullptr;       // [Hkv] attention, [1] head
+  float* attn_part = nullptr;  // split partials [Hkv][splits][R][d + 2]
+  float* lm_part_val = nullptr;  // per-block argmax partials of the head GEMV
+  int* lm_part_idx = nullptr;
+  int64_t cache_rows = 0;        // capacity rounded up to the attention tile
   int32_t* staging = nullptr;        // pinned host [capacity + 8]
   hipStream_t stream = nullptr;
   std::map<int, hipGraphExec_t> graphs;
   bool use_graphs = true;
+  bool combine_kernel = false;  // merge attention splits in a separate kernel, not the O prologue
 
   ~DeviceState() {
     if (stream) (void)hipStreamSynchronize(stream);
@@ -86,7 +87,9 @@ struct DeviceState {
 
 namespace {
 
-constexpr int kSplitBuckets[] = {8, 32, 128, 512};
+// Attention split counts: the smallest bucket holding one tile per split is
+// used, so the step graph only changes at bucket boundaries.
+constexpr int kSplitBuckets[] = {8, 16, 32, 64, 128, 256, 512};
 constexpr int kMaxSplits = 512;
 
 void require_size(const std::vector<float>& v, int64_t expected, const std::string& name) {
@@ -182,8 +185,7 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
     ar.plan(2 * F * H * 2);
     ar.plan(H * F * 2);
   }
-  ar.plan(max_pos * half_d * 4);
-  ar.plan(max_pos * half_d * 4);
+  ar.plan(half_d * 4);
   ar.allocate();
 
   dm->embed = upload<__half>(ar, to_half(weights.embed_tokens).data(), V * H);
@@ -214,29 +216,24 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
     dm->layers.push_back(d);
     wbytes += 2 * H * 4 + 2 * D * 4 + ((qs + 2 * kvs) * H + H * qs + 2 * F * H + H * F) * 2;
   }
-  // RoPE tables with the reference formula (decoder_layer.cpp:109-119):
-  // inv_freq = 1 / powf(theta, 2i / d), angle = float(pos) * inv_freq.
+  // RoPE frequencies with the reference formula (decoder_layer.cpp:114):
+  // inv_freq = 1 / powf(theta, 2i / d); the kernels evaluate
+  // cos/sin(float(pos) * inv_freq) on the device.
   {
     std::vector<float> inv(static_cast<size_t>(half_d));
     for (int64_t i = 0; i < half_d; ++i)
       inv[static_cast<size_t>(i)] =
           1.0F / std::pow(c.rope_theta, static_cast<float>(i * 2) / static_cast<float>(D));
-    std::vector<float> cs(static_cast<size_t>(max_pos * half_d)), sn(cs.size());
-    for (int64_t p = 0; p < max_pos; ++p)
-      for (int64_t i = 0; i < half_d; ++i) {
-        const float angle = static_cast<float>(p) * inv[static_cast<size_t>(i)];
-        cs[static_cast<size_t>(p * half_d + i)] = std::cos(angle);
-        sn[static_cast<size_t>(p * half_d + i)] = std::sin(angle);
-      }
-    dm->rope_cos = upload<float>(ar, cs.data(), cs.size());
-    dm->rope_sin = upload<float>(ar, sn.data(), sn.size());
+    dm->inv_freq = upload<float>(ar, inv.data(), inv.size());
   }
+  (void)max_pos;
   dm->weight_bytes = wbytes;
   dm->plan_qkv = plan_or_throw(static_cast<int>(qs + 2 * kvs), static_cast<int>(H), mmr::kEpiStore, "qkv_proj");
   dm->plan_o = plan_or_throw(static_cast<int>(H), static_cast<int>(qs), mmr::kEpiResidual, "o_proj");
   dm->plan_gu = plan_or_throw(static_cast<int>(2 * F), static_cast<int>(H), mmr::kEpiSwiGlu, "gate_up_proj");
   dm->plan_down = plan_or_throw(static_cast<int>(H), static_cast<int>(F), mmr::kEpiResidual, "down_proj");
-  dm->plan_lm = plan_or_throw(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, "lm_head");
+  if (!mmr::gemv_plan(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, 0, 4, &dm->plan_lm))
+    throw std::invalid_argument("unsupported GEMV shape for lm_head");
   check_hip(hipDeviceSynchronize(), "weight upload");
   device_ = std::move(dm);
 }
@@ -260,10 +257,13 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->capacity = capacity;
   const char* nog = std::getenv("MMR_NO_GRAPH");
   s->use_graphs = !(nog && nog[0] == '1');
+  const char* ck = std::getenv("MMR_COMBINE_KERNEL");
+  s->combine_kernel = ck && ck[0] == '1';
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
   const int64_t F = c.intermediate_size, V = c.vocab_size;
   const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
-  const std::size_t cache_bytes = static_cast<std::size_t>(Hkv * capacity * D) * kv_elem;
+  s->cache_rows = mmr::attention_cache_rows(capacity, static_cast<int>(D));
+  const std::size_t cache_bytes = static_cast<std::size_t>(Hkv * s->cache_rows * D) * kv_elem;
   Arena& ar = s->arena;
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
     ar.plan(cache_bytes);
@@ -279,8 +279,8 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   ar.plan(F * 4);
   ar.plan(V * 4);
   ar.plan(part_floats * 4);
-  ar.plan(8);
-  ar.plan((Hkv + 1) * 4);
+  ar.plan(device_->plan_lm.blocks * 4);
+  ar.plan(device_->plan_lm.blocks * 4);
   ar.allocate();
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
     s->kcache.push_back(ar.take<char>(cache_bytes));
@@ -298,15 +298,14 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->act = ar.take<float>(F);
   s->logits = ar.take<float>(V);
   s->attn_part = ar.take<float>(part_floats);
-  s->lm_best = ar.take<unsigned long long>(1);
-  s->counters = ar.take<unsigned int>(Hkv + 1);
+  s->lm_part_val = ar.take<float>(device_->plan_lm.blocks);
+  s->lm_part_idx = ar.take<int>(device_->plan_lm.blocks);
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
                           hipHostMallocDefault),
             "hipHostMalloc staging");
   check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
   check_hip(hipMemsetAsync(scalars, 0, 4 * sizeof(int32_t), s->stream), "hipMemsetAsync");
-  check_hip(hipMemsetAsync(s->counters, 0, (Hkv + 1) * sizeof(unsigned int), s->stream), "hipMemsetAsync");
-  check_hip(hipMemsetAsync(s->lm_best, 0, sizeof(unsigned long long), s->stream), "hipMemsetAsync");
+
   check_hip(hipMemsetAsync(s->seq, 0, (capacity + 1) * sizeof(int32_t), s->stream), "hipMemsetAsync");
   check_hip(hipStreamSynchronize(s->stream), "state init");
   DecoderState state;
@@ -317,10 +316,11 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
 
 namespace {
 
-enum StepKernel : int { kQkv = 0, kAttention = 1, kOProj = 2, kGateUp = 3, kDown = 4, kHead = 5 };
+enum StepKernel : int { kQkv = 0, kAttention = 1, kOProj = 2, kGateUp = 3, kDown = 4, kHead = 5, kFinalize = 6 };
 
-// One kernel of the decode step; `bookkeeping` (head only) lets the argmax
-// write seq[pos + 1] and advance the device position.
+// One kernel (or, for kOProj with many splits, the combine + GEMV pair) of
+// the decode step; `bookkeeping` (finalize only) lets it write seq[pos + 1]
+// and advance the device position.
 void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool bookkeeping) {
   const DeviceModel& m = *s.model;
   const auto& c = m.cfg;
@@ -357,20 +357,17 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       t.q_norm = L.q_norm;
       t.k_norm = L.k_norm;
       t.eps = c.rms_norm_eps;
-      t.rope_cos = m.rope_cos;
-      t.rope_sin = m.rope_sin;
+      t.inv_freq = m.inv_freq;
       t.pos = s.pos;
       t.kcache = s.kcache[l];
       t.vcache = s.vcache[l];
       t.capacity = static_cast<int>(s.capacity);
-      t.max_pos = static_cast<int>(c.max_position_embeddings);
+      t.rows = static_cast<int>(s.cache_rows);
       t.hq = Hq;
       t.hkv = Hkv;
       t.d = D;
       t.splits = splits;
       t.part = s.attn_part;
-      t.counters = s.counters;
-      t.out = s.attn;
       t.err = s.err;
       check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "attention");
       return;
@@ -380,10 +377,22 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       a.w = L.o;
       a.rows = H;
       a.k = Hq * D;
-      a.x = s.attn;
       a.y = s.h;
       a.residual = s.h;
-      check_hip(mmr::launch_gemv(a, mmr::kProPlain, mmr::kEpiResidual, m.plan_o, s.stream), "o gemv");
+      mmr::GemvPrologue pro = mmr::kProPlain;
+      if (!s.combine_kernel && splits <= mmr::kCombineMaxSplits && Hq * D <= 1024 && Hq * splits <= 256) {
+        pro = mmr::kProAttnCombine;
+        a.part = s.attn_part;
+        a.splits = splits;
+        a.hq = Hq;
+        a.hkv = Hkv;
+        a.head_dim = D;
+      } else {
+        check_hip(mmr::launch_attention_combine(s.attn_part, Hq, Hkv, D, splits, s.attn, s.stream),
+                  "attention combine");
+        a.x = s.attn;
+      }
+      check_hip(mmr::launch_gemv(a, pro, mmr::kEpiResidual, m.plan_o, s.stream), "o gemv");
       return;
     }
     case kGateUp: {
@@ -418,16 +427,24 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       a.norm_w = m.final_norm;
       a.eps = c.rms_norm_eps;
       a.y = s.logits;
-      a.best = s.lm_best;
-      a.counter = s.counters + Hkv;
-      a.token_out = s.token_out;
-      if (bookkeeping) {
-        a.step_seq = s.seq;
-        a.step_pos = s.pos;
-        a.step_prompt_len = s.prompt_len;
-        a.seq_len = static_cast<int>(s.capacity + 1);
-      }
+      a.part_val = s.lm_part_val;
+      a.part_idx = s.lm_part_idx;
       check_hip(mmr::launch_gemv(a, mmr::kProRmsNormFinal, mmr::kEpiArgmax, m.plan_lm, s.stream), "lm_head gemv");
+      return;
+    }
+    case kFinalize: {
+      mmr::ArgmaxFinalizeArgs f;
+      f.part_val = s.lm_part_val;
+      f.part_idx = s.lm_part_idx;
+      f.parts = m.plan_lm.blocks;
+      f.token_out = s.token_out;
+      if (bookkeeping) {
+        f.seq = s.seq;
+        f.pos = s.pos;
+        f.prompt_len = s.prompt_len;
+        f.seq_len = static_cast<int>(s.capacity + 1);
+      }
+      check_hip(mmr::launch_argmax_finalize(f, s.stream), "argmax finalize");
       return;
     }
     default:
@@ -438,7 +455,8 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
 void enqueue_step_kernels(const DeviceState& s, int splits) {
   for (size_t l = 0; l < s.model->layers.size(); ++l)
     for (int k = kQkv; k <= kDown; ++k) enqueue_kernel(s, k, l, splits, false);
-  enqueue_kernel(s, kHead, 0, splits, true);
+  enqueue_kernel(s, kHead, 0, splits, false);
+  enqueue_kernel(s, kFinalize, 0, splits, true);
 }
 
 hipGraphExec_t capture_step(DeviceState& s, int splits) {
@@ -522,7 +540,7 @@ void LanguageModel::enqueue_prefill(DecoderState& state, const std::vector<int32
 void LanguageModel::enqueue_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const {
   DeviceState& s = *state.device;
   const int64_t L = config_.num_hidden_layers;
-  if (kernel < kQkv || kernel > kHead) throw std::invalid_argument("unknown step kernel");
+  if (kernel < kQkv || kernel > kFinalize) throw std::invalid_argument("unknown step kernel");
   if (layer < 0 || layer >= L || count < 0) throw std::invalid_argument("layer / count out of range");
   if (kernel == kAttention && state.position >= s.capacity) throw std::length_error("KV cache capacity exhausted");
   const int splits = choose_splits(state.position + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));

@@ -86,8 +86,9 @@ class LanguageModel {
   // Logits of the last executed step.
   std::vector<float> read_logits(DecoderState& state) const;
   // Enqueue `count` launches of one step kernel (0 qkv, 1 attention, 2 o,
-  // 3 gate_up, 4 down, 5 lm_head without bookkeeping), cycling over layers
-  // from `layer`.  Used to time single kernels; overwrites scratch buffers.
+  // 3 gate_up, 4 down, 5 lm_head, 6 argmax finalize without bookkeeping),
+  // cycling over layers from `layer`.  Used to time single kernels;
+  // overwrites scratch buffers.
   void enqueue_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const;
   // Reset position to 0 (the cache contents are overwritten as it refills).
   void reset_state(DecoderState& state) const;

@@ -106,6 +106,7 @@ _SIGS = {
     "mmr_kv_cache_create": ([I64, I64, I64, C.c_int, C.POINTER(VP)], C.c_int),
     "mmr_kv_cache_destroy": ([VP], C.c_int),
     "mmr_kv_cache_data": ([VP, C.POINTER(VP), C.POINTER(VP)], C.c_int),
+    "mmr_kv_cache_rows": ([VP, C.POINTER(I64)], C.c_int),
     "mmr_decode_qkv_postprocess": ([VP, VP, VP, VP, I64, I64, I64, I64, I64, VP, F32, VP, VP], C.c_int),
     "mmr_attention_workspace_size": ([I64, I64, I64, C.c_int], SZ),
     "mmr_attention_from_cache": ([VP, VP, I64, I64, I64, I64, VP, VP, SZ, C.c_int, VP], C.c_int),
@@ -329,6 +330,9 @@ class KvCache:
         self.handle = h.value
         self.kv_heads, self.head_dim, self.capacity, self.kv_dtype = kv_heads, head_dim, capacity, kv_dtype
         self.np_dtype = np.float16 if kv_dtype == KV_F16 else np.float32
+        rows = C.c_int64(0)
+        check(_lib.mmr_kv_cache_rows(self.handle, C.byref(rows)))
+        self.rows = int(rows.value)  # capacity rounded up to the attention tile
 
     def pointers(self) -> tuple[int, int]:
         k, v = VP(), VP()
@@ -336,10 +340,10 @@ class KvCache:
         return k.value, v.value
 
     def _nbytes(self) -> int:
-        return self.kv_heads * self.capacity * self.head_dim * np.dtype(self.np_dtype).itemsize
+        return self.kv_heads * self.rows * self.head_dim * np.dtype(self.np_dtype).itemsize
 
     def upload(self, keys: np.ndarray, values: np.ndarray) -> None:
-        """keys/values shaped [kv_heads, capacity, head_dim] (cache layout)."""
+        """keys/values shaped [kv_heads, rows, head_dim] (cache layout)."""
         kp, vp = self.pointers()
         for ptr, a in ((kp, keys), (vp, values)):
             a = np.ascontiguousarray(a, dtype=self.np_dtype)
@@ -350,7 +354,7 @@ class KvCache:
         kp, vp = self.pointers()
         out = []
         for ptr in (kp, vp):
-            a = np.empty((self.kv_heads, self.capacity, self.head_dim), self.np_dtype)
+            a = np.empty((self.kv_heads, self.rows, self.head_dim), self.np_dtype)
             check(_lib.mmr_memcpy_d2h(_ptr(a), ptr, a.nbytes))
             out.append(a)
         return out[0], out[1]

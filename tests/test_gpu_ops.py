@@ -91,7 +91,7 @@ def test_argmax_matches_oracle_and_first_index(gpu, oracle):
     nw = np.ones(H, np.float32)
     dw, dh, dn = (mmr.DeviceArray.from_numpy(a) for a in (w16.view(np.uint16), h, nw))
     logits, tok = mmr.DeviceArray(V, np.float32), mmr.DeviceArray(1, np.int32)
-    ws = mmr.DeviceArray(mmr.matvec_argmax_workspace_size(V, H), np.uint8, zero=True)
+    ws = mmr.DeviceArray(mmr.matvec_argmax_workspace_size(V, H), np.uint8)
     mmr.matvec_argmax_f16(dw, V, H, dh, tok, ws, logits=logits, norm_w=dn, eps=eps)
     ref = oracle.matvec(w32, oracle.rms_norm_final(h, nw, eps))
     assert rel_err(logits.numpy(), ref) < TOL
@@ -102,14 +102,14 @@ def test_argmax_matches_oracle_and_first_index(gpu, oracle):
         w2 = w16.copy()
         w2[dup] = w16[win]
         dw.upload(w2.view(np.uint16))
-        for rep in range(3):  # re-armed workspace: repeated calls stay correct
+        for rep in range(3):  # repeated calls on the same workspace stay correct
             mmr.matvec_argmax_f16(dw, V, H, dh, tok, ws, norm_w=dn, eps=eps)
             assert int(tok.numpy()[0]) == min(win, dup)
 
 
-def cache_layout(keys_ref, tokens, hkv, d, capacity):
-    """[token][kv_head][d] (reference) -> [kv_head][capacity][d] (cache)."""
-    out = np.zeros((hkv, capacity, d), keys_ref.dtype)
+def cache_layout(keys_ref, tokens, hkv, d, rows):
+    """[token][kv_head][d] (reference) -> [kv_head][rows][d] (cache)."""
+    out = np.zeros((hkv, rows, d), keys_ref.dtype)
     out[:, :tokens, :] = keys_ref.reshape(tokens, hkv, d).transpose(1, 0, 2)
     return out
 
@@ -128,14 +128,14 @@ def test_attention_from_cache_matches_oracle(gpu, oracle, kv, tokens):
     v = rng.standard_normal(tokens * hkv * d).astype(np_kv).astype(np.float32)
     cap = tokens + 3
     cache = mmr.KvCache(hkv, d, cap, mmr.KV_F16 if kv == "f16" else mmr.KV_F32)
-    cache.upload(cache_layout(k, tokens, hkv, d, cap), cache_layout(v, tokens, hkv, d, cap))
+    cache.upload(cache_layout(k, tokens, hkv, d, cache.rows), cache_layout(v, tokens, hkv, d, cache.rows))
     dq, out = mmr.DeviceArray.from_numpy(q), mmr.DeviceArray(hq * d, np.float32)
-    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 512), np.uint8, zero=True)
+    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 512), np.uint8)
     ref = oracle.attention_step(q, k, v, tokens, hq, hkv, d)
     mmr.attention_from_cache(dq, cache, tokens, hq, hkv, d, out, ws)
     got = out.numpy()
     assert rel_err(got, ref) < TOL
-    for splits in (1, 3, 512):  # any split count gives the same result
+    for splits in (1, 3, 7, 512):  # any split count gives the same result
         mmr.attention_from_cache(dq, cache, tokens, hq, hkv, d, out, ws, splits=splits)
         assert rel_err(out.numpy(), got) < 1e-5
 
@@ -149,9 +149,9 @@ def test_attention_reference_patterned_case(gpu, oracle):
     k = ((i % 17) - 8).astype(np.float32) * 0.025
     v = ((i % 11) - 5).astype(np.float32) * 0.0375
     cache = mmr.KvCache(hkv, d, 8, mmr.KV_F32)
-    cache.upload(cache_layout(k, T, hkv, d, 8), cache_layout(v, T, hkv, d, 8))
+    cache.upload(cache_layout(k, T, hkv, d, cache.rows), cache_layout(v, T, hkv, d, cache.rows))
     dq, out = mmr.DeviceArray.from_numpy(q), mmr.DeviceArray(hq * d, np.float32)
-    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 0), np.uint8, zero=True)
+    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 0), np.uint8)
     mmr.attention_from_cache(dq, cache, T, hq, hkv, d, out, ws)
     assert rel_err(out.numpy(), oracle.attention_step(q, k, v, T, hq, hkv, d)) < TOL
 
@@ -176,12 +176,17 @@ def test_qkv_postprocess_and_append(gpu, oracle, d):
     assert rel_err(keys[:, tokens - 1, :].reshape(-1), k_ref) < 1e-5
     np.testing.assert_array_equal(vals[:, tokens - 1, :].reshape(-1), qkv[(hq + hkv) * d:])
     assert not keys[:, tokens:, :].any() and not keys[:, : tokens - 1, :].any()
+    assert cache.rows % 32 == 0 and cache.rows >= 16
 
 
+@pytest.mark.parametrize("d", [32, 64, 96, 128])
 @pytest.mark.parametrize("kv", ["f16", "f32"])
-def test_fused_append_attention_matches_oracle(gpu, oracle, kv):
+def test_fused_append_attention_matches_oracle(gpu, oracle, kv, d):
+    # regression: the appended key must be the rotated one for every head_dim
+    # (d = 64 once stored a half-rotated key: a missing barrier between RoPE
+    # and the rounding of the new key)
     mmr = gpu
-    hq, hkv, d, eps, theta = 8, 2, 96, 1e-5, 1e6
+    hq, hkv, eps, theta = 8, 2, 1e-5, 1e6
     rng = np.random.default_rng(21)
     np_kv = np.float16 if kv == "f16" else np.float32
     cap = 300
@@ -190,7 +195,7 @@ def test_fused_append_attention_matches_oracle(gpu, oracle, kv):
     qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     dqn, dkn = mmr.DeviceArray.from_numpy(qn), mmr.DeviceArray.from_numpy(kn)
-    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 8), np.uint8, zero=True)
+    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 8), np.uint8)
     err = mmr.DeviceArray(1, np.int32, zero=True)
     pos_d = mmr.DeviceArray(1, np.int32)
     out = mmr.DeviceArray(hq * d, np.float32)
@@ -204,9 +209,15 @@ def test_fused_append_attention_matches_oracle(gpu, oracle, kv):
                                            eps, theta)
         keys_ref.append(k_ref.astype(np_kv).astype(np.float32))
         vals_ref.append(qkv[(hq + hkv) * d:].astype(np_kv).astype(np.float32))
-        if pos in (0, 1, 63, 64, 200, cap - 1):
+        if pos in (0, 1, 2, 3, 63, 64, 200, cap - 1):
             ref = oracle.attention_step(q_ref, np.concatenate(keys_ref), np.concatenate(vals_ref), pos + 1, hq, hkv, d)
             assert rel_err(out.numpy(), ref) < TOL, pos
+            keys, _ = cache.download()
+            stored = keys[:, : pos + 1, :].transpose(1, 0, 2).reshape(-1).astype(np.float32)
+            # fp32 cache: fp32 rounding only; fp16 cache: a key within 1e-7 of an
+            # fp16 rounding boundary may land on the neighbouring value (2^-11 rel)
+            key_tol = 1e-5 if kv == "f32" else 1e-3
+            assert rel_err(stored, np.concatenate(keys_ref)) < key_tol, pos
     assert int(err.numpy()[0]) == 0
     pos_d.upload(np.array([cap], np.int32))  # out of range: flagged, nothing written
     mmr.decode_attention_fused(mmr.DeviceArray.from_numpy(qkv), dqn, dkn, eps, rope, pos_d, cache, hq, hkv, d, out,

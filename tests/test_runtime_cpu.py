@@ -158,4 +158,4 @@ def test_op_argument_checks_need_no_device(mmr):
         mmr.check(mmr.lib().mmr_attention_from_cache(1, 1, 4, 8, 2, 80, 1, 1, 1 << 20, 0, None))
     assert mmr.matvec_argmax_workspace_size(6400, 768) > 0
     assert mmr.matvec_argmax_workspace_size(6400, 770) == 0
-    assert mmr.attention_workspace_size(8, 2, 96, 64) == 256 + 2 * 64 * 4 * 98 * 4
+    assert mmr.attention_workspace_size(8, 2, 96, 64) == 2 * 64 * 4 * 98 * 4
