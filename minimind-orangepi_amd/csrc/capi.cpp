@@ -125,7 +125,8 @@ int auto_splits(int64_t tokens, int64_t head_dim) {
   return static_cast<int>(tiles < 1 ? 1 : (tiles > 512 ? 512 : tiles));
 }
 
-// Attention workspace: the split partials [Hkv][splits][R][d + 2] (fp32).
+// Attention workspace: the split partials, o [Hkv][splits][R][d] then (m, l)
+// [Hkv][splits][R][2], fp32.
 size_t attention_ws_bytes(int64_t hq, int64_t hkv, int64_t d, int splits) {
   return mmr::attention_partial_floats(static_cast<int>(hq), static_cast<int>(hkv), static_cast<int>(d), splits) * 4;
 }

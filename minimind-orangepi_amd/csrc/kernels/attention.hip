@@ -76,6 +76,20 @@ __device__ __forceinline__ void wave_rope(float* x, float c, float s, int lane) 
   }
 }
 
+__device__ __forceinline__ void pv_fma(float2& acc, float p, const float2& v) {
+  acc.x = fmaf(p, v.x, acc.x);
+  acc.y = fmaf(p, v.y, acc.y);
+}
+
+// P.V work split: thread = (dimension pair, token group); the largest power of
+// two <= 8 groups that fits 256 threads and divides the tile.
+template <int D, int TT>
+constexpr int attn_pv_groups() {
+  int g = 8;
+  while (g > 1 && (g * (D / 2) > kAttnThreads || TT % g != 0)) g /= 2;
+  return g;
+}
+
 template <typename KV, int D, int MODE>
 __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs a) {
   constexpr int TT = attn_tile_tokens<D>();
@@ -83,14 +97,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   constexpr int CH = 16 / static_cast<int>(sizeof(KV));
   constexpr int kChunks = TT * D / CH;  // 16-byte chunks per K (or V) tile
   constexpr int kPerThread = (kChunks + kAttnThreads - 1) / kAttnThreads;
+  constexpr int kPairs = D / 2;
+  constexpr int kPvGroups = attn_pv_groups<D, TT>();
+  constexpr int kPvTokens = TT / kPvGroups;
   __shared__ __align__(16) float q_s[kAttnMaxGroup][D];
   __shared__ __align__(16) float k_s[TT][LD];
   __shared__ __align__(16) float v_s[TT][LD];
   __shared__ __align__(16) float p_s[TT][kAttnMaxGroup];  // token-major: one 16-byte read per 4 heads
   __shared__ float alpha_s[kAttnMaxGroup];
-  // P.V token groups: 256 threads cover d dims x kPvGroups groups of tokens.
-  constexpr int kPvGroups = (D <= 64) ? ((kAttnThreads / D) < 8 ? (kAttnThreads / D) : 8) : 2;
-  constexpr int kPvTokens = TT / kPvGroups;
   static_assert(kPvGroups * kAttnMaxGroup * D <= TT * LD, "P.V reduction must fit in k_s");
   __shared__ float knew_s[D];
   __shared__ float vnew_s[D];
@@ -169,13 +183,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
 
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.0f, 0.0f};
-  // P.V ownership: thread = (dimension pv_dim, token group pv_group).
-  const int pv_dim = threadIdx.x % D;
-  const int pv_group = threadIdx.x / D;
-  const bool pv_active = static_cast<int>(threadIdx.x) < kPvGroups * D;
-  float pacc[kAttnMaxGroup];
+  // P.V ownership: thread = (dimensions 2 * pv_pair + {0, 1}, token group).
+  const int pv_pair = threadIdx.x % kPairs;
+  const int pv_group = threadIdx.x / kPairs;
+  const bool pv_active = static_cast<int>(threadIdx.x) < kPvGroups * kPairs;
+  float2 pacc[kAttnMaxGroup];
 #pragma unroll
-  for (int h = 0; h < kAttnMaxGroup; ++h) pacc[h] = 0.0f;
+  for (int h = 0; h < kAttnMaxGroup; ++h) pacc[h] = make_float2(0.0f, 0.0f);
 
   if (split < n_tiles) {
     // ---- 3. queries (and the new key/value), RoPE angle from the position ----
@@ -247,14 +261,24 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
           vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
         }
       }
+      // Rows past the context are zero-filled: P.V runs over the whole tile
+      // with zero probabilities there, and 0 * (stale LDS) could be NaN.
 #pragma unroll
       for (int i = 0; i < kPerThread; ++i) {
         const int c = threadIdx.x + i * kAttnThreads;
         const int r = (c * CH) / D;
         const int col = (c * CH) % D;
-        if (c < kChunks && r < rows && !(MODE == kAttnFused && t0 + r == p)) {
-          chunk_to_float<KV>(kc[i], &k_s[r][col]);
-          chunk_to_float<KV>(vc[i], &v_s[r][col]);
+        if (c < kChunks && !(MODE == kAttnFused && t0 + r == p)) {
+          if (r < rows) {
+            chunk_to_float<KV>(kc[i], &k_s[r][col]);
+            chunk_to_float<KV>(vc[i], &v_s[r][col]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+              k_s[r][col + e] = 0.0f;
+              v_s[r][col + e] = 0.0f;
+            }
+          }
         }
       }
       if (MODE == kAttnFused && p >= t0 && p < t0 + rows) {
@@ -296,28 +320,41 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
       }
       __syncthreads();
 
-      // ---- P.V: thread = (dimension, token group), every head at once; the
-      // probabilities of one token for all heads are one 16-byte LDS read ----
+      // ---- P.V: thread = (dimension pair, token group), every head at once;
+      // fixed trip count so all LDS reads of the group issue back to back ----
       if (pv_active) {
 #pragma unroll
-        for (int h = 0; h < kAttnMaxGroup; ++h)
-          if (h < R) pacc[h] *= alpha_s[h];
+        for (int h = 0; h < kAttnMaxGroup; ++h) {
+          if (h < R) {
+            pacc[h].x *= alpha_s[h];
+            pacc[h].y *= alpha_s[h];
+          }
+        }
         const int tb = pv_group * kPvTokens;
-        const int n = min(kPvTokens, rows - tb);
-        for (int i = 0; i < n; ++i) {
-          const int t = tb + i;
-          const float v = v_s[t][pv_dim];
-          const float4 p0 = *reinterpret_cast<const float4*>(&p_s[t][0]);
-          pacc[0] = fmaf(p0.x, v, pacc[0]);
-          pacc[1] = fmaf(p0.y, v, pacc[1]);
-          pacc[2] = fmaf(p0.z, v, pacc[2]);
-          pacc[3] = fmaf(p0.w, v, pacc[3]);
-          if (R > 4) {
-            const float4 p1 = *reinterpret_cast<const float4*>(&p_s[t][4]);
-            pacc[4] = fmaf(p1.x, v, pacc[4]);
-            pacc[5] = fmaf(p1.y, v, pacc[5]);
-            pacc[6] = fmaf(p1.z, v, pacc[6]);
-            pacc[7] = fmaf(p1.w, v, pacc[7]);
+        if (R <= 4) {
+#pragma unroll
+          for (int i = 0; i < kPvTokens; ++i) {
+            const float2 v = *reinterpret_cast<const float2*>(&v_s[tb + i][2 * pv_pair]);
+            const float4 p0 = *reinterpret_cast<const float4*>(&p_s[tb + i][0]);
+            pv_fma(pacc[0], p0.x, v);
+            pv_fma(pacc[1], p0.y, v);
+            pv_fma(pacc[2], p0.z, v);
+            pv_fma(pacc[3], p0.w, v);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < kPvTokens; ++i) {
+            const float2 v = *reinterpret_cast<const float2*>(&v_s[tb + i][2 * pv_pair]);
+            const float4 p0 = *reinterpret_cast<const float4*>(&p_s[tb + i][0]);
+            const float4 p1 = *reinterpret_cast<const float4*>(&p_s[tb + i][4]);
+            pv_fma(pacc[0], p0.x, v);
+            pv_fma(pacc[1], p0.y, v);
+            pv_fma(pacc[2], p0.z, v);
+            pv_fma(pacc[3], p0.w, v);
+            pv_fma(pacc[4], p1.x, v);
+            pv_fma(pacc[5], p1.y, v);
+            pv_fma(pacc[6], p1.z, v);
+            pv_fma(pacc[7], p1.w, v);
           }
         }
       }
@@ -331,43 +368,47 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   if (pv_active) {
 #pragma unroll
     for (int h = 0; h < kAttnMaxGroup; ++h)
-      if (h < R) red[(pv_group * kAttnMaxGroup + h) * D + pv_dim] = pacc[h];
+      if (h < R) *reinterpret_cast<float2*>(&red[(pv_group * kAttnMaxGroup + h) * D + 2 * pv_pair]) = pacc[h];
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int h = wave + j * kAttnWaves;
     if (h < R && lane == 0) {
-      float* dst = a.part + attn_partial_offset(g, split, h, S, R, D);
+      float* dst = a.part + attn_ml_offset(g, split, h, S, R, D, a.hkv);
       dst[0] = m_run[j];
       dst[1] = l_run[j];
     }
   }
   __syncthreads();
+  // The R heads' o rows of this (group, split) are contiguous: coalesced.
+  float* obase = a.part + attn_o_offset(g, split, 0, S, R, D);
   for (int idx = threadIdx.x; idx < R * D; idx += kAttnThreads) {
     const int h = idx / D, dim = idx - (idx / D) * D;
     float o = 0.0f;
 #pragma unroll
     for (int gidx = 0; gidx < kPvGroups; ++gidx) o += red[(gidx * kAttnMaxGroup + h) * D + dim];
-    a.part[attn_partial_offset(g, split, h, S, R, D) + 2 + dim] = o;
+    obase[idx] = o;
   }
 }
 
 // Log-sum-exp combine of the split partials: one block of 128 threads per
-// query head, thread = dimension; fixed split order, so deterministic.
+// query head, thread = dimension; fixed split order, so deterministic.  The
+// O-projection prologue (kProAttnCombine) performs the same operations in the
+// same order, so both paths give identical bits.
 __global__ __launch_bounds__(128) void attention_combine_kernel(const float* part, int hq, int hkv, int d, int splits,
                                                                  float* out) {
   const int qh = blockIdx.x;
   const int R = hq / hkv;
   const int g = qh / R, h = qh % R;
   float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, part[attn_partial_offset(g, s, h, splits, R, d)]);
+  for (int s = 0; s < splits; ++s) M = fmaxf(M, part[attn_ml_offset(g, s, h, splits, R, d, hkv)]);
   float L = 0.0f, o = 0.0f;
   const int dim = threadIdx.x;
   for (int s = 0; s < splits; ++s) {
-    const float* pp = part + attn_partial_offset(g, s, h, splits, R, d);
-    const float w = expf(pp[0] - M);
-    L = fmaf(pp[1], w, L);
-    if (dim < d) o = fmaf(pp[2 + dim], w, o);
+    const float* ml = part + attn_ml_offset(g, s, h, splits, R, d, hkv);
+    const float w = expf(ml[0] - M);
+    L = fmaf(ml[1], w, L);
+    if (dim < d) o = fmaf(part[attn_o_offset(g, s, h, splits, R, d) + dim], w, o);
   }
   if (dim < d) out[qh * d + dim] = o * (1.0f / L);
 }

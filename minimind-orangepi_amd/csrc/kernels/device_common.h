@@ -21,19 +21,66 @@ __device__ __forceinline__ void half8_to_float8(const uint4& u, float* f) {
   }
 }
 
-// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64).
-template <int kWidth>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = kWidth / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWidth);
+// Cross-lane reductions without an LDS round trip.  Inside a 16-lane row the
+// partners come from DPP permutations (GFX9 encodings): quad_perm [1,0,3,2]
+// and [2,3,0,1] pair lanes within a quad, row_half_mirror (lane i <-> 7 - i of
+// each half-row) pairs the two quads of a half-row once each quad is uniform,
+// and row_mirror (i <-> 15 - i) pairs the two half-rows.  Rows are then
+// combined with v_readlane from lanes 0, 16, 32 and 48.  Each step combines
+// two disjoint, already uniform halves, so every lane of a group ends with the
+// same bits.  Every lane of the wave must be active (wave-uniform control
+// flow), as for any cross-lane operation.
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;
+constexpr int kQuadXor2 = 0x4E;
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+}  // namespace dpp
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  const int b = __float_as_int(v);
+  return __int_as_float(__builtin_amdgcn_update_dpp(b, b, kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+struct OpSum {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Reduction over aligned groups of kWidth lanes (a power of two <= 64); the
+// result is in every lane of the group.
+template <int kWidth, typename Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  static_assert(kWidth >= 1 && kWidth <= 64 && (kWidth & (kWidth - 1)) == 0, "width must be a power of two <= 64");
+  if constexpr (kWidth >= 2) v = op(v, dpp_move<dpp::kQuadXor1>(v));
+  if constexpr (kWidth >= 4) v = op(v, dpp_move<dpp::kQuadXor2>(v));
+  if constexpr (kWidth >= 8) v = op(v, dpp_move<dpp::kRowHalfMirror>(v));
+  if constexpr (kWidth >= 16) v = op(v, dpp_move<dpp::kRowMirror>(v));
+  if constexpr (kWidth == 32) {
+    const float lo = op(read_lane(v, 0), read_lane(v, 16));
+    const float hi = op(read_lane(v, 32), read_lane(v, 48));
+    v = (__lane_id() < 32) ? lo : hi;
+  } else if constexpr (kWidth == 64) {
+    v = op(op(read_lane(v, 0), read_lane(v, 16)), op(read_lane(v, 32), read_lane(v, 48)));
+  }
   return v;
 }
 
 template <int kWidth>
+__device__ __forceinline__ float group_sum(float v) {
+  return group_reduce<kWidth>(v, OpSum{});
+}
+
+template <int kWidth>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int off = kWidth / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWidth));
-  return v;
+  return group_reduce<kWidth>(v, OpMax{});
 }
 
 // (value, index) pair ordering used by every argmax in the runtime: larger

@@ -100,52 +100,59 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
       }
     }
   } else if constexpr (PRO == kProAttnCombine) {
-    // Log-sum-exp merge of the attention split partials, done by the whole
-    // block into LDS (k = hq * head_dim <= 1024, splits <= 16):
-    //   w[h][s] = exp(m[h][s] - M_h) / sum_s l[h][s] exp(m[h][s] - M_h),
-    //   x[h*d + i] = sum_s o[h][s][i] * w[h][s]   (fixed split order).
-    __shared__ __align__(16) float s_x[1024];
-    __shared__ float s_m[kGemvBlock];  // normalised split weights w[head][split]
-    // All partial loads are unconditional (clamped indices) so that they
-    // issue back to back; out-of-range values are never consumed.
+    // Log-sum-exp merge of the attention split partials into LDS, computed by
+    // every block (k = hq * head_dim <= 1024, splits <= 16, hq <= 16):
+    //   M_h = max_s m[h][s],  e[h][s] = exp(m[h][s] - M_h),
+    //   L_h = sum_s l[h][s] e[h][s],  x[h*d + i] = (sum_s o[h][s][i] e[h][s]) / L_h,
+    // both sums in split order: the same operations as
+    // attention_combine_kernel, so the two paths agree bit for bit.
+    __shared__ __align__(16) float s_x[kCombineMaxDim];
+    __shared__ __align__(16) float s_e[kCombineMaxHeads][kCombineMaxSplits];
+    __shared__ __align__(16) float s_l[kCombineMaxHeads][kCombineMaxSplits];
     const int S = a.splits, D = a.head_dim, R = a.hq / a.hkv;
-    float ov[4][kCombineMaxSplits];
+    // Thread t owns x[4t, 4t + 4); its 16 float4 partial loads are
+    // unconditional (split index clamped) so they issue back to back.
+    const int t4 = min(static_cast<int>(threadIdx.x), k / 4 - 1);
+    const int head = (4 * t4) / D, dim = 4 * t4 - head * D;
+    float4 ov[kCombineMaxSplits];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = min(static_cast<int>(threadIdx.x) + i * kGemvBlock, k - 1);
-      const int head = kk / D, dim = kk - head * D;
-#pragma unroll
-      for (int s = 0; s < kCombineMaxSplits; ++s)
-        ov[i][s] = a.part[attn_partial_offset(head / R, min(s, S - 1), head % R, S, R, D) + 2 + dim];
-    }
+    for (int s = 0; s < kCombineMaxSplits; ++s)
+      ov[s] = *reinterpret_cast<const float4*>(a.part + attn_o_offset(head / R, min(s, S - 1), head % R, S, R, D) + dim);
     {
-      // One lane per (head, split): S is a power of two <= 16 and hq * S <= 256
-      // (host-checked), so each head's splits are S adjacent lanes of one wave
-      // and M_h, L_h are butterfly reductions over those lanes.
-      const int t = min(static_cast<int>(threadIdx.x), a.hq * S - 1);
-      const int head = t / S, s = t - (t / S) * S;
-      const float* pp = a.part + attn_partial_offset(head / R, s, head % R, S, R, D);
-      const float m = pp[0];
-      const float l = pp[1];
-      float M = m;
-      for (int off = S / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, S));
-      const float e = expf(m - M);
-      float L = l * e;
-      for (int off = S / 2; off > 0; off >>= 1) L += __shfl_xor(L, off, S);
-      if (static_cast<int>(threadIdx.x) < a.hq * S) s_m[threadIdx.x] = e * (1.0f / L);
+      // Lane (head, split) = (threadIdx / 16, threadIdx % 16): one 16-lane row
+      // per head, so M_h is a row reduction.  Splits >= S get weight 0.
+      const int wh = min(static_cast<int>(threadIdx.x) / kCombineMaxSplits, a.hq - 1);
+      const int ws = static_cast<int>(threadIdx.x) % kCombineMaxSplits;
+      const float2 ml =
+          *reinterpret_cast<const float2*>(a.part + attn_ml_offset(wh / R, min(ws, S - 1), wh % R, S, R, D, a.hkv));
+      const bool live = ws < S;
+      const float m = live ? ml.x : -INFINITY;
+      const float M = group_max<kCombineMaxSplits>(m);
+      s_e[threadIdx.x / kCombineMaxSplits][ws] = live ? expf(m - M) : 0.0f;
+      s_l[threadIdx.x / kCombineMaxSplits][ws] = live ? ml.y : 0.0f;
     }
     __syncthreads();
+    if (static_cast<int>(threadIdx.x) < k / 4) {
+      float L = 0.0f;
+      float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = threadIdx.x + i * kGemvBlock;
-      if (kk < k) {
-        const int head = kk / D;
-        float x = 0.0f;
+      for (int s4 = 0; s4 < kCombineMaxSplits / 4; ++s4) {
+        const float4 e4 = *reinterpret_cast<const float4*>(&s_e[head][4 * s4]);
+        const float4 l4 = *reinterpret_cast<const float4*>(&s_l[head][4 * s4]);
+        const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
-        for (int s = 0; s < kCombineMaxSplits; ++s)
-          if (s < S) x = fmaf(ov[i][s], s_m[head * S + s], x);
-        s_x[kk] = x;
+        for (int j = 0; j < 4; ++j) {
+          const float4& o = ov[4 * s4 + j];
+          L = fmaf(lv[j], ev[j], L);
+          x.x = fmaf(o.x, ev[j], x.x);
+          x.y = fmaf(o.y, ev[j], x.y);
+          x.z = fmaf(o.z, ev[j], x.z);
+          x.w = fmaf(o.w, ev[j], x.w);
+        }
       }
+      const float inv = 1.0f / L;
+      *reinterpret_cast<float4*>(&s_x[4 * threadIdx.x]) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
     }
     __syncthreads();
 #pragma unroll

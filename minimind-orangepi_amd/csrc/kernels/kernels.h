@@ -25,7 +25,10 @@ enum GemvPrologue : int {
   kProAttnCombine = 4  // x := log-sum-exp combine of the attention split partials
                        //      (part, splits, hq, hkv, head_dim; k = hq * head_dim)
 };
-constexpr int kCombineMaxSplits = 16;  // kProAttnCombine supports splits <= 16, k <= 1024
+// kProAttnCombine limits: splits <= 16, hq <= 16, k = hq * head_dim <= 1024.
+constexpr int kCombineMaxSplits = 16;
+constexpr int kCombineMaxHeads = 16;
+constexpr int kCombineMaxDim = 1024;
 
 enum GemvEpilogue : int {
   kEpiStore = 0,     // y[r] = dot

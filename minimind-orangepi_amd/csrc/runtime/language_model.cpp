@@ -67,7 +67,7 @@ struct DeviceState {
   float* attn = nullptr;
   float* act = nullptr;
   float* logits = nullptr;
-  float* attn_part = nullptr;  // split partials [Hkv][splits][R][d + 2]
+  float* attn_part = nullptr;  // split partials: o [Hkv][splits][R][d], then (m, l) [Hkv][splits][R][2]
   float* lm_part_val = nullptr;  // per-block argmax partials of the head GEMV
   int* lm_part_idx = nullptr;
   int64_t cache_rows = 0;        // capacity rounded up to the attention tile
@@ -380,7 +380,8 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       a.y = s.h;
       a.residual = s.h;
       mmr::GemvPrologue pro = mmr::kProPlain;
-      if (!s.combine_kernel && splits <= mmr::kCombineMaxSplits && Hq * D <= 1024 && Hq * splits <= 256) {
+      if (!s.combine_kernel && splits <= mmr::kCombineMaxSplits && Hq <= mmr::kCombineMaxHeads &&
+          Hq * D <= mmr::kCombineMaxDim) {
         pro = mmr::kProAttnCombine;
         a.part = s.attn_part;
         a.splits = splits;
