@@ -2,6 +2,7 @@
 """Decode throughput of the MiniMind2 gfx950 runtime.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f32|f16] [--no-cpu-baseline]
+                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--traffic-probe N]
 
 Workload: MiniMind2 dense (hidden 768, 16 layers, 8/2 heads, d 96, FFN 2048,
 vocab 6400), fp16 weights drawn N(0, 0.02) from seed 0, a 512-token uniform
@@ -15,14 +16,24 @@ The same line carries
     `--kernel-reps` times over the 16 layers' weights, timed with HIP events on
     the stream it runs on; achieved = algorithmic bytes / average duration;
   * kernels: the same measurement for every kernel of the step;
+  * copy_probe: a device-to-device copy of --copy-probe-mib MiB (HIP's blit
+    kernel), the achievable-bandwidth yardstick and the calibration dispatch
+    of the FETCH_SIZE / WRITE_SIZE counter runs;
+  * roofline.traffic: L2-to-memory bytes per launch of the dominant kernel from
+    the committed counter summary (profiles/gemv_gate_up_minimind2_traffic.md),
+    null when that file is absent;
   * cpu_baseline: the reference's own CPU path (oracle/_ref/ref_driver, built
     from the unmodified reference sources) on a bounded sample on this host.
+
+--no-graph launches the step kernels one by one instead of replaying the
+hipGraph (same kernels); rocprofv3's kernel tracing needs it.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import subprocess
 import sys
 import tempfile
@@ -69,6 +80,87 @@ def kernel_bytes(c: dict, kernel: str, n_keys: int, kv_bytes: int) -> int:
     raise KeyError(kernel)
 
 
+GEMV_SHAPES = [("qkv", 1152, 768), ("o", 768, 768), ("gate_up", 4096, 768), ("down", 768, 2048),
+               ("lm_head_argmax", 6400, 768)]
+
+
+def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
+    """BASELINE configs[1] shapes through the C ABI (mmr_matvec_f16 and
+    mmr_matvec_argmax_f16), each timed over rotated weight copies: `mall` keeps
+    the rotation at <= 160 MiB (resident in the 256 MB Infinity Cache), `hbm`
+    at >= 640 MiB (every launch streams from HBM).  GB/s = algorithmic bytes
+    (W fp16 + x fp32 + y fp32, or the int32 token for argmax) / mean launch time."""
+    lib = mmr.lib()
+    out = {}
+    rng = np.random.default_rng(7)
+    for name, n, k in GEMV_SHAPES:
+        x = mmr.DeviceArray.from_numpy(rng.standard_normal(k).astype(np.float32))
+        y = mmr.DeviceArray(n, np.float32)
+        tok = mmr.DeviceArray(1, np.int32)
+        ws_bytes = mmr.matvec_argmax_workspace_size(n, k)
+        ws = mmr.DeviceArray(max(ws_bytes, 1), np.uint8)
+        wbytes = n * k * 2
+        argmax = name.endswith("argmax")
+        alg = wbytes + k * 4 + (4 if argmax else n * 4)
+        res = {"rows": n, "cols": k, "bytes": alg}
+        for label, budget in (("mall", 160 << 20), ("hbm", 640 << 20)):
+            copies = max(2, budget // wbytes) if label == "mall" else max(2, -(-budget // wbytes))
+            big = mmr.DeviceArray(copies * wbytes, np.uint8, zero=True)
+
+            def launch(i):
+                w = big.ptr + (i % copies) * wbytes
+                if argmax:
+                    mmr.check(lib.mmr_matvec_argmax_f16(w, n, k, x.ptr, None, 0.0, None, tok.ptr, ws.ptr, ws_bytes,
+                                                        stream.handle))
+                else:
+                    mmr.check(lib.mmr_matvec_f16(w, n, k, x.ptr, None, y.ptr, stream.handle))
+
+            for i in range(copies):
+                launch(i)
+            ev[0].record(stream)
+            for i in range(reps):
+                launch(i)
+            ev[1].record(stream)
+            stream.synchronize()
+            us = ev[0].elapsed_ms(ev[1]) * 1e3 / reps
+            res[label] = {"avg_us": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+                          "rotation_mib": round(copies * wbytes / 2**20, 1)}
+            big.free()
+        log(f"gemv {name:15s} {n}x{k}: MALL {res['mall']['avg_us']:.3f} us {res['mall']['gbs']:.0f} GB/s | "
+            f"HBM {res['hbm']['avg_us']:.3f} us {res['hbm']['gbs']:.0f} GB/s")
+        out[name] = res
+    return out
+
+
+def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
+    """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: the dominant
+    kernel alone -- gate_up GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU
+    epilogue, the decode step's automatic launch plan) through the C ABI over a
+    16-copy weight rotation like the 16 layers of the step -- then one
+    device-to-device copy of `copy_mib` MiB, the calibration dispatch whose
+    bytes are known."""
+    H, F, layers = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"], MINIMIND2["num_hidden_layers"]
+    rng = np.random.default_rng(3)
+    wbytes = 2 * F * H * 2
+    w = mmr.DeviceArray(layers * wbytes, np.uint8, zero=True)
+    x = mmr.DeviceArray.from_numpy(rng.standard_normal(H).astype(np.float32))
+    g = mmr.DeviceArray.from_numpy(np.ones(H, np.float32))
+    y = mmr.DeviceArray(F, np.float32)
+    stream = mmr.Stream()
+    lib = mmr.lib()
+    for i in range(launches):
+        mmr.check(lib.mmr_matvec_f16_ex(w.ptr + (i % layers) * wbytes, 2 * F, H, x.ptr, g.ptr, 1e-5, mmr.PRO_RMSNORM,
+                                        mmr.EPI_SWIGLU, None, y.ptr, 0, 0, stream.handle))
+    stream.synchronize()
+    n = copy_mib << 20
+    src, dst = mmr.DeviceArray(n, np.uint8, zero=True), mmr.DeviceArray(n, np.uint8)
+    dst.copy_from(src, stream)
+    stream.synchronize()
+    print(json.dumps({"traffic_probe": {"gate_up_launches": launches, "gate_up_alg_bytes": kernel_bytes(
+        MINIMIND2, "gate_up", 0, 0), "copy_bytes": n}}), flush=True)
+    return 0
+
+
 def cpu_baseline(mmr, cfg, prompt, sample_steps: int) -> dict | None:
     """The reference CPU path (single-threaded, as shipped) on a bounded sample."""
     ref = ROOT / "oracle" / "_ref" / "ref_driver"
@@ -109,6 +201,11 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=320)
     ap.add_argument("--cpu-sample-steps", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=256)
+    ap.add_argument("--no-gemv-sweep", action="store_true")
+    ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
+                    help="run only the counter-run workload (gate_up launches + one copy) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -121,7 +218,12 @@ def main() -> int:
         print("--steps out of range", file=sys.stderr)
         return 2
 
+    if args.no_graph:
+        os.environ["MMR_NO_GRAPH"] = "1"  # read when the decode state is created
     import mmr  # noqa: E402  (fails loudly if libmmr.so is not built)
+
+    if args.traffic_probe > 0:
+        return traffic_probe(mmr, args.traffic_probe, max(args.copy_probe_mib, 1))
 
     if mmr.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
@@ -194,6 +296,32 @@ def main() -> int:
     dom = "gate_up"
     ach = kernels[dom]["gbs"]
 
+    copy_probe = None
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 20
+        src, dst = mmr.DeviceArray(n, np.uint8, zero=True), mmr.DeviceArray(n, np.uint8)
+        dst.copy_from(src, stream)  # warm
+        reps = 4
+        ev[0].record(stream)
+        for _ in range(reps):
+            dst.copy_from(src, stream)
+        ev[1].record(stream)
+        state.synchronize()
+        ms = ev[0].elapsed_ms(ev[1]) / reps
+        copy_probe = {"bytes_per_copy": n, "ms": round(ms, 4), "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1),
+                      "note": "read + write bytes / time of one device-to-device copy"}
+        log(f"copy probe: {args.copy_probe_mib} MiB d2d in {ms:.3f} ms -> {copy_probe['gbs']} GB/s (read+write)")
+        src.free()
+        dst.free()
+
+    sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
+
+    traffic = None
+    tfile = ROOT / "profiles" / "gemv_gate_up_minimind2_traffic.md"
+    if tfile.exists():
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", tfile.read_text())
+        traffic = int(m.group(1)) if m else None
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(mmr, cfg, prompt, args.cpu_sample_steps)
@@ -221,9 +349,13 @@ def main() -> int:
         "step_gbs": round(step_bytes / (decode_ms / args.steps * 1e-3) / 1e9, 1),
         "sum_kernel_us_per_step": round(per_step_us, 2),
         "kernels": kernels,
+        "copy_probe": copy_probe,
+        "gemv_sweep": sweep,
+        "launch_mode": "eager (--no-graph)" if args.no_graph else "hipGraph replay",
         "roofline": {"bound": "hbm", "kernel": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",
                      "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": traffic, "traffic_source": "profiles/gemv_gate_up_minimind2_traffic.md"
+                     if traffic is not None else None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -66,6 +66,8 @@ int mmr_free(void* ptr);
 int mmr_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int mmr_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int mmr_memset(void* dst, int value, size_t bytes);
+/* Device-to-device copy enqueued on `stream` (HIP's blit kernel). */
+int mmr_memcpy_d2d_async(void* dst, const void* src, size_t bytes, mmr_stream_t stream);
 int mmr_stream_create(mmr_stream_t* stream);
 int mmr_stream_destroy(mmr_stream_t stream);
 int mmr_stream_synchronize(mmr_stream_t stream);
@@ -213,7 +215,8 @@ int mmr_read_logits(const mmr_model* model, mmr_state* state, float* logits);
 
 /* Enqueue `count` launches of one kernel of the decode step on the state's
  * stream, cycling over layers from `layer` (kernel: 0 qkv, 1 attention,
- * 2 o, 3 gate_up, 4 down, 5 lm_head without step bookkeeping).  For timing
+ * 2 o, 3 gate_up, 4 down, 5 lm_head, 6 argmax finalize without step
+ * bookkeeping).  For timing
  * with events recorded on the state's stream; overwrites scratch buffers. */
 int mmr_launch_step_kernel(const mmr_model* model, mmr_state* state, int kernel, int64_t layer, int64_t count);
 

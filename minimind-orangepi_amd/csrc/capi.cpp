@@ -168,6 +168,11 @@ int mmr_memcpy_h2d(void* dst, const void* src, size_t bytes) {
 int mmr_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   return guarded([&] { hip(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H"); });
 }
+int mmr_memcpy_d2d_async(void* dst, const void* src, size_t bytes, mmr_stream_t stream) {
+  return guarded([&] {
+    hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)), "hipMemcpyAsync D2D");
+  });
+}
 int mmr_memset(void* dst, int value, size_t bytes) {
   return guarded([&] { hip(hipMemset(dst, value, bytes), "hipMemset"); });
 }

@@ -28,7 +28,7 @@ OK, ERR_INVALID_ARGUMENT, ERR_OUT_OF_RANGE, ERR_RUNTIME, ERR_LENGTH = 0, 1, 2, 3
 KV_F16, KV_F32 = 0, 1
 PRO_PLAIN, PRO_RMSNORM, PRO_RMSNORM_FINAL = 0, 1, 2
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
-KERNEL_QKV, KERNEL_ATTENTION, KERNEL_O, KERNEL_GATE_UP, KERNEL_DOWN, KERNEL_LM_HEAD = range(6)
+KERNEL_QKV, KERNEL_ATTENTION, KERNEL_O, KERNEL_GATE_UP, KERNEL_DOWN, KERNEL_LM_HEAD, KERNEL_FINALIZE = range(7)
 
 
 class MmrError(RuntimeError):
@@ -87,6 +87,7 @@ _SIGS = {
     "mmr_memcpy_h2d": ([VP, VP, SZ], C.c_int),
     "mmr_memcpy_d2h": ([VP, VP, SZ], C.c_int),
     "mmr_memset": ([VP, C.c_int, SZ], C.c_int),
+    "mmr_memcpy_d2d_async": ([VP, VP, SZ, VP], C.c_int),
     "mmr_stream_create": ([C.POINTER(VP)], C.c_int),
     "mmr_stream_destroy": ([VP], C.c_int),
     "mmr_stream_synchronize": ([VP], C.c_int),
@@ -209,6 +210,11 @@ class DeviceArray:
     def zero(self) -> None:
         check(_lib.mmr_memset(self.ptr, 0, max(self.nbytes, 1)))
 
+    def copy_from(self, other: "DeviceArray", stream: "Stream | None" = None) -> None:
+        """Device-to-device copy of `other` (same byte size), enqueued on `stream`."""
+        assert other.nbytes == self.nbytes
+        check(_lib.mmr_memcpy_d2d_async(self.ptr, other.ptr, self.nbytes, _stream_handle(stream)))
+
     def free(self) -> None:
         if self.ptr:
             _lib.mmr_free(self.ptr)
@@ -248,7 +254,7 @@ class Event:
         self.handle = h.value
 
     def record(self, stream) -> None:
-        check(_lib.mmr_event_record(self.handle, stream.handle if isinstance(stream, Stream) else stream))
+        check(_lib.mmr_event_record(self.handle, _stream_handle(stream)))
 
     def elapsed_ms(self, end: "Event") -> float:
         ms = C.c_float(0.0)
@@ -264,6 +270,11 @@ class Event:
 
 def synchronize() -> None:
     check(_lib.mmr_device_synchronize())
+
+
+def _stream_handle(stream) -> int | None:
+    """A Stream, a raw hipStream_t handle (int) or None (the null stream)."""
+    return stream.handle if isinstance(stream, Stream) else stream
 
 
 def f32_to_f16(a: np.ndarray) -> np.ndarray:
