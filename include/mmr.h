@@ -163,6 +163,29 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
                                int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, void* workspace,
                                size_t workspace_bytes, int splits, int32_t* error, mmr_stream_t stream);
 
+/* ---- prefill (run_dense_prefill_layer_device, decoder_layer.cpp:661-734) ----
+ * Batched projection: device_matmul / device_matmul_add with batch = seq_len
+ * (ascend_matmul.h:102-107) and cube_matmul (ascend_matmul.h:122-126).
+ * y[b][r] = sum_c W[r*cols + c] * x[b][c] (+ residual[b][r]); W fp16
+ * row-major [rows][cols], x [batch][cols], y/residual [batch][rows] fp32;
+ * fp32 matrix cores with fp32 accumulation.  cols % 32 == 0; residual may
+ * alias y. */
+int mmr_matmul_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, int64_t batch,
+                   const float* residual, float* y, mmr_stream_t stream);
+/* Rows of the fused qkv projection for positions start_position ..
+ * start_position + seq_len - 1: device_qkv_split_rows + q/k
+ * device_rms_norm_rows + device_rope_rows (ascend_custom_ops.h:80-107) and
+ * the KV-cache write of device_prefill_attention (ascend_custom_ops.h:122-130).
+ * qkv [seq_len][(Hq + 2 Hkv) d]; query [seq_len][Hq d]. */
+int mmr_prefill_qkv_rows(const float* qkv, const float* q_norm, const float* k_norm, float eps,
+                         const mmr_rope_table* rope, mmr_kv_cache* cache, int64_t start_position, int64_t seq_len,
+                         int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* query, mmr_stream_t stream);
+/* Causal attention of device_prefill_attention (ascend_custom_ops.h:122-130):
+ * query rows at positions start_position + i attend cache keys 0 ..
+ * start_position + i.  out [seq_len][Hq d]. */
+int mmr_prefill_attention(const float* query, const mmr_kv_cache* cache, int64_t start_position, int64_t seq_len,
+                          int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, mmr_stream_t stream);
+
 /* ---- support ops (ascend_custom_ops.h:70-79,109-120) ----------------------- */
 int mmr_rms_norm_rows(const float* in, const float* w, float eps, int64_t rows, int64_t cols, float* out,
                       mmr_stream_t stream);

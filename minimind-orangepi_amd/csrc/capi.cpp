@@ -476,6 +476,87 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
   });
 }
 
+int mmr_matmul_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, int64_t batch,
+                   const float* residual, float* y, mmr_stream_t stream) {
+  return guarded([&] {
+    require(w && x && y, "null buffer");
+    require(rows > 0 && cols > 0 && batch > 0, "rows, cols and batch must be positive");
+    require(rows <= (1 << 24) && cols <= (1 << 24) && batch <= (1 << 24), "matrix too large");
+    require(cols % 32 == 0, "cols must be a multiple of 32");
+    mmr::GemmArgs g;
+    g.a = x;
+    g.lda = static_cast<int>(cols);
+    g.w = reinterpret_cast<const __half*>(w);
+    g.residual = residual;
+    g.c = y;
+    g.ldc = static_cast<int>(rows);
+    g.m = static_cast<int>(batch);
+    g.n = static_cast<int>(rows);
+    g.k = static_cast<int>(cols);
+    hip(mmr::launch_gemm(g, as_stream(stream)), "gemm launch");
+  });
+}
+
+int mmr_prefill_qkv_rows(const float* qkv, const float* q_norm, const float* k_norm, float eps,
+                         const mmr_rope_table* rope, mmr_kv_cache* cache, int64_t start_position, int64_t seq_len,
+                         int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* query, mmr_stream_t stream) {
+  return guarded([&] {
+    require(qkv && q_norm && k_norm && rope && cache && query, "null argument");
+    check_attention_shape(q_heads, kv_heads, head_dim);
+    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(rope->head_dim == head_dim, "rope table head_dim mismatch");
+    require(seq_len >= 1 && start_position >= 0, "seq_len must be positive and start_position non-negative");
+    require(start_position + seq_len <= cache->capacity, "prompt exceeds the cache capacity");
+    require(start_position + seq_len <= rope->max_positions, "positions outside the rope table");
+    mmr::QkvRowsArgs a;
+    a.qkv = qkv;
+    a.qkv_stride = static_cast<int>((q_heads + 2 * kv_heads) * head_dim);
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.eps = eps;
+    a.inv_freq = rope->data();
+    a.start = static_cast<int>(start_position);
+    a.tokens = static_cast<int>(seq_len);
+    a.kcache = cache->keys.data();
+    a.vcache = cache->values.data();
+    a.rows = static_cast<int>(cache->rows);
+    a.hq = static_cast<int>(q_heads);
+    a.hkv = static_cast<int>(kv_heads);
+    a.d = static_cast<int>(head_dim);
+    a.query = query;
+    a.query_stride = static_cast<int>(q_heads * head_dim);
+    hip(mmr::launch_qkv_rows(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32, as_stream(stream)),
+        "qkv rows launch");
+  });
+}
+
+int mmr_prefill_attention(const float* query, const mmr_kv_cache* cache, int64_t start_position, int64_t seq_len,
+                          int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, mmr_stream_t stream) {
+  return guarded([&] {
+    require(query && cache && out, "null argument");
+    check_attention_shape(q_heads, kv_heads, head_dim);
+    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(seq_len >= 1 && start_position >= 0, "seq_len must be positive and start_position non-negative");
+    require(start_position + seq_len <= cache->capacity, "prompt exceeds the cache capacity");
+    mmr::PrefillAttnArgs a;
+    a.query = query;
+    a.query_stride = static_cast<int>(q_heads * head_dim);
+    a.kcache = cache->keys.data();
+    a.vcache = cache->values.data();
+    a.rows = static_cast<int>(cache->rows);
+    a.start = static_cast<int>(start_position);
+    a.tokens = static_cast<int>(seq_len);
+    a.hq = static_cast<int>(q_heads);
+    a.hkv = static_cast<int>(kv_heads);
+    a.d = static_cast<int>(head_dim);
+    a.out = out;
+    a.out_stride = static_cast<int>(q_heads * head_dim);
+    hip(mmr::launch_prefill_attention(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
+                                      as_stream(stream)),
+        "prefill attention launch");
+  });
+}
+
 int mmr_rms_norm_rows(const float* in, const float* w, float eps, int64_t rows, int64_t cols, float* out,
                       mmr_stream_t stream) {
   return guarded([&] {

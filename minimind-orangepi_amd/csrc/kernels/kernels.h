@@ -152,6 +152,62 @@ struct QkvPostArgs {
 };
 hipError_t launch_qkv_postprocess(const QkvPostArgs& a, KvDtype kv, hipStream_t stream);
 
+// ------------------------------------------------------------- prefill ----
+// C[m][n] = (residual[m][n] +) sum_k A[m][k] * W[n][k]: A fp32 (row stride
+// lda), W fp16 row-major [n][k], C fp32 (row stride ldc); residual may alias
+// C.  fp32 matrix cores, fp32 accumulation.  k % 32 == 0, lda % 4 == 0.
+struct GemmArgs {
+  const float* a = nullptr;
+  int lda = 0;
+  const __half* w = nullptr;
+  const float* residual = nullptr;
+  float* c = nullptr;
+  int ldc = 0;
+  int m = 0, n = 0, k = 0;
+};
+bool gemm_supported(int m, int n, int k);
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+
+// Rows of the fused qkv projection for tokens at positions start ..
+// start + tokens - 1: per-head q/k RMSNorm + RoPE, q -> query rows, k/v
+// written to the cache at their positions.
+struct QkvRowsArgs {
+  const float* qkv = nullptr;  // [tokens][qkv_stride]
+  int qkv_stride = 0;
+  const float* q_norm = nullptr;
+  const float* k_norm = nullptr;
+  float eps = 0.0f;
+  const float* inv_freq = nullptr;  // [D/2]
+  int start = 0;
+  int tokens = 0;
+  void* kcache = nullptr;
+  void* vcache = nullptr;
+  int rows = 0;  // cache rows per KV head
+  int hq = 0, hkv = 0, d = 0;
+  float* query = nullptr;  // [tokens][query_stride]
+  int query_stride = 0;
+};
+hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream);
+
+// out[i] = silu(gate_up[2i]) * gate_up[2i + 1] for i < n (interleaved rows).
+hipError_t launch_swiglu_pairs(const float* gate_up, int64_t n, float* out, hipStream_t stream);
+
+// Causal attention of query rows at positions start .. start + tokens - 1
+// over cache keys 0 .. each query's position.
+struct PrefillAttnArgs {
+  const float* query = nullptr;  // [tokens][query_stride], normalised + rotated
+  int query_stride = 0;
+  const void* kcache = nullptr;
+  const void* vcache = nullptr;
+  int rows = 0;
+  int start = 0;
+  int tokens = 0;
+  int hq = 0, hkv = 0, d = 0;
+  float* out = nullptr;  // [tokens][out_stride]
+  int out_stride = 0;
+};
+hipError_t launch_prefill_attention(const PrefillAttnArgs& a, KvDtype kv, hipStream_t stream);
+
 // ------------------------------------------------------------- support ----
 hipError_t launch_rms_norm_rows(const float* in, const float* w, float eps, int rows, int cols, float* out,
                                 hipStream_t stream);

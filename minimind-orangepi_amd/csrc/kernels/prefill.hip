@@ -1,0 +1,397 @@
+// prefill.hip -- prompt (prefill) kernels for gfx950: fp16-weight GEMM on the
+// fp32 matrix cores, per-row q/k norm + RoPE + KV-cache write, interleaved
+// SwiGLU rows, and causal attention over the cache.
+//
+// Replaces the reference's device prefill layer (run_dense_prefill_layer_device,
+// decoder_layer.cpp:661-734): device_matmul / device_matmul_add with batch =
+// seq_len (ascend_matmul.h:102-107, aclnnMm at ascend_matmul.cpp:553-556),
+// device_qkv_split_rows + q/k device_rms_norm_rows + device_rope_rows
+// (ascend_custom_ops.h:80-107), device_prefill_attention (ascend_custom_ops.h:
+// 122-130, kernel K8) and device_swiglu_rows.  The CPU semantics being matched
+// are those of token-by-token decode (decoder_layer.cpp:312-407), which is what
+// the reference runs on the CPU for a prompt (language_model.cpp:384-386).
+//
+// GEMM: C[m][n] (+)= sum_k A[m][k] * W[n][k], A fp32 row-major, W fp16
+// row-major (the decode GEMVs' weights), fp32 accumulation.  The contraction
+// runs on v_mfma_f32_16x16x4f32 with A in fp32 and W widened to fp32 in LDS,
+// so no operand is rounded below the CPU path's fp32.  A 256-thread block
+// computes a BM x BN tile with 2 x 2 waves; K advances 32 at a time through
+// LDS rows padded to 36 floats, which makes the 16-byte fragment reads of a
+// wave hit 64 distinct banks.  Within a 16-wide K slice, MFMA instruction s
+// takes k = 4 * (lane / 16) + s from each lane, so every lane fetches its four
+// k values with one 16-byte LDS read.
+#include "device_common.h"
+#include "kernels.h"
+
+namespace mmr {
+namespace {
+
+using f32x4 = float __attribute__((ext_vector_type(4)));
+
+constexpr int kGemmThreads = 256;
+constexpr int kGemmBK = 32;
+constexpr int kGemmLDK = kGemmBK + 4;
+
+template <int BM, int BN, bool kResidual>
+__global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
+  constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
+  constexpr int kAIters = BM * (kGemmBK / 4) / kGemmThreads;
+  constexpr int kBIters = BN * (kGemmBK / 8) / kGemmThreads;
+  static_assert(kAIters >= 1 && kBIters >= 1, "tile too small for the block");
+  __shared__ __align__(16) float As[BM][kGemmLDK];
+  __shared__ __align__(16) float Bs[BN][kGemmLDK];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+  static_assert(kAIters <= 2 && kBIters == 1, "register staging holds two A chunks and one B chunk");
+  // Staging registers, named (not an array) so they never leave registers.
+  float4 ra0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), ra1 = ra0;
+  uint4 rb0 = make_uint4(0u, 0u, 0u, 0u);
+  // Row indices are clamped into range: every load is in bounds, and rows
+  // past m / n are never stored.
+  const int a_r0 = tid / (kGemmBK / 4), a_q = tid % (kGemmBK / 4);
+  const int a_r1 = a_r0 + kGemmThreads / (kGemmBK / 4);
+  const int b_r = tid / (kGemmBK / 8), b_q = tid % (kGemmBK / 8);
+  const float* a_src0 = g.a + static_cast<int64_t>(min(m0 + a_r0, g.m - 1)) * g.lda + a_q * 4;
+  const float* a_src1 = g.a + static_cast<int64_t>(min(m0 + a_r1, g.m - 1)) * g.lda + a_q * 4;
+  const __half* b_src = g.w + static_cast<int64_t>(min(n0 + b_r, g.n - 1)) * g.k + b_q * 8;
+#define MMR_GEMM_LOAD(k0)                                                      \
+  do {                                                                          \
+    ra0 = *reinterpret_cast<const float4*>(a_src0 + (k0));                      \
+    if constexpr (kAIters > 1) ra1 = *reinterpret_cast<const float4*>(a_src1 + (k0)); \
+    rb0 = *reinterpret_cast<const uint4*>(b_src + (k0));                        \
+  } while (0)
+#define MMR_GEMM_STORE()                                                       \
+  do {                                                                          \
+    *reinterpret_cast<float4*>(&As[a_r0][a_q * 4]) = ra0;                       \
+    if constexpr (kAIters > 1) *reinterpret_cast<float4*>(&As[a_r1][a_q * 4]) = ra1; \
+    float f[8];                                                                 \
+    half8_to_float8(rb0, f);                                                    \
+    *reinterpret_cast<float4*>(&Bs[b_r][b_q * 8]) = make_float4(f[0], f[1], f[2], f[3]);     \
+    *reinterpret_cast<float4*>(&Bs[b_r][b_q * 8 + 4]) = make_float4(f[4], f[5], f[6], f[7]); \
+  } while (0)
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int nk = g.k / kGemmBK;
+  MMR_GEMM_LOAD(0);
+  MMR_GEMM_STORE();
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    // The next tile's loads are in flight during this tile's MFMAs; on the
+    // last tile they reload it (unconditional, so the values stay in registers).
+    MMR_GEMM_LOAD(min(kt + 1, nk - 1) * kGemmBK);
+#pragma unroll
+    for (int kb = 0; kb < kGemmBK; kb += 16) {
+      const int kk = kb + 4 * (lane / 16);
+      float4 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const float4*>(&As[wm * (BM / 2) + i * 16 + lane % 16][kk]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const float4*>(&Bs[wn * (BN / 2) + j * 16 + lane % 16][kk]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    MMR_GEMM_STORE();
+    __syncthreads();
+  }
+#undef MMR_GEMM_LOAD
+#undef MMR_GEMM_STORE
+
+  // Output fragment: lane holds rows 4 * (lane / 16) + {0..3} of column
+  // lane % 16 of each 16 x 16 tile.  Residual loads are issued together
+  // (clamped indices), then the in-range elements are stored.
+  float res[TM][TN][4];
+  if constexpr (kResidual) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = min(n0 + wn * (BN / 2) + j * 16 + lane % 16, g.n - 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = min(m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r, g.m - 1);
+          res[i][j][r] = g.residual[static_cast<int64_t>(row) * g.ldc + col];
+        }
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
+        if (row < g.m && col < g.n) {
+          const float v = acc[i][j][r];
+          g.c[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
+        }
+      }
+    }
+}
+
+// Per (token, head) q/k RMSNorm + RoPE of one row of the fused qkv output,
+// q to `query`, k/v rounded to the cache dtype and written at cache index
+// start + token (decoder_layer.cpp:342-359 per token).  One wave per head;
+// grid (hq + hkv, tokens).
+template <typename KV, int D>
+__global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
+  __shared__ float x_s[D];
+  const int b = blockIdx.x;
+  const int t = blockIdx.y;
+  const int lane = threadIdx.x;
+  const bool is_q = b < a.hq;
+  const int head = is_q ? b : b - a.hq;
+  const float* row = a.qkv + static_cast<int64_t>(t) * a.qkv_stride;
+  const float* src = row + (is_q ? head * D : a.hq * D + head * D);
+  const float* w = is_q ? a.q_norm : a.k_norm;
+  const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
+  float x0 = src[d0], x1 = src[d1];
+  const float w0 = w[d0], w1 = w[d1];
+  const float f = a.inv_freq[min(lane, D / 2 - 1)];
+  x0 = lane < D ? x0 : 0.0f;
+  x1 = lane + kWave < D ? x1 : 0.0f;
+  const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps);
+  if (lane < D) x_s[lane] = x0 * (scale * w0);
+  if (lane + kWave < D) x_s[lane + kWave] = x1 * (scale * w1);
+  const int pos = a.start + t;
+  float rc = 1.0f, rs = 0.0f;
+  if (lane < D / 2) sincosf(static_cast<float>(pos) * f, &rs, &rc);
+  __syncthreads();
+  if (lane < D / 2) {
+    const float first = x_s[lane];
+    const float second = x_s[lane + D / 2];
+    x_s[lane] = first * rc - second * rs;
+    x_s[lane + D / 2] = second * rc + first * rs;
+  }
+  __syncthreads();
+  if (is_q) {
+    float* dst = a.query + static_cast<int64_t>(t) * a.query_stride + head * D;
+    for (int i = lane; i < D; i += kWave) dst[i] = x_s[i];
+  } else {
+    const float* vsrc = row + a.hq * D + a.hkv * D + head * D;
+    KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
+    KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
+    for (int i = lane; i < D; i += kWave) {
+      kdst[i] = from_float<KV>(x_s[i]);
+      vdst[i] = from_float<KV>(vsrc[i]);
+    }
+  }
+}
+
+// out[t][i] = silu(gu[t][2i]) * gu[t][2i + 1] (decoder_layer.cpp:175-182 on
+// the interleaved gate/up rows of the runtime's fused weight).
+__global__ void swiglu_pairs_kernel(const float* gu, int64_t n, float* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float2 p = reinterpret_cast<const float2*>(gu)[i];
+  out[i] = (p.x / (1.0f + expf(-p.x))) * p.y;
+}
+
+// Causal attention of `tokens` queries at positions start .. start + tokens - 1
+// over the cache (keys 0 .. position of each query, decoder_layer.cpp:184-234
+// per token).  One wave per (16 queries, query head): lane = (query q = lane /
+// 4, key slot ks = lane % 4); each lane keeps its query and an online-softmax
+// (m, l, o[d]) over keys ks, ks + 4, ... of each 64-key tile staged in LDS, and
+// the four slots of a query merge with quad DPP reductions at the end.
+constexpr int kPrefillQueries = 16;
+constexpr int kPrefillKeys = 64;
+
+template <typename KV, int D>
+__global__ __launch_bounds__(kWave) void prefill_attention_kernel(PrefillAttnArgs a) {
+  constexpr int LD = D + 4;
+  constexpr int CH = 16 / static_cast<int>(sizeof(KV));
+  constexpr int kChunks = kPrefillKeys * D / CH;
+  constexpr int kSlotKeys = kPrefillKeys / 4;
+  __shared__ __align__(16) float k_s[kPrefillKeys][LD];
+  __shared__ __align__(16) float v_s[kPrefillKeys][LD];
+  const int lane = threadIdx.x;
+  const int qi = lane / 4, ks = lane % 4;
+  const int h = blockIdx.y;
+  const int R = a.hq / a.hkv;
+  const int g = h / R;
+  const int q0 = blockIdx.x * kPrefillQueries;
+  const int qrow = min(q0 + qi, a.tokens - 1);
+  const int qpos = a.start + qrow;
+  const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.rows * D;
+  const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
+
+  float q[D];
+  const float* qsrc = a.query + static_cast<int64_t>(qrow) * a.query_stride + h * D;
+#pragma unroll
+  for (int i = 0; i < D / 4; ++i) {
+    const float4 v = reinterpret_cast<const float4*>(qsrc)[i];
+    q[4 * i] = v.x;
+    q[4 * i + 1] = v.y;
+    q[4 * i + 2] = v.z;
+    q[4 * i + 3] = v.w;
+  }
+  float o[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) o[i] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  const float sqrt_d = sqrtf(static_cast<float>(D));
+
+  const int last_key = a.start + min(q0 + kPrefillQueries, a.tokens) - 1;  // the block's last query position
+  const int n_tiles = last_key / kPrefillKeys + 1;
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int t0 = tile * kPrefillKeys;
+    __syncthreads();  // previous tile fully consumed
+    for (int c = lane; c < kChunks; c += kWave) {
+      const int r = (c * CH) / D, col = (c * CH) % D;
+      const int key = min(t0 + r, last_key);  // rows past the last key are never scored
+      const int64_t off = static_cast<int64_t>(key) * D + col;
+      const uint4 kc = *reinterpret_cast<const uint4*>(kbase + off);
+      const uint4 vc = *reinterpret_cast<const uint4*>(vbase + off);
+      if constexpr (sizeof(KV) == 2) {
+        half8_to_float8(kc, &k_s[r][col]);
+        half8_to_float8(vc, &v_s[r][col]);
+      } else {
+        *reinterpret_cast<uint4*>(&k_s[r][col]) = kc;
+        *reinterpret_cast<uint4*>(&v_s[r][col]) = vc;
+      }
+    }
+    __syncthreads();
+    float s[kSlotKeys];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kSlotKeys; ++i) {
+      const int j = ks + 4 * i;
+      float dot = 0.0f;
+#pragma unroll
+      for (int dd = 0; dd < D; dd += 4) {
+        const float4 kv = *reinterpret_cast<const float4*>(&k_s[j][dd]);
+        dot = fmaf(q[dd], kv.x, dot);
+        dot = fmaf(q[dd + 1], kv.y, dot);
+        dot = fmaf(q[dd + 2], kv.z, dot);
+        dot = fmaf(q[dd + 3], kv.w, dot);
+      }
+      s[i] = (t0 + j <= qpos) ? dot / sqrt_d : -INFINITY;  // decoder_layer.cpp:213
+      mt = fmaxf(mt, s[i]);
+    }
+    const float m_new = fmaxf(m, mt);
+    if (m_new != -INFINITY) {  // lane-uniform per query slot; no key yet means nothing to add
+      const float alpha = expf(m - m_new);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < D; ++i) o[i] *= alpha;
+#pragma unroll
+      for (int i = 0; i < kSlotKeys; ++i) {
+        const float p = expf(s[i] - m_new);  // exp(-inf) = 0 for masked keys
+        l += p;
+        const int j = ks + 4 * i;
+#pragma unroll
+        for (int dd = 0; dd < D; dd += 4) {
+          const float4 vv = *reinterpret_cast<const float4*>(&v_s[j][dd]);
+          o[dd] = fmaf(p, vv.x, o[dd]);
+          o[dd + 1] = fmaf(p, vv.y, o[dd + 1]);
+          o[dd + 2] = fmaf(p, vv.z, o[dd + 2]);
+          o[dd + 3] = fmaf(p, vv.w, o[dd + 3]);
+        }
+      }
+      m = m_new;
+    }
+  }
+
+  // Merge the four key slots of each query (lanes 4q .. 4q + 3).
+  const float M = group_max<4>(m);
+  const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+  const float L = group_sum<4>(l * w);
+  const float inv = 1.0f / L;
+  float* dst = a.out + static_cast<int64_t>(qrow) * a.out_stride + h * D;
+  const bool live = q0 + qi < a.tokens;
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const float oi = group_sum<4>(o[i] * w);
+    if (live && (i % 4) == ks) dst[i] = oi * inv;
+  }
+}
+
+template <int BM, int BN>
+hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
+  const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+  if (g.residual) {
+    gemm_f16w_kernel<BM, BN, true><<<grid, kGemmThreads, 0, s>>>(g);
+  } else {
+    gemm_f16w_kernel<BM, BN, false><<<grid, kGemmThreads, 0, s>>>(g);
+  }
+  return hipGetLastError();
+}
+
+template <typename KV>
+hipError_t launch_qkv_rows_kv(const QkvRowsArgs& a, hipStream_t s) {
+  const dim3 grid(a.hq + a.hkv, a.tokens);
+  switch (a.d) {
+    case 16: qkv_rows_kernel<KV, 16><<<grid, kWave, 0, s>>>(a); break;
+    case 32: qkv_rows_kernel<KV, 32><<<grid, kWave, 0, s>>>(a); break;
+    case 64: qkv_rows_kernel<KV, 64><<<grid, kWave, 0, s>>>(a); break;
+    case 96: qkv_rows_kernel<KV, 96><<<grid, kWave, 0, s>>>(a); break;
+    case 128: qkv_rows_kernel<KV, 128><<<grid, kWave, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename KV>
+hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) {
+  const dim3 grid((a.tokens + kPrefillQueries - 1) / kPrefillQueries, a.hq);
+  switch (a.d) {
+    case 16: prefill_attention_kernel<KV, 16><<<grid, kWave, 0, s>>>(a); break;
+    case 32: prefill_attention_kernel<KV, 32><<<grid, kWave, 0, s>>>(a); break;
+    case 64: prefill_attention_kernel<KV, 64><<<grid, kWave, 0, s>>>(a); break;
+    case 96: prefill_attention_kernel<KV, 96><<<grid, kWave, 0, s>>>(a); break;
+    case 128: prefill_attention_kernel<KV, 128><<<grid, kWave, 0, s>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_supported(int m, int n, int k) { return m > 0 && n > 0 && k > 0 && k % kGemmBK == 0; }
+
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
+  if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < g.n) return hipErrorInvalidValue;
+  // 64 x 64 tiles, or 32-row tiles when that is what fills the chip.
+  const int64_t tiles64 = static_cast<int64_t>((g.m + 63) / 64) * ((g.n + 63) / 64);
+  if (tiles64 >= 256 || g.m <= 32) return g.m <= 32 ? launch_gemm_tile<32, 64>(g, s) : launch_gemm_tile<64, 64>(g, s);
+  return launch_gemm_tile<32, 64>(g, s);
+}
+
+hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream) {
+  if (!attention_supported(a.hq, a.hkv, a.d) || a.tokens <= 0) return hipErrorInvalidValue;
+  return kv == kKvF16 ? launch_qkv_rows_kv<__half>(a, stream) : launch_qkv_rows_kv<float>(a, stream);
+}
+
+hipError_t launch_swiglu_pairs(const float* gate_up, int64_t n, float* out, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  swiglu_pairs_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(gate_up, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillAttnArgs& a, KvDtype kv, hipStream_t stream) {
+  if (!attention_supported(a.hq, a.hkv, a.d) || a.tokens <= 0 || a.start < 0) return hipErrorInvalidValue;
+  return kv == kKvF16 ? launch_prefill_attention_kv<__half>(a, stream)
+                      : launch_prefill_attention_kv<float>(a, stream);
+}
+
+}  // namespace mmr

@@ -48,6 +48,7 @@ struct DeviceModel {
   std::vector<LayerDev> layers;
   const float* inv_freq = nullptr;  // [d/2] RoPE frequencies, formula of decoder_layer.cpp:114
   mmr::GemvPlan plan_qkv, plan_o, plan_gu, plan_down, plan_lm;
+  bool gemm_prefill = false;  // every projection's K suits the prefill GEMM
   std::size_t weight_bytes = 0;
 };
 
@@ -72,6 +73,16 @@ struct DeviceState {
   int* lm_part_idx = nullptr;
   int64_t cache_rows = 0;        // capacity rounded up to the attention tile
   int32_t* staging = nullptr;        // pinned host [capacity + 8]
+  // Prefill chunk buffers (rows = prompt tokens of one chunk, <= pf_chunk).
+  int64_t pf_chunk = 0;
+  float* pf_h = nullptr;    // [chunk][H] residual stream
+  float* pf_x = nullptr;    // [chunk][H] normalised rows
+  float* pf_qkv = nullptr;  // [chunk][(Hq + 2 Hkv) d]
+  float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
+  float* pf_attn = nullptr; // [chunk][Hq d]
+  float* pf_gu = nullptr;   // [chunk][2F] interleaved gate/up
+  float* pf_act = nullptr;  // [chunk][F]
+  bool prefill_tokenwise = false;  // prefill through the decode step instead of the GEMM path
   hipStream_t stream = nullptr;
   std::map<int, hipGraphExec_t> graphs;
   bool use_graphs = true;
@@ -91,6 +102,8 @@ namespace {
 // used, so the step graph only changes at bucket boundaries.
 constexpr int kSplitBuckets[] = {8, 16, 32, 64, 128, 256, 512};
 constexpr int kMaxSplits = 512;
+// Prompt tokens per prefill chunk (GEMM rows); longer prompts run in chunks.
+constexpr int64_t kPrefillChunk = 512;
 
 void require_size(const std::vector<float>& v, int64_t expected, const std::string& name) {
   if (static_cast<int64_t>(v.size()) != expected) throw std::invalid_argument(name + " has invalid size");
@@ -234,6 +247,10 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
   dm->plan_down = plan_or_throw(static_cast<int>(H), static_cast<int>(F), mmr::kEpiResidual, "down_proj");
   if (!mmr::gemv_plan(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, 0, 4, &dm->plan_lm))
     throw std::invalid_argument("unsupported GEMV shape for lm_head");
+  dm->gemm_prefill = mmr::gemm_supported(1, static_cast<int>(qs + 2 * kvs), static_cast<int>(H)) &&
+                     mmr::gemm_supported(1, static_cast<int>(H), static_cast<int>(qs)) &&
+                     mmr::gemm_supported(1, static_cast<int>(2 * F), static_cast<int>(H)) &&
+                     mmr::gemm_supported(1, static_cast<int>(H), static_cast<int>(F));
   check_hip(hipDeviceSynchronize(), "weight upload");
   device_ = std::move(dm);
 }
@@ -259,6 +276,8 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->use_graphs = !(nog && nog[0] == '1');
   const char* ck = std::getenv("MMR_COMBINE_KERNEL");
   s->combine_kernel = ck && ck[0] == '1';
+  const char* pt = std::getenv("MMR_PREFILL_TOKENWISE");
+  s->prefill_tokenwise = (pt && pt[0] == '1') || !device_->gemm_prefill;
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
   const int64_t F = c.intermediate_size, V = c.vocab_size;
   const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
@@ -281,6 +300,20 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   ar.plan(part_floats * 4);
   ar.plan(device_->plan_lm.blocks * 4);
   ar.plan(device_->plan_lm.blocks * 4);
+  const int64_t qkv_w = Hq * D + 2 * Hkv * D;
+  int64_t chunk = kPrefillChunk;
+  if (const char* pc = std::getenv("MMR_PREFILL_CHUNK")) chunk = std::max<int64_t>(1, std::atoll(pc));
+  s->pf_chunk = s->prefill_tokenwise ? 0 : std::min<int64_t>(capacity, chunk);
+  const int64_t C = s->pf_chunk;
+  if (C > 0) {
+    ar.plan(C * H * 4);
+    ar.plan(C * H * 4);
+    ar.plan(C * qkv_w * 4);
+    ar.plan(C * Hq * D * 4);
+    ar.plan(C * Hq * D * 4);
+    ar.plan(C * 2 * F * 4);
+    ar.plan(C * F * 4);
+  }
   ar.allocate();
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
     s->kcache.push_back(ar.take<char>(cache_bytes));
@@ -300,6 +333,15 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->attn_part = ar.take<float>(part_floats);
   s->lm_part_val = ar.take<float>(device_->plan_lm.blocks);
   s->lm_part_idx = ar.take<int>(device_->plan_lm.blocks);
+  if (C > 0) {
+    s->pf_h = ar.take<float>(C * H);
+    s->pf_x = ar.take<float>(C * H);
+    s->pf_qkv = ar.take<float>(C * qkv_w);
+    s->pf_q = ar.take<float>(C * Hq * D);
+    s->pf_attn = ar.take<float>(C * Hq * D);
+    s->pf_gu = ar.take<float>(C * 2 * F);
+    s->pf_act = ar.take<float>(C * F);
+  }
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
                           hipHostMallocDefault),
             "hipHostMalloc staging");
@@ -460,6 +502,81 @@ void enqueue_step_kernels(const DeviceState& s, int splits) {
   enqueue_kernel(s, kFinalize, 0, splits, true);
 }
 
+// One prefill chunk: prompt tokens at positions start .. start + n - 1 through
+// every layer with batched kernels (the device prefill layer of
+// decoder_layer.cpp:661-734, chunked): embedding rows -> per layer RMSNorm
+// rows, qkv GEMM, q/k norm + RoPE + KV write, causal attention, O GEMM +
+// residual, RMSNorm rows, gate_up GEMM, SwiGLU rows, down GEMM + residual.
+// The residual stream of the chunk ends in s.pf_h.
+void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
+  const DeviceModel& m = *s.model;
+  const auto& c = m.cfg;
+  const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
+  const int Hq = static_cast<int>(c.num_attention_heads), Hkv = static_cast<int>(c.num_key_value_heads);
+  const int F = static_cast<int>(c.intermediate_size), V = static_cast<int>(c.vocab_size);
+  const int qkv_w = (Hq + 2 * Hkv) * D;
+  const int rows = static_cast<int>(n);
+  check_hip(mmr::launch_embedding_gather(m.embed, s.seq + start, rows, V, H, s.pf_h, s.err, s.stream),
+            "prefill embedding");
+  auto gemm = [&](const float* a, int lda, const __half* w, int N, int K, float* out, bool residual) {
+    mmr::GemmArgs g;
+    g.a = a;
+    g.lda = lda;
+    g.w = w;
+    g.residual = residual ? out : nullptr;
+    g.c = out;
+    g.ldc = N;
+    g.m = rows;
+    g.n = N;
+    g.k = K;
+    check_hip(mmr::launch_gemm(g, s.stream), "prefill gemm");
+  };
+  for (size_t l = 0; l < m.layers.size(); ++l) {
+    const LayerDev& L = m.layers[l];
+    check_hip(mmr::launch_rms_norm_rows(s.pf_h, L.input_norm, c.rms_norm_eps, rows, H, s.pf_x, s.stream),
+              "prefill input norm");
+    gemm(s.pf_x, H, L.qkv, qkv_w, H, s.pf_qkv, false);
+    mmr::QkvRowsArgs q;
+    q.qkv = s.pf_qkv;
+    q.qkv_stride = qkv_w;
+    q.q_norm = L.q_norm;
+    q.k_norm = L.k_norm;
+    q.eps = c.rms_norm_eps;
+    q.inv_freq = m.inv_freq;
+    q.start = static_cast<int>(start);
+    q.tokens = rows;
+    q.kcache = s.kcache[l];
+    q.vcache = s.vcache[l];
+    q.rows = static_cast<int>(s.cache_rows);
+    q.hq = Hq;
+    q.hkv = Hkv;
+    q.d = D;
+    q.query = s.pf_q;
+    q.query_stride = Hq * D;
+    check_hip(mmr::launch_qkv_rows(q, s.kv, s.stream), "prefill qkv rows");
+    mmr::PrefillAttnArgs at;
+    at.query = s.pf_q;
+    at.query_stride = Hq * D;
+    at.kcache = s.kcache[l];
+    at.vcache = s.vcache[l];
+    at.rows = static_cast<int>(s.cache_rows);
+    at.start = static_cast<int>(start);
+    at.tokens = rows;
+    at.hq = Hq;
+    at.hkv = Hkv;
+    at.d = D;
+    at.out = s.pf_attn;
+    at.out_stride = Hq * D;
+    check_hip(mmr::launch_prefill_attention(at, s.kv, s.stream), "prefill attention");
+    gemm(s.pf_attn, Hq * D, L.o, H, Hq * D, s.pf_h, true);
+    check_hip(mmr::launch_rms_norm_rows(s.pf_h, L.post_norm, c.rms_norm_eps, rows, H, s.pf_x, s.stream),
+              "prefill post norm");
+    gemm(s.pf_x, H, L.gate_up, 2 * F, H, s.pf_gu, false);
+    check_hip(mmr::launch_swiglu_pairs(s.pf_gu, static_cast<int64_t>(rows) * F, s.pf_act, s.stream), "prefill swiglu");
+    gemm(s.pf_act, F, L.down, H, F, s.pf_h, true);
+  }
+}
+
 hipGraphExec_t capture_step(DeviceState& s, int splits) {
   hipGraph_t graph = nullptr;
   check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -535,7 +652,30 @@ void LanguageModel::enqueue_prefill(DecoderState& state, const std::vector<int32
   check_hip(hipMemcpyAsync(s.prompt_len, s.staging + s.capacity + 1, sizeof(int32_t), hipMemcpyHostToDevice,
                            s.stream),
             "hipMemcpyAsync prompt_len");
-  for (int64_t i = 0; i < n; ++i) launch_step(state);
+  if (s.prefill_tokenwise) {
+    for (int64_t i = 0; i < n; ++i) launch_step(state);
+    return;
+  }
+  // Chunked GEMM prefill; the head (final norm, lm_head, argmax) then runs on
+  // the last prompt row with the device position at that row, so the
+  // finalize kernel writes the prediction to seq[position + n] and advances
+  // the position past the prompt, exactly as the last decode step would.
+  const int64_t start = state.position;
+  int64_t last_rows = 0;
+  for (int64_t b = start; b < start + n; b += s.pf_chunk) {
+    last_rows = std::min<int64_t>(s.pf_chunk, start + n - b);
+    enqueue_prefill_chunk(s, b, last_rows);
+  }
+  s.staging[s.capacity + 2] = static_cast<int32_t>(start + n - 1);
+  check_hip(hipMemcpyAsync(s.pos, s.staging + s.capacity + 2, sizeof(int32_t), hipMemcpyHostToDevice, s.stream),
+            "hipMemcpyAsync pos");
+  check_hip(hipMemcpyAsync(s.h, s.pf_h + (last_rows - 1) * config_.hidden_size, config_.hidden_size * sizeof(float),
+                           hipMemcpyDeviceToDevice, s.stream),
+            "hipMemcpyAsync last row");
+  const int splits = choose_splits(start + n, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  ::minimind::model::enqueue_kernel(s, kHead, 0, splits, false);
+  ::minimind::model::enqueue_kernel(s, kFinalize, 0, splits, true);
+  state.position += n;
 }
 
 void LanguageModel::enqueue_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const {

@@ -113,6 +113,9 @@ _SIGS = {
     "mmr_attention_from_cache": ([VP, VP, I64, I64, I64, I64, VP, VP, SZ, C.c_int, VP], C.c_int),
     "mmr_decode_attention_fused": ([VP, VP, VP, F32, VP, VP, VP, I64, I64, I64, VP, VP, SZ, C.c_int, VP, VP],
                                    C.c_int),
+    "mmr_matmul_f16": ([VP, I64, I64, VP, I64, VP, VP, VP], C.c_int),
+    "mmr_prefill_qkv_rows": ([VP, VP, VP, F32, VP, VP, I64, I64, I64, I64, I64, VP, VP], C.c_int),
+    "mmr_prefill_attention": ([VP, VP, I64, I64, I64, I64, I64, VP, VP], C.c_int),
     "mmr_rms_norm_rows": ([VP, VP, F32, I64, I64, VP, VP], C.c_int),
     "mmr_add": ([VP, VP, I64, VP, VP], C.c_int),
     "mmr_swiglu_rows": ([VP, I64, I64, VP, VP], C.c_int),
@@ -398,6 +401,22 @@ def decode_attention_fused(qkv, q_norm, k_norm, eps, rope: RopeTable, position, 
     check(_lib.mmr_decode_attention_fused(qkv.ptr, q_norm.ptr, k_norm.ptr, eps, rope.handle, position.ptr,
                                           cache.handle, q_heads, kv_heads, head_dim, out.ptr, workspace.ptr,
                                           workspace.nbytes, splits, error.ptr, _s(stream)))
+
+
+def matmul_f16(w, rows, cols, x, batch, y, residual=None, stream=None) -> None:
+    check(_lib.mmr_matmul_f16(w.ptr, rows, cols, x.ptr, batch, residual.ptr if residual else None, y.ptr, _s(stream)))
+
+
+def prefill_qkv_rows(qkv, q_norm, k_norm, eps, rope: RopeTable, cache: KvCache, start_position, seq_len, q_heads,
+                     kv_heads, head_dim, query, stream=None) -> None:
+    check(_lib.mmr_prefill_qkv_rows(qkv.ptr, q_norm.ptr, k_norm.ptr, eps, rope.handle, cache.handle, start_position,
+                                    seq_len, q_heads, kv_heads, head_dim, query.ptr, _s(stream)))
+
+
+def prefill_attention(query, cache: KvCache, start_position, seq_len, q_heads, kv_heads, head_dim, out,
+                      stream=None) -> None:
+    check(_lib.mmr_prefill_attention(query.ptr, cache.handle, start_position, seq_len, q_heads, kv_heads, head_dim,
+                                     out.ptr, _s(stream)))
 
 
 def rms_norm_rows(x, w, eps, rows, cols, out, stream=None) -> None:

@@ -1,0 +1,169 @@
+"""GPU parity of the prefill path: the batched projection (fp32 matrix cores),
+the q/k norm + RoPE + KV-write rows, causal prefill attention, and the chunked
+model prefill against token-by-token decode.
+
+Floating-point bound: max |gpu - ref| / max |ref| <= 2e-3 (the north-star
+bound), with tighter checks where the arithmetic allows (the GEMM against an
+fp64 product: 1e-5).  Token ids are compared exactly.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import load_golden, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def f16_weights(rng, rows, cols, std=0.02):
+    w = (rng.standard_normal((rows, cols)) * std).astype(np.float16)
+    return w, w.astype(np.float32)
+
+
+# (batch, rows, cols): MiniMind2 prefill projections at several prompt lengths,
+# the lm_head shape, and ragged batches / small shapes (tile edges)
+MATMUL_SHAPES = [(1, 1152, 768), (7, 768, 768), (64, 4096, 768), (100, 768, 2048), (512, 1152, 768),
+                 (512, 4096, 768), (33, 100, 64), (65, 6400, 768), (3, 13, 32)]
+
+
+@pytest.mark.parametrize("batch,rows,cols", MATMUL_SHAPES)
+def test_matmul_matches_fp64_and_oracle(gpu, oracle, batch, rows, cols):
+    mmr = gpu
+    print(f"[case] matmul {batch}x{rows}x{cols}", flush=True)
+    rng = np.random.default_rng(batch * 31 + rows + cols)
+    w16, w32 = f16_weights(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    dw, dx = mmr.DeviceArray.from_numpy(w16.view(np.uint16)), mmr.DeviceArray.from_numpy(x)
+    dy = mmr.DeviceArray((batch, rows), np.float32)
+    mmr.matmul_f16(dw, rows, cols, dx, batch, dy)
+    got = dy.numpy()
+    exact = x.astype(np.float64) @ w32.astype(np.float64).T
+    assert rel_err(got, exact) < 1e-5  # a transposed or misplaced fragment is O(1)
+    for b in {0, batch // 2, batch - 1}:  # the reference's sequential fp32 matvec per row
+        assert rel_err(got[b], oracle.matvec(w32, x[b])) < TOL
+    # residual epilogue (device_matmul_add), residual aliasing the output
+    res = rng.standard_normal((batch, rows)).astype(np.float32)
+    dr = mmr.DeviceArray.from_numpy(res)
+    mmr.matmul_f16(dw, rows, cols, dx, batch, dr, residual=dr)
+    assert rel_err(dr.numpy(), res + exact) < 1e-5
+
+
+def test_matmul_rejects_bad_shapes(gpu):
+    mmr = gpu
+    d = mmr.DeviceArray(64, np.float32)
+    with pytest.raises(mmr.InvalidArgument, match="multiple of 32"):
+        mmr.check(mmr.lib().mmr_matmul_f16(d.ptr, 4, 48, d.ptr, 1, None, d.ptr, None))
+    with pytest.raises(mmr.InvalidArgument, match="positive"):
+        mmr.check(mmr.lib().mmr_matmul_f16(d.ptr, 4, 32, d.ptr, 0, None, d.ptr, None))
+
+
+def cache_layout(rows_ref, tokens, hkv, d, rows):
+    """[token][kv_head][d] (reference) -> [kv_head][rows][d] (cache)."""
+    out = np.zeros((hkv, rows, d), rows_ref.dtype)
+    out[:, :tokens, :] = rows_ref.reshape(tokens, hkv, d).transpose(1, 0, 2)
+    return out
+
+
+@pytest.mark.parametrize("d", [64, 96, 128])
+@pytest.mark.parametrize("start", [0, 37])
+def test_prefill_qkv_rows_match_per_token_postprocess(gpu, oracle, d, start):
+    mmr = gpu
+    hq, hkv, eps, theta, T = 8, 2, 1e-5, 1e6, 21
+    rng = np.random.default_rng(d + start)
+    qkv = rng.standard_normal((T, (hq + 2 * hkv) * d)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    rope = mmr.RopeTable(1024, d, theta)
+    cache = mmr.KvCache(hkv, d, start + T + 5, mmr.KV_F32)
+    dqkv, dqn, dkn = (mmr.DeviceArray.from_numpy(a) for a in (qkv, qn, kn))
+    query = mmr.DeviceArray((T, hq * d), np.float32)
+    mmr.prefill_qkv_rows(dqkv, dqn, dkn, eps, rope, cache, start, T, hq, hkv, d, query)
+    q_all, keys = query.numpy(), cache.download()[0]
+    vals = cache.download()[1]
+    for t in range(T):
+        q_ref, k_ref = oracle.qk_norm_rope(qkv[t, : hq * d], qkv[t, hq * d: (hq + hkv) * d], qn, kn, hq, hkv, d,
+                                           start + t, eps, theta)
+        assert rel_err(q_all[t], q_ref) < 1e-5, t
+        assert rel_err(keys[:, start + t, :].reshape(-1), k_ref) < 1e-5, t
+        np.testing.assert_array_equal(vals[:, start + t, :].reshape(-1), qkv[t, (hq + hkv) * d:])
+    assert not keys[:, :start, :].any() and not keys[:, start + T:, :].any()  # nothing else written
+
+
+@pytest.mark.parametrize("kv", ["f16", "f32"])
+@pytest.mark.parametrize("d", [64, 96, 128])
+@pytest.mark.parametrize("start,T", [(0, 1), (0, 16), (0, 17), (0, 100), (70, 33), (130, 64)])
+def test_prefill_attention_matches_oracle(gpu, oracle, kv, d, start, T):
+    mmr = gpu
+    print(f"[case] prefill attention kv={kv} d={d} start={start} T={T}", flush=True)
+    hq, hkv = 8, 2
+    rng = np.random.default_rng(d * 1000 + start + T)
+    np_kv = np.float16 if kv == "f16" else np.float32
+    n = start + T
+    k = rng.standard_normal(n * hkv * d).astype(np_kv).astype(np.float32)
+    v = rng.standard_normal(n * hkv * d).astype(np_kv).astype(np.float32)
+    q = rng.standard_normal((T, hq * d)).astype(np.float32)
+    cache = mmr.KvCache(hkv, d, n + 3, mmr.KV_F16 if kv == "f16" else mmr.KV_F32)
+    cache.upload(cache_layout(k, n, hkv, d, cache.rows), cache_layout(v, n, hkv, d, cache.rows))
+    dq, out = mmr.DeviceArray.from_numpy(q), mmr.DeviceArray((T, hq * d), np.float32)
+    mmr.prefill_attention(dq, cache, start, T, hq, hkv, d, out)
+    got = out.numpy()
+    for t in sorted({0, T // 3, T // 2, T - 1}):
+        keys = start + t + 1  # causal: keys 0 .. own position
+        ref = oracle.attention_step(q[t], k[: keys * hkv * d], v[: keys * hkv * d], keys, hq, hkv, d)
+        assert rel_err(got[t], ref) < TOL, t
+
+
+def synth_model(mmr, g):
+    return mmr.Model.synthetic(mmr.make_config(**g["config"]), g["seed"], g["std"], g["round_fp16"])
+
+
+@pytest.mark.parametrize("case,chunk", [("mini", None), ("mini", 7), ("cfg0", None), ("cfg0", 64)])
+def test_gemm_prefill_matches_tokenwise_prefill(gpu, monkeypatch, case, chunk):
+    # the chunked GEMM prefill (one or several chunks) against the same prompt
+    # fed token by token through the decode step: same next token, logits
+    # within the bound, then identical greedy continuations
+    mmr = gpu
+    print(f"[case] prefill {case} chunk={chunk}", flush=True)
+    g = load_golden(case)
+    m = synth_model(mmr, g)
+    rng = np.random.default_rng(5)
+    prompt = [int(t) for t in rng.integers(0, g["config"]["vocab_size"], 150)]
+    monkeypatch.setenv("MMR_PREFILL_TOKENWISE", "1")
+    tok = m.make_state(200)
+    monkeypatch.delenv("MMR_PREFILL_TOKENWISE")
+    if chunk:
+        monkeypatch.setenv("MMR_PREFILL_CHUNK", str(chunk))
+    gem = m.make_state(200)
+    for st in (tok, gem):
+        st.enqueue_prefill(prompt)
+        st.synchronize()
+        assert st.position == len(prompt)
+    assert rel_err(gem.read_logits(), tok.read_logits()) < 1e-4
+    assert gem.read_sequence(0, len(prompt) + 1).tolist() == tok.read_sequence(0, len(prompt) + 1).tolist()
+    for st in (tok, gem):
+        st.enqueue_decode(24)
+        st.synchronize()
+    assert gem.read_sequence(len(prompt), 25).tolist() == tok.read_sequence(len(prompt), 25).tolist()
+
+
+def test_gemm_prefill_on_used_state_and_fp16_cache(gpu, monkeypatch):
+    # a second prompt appended to a state that already holds a sequence, and an
+    # fp16 KV cache: GEMM prefill and token-by-token decode agree
+    mmr = gpu
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    monkeypatch.setenv("MMR_PREFILL_TOKENWISE", "1")
+    tok = m.make_state(128, mmr.KV_F16)
+    monkeypatch.delenv("MMR_PREFILL_TOKENWISE")
+    gem = m.make_state(128, mmr.KV_F16)
+    for st in (tok, gem):
+        st.enqueue_prefill(g["prompt"])
+        st.enqueue_decode(5)
+        st.enqueue_prefill([3, 1, 4, 1, 5, 9, 2, 6])
+        st.synchronize()
+    assert tok.position == gem.position == len(g["prompt"]) + 5 + 8
+    n = tok.position + 1
+    assert gem.read_sequence(0, n).tolist() == tok.read_sequence(0, n).tolist()
+    assert rel_err(gem.read_logits(), tok.read_logits()) < 1e-4
