@@ -28,6 +28,21 @@ namespace {
 
 using f32x4 = float __attribute__((ext_vector_type(4)));
 
+// One 16-byte KV chunk (8 fp16 or 4 fp32 values) -> fp32.
+template <typename KV>
+__device__ __forceinline__ void chunk_to_float_n(const uint4& c, float* f);
+template <>
+__device__ __forceinline__ void chunk_to_float_n<__half>(const uint4& c, float* f) {
+  half8_to_float8(c, f);
+}
+template <>
+__device__ __forceinline__ void chunk_to_float_n<float>(const uint4& c, float* f) {
+  f[0] = __uint_as_float(c.x);
+  f[1] = __uint_as_float(c.y);
+  f[2] = __uint_as_float(c.z);
+  f[3] = __uint_as_float(c.w);
+}
+
 constexpr int kGemmThreads = 256;
 constexpr int kGemmBK = 32;
 constexpr int kGemmLDK = kGemmBK + 4;
@@ -209,120 +224,157 @@ __global__ void swiglu_pairs_kernel(const float* gu, int64_t n, float* out) {
 
 // Causal attention of `tokens` queries at positions start .. start + tokens - 1
 // over the cache (keys 0 .. position of each query, decoder_layer.cpp:184-234
-// per token).  One wave per (16 queries, query head): lane = (query q = lane /
-// 4, key slot ks = lane % 4); each lane keeps its query and an online-softmax
-// (m, l, o[d]) over keys ks, ks + 4, ... of each 64-key tile staged in LDS, and
-// the four slots of a query merge with quad DPP reductions at the end.
+// per token), on the fp32 matrix cores.
+//
+// Block = (16 queries, KV group g), one wave per query head of the group, so
+// each 64-key tile of K and V is staged in LDS once for all of them (K
+// row-major, V transposed).  Per 16-key sub-tile a wave forms S^T = K Q^T
+// (v_mfma_f32_16x16x4f32, D/16 slices x 4): lane l holds S^T[key 4(l/16)+i]
+// [query l%16].  That is exactly the B-operand layout of O^T += V^T P^T, so the
+// probabilities never move between lanes; only the per-query tile maximum
+// needs the four 16-lane rows (two xor shuffles).  Online softmax per query:
+// scores are dot / sqrt(d) (a division, as the reference), masked above the
+// query's position; the running sum l stays per lane and is reduced once at
+// the end.
 constexpr int kPrefillQueries = 16;
 constexpr int kPrefillKeys = 64;
 
-template <typename KV, int D>
-__global__ __launch_bounds__(kWave) void prefill_attention_kernel(PrefillAttnArgs a) {
-  constexpr int LD = D + 4;
+// NW waves per block (4 for groups of up to 4 query heads, else 8); waves past
+// the group size only help staging.
+template <typename KV, int D, int NW>
+__global__ __launch_bounds__(kWave* NW) void prefill_attention_kernel(PrefillAttnArgs a) {
+  constexpr int NT = kWave * NW;
+  constexpr int LDK = D + 4;               // K rows: 16-byte fragment reads hit distinct banks
+  constexpr int LDV = kPrefillKeys + 4;    // V^T rows
   constexpr int CH = 16 / static_cast<int>(sizeof(KV));
   constexpr int kChunks = kPrefillKeys * D / CH;
-  constexpr int kSlotKeys = kPrefillKeys / 4;
-  __shared__ __align__(16) float k_s[kPrefillKeys][LD];
-  __shared__ __align__(16) float v_s[kPrefillKeys][LD];
-  const int lane = threadIdx.x;
-  const int qi = lane / 4, ks = lane % 4;
-  const int h = blockIdx.y;
+  constexpr int kPer = (kChunks + NT - 1) / NT;
+  constexpr int DT = D / 16;               // 16-wide slices of the head dimension
+  __shared__ __align__(16) float k_s[kPrefillKeys][LDK];
+  __shared__ __align__(16) float vt_s[D][LDV];
   const int R = a.hq / a.hkv;
-  const int g = h / R;
+  const int g = blockIdx.y;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int h = g * R + min(wave, R - 1);  // waves past the group load a valid row and never store
   const int q0 = blockIdx.x * kPrefillQueries;
+  const int qi = lane % 16, kq = lane / 16;  // query column, k slot
   const int qrow = min(q0 + qi, a.tokens - 1);
-  const int qpos = a.start + qrow;
+  const int qpos = a.start + q0 + qi;
   const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.rows * D;
   const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
 
-  float q[D];
+  // Q^T fragments: dims 16j + 4 kq + {0..3} of query qi.
+  float4 qf[DT];
   const float* qsrc = a.query + static_cast<int64_t>(qrow) * a.query_stride + h * D;
 #pragma unroll
-  for (int i = 0; i < D / 4; ++i) {
-    const float4 v = reinterpret_cast<const float4*>(qsrc)[i];
-    q[4 * i] = v.x;
-    q[4 * i + 1] = v.y;
-    q[4 * i + 2] = v.z;
-    q[4 * i + 3] = v.w;
-  }
-  float o[D];
+  for (int j = 0; j < DT; ++j) qf[j] = *reinterpret_cast<const float4*>(qsrc + 16 * j + 4 * kq);
+
+  f32x4 ot[DT];  // O^T[d = 16 dt + 4 kq + i][query qi]
 #pragma unroll
-  for (int i = 0; i < D; ++i) o[i] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
+  for (int j = 0; j < DT; ++j) ot[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m_run = -INFINITY, l_part = 0.0f;
   const float sqrt_d = sqrtf(static_cast<float>(D));
 
   const int last_key = a.start + min(q0 + kPrefillQueries, a.tokens) - 1;  // the block's last query position
   const int n_tiles = last_key / kPrefillKeys + 1;
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int t0 = tile * kPrefillKeys;
-    __syncthreads();  // previous tile fully consumed
-    for (int c = lane; c < kChunks; c += kWave) {
-      const int r = (c * CH) / D, col = (c * CH) % D;
-      const int key = min(t0 + r, last_key);  // rows past the last key are never scored
+    // chunk c: key c % 64, dims (c / 64) * CH ..: consecutive lanes take
+    // consecutive keys, so the transposed V writes are conflict-free.  All of
+    // a thread's loads are issued before the first LDS write.
+    uint4 kc[kPer], vc[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = min(static_cast<int>(threadIdx.x) + i * NT, kChunks - 1);
+      const int r = c % kPrefillKeys, col = (c / kPrefillKeys) * CH;
+      const int key = min(t0 + r, last_key);  // rows past the last key are masked
       const int64_t off = static_cast<int64_t>(key) * D + col;
-      const uint4 kc = *reinterpret_cast<const uint4*>(kbase + off);
-      const uint4 vc = *reinterpret_cast<const uint4*>(vbase + off);
-      if constexpr (sizeof(KV) == 2) {
-        half8_to_float8(kc, &k_s[r][col]);
-        half8_to_float8(vc, &v_s[r][col]);
-      } else {
-        *reinterpret_cast<uint4*>(&k_s[r][col]) = kc;
-        *reinterpret_cast<uint4*>(&v_s[r][col]) = vc;
+      kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
+      vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+    }
+    __syncthreads();  // previous tile consumed by every wave
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = static_cast<int>(threadIdx.x) + i * NT;
+      if (c < kChunks) {
+        const int r = c % kPrefillKeys, col = (c / kPrefillKeys) * CH;
+        float kf[CH], vf[CH];
+        chunk_to_float_n<KV>(kc[i], kf);
+        chunk_to_float_n<KV>(vc[i], vf);
+#pragma unroll
+        for (int e = 0; e < CH; e += 4)
+          *reinterpret_cast<float4*>(&k_s[r][col + e]) = make_float4(kf[e], kf[e + 1], kf[e + 2], kf[e + 3]);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) vt_s[col + e][r] = vf[e];
       }
     }
     __syncthreads();
-    float s[kSlotKeys];
-    float mt = -INFINITY;
+    if (wave < R) {
+      // S^T for the four 16-key sub-tiles.
+      f32x4 st[4];
 #pragma unroll
-    for (int i = 0; i < kSlotKeys; ++i) {
-      const int j = ks + 4 * i;
-      float dot = 0.0f;
+      for (int kt = 0; kt < 4; ++kt) {
+        st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int dd = 0; dd < D; dd += 4) {
-        const float4 kv = *reinterpret_cast<const float4*>(&k_s[j][dd]);
-        dot = fmaf(q[dd], kv.x, dot);
-        dot = fmaf(q[dd + 1], kv.y, dot);
-        dot = fmaf(q[dd + 2], kv.z, dot);
-        dot = fmaf(q[dd + 3], kv.w, dot);
-      }
-      s[i] = (t0 + j <= qpos) ? dot / sqrt_d : -INFINITY;  // decoder_layer.cpp:213
-      mt = fmaxf(mt, s[i]);
-    }
-    const float m_new = fmaxf(m, mt);
-    if (m_new != -INFINITY) {  // lane-uniform per query slot; no key yet means nothing to add
-      const float alpha = expf(m - m_new);
-      l *= alpha;
-#pragma unroll
-      for (int i = 0; i < D; ++i) o[i] *= alpha;
-#pragma unroll
-      for (int i = 0; i < kSlotKeys; ++i) {
-        const float p = expf(s[i] - m_new);  // exp(-inf) = 0 for masked keys
-        l += p;
-        const int j = ks + 4 * i;
-#pragma unroll
-        for (int dd = 0; dd < D; dd += 4) {
-          const float4 vv = *reinterpret_cast<const float4*>(&v_s[j][dd]);
-          o[dd] = fmaf(p, vv.x, o[dd]);
-          o[dd + 1] = fmaf(p, vv.y, o[dd + 1]);
-          o[dd + 2] = fmaf(p, vv.z, o[dd + 2]);
-          o[dd + 3] = fmaf(p, vv.w, o[dd + 3]);
+        for (int j = 0; j < DT; ++j) {
+          const float4 kf = *reinterpret_cast<const float4*>(&k_s[kt * 16 + qi][16 * j + 4 * kq]);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[j].x, st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[j].y, st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[j].z, st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[j].w, st[kt], 0, 0, 0);
         }
       }
-      m = m_new;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = t0 + kt * 16 + 4 * kq + i;
+          const float sc = st[kt][i] / sqrt_d;  // decoder_layer.cpp:213
+          st[kt][i] = key <= qpos ? sc : -INFINITY;
+          mx = fmaxf(mx, st[kt][i]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      // Every query sees key 0 in tile 0, so m_new is finite from then on.
+      const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) ot[j] *= alpha;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          st[kt][i] = expf(st[kt][i] - m_new);  // 0 for masked keys
+          l_part += st[kt][i];
+        }
+      m_run = m_new;
+      // O^T += V^T P^T over the 64 keys.
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+          const float4 vf = *reinterpret_cast<const float4*>(&vt_s[16 * j + qi][kt * 16 + 4 * kq]);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, st[kt][0], ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, st[kt][1], ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, st[kt][2], ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, st[kt][3], ot[j], 0, 0, 0);
+        }
     }
   }
-
-  // Merge the four key slots of each query (lanes 4q .. 4q + 3).
-  const float M = group_max<4>(m);
-  const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
-  const float L = group_sum<4>(l * w);
-  const float inv = 1.0f / L;
-  float* dst = a.out + static_cast<int64_t>(qrow) * a.out_stride + h * D;
-  const bool live = q0 + qi < a.tokens;
+  if (wave < R) {
+    float l = l_part + __shfl_xor(l_part, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = 1.0f / l;
+    if (q0 + qi < a.tokens) {
+      float* dst = a.out + static_cast<int64_t>(q0 + qi) * a.out_stride + h * D;
 #pragma unroll
-  for (int i = 0; i < D; ++i) {
-    const float oi = group_sum<4>(o[i] * w);
-    if (live && (i % 4) == ks) dst[i] = oi * inv;
+      for (int j = 0; j < DT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[16 * j + 4 * kq + i] = ot[j][i] * inv;
+    }
   }
 }
 
@@ -351,18 +403,24 @@ hipError_t launch_qkv_rows_kv(const QkvRowsArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <typename KV>
-hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) {
-  const dim3 grid((a.tokens + kPrefillQueries - 1) / kPrefillQueries, a.hq);
+template <typename KV, int NW>
+hipError_t launch_prefill_attention_nw(const PrefillAttnArgs& a, hipStream_t s) {
+  const dim3 grid((a.tokens + kPrefillQueries - 1) / kPrefillQueries, a.hkv);
+  const dim3 block(kWave * NW);
   switch (a.d) {
-    case 16: prefill_attention_kernel<KV, 16><<<grid, kWave, 0, s>>>(a); break;
-    case 32: prefill_attention_kernel<KV, 32><<<grid, kWave, 0, s>>>(a); break;
-    case 64: prefill_attention_kernel<KV, 64><<<grid, kWave, 0, s>>>(a); break;
-    case 96: prefill_attention_kernel<KV, 96><<<grid, kWave, 0, s>>>(a); break;
-    case 128: prefill_attention_kernel<KV, 128><<<grid, kWave, 0, s>>>(a); break;
+    case 16: prefill_attention_kernel<KV, 16, NW><<<grid, block, 0, s>>>(a); break;
+    case 32: prefill_attention_kernel<KV, 32, NW><<<grid, block, 0, s>>>(a); break;
+    case 64: prefill_attention_kernel<KV, 64, NW><<<grid, block, 0, s>>>(a); break;
+    case 96: prefill_attention_kernel<KV, 96, NW><<<grid, block, 0, s>>>(a); break;
+    case 128: prefill_attention_kernel<KV, 128, NW><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <typename KV>
+hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) {
+  return a.hq / a.hkv <= 4 ? launch_prefill_attention_nw<KV, 4>(a, s) : launch_prefill_attention_nw<KV, 8>(a, s);
 }
 
 }  // namespace

@@ -115,6 +115,29 @@ def test_prefill_attention_matches_oracle(gpu, oracle, kv, d, start, T):
         assert rel_err(got[t], ref) < TOL, t
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 1), (4, 4), (6, 2), (16, 2)])
+def test_prefill_attention_group_sizes(gpu, oracle, hq, hkv):
+    # query heads per KV head R = 8, 1, 3, 8 (the block holds 4 or 8 waves;
+    # waves past R only stage K/V)
+    mmr = gpu
+    print(f"[case] prefill attention hq={hq} hkv={hkv}", flush=True)
+    d, start, T = 64, 20, 45
+    rng = np.random.default_rng(hq * 10 + hkv)
+    n = start + T
+    k = rng.standard_normal(n * hkv * d).astype(np.float32)
+    v = rng.standard_normal(n * hkv * d).astype(np.float32)
+    q = rng.standard_normal((T, hq * d)).astype(np.float32)
+    cache = mmr.KvCache(hkv, d, n, mmr.KV_F32)
+    cache.upload(cache_layout(k, n, hkv, d, cache.rows), cache_layout(v, n, hkv, d, cache.rows))
+    dq, out = mmr.DeviceArray.from_numpy(q), mmr.DeviceArray((T, hq * d), np.float32)
+    mmr.prefill_attention(dq, cache, start, T, hq, hkv, d, out)
+    got = out.numpy()
+    for t in (0, 17, T - 1):
+        keys = start + t + 1
+        ref = oracle.attention_step(q[t], k[: keys * hkv * d], v[: keys * hkv * d], keys, hq, hkv, d)
+        assert rel_err(got[t], ref) < TOL, t
+
+
 def synth_model(mmr, g):
     return mmr.Model.synthetic(mmr.make_config(**g["config"]), g["seed"], g["std"], g["round_fp16"])
 
