@@ -482,7 +482,7 @@ int mmr_matmul_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x
     require(w && x && y, "null buffer");
     require(rows > 0 && cols > 0 && batch > 0, "rows, cols and batch must be positive");
     require(rows <= (1 << 24) && cols <= (1 << 24) && batch <= (1 << 24), "matrix too large");
-    require(cols % 32 == 0, "cols must be a multiple of 32");
+    require(cols % 8 == 0, "cols must be a multiple of 8");
     mmr::GemmArgs g;
     g.a = x;
     g.lda = static_cast<int>(cols);

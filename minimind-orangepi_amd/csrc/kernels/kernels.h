@@ -120,7 +120,7 @@ struct AttnArgs {
   int rows = 0;                     // allocated rows per head (capacity rounded up to the tile)
   int hq = 0, hkv = 0, d = 0;
   int splits = 1;
-  float* part = nullptr;            // [Hkv][splits][R][D+2]
+  float* part = nullptr;            // o [Hkv][splits][R][D], then (m, l) [Hkv][splits][R][2]
   int32_t* err = nullptr;           // set to 1 when *pos is out of range
 };
 
@@ -155,7 +155,7 @@ hipError_t launch_qkv_postprocess(const QkvPostArgs& a, KvDtype kv, hipStream_t 
 // ------------------------------------------------------------- prefill ----
 // C[m][n] = (residual[m][n] +) sum_k A[m][k] * W[n][k]: A fp32 (row stride
 // lda), W fp16 row-major [n][k], C fp32 (row stride ldc); residual may alias
-// C.  fp32 matrix cores, fp32 accumulation.  k % 32 == 0, lda % 4 == 0.
+// C.  fp32 matrix cores, fp32 accumulation.  k % 8 == 0, lda % 4 == 0.
 struct GemmArgs {
   const float* a = nullptr;
   int lda = 0;

@@ -44,15 +44,63 @@ __device__ __forceinline__ void chunk_to_float_n<float>(const uint4& c, float* f
 }
 
 constexpr int kGemmThreads = 256;
-constexpr int kGemmBK = 32;
+constexpr int kGemmBK = 128;  // K per LDS tile: the next tile's loads overlap 64-128 MFMAs per wave
 constexpr int kGemmLDK = kGemmBK + 4;
+
+// Per-thread staging registers of one K tile: BM x BK fp32 of A as float4s,
+// BN x BK fp16 of W as 8-half chunks; thread t takes chunks t, t + 256, ...
+// so consecutive lanes read consecutive 16-byte pieces of a row.
+template <int BM, int BN>
+struct GemmStage {
+  static constexpr int kA = BM * kGemmBK / 4 / kGemmThreads;
+  static constexpr int kB = BN * kGemmBK / 8 / kGemmThreads;
+  float4 a[kA];
+  uint4 b[kB];
+
+  __device__ __forceinline__ void load(const GemmArgs& g, int m0, int n0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < kA; ++i) {
+      const int idx = tid + i * kGemmThreads;
+      const int r = idx / (kGemmBK / 4), q = idx % (kGemmBK / 4);
+      const int row = min(m0 + r, g.m - 1);  // clamped: in bounds, never stored
+      const int kc = k0 + q * 4;               // past k (last, partial tile): clamped load, zeroed
+      const float4 v = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(row) * g.lda + min(kc, g.k - 4));
+      a[i] = kc < g.k ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int idx = tid + i * kGemmThreads;
+      const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
+      const int row = min(n0 + r, g.n - 1);
+      const int kc = k0 + q * 8;
+      const uint4 v = *reinterpret_cast<const uint4*>(g.w + static_cast<int64_t>(row) * g.k + min(kc, g.k - 8));
+      b[i] = kc < g.k ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+
+  __device__ __forceinline__ void store(float (*As)[kGemmLDK], float (*Bs)[kGemmLDK], int tid) const {
+#pragma unroll
+    for (int i = 0; i < kA; ++i) {
+      const int idx = tid + i * kGemmThreads;
+      const int r = idx / (kGemmBK / 4), q = idx % (kGemmBK / 4);
+      *reinterpret_cast<float4*>(&As[r][q * 4]) = a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int idx = tid + i * kGemmThreads;
+      const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
+      float f[8];
+      half8_to_float8(b[i], f);
+      *reinterpret_cast<float4*>(&Bs[r][q * 8]) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4*>(&Bs[r][q * 8 + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+};
 
 template <int BM, int BN, bool kResidual>
 __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
-  constexpr int kAIters = BM * (kGemmBK / 4) / kGemmThreads;
-  constexpr int kBIters = BN * (kGemmBK / 8) / kGemmThreads;
-  static_assert(kAIters >= 1 && kBIters >= 1, "tile too small for the block");
+  static_assert(GemmStage<BM, BN>::kA >= 1 && GemmStage<BM, BN>::kB >= 1, "tile too small for the block");
   __shared__ __align__(16) float As[BM][kGemmLDK];
   __shared__ __align__(16) float Bs[BN][kGemmLDK];
   const int tid = threadIdx.x;
@@ -61,48 +109,21 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   const int wm = wave / 2, wn = wave % 2;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-  static_assert(kAIters <= 2 && kBIters == 1, "register staging holds two A chunks and one B chunk");
-  // Staging registers, named (not an array) so they never leave registers.
-  float4 ra0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), ra1 = ra0;
-  uint4 rb0 = make_uint4(0u, 0u, 0u, 0u);
-  // Row indices are clamped into range: every load is in bounds, and rows
-  // past m / n are never stored.
-  const int a_r0 = tid / (kGemmBK / 4), a_q = tid % (kGemmBK / 4);
-  const int a_r1 = a_r0 + kGemmThreads / (kGemmBK / 4);
-  const int b_r = tid / (kGemmBK / 8), b_q = tid % (kGemmBK / 8);
-  const float* a_src0 = g.a + static_cast<int64_t>(min(m0 + a_r0, g.m - 1)) * g.lda + a_q * 4;
-  const float* a_src1 = g.a + static_cast<int64_t>(min(m0 + a_r1, g.m - 1)) * g.lda + a_q * 4;
-  const __half* b_src = g.w + static_cast<int64_t>(min(n0 + b_r, g.n - 1)) * g.k + b_q * 8;
-#define MMR_GEMM_LOAD(k0)                                                      \
-  do {                                                                          \
-    ra0 = *reinterpret_cast<const float4*>(a_src0 + (k0));                      \
-    if constexpr (kAIters > 1) ra1 = *reinterpret_cast<const float4*>(a_src1 + (k0)); \
-    rb0 = *reinterpret_cast<const uint4*>(b_src + (k0));                        \
-  } while (0)
-#define MMR_GEMM_STORE()                                                       \
-  do {                                                                          \
-    *reinterpret_cast<float4*>(&As[a_r0][a_q * 4]) = ra0;                       \
-    if constexpr (kAIters > 1) *reinterpret_cast<float4*>(&As[a_r1][a_q * 4]) = ra1; \
-    float f[8];                                                                 \
-    half8_to_float8(rb0, f);                                                    \
-    *reinterpret_cast<float4*>(&Bs[b_r][b_q * 8]) = make_float4(f[0], f[1], f[2], f[3]);     \
-    *reinterpret_cast<float4*>(&Bs[b_r][b_q * 8 + 4]) = make_float4(f[4], f[5], f[6], f[7]); \
-  } while (0)
-
   f32x4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int nk = g.k / kGemmBK;
-  MMR_GEMM_LOAD(0);
-  MMR_GEMM_STORE();
+  GemmStage<BM, BN> stage;
+  const int nk = (g.k + kGemmBK - 1) / kGemmBK;
+  stage.load(g, m0, n0, 0, tid);
+  stage.store(As, Bs, tid);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     // The next tile's loads are in flight during this tile's MFMAs; on the
     // last tile they reload it (unconditional, so the values stay in registers).
-    MMR_GEMM_LOAD(min(kt + 1, nk - 1) * kGemmBK);
+    stage.load(g, m0, n0, min(kt + 1, nk - 1) * kGemmBK, tid);
 #pragma unroll
     for (int kb = 0; kb < kGemmBK; kb += 16) {
       const int kk = kb + 4 * (lane / 16);
@@ -124,11 +145,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
         }
     }
     __syncthreads();
-    MMR_GEMM_STORE();
+    stage.store(As, Bs, tid);
     __syncthreads();
   }
-#undef MMR_GEMM_LOAD
-#undef MMR_GEMM_STORE
 
   // Output fragment: lane holds rows 4 * (lane / 16) + {0..3} of column
   // lane % 16 of each 16 x 16 tile.  Residual loads are issued together
@@ -425,14 +444,16 @@ hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) 
 
 }  // namespace
 
-bool gemm_supported(int m, int n, int k) { return m > 0 && n > 0 && k > 0 && k % kGemmBK == 0; }
+bool gemm_supported(int m, int n, int k) { return m > 0 && n > 0 && k > 0 && k % 8 == 0; }
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < g.n) return hipErrorInvalidValue;
-  // 64 x 64 tiles, or 32-row tiles when that is what fills the chip.
-  const int64_t tiles64 = static_cast<int64_t>((g.m + 63) / 64) * ((g.n + 63) / 64);
-  if (tiles64 >= 256 || g.m <= 32) return g.m <= 32 ? launch_gemm_tile<32, 64>(g, s) : launch_gemm_tile<64, 64>(g, s);
-  return launch_gemm_tile<32, 64>(g, s);
+  // The largest tile that still gives every CU a block (256 CUs), else the
+  // smallest tile.
+  auto blocks = [&](int bm, int bn) { return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn); };
+  if (blocks(64, 64) >= 256) return launch_gemm_tile<64, 64>(g, s);
+  if (blocks(32, 64) >= 256) return launch_gemm_tile<32, 64>(g, s);
+  return launch_gemm_tile<32, 32>(g, s);
 }
 
 hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream) {

@@ -25,7 +25,8 @@ def f16_weights(rng, rows, cols, std=0.02):
 # (batch, rows, cols): MiniMind2 prefill projections at several prompt lengths,
 # the lm_head shape, and ragged batches / small shapes (tile edges)
 MATMUL_SHAPES = [(1, 1152, 768), (7, 768, 768), (64, 4096, 768), (100, 768, 2048), (512, 1152, 768),
-                 (512, 4096, 768), (33, 100, 64), (65, 6400, 768), (3, 13, 32)]
+                 (512, 4096, 768), (512, 768, 768), (512, 768, 2048), (33, 100, 64), (65, 6400, 768), (3, 13, 32),
+                 (40, 96, 1408), (9, 24, 200)]
 
 
 @pytest.mark.parametrize("batch,rows,cols", MATMUL_SHAPES)
@@ -53,8 +54,8 @@ def test_matmul_matches_fp64_and_oracle(gpu, oracle, batch, rows, cols):
 def test_matmul_rejects_bad_shapes(gpu):
     mmr = gpu
     d = mmr.DeviceArray(64, np.float32)
-    with pytest.raises(mmr.InvalidArgument, match="multiple of 32"):
-        mmr.check(mmr.lib().mmr_matmul_f16(d.ptr, 4, 48, d.ptr, 1, None, d.ptr, None))
+    with pytest.raises(mmr.InvalidArgument, match="multiple of 8"):
+        mmr.check(mmr.lib().mmr_matmul_f16(d.ptr, 4, 44, d.ptr, 1, None, d.ptr, None))
     with pytest.raises(mmr.InvalidArgument, match="positive"):
         mmr.check(mmr.lib().mmr_matmul_f16(d.ptr, 4, 32, d.ptr, 0, None, d.ptr, None))
 
