@@ -33,6 +33,7 @@ extern "C" {
 typedef void* mmr_stream_t;
 typedef struct mmr_model mmr_model;
 typedef struct mmr_state mmr_state;
+typedef struct mmr_batch_state mmr_batch_state;
 typedef struct mmr_rope_table mmr_rope_table;
 typedef struct mmr_kv_cache mmr_kv_cache;
 
@@ -235,6 +236,29 @@ int mmr_enqueue_decode(const mmr_model* model, mmr_state* state, int64_t steps, 
 int mmr_state_synchronize(const mmr_model* model, mmr_state* state);
 int mmr_read_sequence(const mmr_model* model, mmr_state* state, int64_t first, int64_t count, int32_t* out);
 int mmr_read_logits(const mmr_model* model, mmr_state* state, float* logits);
+
+/* ---- batched decode.  No counterpart in the reference,
+ * whose DecoderState holds one sequence (language_model.h:22-25): `batch`
+ * independent sequences advance one greedy token per step in lockstep, each
+ * at its own position, with a paged KV cache (64-token pages through a
+ * per-sequence page table) and the projections as batch-row GEMMs.  Each
+ * sequence decodes exactly as mmr_forward_next_token would decode it alone;
+ * there is no EOS stop (callers cut sequences at EOS). */
+int mmr_batch_state_create(const mmr_model* model, int64_t batch, int64_t capacity, int kv_dtype,
+                           mmr_batch_state** out);
+int mmr_batch_state_free(mmr_batch_state* state);
+/* batch, capacity (positions per sequence), steps run since the prompts; any may be NULL */
+int mmr_batch_state_info(const mmr_batch_state* state, int64_t* batch, int64_t* capacity, int64_t* steps);
+int mmr_batch_state_stream(const mmr_batch_state* state, mmr_stream_t* stream);
+/* tokens: the prompts concatenated; lengths[batch].  Fresh state only; runs
+ * max(lengths) steps (shorter prompts start generating earlier). */
+int mmr_batch_prefill(const mmr_model* model, mmr_batch_state* state, const int32_t* tokens, const int64_t* lengths,
+                      int64_t batch);
+int mmr_batch_decode(const mmr_model* model, mmr_batch_state* state, int64_t steps);
+int mmr_batch_synchronize(const mmr_model* model, mmr_batch_state* state);
+int mmr_batch_read_sequence(const mmr_model* model, mmr_batch_state* state, int64_t index, int64_t first,
+                            int64_t count, int32_t* out);
+int mmr_batch_read_logits(const mmr_model* model, mmr_batch_state* state, int64_t index, float* logits);
 
 /* Enqueue `count` launches of one kernel of the decode step on the state's
  * stream, cycling over layers from `layer` (kernel: 0 qkv, 1 attention,

@@ -24,6 +24,9 @@ struct mmr_model {
 struct mmr_state {
   DecoderState st;
 };
+struct mmr_batch_state {
+  BatchState st;
+};
 struct mmr_rope_table {
   DeviceBuffer inv_freq;  // [d/2]: 1 / powf(theta, 2i / d); cos/sin(pos * inv_freq) on the device
   int64_t max_positions = 0;
@@ -778,6 +781,84 @@ int mmr_read_sequence(const mmr_model* model, mmr_state* state, int64_t first, i
     require(model && state && (out || count == 0), "null argument");
     const auto ids = model->lm->read_sequence(state->st, first, count);
     std::memcpy(out, ids.data(), ids.size() * sizeof(int32_t));
+  });
+}
+
+int mmr_batch_state_create(const mmr_model* model, int64_t batch, int64_t capacity, int kv_dtype,
+                           mmr_batch_state** out) {
+  return guarded([&] {
+    require(model && out, "null argument");
+    require(kv_dtype == MMR_KV_F16 || kv_dtype == MMR_KV_F32, "unknown kv dtype");
+    auto s = std::make_unique<mmr_batch_state>();
+    s->st = model->lm->make_batch_state(batch, capacity,
+                                        kv_dtype == MMR_KV_F16 ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32);
+    *out = s.release();
+  });
+}
+
+int mmr_batch_state_free(mmr_batch_state* state) {
+  return guarded([&] { delete state; });
+}
+
+int mmr_batch_state_info(const mmr_batch_state* state, int64_t* batch, int64_t* capacity, int64_t* steps) {
+  return guarded([&] {
+    require(state, "null argument");
+    if (batch) *batch = state->st.batch();
+    if (capacity) *capacity = state->st.capacity();
+    if (steps) *steps = state->st.steps;
+  });
+}
+
+int mmr_batch_state_stream(const mmr_batch_state* state, mmr_stream_t* stream) {
+  return guarded([&] {
+    require(state && stream, "null argument");
+    *stream = state->st.stream();
+  });
+}
+
+int mmr_batch_prefill(const mmr_model* model, mmr_batch_state* state, const int32_t* tokens, const int64_t* lengths,
+                      int64_t batch) {
+  return guarded([&] {
+    require(model && state && tokens && lengths, "null argument");
+    std::vector<std::vector<int32_t>> prompts(static_cast<size_t>(std::max<int64_t>(batch, 0)));
+    int64_t off = 0;
+    for (int64_t b = 0; b < batch; ++b) {
+      require(lengths[b] >= 0, "negative prompt length");
+      prompts[b].assign(tokens + off, tokens + off + lengths[b]);
+      off += lengths[b];
+    }
+    model->lm->enqueue_batch_prefill(state->st, prompts);
+  });
+}
+
+int mmr_batch_decode(const mmr_model* model, mmr_batch_state* state, int64_t steps) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->enqueue_batch_decode(state->st, steps);
+  });
+}
+
+int mmr_batch_synchronize(const mmr_model* model, mmr_batch_state* state) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->synchronize(state->st);
+  });
+}
+
+int mmr_batch_read_sequence(const mmr_model* model, mmr_batch_state* state, int64_t index, int64_t first,
+                            int64_t count, int32_t* out) {
+  return guarded([&] {
+    require(model && state && (out || count == 0), "null argument");
+    const auto ids = model->lm->read_batch_sequence(state->st, index, first, count);
+    std::memcpy(out, ids.data(), ids.size() * sizeof(int32_t));
+  });
+}
+
+int mmr_batch_read_logits(const mmr_model* model, mmr_batch_state* state, int64_t index, float* logits) {
+  return guarded([&] {
+    require(model && state && logits, "null argument");
+    const auto v = model->lm->read_batch_logits(state->st, index);
+    std::memcpy(logits, v.data(), v.size() * sizeof(float));
   });
 }
 

@@ -90,7 +90,25 @@ constexpr int attn_pv_groups() {
   return g;
 }
 
-template <typename KV, int D, int MODE>
+// Element offset of token t's K (or V) row for KV head g: the contiguous
+// cache is [Hkv][rows][D]; the paged cache is [page][Hkv][kKvPage][D] with
+// this sequence's page table mapping t / kKvPage to a page.  A tile never
+// crosses a page (tiles are <= kKvPage tokens and aligned).
+template <int D, bool PAGED>
+struct KvRows {
+  const int32_t* pages = nullptr;
+  int64_t head_base = 0;
+  int hkv = 0, g = 0;
+  __device__ __forceinline__ int64_t row(int t) const {
+    if constexpr (PAGED) {
+      return ((static_cast<int64_t>(pages[t / kKvPage]) * hkv + g) * kKvPage + t % kKvPage) * D;
+    } else {
+      return head_base + static_cast<int64_t>(t) * D;
+    }
+  }
+};
+
+template <typename KV, int D, int MODE, bool PAGED>
 __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs a) {
   constexpr int TT = attn_tile_tokens<D>();
   constexpr int LD = D + 4;  // padded row: conflict-free 16-byte LDS reads
@@ -111,24 +129,32 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
+  const int b = blockIdx.z;  // sequence of a batch (0 for a single sequence)
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int R = a.hq / a.hkv;
   const int S = a.splits;
-  const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.rows * D;
-  const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
+  const KV* kbase = reinterpret_cast<const KV*>(a.kcache);
+  const KV* vbase = reinterpret_cast<const KV*>(a.vcache);
+  KvRows<D, PAGED> kv_rows;
+  kv_rows.pages = a.page_table + static_cast<int64_t>(b) * a.pages_per_seq;
+  kv_rows.head_base = static_cast<int64_t>(g) * a.rows * D;
+  kv_rows.hkv = a.hkv;
+  kv_rows.g = g;
+  float* part = a.part + static_cast<int64_t>(b) * a.part_stride;
+  const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
 
   // ---- 1. independent loads, issued before the position is known ----
   int p = -1;
-  if constexpr (MODE == kAttnFused) p = *a.pos;
+  if constexpr (MODE == kAttnFused) p = a.pos[b];
   uint4 kc[kPerThread], vc[kPerThread];
   const int t_spec = split * TT;
   const bool spec = t_spec + TT <= a.rows;
-  const int t_load = spec ? t_spec : 0;  // always in range; unused unless spec
+  const int64_t t_load = kv_rows.row(spec ? t_spec : 0);  // always in range; unused unless spec
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
     const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
-    const int64_t off = static_cast<int64_t>(t_load) * D + c * CH;
+    const int64_t off = t_load + c * CH;
     kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
     vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
   }
@@ -141,14 +167,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int h = min(wave + j * kAttnWaves, R - 1);
-    const float* src = (MODE == kAttnFused ? a.qkv : a.q) + (g * R + h) * D;
+    const float* src = (MODE == kAttnFused ? qkv_row : a.q) + (g * R + h) * D;
     qx0[j] = src[d0];
     qx1[j] = src[d1];
   }
   float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
   float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
   if constexpr (MODE == kAttnFused) {
-    const float* kraw = a.qkv + a.hq * D + g * D;
+    const float* kraw = qkv_row + a.hq * D + g * D;
     const float* vraw = kraw + a.hkv * D;
     kx0 = kraw[d0];
     vx0 = vraw[d0];
@@ -174,7 +200,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   int n_keys;
   if constexpr (MODE == kAttnFused) {
     const bool ok = p >= 0 && p < a.capacity;
-    if (!ok && threadIdx.x == 0 && split == 0 && g == 0) *a.err = 1;
+    if (!ok && threadIdx.x == 0 && split == 0 && g == 0) *a.err = 1;  // vector store, once per sequence
     n_keys = ok ? p + 1 : 0;
   } else {
     n_keys = a.tokens < a.capacity ? a.tokens : a.capacity;
@@ -230,8 +256,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
       if (owns_new && wave == kAttnWaves - 1) {
         // Round to the cache dtype once, so this step and later steps see the
         // same key/value.
-        KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(g) * a.rows + p) * D;
-        KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(g) * a.rows + p) * D;
+        KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
+        KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
         for (int i = lane; i < D; i += kWave) {
           const KV kq = from_float<KV>(knew_s[i]);
           const KV vq = from_float<KV>(vnew_s[i]);
@@ -252,11 +278,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
       if (!(tile == split && spec)) {
         // Later tiles (or an unaligned capacity): fetch the tile into the same
         // registers, all loads issued before any is consumed.
+        const int64_t tile_base = kv_rows.row(t0);
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
           const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
           const int r = min((c * CH) / D, rows - 1);
-          const int64_t off = static_cast<int64_t>(t0 + r) * D + (c * CH) % D;
+          const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
           kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
           vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
         }
@@ -374,14 +401,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   for (int j = 0; j < 2; ++j) {
     const int h = wave + j * kAttnWaves;
     if (h < R && lane == 0) {
-      float* dst = a.part + attn_ml_offset(g, split, h, S, R, D, a.hkv);
+      float* dst = part + attn_ml_offset(g, split, h, S, R, D, a.hkv);
       dst[0] = m_run[j];
       dst[1] = l_run[j];
     }
   }
   __syncthreads();
   // The R heads' o rows of this (group, split) are contiguous: coalesced.
-  float* obase = a.part + attn_o_offset(g, split, 0, S, R, D);
+  float* obase = part + attn_o_offset(g, split, 0, S, R, D);
   for (int idx = threadIdx.x; idx < R * D; idx += kAttnThreads) {
     const int h = idx / D, dim = idx - (idx / D) * D;
     float o = 0.0f;
@@ -396,8 +423,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
 // O-projection prologue (kProAttnCombine) performs the same operations in the
 // same order, so both paths give identical bits.
 __global__ __launch_bounds__(128) void attention_combine_kernel(const float* part, int hq, int hkv, int d, int splits,
-                                                                 float* out) {
+                                                                 int64_t part_stride, float* out) {
   const int qh = blockIdx.x;
+  part += static_cast<int64_t>(blockIdx.y) * part_stride;  // sequence of a batch
+  out += static_cast<int64_t>(blockIdx.y) * hq * d;
   const int R = hq / hkv;
   const int g = qh / R, h = qh % R;
   float M = -INFINITY;
@@ -447,11 +476,14 @@ __global__ __launch_bounds__(kWave) void qkv_postprocess_kernel(QkvPostArgs a) {
 
 template <typename KV, int D>
 hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
-  const dim3 grid(a.splits, a.hkv), block(kAttnThreads);
-  if (mode == kAttnFused) {
-    attention_split_kernel<KV, D, kAttnFused><<<grid, block, 0, s>>>(a);
+  const dim3 grid(a.splits, a.hkv, a.batch), block(kAttnThreads);
+  if (a.page_table) {
+    if (mode != kAttnFused) return hipErrorInvalidValue;
+    attention_split_kernel<KV, D, kAttnFused, true><<<grid, block, 0, s>>>(a);
+  } else if (mode == kAttnFused) {
+    attention_split_kernel<KV, D, kAttnFused, false><<<grid, block, 0, s>>>(a);
   } else {
-    attention_split_kernel<KV, D, kAttnFromCache><<<grid, block, 0, s>>>(a);
+    attention_split_kernel<KV, D, kAttnFromCache, false><<<grid, block, 0, s>>>(a);
   }
   return hipGetLastError();
 }
@@ -501,14 +533,17 @@ size_t attention_partial_floats(int hq, int hkv, int d, int splits) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream) {
-  if (!attention_supported(a.hq, a.hkv, a.d) || a.splits <= 0) return hipErrorInvalidValue;
+  if (!attention_supported(a.hq, a.hkv, a.d) || a.splits <= 0 || a.batch <= 0) return hipErrorInvalidValue;
+  if (a.batch > 1 && (a.part_stride < static_cast<int64_t>(attention_partial_floats(a.hq, a.hkv, a.d, a.splits)) ||
+                      (mode == kAttnFused && a.qkv_stride <= 0)))
+    return hipErrorInvalidValue;
   return kv == kKvF16 ? launch_attn_kv<__half>(a, mode, stream) : launch_attn_kv<float>(a, mode, stream);
 }
 
 hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
-                                    hipStream_t stream) {
-  if (!attention_supported(hq, hkv, d) || splits <= 0) return hipErrorInvalidValue;
-  attention_combine_kernel<<<hq, 128, 0, stream>>>(part, hq, hkv, d, splits, out);
+                                    hipStream_t stream, int batch, int64_t part_stride) {
+  if (!attention_supported(hq, hkv, d) || splits <= 0 || batch <= 0) return hipErrorInvalidValue;
+  attention_combine_kernel<<<dim3(hq, batch), 128, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
   return hipGetLastError();
 }
 

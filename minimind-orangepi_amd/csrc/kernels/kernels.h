@@ -122,7 +122,18 @@ struct AttnArgs {
   int splits = 1;
   float* part = nullptr;            // o [Hkv][splits][R][D], then (m, l) [Hkv][splits][R][2]
   int32_t* err = nullptr;           // set to 1 when *pos is out of range
+  // Batch of sequences (grid z): sequence b reads qkv + b * qkv_stride and
+  // pos[b], writes part + b * part_stride.
+  int batch = 1;
+  int64_t qkv_stride = 0;
+  int64_t part_stride = 0;
+  // Paged cache (fused mode): kcache / vcache are page pools
+  // [page][Hkv][kKvPage][D]; page_table[b * pages_per_seq + t / kKvPage] is
+  // the page of sequence b's token t; rows = pages_per_seq * kKvPage.
+  const int32_t* page_table = nullptr;
+  int pages_per_seq = 0;
 };
+constexpr int kKvPage = 64;  // tokens per KV page (a multiple of every attention tile)
 
 constexpr int kAttnMaxGroup = 8;  // Hq / Hkv supported
 size_t attention_partial_floats(int hq, int hkv, int d, int splits);
@@ -132,7 +143,7 @@ bool attention_supported(int hq, int hkv, int d);
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream);
 // Merge the split partials into out [Hq*D] (one block per query head).
 hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
-                                    hipStream_t stream);
+                                    hipStream_t stream, int batch = 1, int64_t part_stride = 0);
 
 // qkv post-process as a standalone op (reference K2): per-head q/k RMSNorm +
 // RoPE at `position`, q -> query_out, k/v appended at cache index `index`.
@@ -208,9 +219,23 @@ struct PrefillAttnArgs {
 };
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, KvDtype kv, hipStream_t stream);
 
+// --------------------------------------------------------------- batch ----
+// Decode of a batch of independent sequences, sequence b at its own device
+// position pos[b] with its tokens in seq[b * seq_stride ..].
+// h[b][:] = embed[seq[b][pos[b]]] (fp16 -> fp32); out-of-range ids are clamped
+// (the host validates every id it uploads).
+hipError_t launch_batch_embed(const __half* embed, const int32_t* seq, int seq_stride, const int32_t* pos, int batch,
+                              int vocab, int hidden, float* h, hipStream_t stream);
+// Per sequence: first index of the maximum of logits[b][:vocab]; token_out[b]
+// receives it, and the step bookkeeping of launch_argmax_finalize runs per
+// sequence (seq[b][p + 1] when p + 1 >= prompt_len[b], then pos[b] = p + 1).
+hipError_t launch_batch_argmax(const float* logits, int vocab, int batch, int32_t* token_out, int32_t* seq,
+                               int seq_stride, int32_t* pos, const int32_t* prompt_len, int seq_len,
+                               hipStream_t stream);
+
 // ------------------------------------------------------------- support ----
 hipError_t launch_rms_norm_rows(const float* in, const float* w, float eps, int rows, int cols, float* out,
-                                hipStream_t stream);
+                                hipStream_t stream, bool final_norm = false);
 hipError_t launch_add(const float* a, const float* b, int64_t n, float* out, hipStream_t stream);
 hipError_t launch_swiglu_rows(const float* gate_up, int rows, int cols, float* out, hipStream_t stream);
 hipError_t launch_embedding_gather(const __half* table, const int32_t* ids, int tokens, int vocab, int hidden,

@@ -17,7 +17,9 @@ namespace {
 
 constexpr int kRowThreads = 256;
 
-// One block per row.  x * (scale * w) as decoder_layer.cpp:32-42.
+// One block per row.  x * (scale * w) as decoder_layer.cpp:32-42, or with
+// kFinal the final norm's (x * scale) * w (language_model.cpp:24-38).
+template <bool kFinal>
 __global__ __launch_bounds__(kRowThreads) void rms_norm_rows_kernel(const float* in, const float* w, float eps,
                                                                     int cols, float* out) {
   __shared__ float partial[kRowThreads / kWave];
@@ -32,7 +34,7 @@ __global__ __launch_bounds__(kRowThreads) void rms_norm_rows_kernel(const float*
 #pragma unroll
   for (int i = 0; i < kRowThreads / kWave; ++i) total += partial[i];
   const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
-  for (int i = threadIdx.x; i < cols; i += kRowThreads) y[i] = x[i] * (scale * w[i]);
+  for (int i = threadIdx.x; i < cols; i += kRowThreads) y[i] = kFinal ? (x[i] * scale) * w[i] : x[i] * (scale * w[i]);
 }
 
 __global__ void add_kernel(const float* a, const float* b, int64_t n, float* out) {
@@ -66,9 +68,13 @@ __global__ void embedding_gather_kernel(const __half* table, const int32_t* ids,
 }  // namespace
 
 hipError_t launch_rms_norm_rows(const float* in, const float* w, float eps, int rows, int cols, float* out,
-                                hipStream_t stream) {
+                                hipStream_t stream, bool final_norm) {
   if (rows <= 0 || cols <= 0) return hipSuccess;
-  rms_norm_rows_kernel<<<rows, kRowThreads, 0, stream>>>(in, w, eps, cols, out);
+  if (final_norm) {
+    rms_norm_rows_kernel<true><<<rows, kRowThreads, 0, stream>>>(in, w, eps, cols, out);
+  } else {
+    rms_norm_rows_kernel<false><<<rows, kRowThreads, 0, stream>>>(in, w, eps, cols, out);
+  }
   return hipGetLastError();
 }
 

@@ -1,0 +1,343 @@
+// batch.cpp -- batched decode: B independent sequences advance one token per
+// step, each at its own position, over a paged KV cache.
+//
+// The reference runtime decodes one sequence per DecoderState
+// (language_model.h:22-25); each sequence of a batch computes exactly what
+// LanguageModel::forward_next_token computes for it alone
+// (language_model.cpp:310-333, decoder_layer.cpp:312-407), with the batch's
+// projections as GEMMs of B rows on the fp32 matrix cores.  Step kernels:
+//   embed rows of seq[b][pos[b]]
+//   per layer: RMSNorm rows -> QKV GEMM -> paged split attention (q/k norm,
+//              RoPE at pos[b], K/V append) -> combine -> O GEMM (+residual)
+//              -> RMSNorm rows -> gate_up GEMM -> SwiGLU rows -> down GEMM
+//              (+residual)
+//   final RMSNorm rows -> lm_head GEMM -> per-sequence argmax + bookkeeping
+// captured once per attention split count into a hipGraph.
+//
+// KV cache: per layer a pool of 64-token pages [page][Hkv][64][d]; sequence
+// b's token t lives in page page_table[b][t / 64].  Pages are assigned at
+// creation, interleaved across sequences (page p of sequence b is physical
+// page p * B + b), so the attention reads every tile through the table.
+#include "language_model.h"
+
+#include "device.h"
+#include "device_model.h"
+#include "../kernels/kernels.h"
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <stdexcept>
+
+namespace minimind::model {
+
+struct BatchDeviceState {
+  std::shared_ptr<const DeviceModel> model;
+  mmr::KvDtype kv = mmr::kKvF16;
+  int64_t batch = 0;
+  int64_t capacity = 0;       // positions per sequence
+  int64_t pages_per_seq = 0;
+  Arena arena;
+  std::vector<void*> kpool, vpool;  // per layer [pages][Hkv][kKvPage][d]
+  int32_t* page_table = nullptr;    // [batch][pages_per_seq]
+  int32_t* seq = nullptr;           // [batch][capacity + 1]
+  int32_t* pos = nullptr;           // [batch]
+  int32_t* prompt_len = nullptr;    // [batch]
+  int32_t* token_out = nullptr;     // [batch]
+  int32_t* err = nullptr;
+  float* h = nullptr;       // [batch][H]
+  float* x = nullptr;       // [batch][H]
+  float* qkv = nullptr;     // [batch][(Hq + 2 Hkv) d]
+  float* attn = nullptr;    // [batch][Hq d]
+  float* gu = nullptr;      // [batch][2F]
+  float* act = nullptr;     // [batch][F]
+  float* logits = nullptr;  // [batch][V]
+  float* part = nullptr;    // attention partials, part_stride floats per sequence
+  int64_t part_stride = 0;
+  int32_t* staging = nullptr;  // pinned host
+  int64_t staging_len = 0;
+  hipStream_t stream = nullptr;
+  std::map<int, hipGraphExec_t> graphs;
+  bool use_graphs = true;
+
+  ~BatchDeviceState() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& g : graphs) (void)hipGraphExecDestroy(g.second);
+    if (stream) (void)hipStreamDestroy(stream);
+    if (staging) (void)hipHostFree(staging);
+  }
+};
+
+BatchState::BatchState() = default;
+BatchState::~BatchState() = default;
+BatchState::BatchState(BatchState&&) noexcept = default;
+BatchState& BatchState::operator=(BatchState&&) noexcept = default;
+int64_t BatchState::batch() const { return device ? device->batch : 0; }
+int64_t BatchState::capacity() const { return device ? device->capacity : 0; }
+void* BatchState::stream() const { return device ? static_cast<void*>(device->stream) : nullptr; }
+
+namespace {
+
+// Attention splits per sequence: about four 64-token tiles per block, capped.
+constexpr int kBatchMaxSplits = 64;
+
+int batch_splits(int64_t n_keys, int tile) {
+  const int64_t tiles = (n_keys + tile - 1) / tile;
+  int s = 1;
+  while (s < kBatchMaxSplits && s * 4 < tiles) s *= 2;
+  return s;
+}
+
+void gemm_rows(const BatchDeviceState& s, const float* a, int lda, const __half* w, int n, int k, float* out,
+               bool residual) {
+  mmr::GemmArgs g;
+  g.a = a;
+  g.lda = lda;
+  g.w = w;
+  g.residual = residual ? out : nullptr;
+  g.c = out;
+  g.ldc = n;
+  g.m = static_cast<int>(s.batch);
+  g.n = n;
+  g.k = k;
+  check_hip(mmr::launch_gemm(g, s.stream), "batch gemm");
+}
+
+void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
+  const DeviceModel& m = *s.model;
+  const auto& c = m.cfg;
+  const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
+  const int Hq = static_cast<int>(c.num_attention_heads), Hkv = static_cast<int>(c.num_key_value_heads);
+  const int F = static_cast<int>(c.intermediate_size), V = static_cast<int>(c.vocab_size);
+  const int qkv_w = (Hq + 2 * Hkv) * D;
+  const int B = static_cast<int>(s.batch);
+  const int seq_stride = static_cast<int>(s.capacity + 1);
+  check_hip(mmr::launch_batch_embed(m.embed, s.seq, seq_stride, s.pos, B, V, H, s.h, s.stream), "batch embed");
+  for (size_t l = 0; l < m.layers.size(); ++l) {
+    const LayerDev& L = m.layers[l];
+    check_hip(mmr::launch_rms_norm_rows(s.h, L.input_norm, c.rms_norm_eps, B, H, s.x, s.stream), "batch norm");
+    gemm_rows(s, s.x, H, L.qkv, qkv_w, H, s.qkv, false);
+    mmr::AttnArgs t;
+    t.qkv = s.qkv;
+    t.qkv_stride = qkv_w;
+    t.q_norm = L.q_norm;
+    t.k_norm = L.k_norm;
+    t.eps = c.rms_norm_eps;
+    t.inv_freq = m.inv_freq;
+    t.pos = s.pos;
+    t.kcache = s.kpool[l];
+    t.vcache = s.vpool[l];
+    t.capacity = static_cast<int>(s.capacity);
+    t.rows = static_cast<int>(s.pages_per_seq * mmr::kKvPage);
+    t.hq = Hq;
+    t.hkv = Hkv;
+    t.d = D;
+    t.splits = splits;
+    t.part = s.part;
+    t.part_stride = s.part_stride;
+    t.err = s.err;
+    t.batch = B;
+    t.page_table = s.page_table;
+    t.pages_per_seq = static_cast<int>(s.pages_per_seq);
+    check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "batch attention");
+    check_hip(mmr::launch_attention_combine(s.part, Hq, Hkv, D, splits, s.attn, s.stream, B, s.part_stride),
+              "batch attention combine");
+    gemm_rows(s, s.attn, Hq * D, L.o, H, Hq * D, s.h, true);
+    check_hip(mmr::launch_rms_norm_rows(s.h, L.post_norm, c.rms_norm_eps, B, H, s.x, s.stream), "batch post norm");
+    gemm_rows(s, s.x, H, L.gate_up, 2 * F, H, s.gu, false);
+    check_hip(mmr::launch_swiglu_pairs(s.gu, static_cast<int64_t>(B) * F, s.act, s.stream), "batch swiglu");
+    gemm_rows(s, s.act, F, L.down, H, F, s.h, true);
+  }
+  check_hip(mmr::launch_rms_norm_rows(s.h, m.final_norm, c.rms_norm_eps, B, H, s.x, s.stream, true),
+            "batch final norm");
+  gemm_rows(s, s.x, H, m.lm_head, V, H, s.logits, false);
+  check_hip(mmr::launch_batch_argmax(s.logits, V, B, s.token_out, s.seq, seq_stride, s.pos, s.prompt_len,
+                                     seq_stride, s.stream),
+            "batch argmax");
+}
+
+hipGraphExec_t capture_batch_step(BatchDeviceState& s, int splits) {
+  hipGraph_t graph = nullptr;
+  check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    enqueue_batch_step_kernels(s, splits);
+  } catch (...) {
+    (void)hipStreamEndCapture(s.stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+    throw;
+  }
+  check_hip(hipStreamEndCapture(s.stream, &graph), "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  check_hip(st, "hipGraphInstantiate");
+  return exec;
+}
+
+}  // namespace
+
+BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCacheDtype kv) const {
+  const auto& c = config_;
+  const DeviceModel& m = *device_;
+  if (batch < 1 || batch > 1024) throw std::invalid_argument("batch must be in [1, 1024]");
+  if (capacity < 1 || capacity > c.max_position_embeddings)
+    throw std::invalid_argument("batch capacity must be in [1, max_position_embeddings]");
+  if (!m.gemm_prefill) throw std::invalid_argument("batched decode needs every projection's K to be a multiple of 8");
+  auto s = std::make_unique<BatchDeviceState>();
+  s->model = device_;
+  s->kv = kv == KvCacheDtype::kFloat16 ? mmr::kKvF16 : mmr::kKvF32;
+  s->batch = batch;
+  s->capacity = capacity;
+  s->pages_per_seq = (capacity + mmr::kKvPage - 1) / mmr::kKvPage;
+  const char* nog = std::getenv("MMR_NO_GRAPH");
+  s->use_graphs = !(nog && nog[0] == '1');
+  const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
+  const int64_t F = c.intermediate_size, V = c.vocab_size;
+  const int64_t pages = batch * s->pages_per_seq;
+  const std::size_t elem = s->kv == mmr::kKvF16 ? 2 : 4;
+  const std::size_t pool_bytes = static_cast<std::size_t>(pages * Hkv * mmr::kKvPage * D) * elem;
+  s->part_stride = static_cast<int64_t>(
+      mmr::attention_partial_floats(static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(D), kBatchMaxSplits));
+  Arena& ar = s->arena;
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+    ar.plan(pool_bytes);
+    ar.plan(pool_bytes);
+  }
+  ar.plan(pages * 4);
+  ar.plan(batch * (capacity + 1) * 4);
+  ar.plan(batch * 4 * 3 + 4);
+  ar.plan(batch * H * 4 * 2);
+  ar.plan(batch * (Hq + 2 * Hkv) * D * 4);
+  ar.plan(batch * Hq * D * 4);
+  ar.plan(batch * 2 * F * 4);
+  ar.plan(batch * F * 4);
+  ar.plan(batch * V * 4);
+  ar.plan(batch * s->part_stride * 4);
+  ar.allocate();
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+    s->kpool.push_back(ar.take<char>(pool_bytes));
+    s->vpool.push_back(ar.take<char>(pool_bytes));
+  }
+  s->page_table = ar.take<int32_t>(pages);
+  s->seq = ar.take<int32_t>(batch * (capacity + 1));
+  int32_t* scalars = ar.take<int32_t>(batch * 3 + 1);
+  s->pos = scalars;
+  s->prompt_len = scalars + batch;
+  s->token_out = scalars + 2 * batch;
+  s->err = scalars + 3 * batch;
+  float* hx = ar.take<float>(batch * H * 2);
+  s->h = hx;
+  s->x = hx + batch * H;
+  s->qkv = ar.take<float>(batch * (Hq + 2 * Hkv) * D);
+  s->attn = ar.take<float>(batch * Hq * D);
+  s->gu = ar.take<float>(batch * 2 * F);
+  s->act = ar.take<float>(batch * F);
+  s->logits = ar.take<float>(batch * V);
+  s->part = ar.take<float>(batch * s->part_stride);
+  s->staging_len = std::max<int64_t>(pages, batch * (capacity + 1)) + 4 * batch + 8;
+  check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), s->staging_len * sizeof(int32_t),
+                          hipHostMallocDefault),
+            "hipHostMalloc staging");
+  check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+  // Page p of sequence b is physical page p * batch + b.
+  for (int64_t b = 0; b < batch; ++b)
+    for (int64_t p = 0; p < s->pages_per_seq; ++p)
+      s->staging[b * s->pages_per_seq + p] = static_cast<int32_t>(p * batch + b);
+  check_hip(hipMemcpyAsync(s->page_table, s->staging, pages * sizeof(int32_t), hipMemcpyHostToDevice, s->stream),
+            "hipMemcpyAsync page table");
+  check_hip(hipMemsetAsync(scalars, 0, (batch * 3 + 1) * sizeof(int32_t), s->stream), "hipMemsetAsync");
+  check_hip(hipMemsetAsync(s->seq, 0, batch * (capacity + 1) * sizeof(int32_t), s->stream), "hipMemsetAsync");
+  check_hip(hipStreamSynchronize(s->stream), "batch state init");
+  BatchState state;
+  state.device = std::move(s);
+  return state;
+}
+
+void LanguageModel::launch_batch_step(BatchState& state) const {
+  BatchDeviceState& s = *state.device;
+  if (state.steps >= s.capacity) throw std::length_error("KV cache capacity exhausted");
+  const int splits = batch_splits(state.steps + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  if (s.use_graphs) {
+    auto it = s.graphs.find(splits);
+    if (it == s.graphs.end()) it = s.graphs.emplace(splits, capture_batch_step(s, splits)).first;
+    check_hip(hipGraphLaunch(it->second, s.stream), "hipGraphLaunch");
+  } else {
+    enqueue_batch_step_kernels(s, splits);
+  }
+  state.steps += 1;
+}
+
+void LanguageModel::enqueue_batch_prefill(BatchState& state, const std::vector<std::vector<int32_t>>& prompts) const {
+  BatchDeviceState& s = *state.device;
+  if (static_cast<int64_t>(prompts.size()) != s.batch) throw std::invalid_argument("one prompt per sequence");
+  if (state.steps != 0) throw std::invalid_argument("batch prefill requires empty KV caches");
+  int64_t longest = 0;
+  for (const auto& p : prompts) {
+    if (p.empty()) throw std::invalid_argument("prompt_tokens cannot be empty");
+    for (int32_t t : p)
+      if (t < 0 || t >= config_.vocab_size) throw std::out_of_range("token id out of vocabulary range");
+    longest = std::max<int64_t>(longest, static_cast<int64_t>(p.size()));
+  }
+  if (longest > s.capacity) throw std::length_error("KV cache capacity exhausted");
+  check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+  const int64_t stride = s.capacity + 1;
+  std::memset(s.staging, 0, static_cast<std::size_t>(s.batch * stride) * sizeof(int32_t));
+  int32_t* lens = s.staging + s.batch * stride;
+  for (int64_t b = 0; b < s.batch; ++b) {
+    std::memcpy(s.staging + b * stride, prompts[b].data(), prompts[b].size() * sizeof(int32_t));
+    lens[b] = static_cast<int32_t>(prompts[b].size());
+  }
+  check_hip(hipMemcpyAsync(s.seq, s.staging, s.batch * stride * sizeof(int32_t), hipMemcpyHostToDevice, s.stream),
+            "hipMemcpyAsync prompts");
+  check_hip(hipMemcpyAsync(s.prompt_len, lens, s.batch * sizeof(int32_t), hipMemcpyHostToDevice, s.stream),
+            "hipMemcpyAsync prompt lengths");
+  check_hip(hipMemsetAsync(s.pos, 0, s.batch * sizeof(int32_t), s.stream), "hipMemsetAsync pos");
+  for (int64_t i = 0; i < longest; ++i) launch_batch_step(state);
+}
+
+void LanguageModel::enqueue_batch_decode(BatchState& state, int64_t n) const {
+  BatchDeviceState& s = *state.device;
+  if (n < 0) throw std::invalid_argument("step count cannot be negative");
+  if (state.steps == 0) throw std::invalid_argument("batch decode needs prompts (enqueue_batch_prefill)");
+  if (state.steps + n > s.capacity) throw std::length_error("KV cache capacity exhausted");
+  for (int64_t i = 0; i < n; ++i) launch_batch_step(state);
+}
+
+void LanguageModel::synchronize(BatchState& state) const {
+  BatchDeviceState& s = *state.device;
+  int32_t* flag = s.staging + s.staging_len - 1;
+  check_hip(hipMemcpyAsync(flag, s.err, sizeof(int32_t), hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync err");
+  check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+  if (*flag != 0) throw std::runtime_error("device kernel reported an out-of-range position");
+}
+
+std::vector<int32_t> LanguageModel::read_batch_sequence(BatchState& state, int64_t index, int64_t first,
+                                                        int64_t count) const {
+  BatchDeviceState& s = *state.device;
+  if (index < 0 || index >= s.batch) throw std::out_of_range("sequence index");
+  if (first < 0 || count < 0 || first + count > s.capacity + 1) throw std::out_of_range("sequence range");
+  std::vector<int32_t> out(static_cast<size_t>(count));
+  if (count == 0) return out;
+  synchronize(state);
+  check_hip(hipMemcpyAsync(s.staging, s.seq + index * (s.capacity + 1) + first, count * sizeof(int32_t),
+                           hipMemcpyDeviceToHost, s.stream),
+            "hipMemcpyAsync seq");
+  synchronize(state);
+  std::memcpy(out.data(), s.staging, count * sizeof(int32_t));
+  return out;
+}
+
+std::vector<float> LanguageModel::read_batch_logits(BatchState& state, int64_t index) const {
+  BatchDeviceState& s = *state.device;
+  if (index < 0 || index >= s.batch) throw std::out_of_range("sequence index");
+  std::vector<float> out(static_cast<size_t>(config_.vocab_size));
+  synchronize(state);
+  check_hip(hipMemcpyAsync(out.data(), s.logits + index * config_.vocab_size, out.size() * sizeof(float),
+                           hipMemcpyDeviceToHost, s.stream),
+            "hipMemcpyAsync logits");
+  synchronize(state);
+  return out;
+}
+
+}  // namespace minimind::model

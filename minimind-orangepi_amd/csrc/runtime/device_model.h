@@ -1,0 +1,37 @@
+// device_model.h -- device copy of the model weights (internal to the runtime).
+#pragma once
+
+#include "config.h"
+#include "device.h"
+#include "../kernels/kernels.h"
+
+#include <cstddef>
+#include <vector>
+
+namespace minimind::model {
+
+struct LayerDev {
+  const float* input_norm = nullptr;
+  const float* post_norm = nullptr;
+  const float* q_norm = nullptr;
+  const float* k_norm = nullptr;
+  const __half* qkv = nullptr;      // [(Hq + 2 Hkv) d][H]  rows q | k | v
+  const __half* o = nullptr;        // [H][Hq d]
+  const __half* gate_up = nullptr;  // [2F][H]  rows gate_0, up_0, gate_1, up_1, ...
+  const __half* down = nullptr;     // [H][F]
+};
+
+struct DeviceModel {
+  MiniMindConfig cfg;
+  Arena arena;
+  const __half* embed = nullptr;    // [V][H]
+  const __half* lm_head = nullptr;  // [V][H] (aliases embed when identical)
+  const float* final_norm = nullptr;
+  std::vector<LayerDev> layers;
+  const float* inv_freq = nullptr;  // [d/2] RoPE frequencies, formula of decoder_layer.cpp:114
+  mmr::GemvPlan plan_qkv, plan_o, plan_gu, plan_down, plan_lm;
+  bool gemm_prefill = false;  // every projection's K suits the prefill GEMM
+  std::size_t weight_bytes = 0;
+};
+
+}  // namespace minimind::model

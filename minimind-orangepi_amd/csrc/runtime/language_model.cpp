@@ -2,20 +2,23 @@
 // model API on top of it.
 //
 // One decode step (language_model.cpp:310-333 + decoder_layer.cpp:312-407 of
-// the reference) is 5 kernels per layer plus one for the head:
+// the reference) is 5 kernels per layer plus two for the head:
 //   qkv   GEMV  RMSNorm prologue (layer 0: embedding gather of seq[pos])
 //   attn        q/k RMSNorm + RoPE, K/V append at pos, split-context GQA
-//               attention with log-sum-exp combine
-//   o     GEMV  residual epilogue  (h += W_o attn)
+//               attention writing per-split (m, l, o) partials
+//   o     GEMV  log-sum-exp combine of the partials in the prologue,
+//               residual epilogue (h += W_o attn)
 //   gu    GEMV  RMSNorm prologue, SwiGLU epilogue over interleaved gate/up rows
 //   down  GEMV  residual epilogue  (h += W_down act)
-//   head  GEMV  final RMSNorm prologue, first-index argmax epilogue; writes
-//               seq[pos + 1] and advances pos on the device
+//   head  GEMV  final RMSNorm prologue, per-block argmax partials, then the
+//               finalize kernel writes seq[pos + 1] and advances pos
 // Every kernel reads the position from device memory, so the step is captured
 // once into a hipGraph (per attention split count) and replayed per token.
+// Prompts run through the chunked prefill kernels (enqueue_prefill).
 #include "language_model.h"
 
 #include "device.h"
+#include "device_model.h"
 #include "../kernels/kernels.h"
 
 #include <algorithm>
@@ -27,30 +30,6 @@
 #include <stdexcept>
 
 namespace minimind::model {
-
-struct LayerDev {
-  const float* input_norm = nullptr;
-  const float* post_norm = nullptr;
-  const float* q_norm = nullptr;
-  const float* k_norm = nullptr;
-  const __half* qkv = nullptr;      // [(Hq + 2 Hkv) d][H]  rows q | k | v
-  const __half* o = nullptr;        // [H][Hq d]
-  const __half* gate_up = nullptr;  // [2F][H]  rows gate_0, up_0, gate_1, up_1, ...
-  const __half* down = nullptr;     // [H][F]
-};
-
-struct DeviceModel {
-  MiniMindConfig cfg;
-  Arena arena;
-  const __half* embed = nullptr;    // [V][H]
-  const __half* lm_head = nullptr;  // [V][H] (aliases embed when identical)
-  const float* final_norm = nullptr;
-  std::vector<LayerDev> layers;
-  const float* inv_freq = nullptr;  // [d/2] RoPE frequencies, formula of decoder_layer.cpp:114
-  mmr::GemvPlan plan_qkv, plan_o, plan_gu, plan_down, plan_lm;
-  bool gemm_prefill = false;  // every projection's K suits the prefill GEMM
-  std::size_t weight_bytes = 0;
-};
 
 struct DeviceState {
   std::shared_ptr<const DeviceModel> model;

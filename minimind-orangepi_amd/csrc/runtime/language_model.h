@@ -51,6 +51,27 @@ struct DecoderState {
   std::unique_ptr<DeviceState> device;
 };
 
+struct BatchDeviceState;
+
+// A batch of independent sequences decoded in lockstep, each at its own
+// position, with a paged KV cache (64-token pages mapped through a per-sequence
+// page table).  The reference has no batched state (its DecoderState holds one
+// sequence, language_model.h:22-25); this serves BASELINE configs[4].
+struct BatchState {
+  BatchState();
+  ~BatchState();
+  BatchState(BatchState&&) noexcept;
+  BatchState& operator=(BatchState&&) noexcept;
+  BatchState(const BatchState&) = delete;
+  BatchState& operator=(const BatchState&) = delete;
+
+  int64_t steps = 0;  // batched steps run since the prompts were set (host mirror)
+  int64_t batch() const;
+  int64_t capacity() const;  // positions per sequence
+  void* stream() const;
+  std::unique_ptr<BatchDeviceState> device;
+};
+
 class LanguageModel {
  public:
   LanguageModel(MiniMindConfig config, DenseModelWeights weights);
@@ -76,8 +97,9 @@ class LanguageModel {
   // previous step produced) and appends its prediction.  `first_token`
   // (if >= 0) is written to seq[position] first.  Returns immediately.
   void enqueue_decode(DecoderState& state, int64_t n, int32_t first_token = -1) const;
-  // Upload prompt tokens and enqueue one step per token (token-by-token
-  // prefill); the last step predicts the first generated token.
+  // Upload prompt tokens and run them through the model (chunked batched
+  // prefill kernels, or one decode step per token where the GEMM shapes are
+  // unsupported); the prompt's last row predicts the first generated token.
   void enqueue_prefill(DecoderState& state, const std::vector<int32_t>& prompt_tokens) const;
   // Wait for the state's stream and raise if a kernel flagged an error.
   void synchronize(DecoderState& state) const;
@@ -93,11 +115,25 @@ class LanguageModel {
   // Reset position to 0 (the cache contents are overwritten as it refills).
   void reset_state(DecoderState& state) const;
 
+  // ---- batched decode (independent sequences in lockstep) ----
+  BatchState make_batch_state(int64_t batch, int64_t capacity, KvCacheDtype kv = KvCacheDtype::kFloat16) const;
+  // Upload one prompt per sequence (lengths may differ) into a fresh batch and
+  // run max-length batched steps: sequence b consumes its prompt, then its own
+  // predictions, so each sequence decodes exactly as it would alone.
+  void enqueue_batch_prefill(BatchState& state, const std::vector<std::vector<int32_t>>& prompts) const;
+  // `n` more batched steps: every sequence appends one greedy token per step.
+  void enqueue_batch_decode(BatchState& state, int64_t n) const;
+  void synchronize(BatchState& state) const;
+  std::vector<int32_t> read_batch_sequence(BatchState& state, int64_t index, int64_t first, int64_t count) const;
+  // Logits of sequence `index` at the last executed step.
+  std::vector<float> read_batch_logits(BatchState& state, int64_t index) const;
+
   const DeviceModel& device_model() const { return *device_; }
   std::size_t device_weight_bytes() const;
 
  private:
   void launch_step(DecoderState& state) const;
+  void launch_batch_step(BatchState& state) const;
 
   MiniMindConfig config_;
   std::shared_ptr<DeviceModel> device_;

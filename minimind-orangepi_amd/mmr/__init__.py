@@ -146,6 +146,15 @@ _SIGS = {
     "mmr_read_sequence": ([VP, VP, I64, I64, VP], C.c_int),
     "mmr_read_logits": ([VP, VP, VP], C.c_int),
     "mmr_launch_step_kernel": ([VP, VP, C.c_int, I64, I64], C.c_int),
+    "mmr_batch_state_create": ([VP, I64, I64, C.c_int, C.POINTER(VP)], C.c_int),
+    "mmr_batch_state_free": ([VP], C.c_int),
+    "mmr_batch_state_info": ([VP, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64)], C.c_int),
+    "mmr_batch_state_stream": ([VP, C.POINTER(VP)], C.c_int),
+    "mmr_batch_prefill": ([VP, VP, VP, VP, I64], C.c_int),
+    "mmr_batch_decode": ([VP, VP, I64], C.c_int),
+    "mmr_batch_synchronize": ([VP, VP], C.c_int),
+    "mmr_batch_read_sequence": ([VP, VP, I64, I64, I64, VP], C.c_int),
+    "mmr_batch_read_logits": ([VP, VP, I64, VP], C.c_int),
 }
 
 EXPORTED = sorted(_SIGS)
@@ -512,6 +521,11 @@ class Model:
         check(_lib.mmr_state_create(self.handle, capacity, kv_dtype, C.byref(h)))
         return State(self, h.value)
 
+    def make_batch_state(self, batch: int, capacity: int, kv_dtype: int = KV_F16) -> "BatchState":
+        h = VP()
+        check(_lib.mmr_batch_state_create(self.handle, batch, capacity, kv_dtype, C.byref(h)))
+        return BatchState(self, h.value)
+
     def generate(self, prompt, max_new_tokens: int) -> list[int]:
         p = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.empty(max(int(max_new_tokens), 1), np.int32)
@@ -597,6 +611,72 @@ class State:
     def free(self) -> None:
         if self.handle:
             _lib.mmr_state_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class BatchState:
+    """Batch of independent sequences decoded in lockstep over a paged KV cache."""
+
+    def __init__(self, model: Model, handle: int):
+        self.model = model
+        self.handle = handle
+
+    def _info(self):
+        b, c, s = C.c_int64(0), C.c_int64(0), C.c_int64(0)
+        check(_lib.mmr_batch_state_info(self.handle, C.byref(b), C.byref(c), C.byref(s)))
+        return int(b.value), int(c.value), int(s.value)
+
+    @property
+    def batch(self) -> int:
+        return self._info()[0]
+
+    @property
+    def capacity(self) -> int:
+        return self._info()[1]
+
+    @property
+    def steps(self) -> int:
+        return self._info()[2]
+
+    @property
+    def stream(self) -> int:
+        s = VP()
+        check(_lib.mmr_batch_state_stream(self.handle, C.byref(s)))
+        return s.value
+
+    def prefill(self, prompts) -> None:
+        lengths = np.array([len(p) for p in prompts], np.int64)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p in prompts])
+                                    if len(prompts) else np.zeros(0, np.int32), dtype=np.int32)
+        check(_lib.mmr_batch_prefill(self.model.handle, self.handle, _ptr(flat) if flat.size else None,
+                                     _ptr(lengths) if lengths.size else None, len(prompts)))
+
+    def decode(self, steps: int) -> None:
+        check(_lib.mmr_batch_decode(self.model.handle, self.handle, steps))
+
+    def synchronize(self) -> None:
+        check(_lib.mmr_batch_synchronize(self.model.handle, self.handle))
+
+    def read_sequence(self, index: int, first: int, count: int) -> np.ndarray:
+        out = np.empty(count, np.int32)
+        check(_lib.mmr_batch_read_sequence(self.model.handle, self.handle, index, first, count,
+                                           _ptr(out) if count else None))
+        return out
+
+    def read_logits(self, index: int) -> np.ndarray:
+        out = np.empty(self.model.config.vocab_size, np.float32)
+        check(_lib.mmr_batch_read_logits(self.model.handle, self.handle, index, _ptr(out)))
+        return out
+
+    def free(self) -> None:
+        if self.handle:
+            _lib.mmr_batch_state_free(self.handle)
             self.handle = None
 
     def __del__(self):
