@@ -2,7 +2,8 @@
 """Decode throughput of the MiniMind2 gfx950 runtime.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f32|f16] [--no-cpu-baseline]
-                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--traffic-probe N]
+                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--batch 32]
+                    [--batch-context 4096] [--traffic-probe N]
 
 Workload: MiniMind2 dense (hidden 768, 16 layers, 8/2 heads, d 96, FFN 2048,
 vocab 6400), fp16 weights drawn N(0, 0.02) from seed 0, a 512-token uniform
@@ -16,6 +17,9 @@ The same line carries
     `--kernel-reps` times over the 16 layers' weights, timed with HIP events on
     the stream it runs on; achieved = algorithmic bytes / average duration;
   * kernels: the same measurement for every kernel of the step;
+  * batched: BASELINE configs[4], 32 sequences with 256-token prompts decoded
+    in lockstep to 4096 positions over a paged fp16 KV cache (aggregate tok/s,
+    p50 / p90 step latency);
   * copy_probe: a device-to-device copy of --copy-probe-mib MiB (HIP's blit
     kernel), the achievable-bandwidth yardstick and the calibration dispatch
     of the FETCH_SIZE / WRITE_SIZE counter runs;
@@ -161,6 +165,37 @@ def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
     return 0
 
 
+def batched_decode(mmr, model, batch: int, prompt_len: int, context: int) -> dict:
+    """`batch` independent sequences with random prompts of
+    `prompt_len` tokens, decoded in lockstep to `context` positions over the
+    paged fp16 KV cache.  Aggregate tok/s = batch * decode steps / decode time;
+    per-step latency from an event after every step."""
+    rng = np.random.default_rng(4)
+    prompts = [[int(t) for t in rng.integers(0, MINIMIND2["vocab_size"], prompt_len)] for _ in range(batch)]
+    bs = model.make_batch_state(batch, context, mmr.KV_F16)
+    steps = context - prompt_len
+    ev = [mmr.Event() for _ in range(steps + 2)]
+    ev[0].record(bs.stream)
+    bs.prefill(prompts)
+    ev[1].record(bs.stream)
+    for i in range(steps):
+        bs.decode(1)
+        ev[i + 2].record(bs.stream)
+    bs.synchronize()
+    step_ms = np.array([ev[i + 1].elapsed_ms(ev[i + 2]) for i in range(steps)])
+    decode_ms = ev[1].elapsed_ms(ev[-1])
+    out = {"batch": batch, "prompt_tokens": prompt_len, "context": context, "kv_cache": "f16 paged (64-token pages)",
+           "prefill_ms": round(ev[0].elapsed_ms(ev[1]), 2), "prefill_mode": "batched decode steps over the prompts",
+           "decode_steps": steps, "decode_ms": round(decode_ms, 2),
+           "aggregate_tok_s": round(batch * steps / (decode_ms * 1e-3), 1),
+           "p50_step_ms": round(float(np.median(step_ms)), 4), "p90_step_ms": round(float(np.percentile(step_ms, 90)), 4),
+           "first_step_ms": round(float(step_ms[0]), 4), "last_step_ms": round(float(step_ms[-1]), 4)}
+    log(f"batched decode B={batch} {prompt_len}->{context}: {out['aggregate_tok_s']} tok/s aggregate, "
+        f"p50 step {out['p50_step_ms']} ms")
+    bs.free()
+    return out
+
+
 def cpu_baseline(mmr, cfg, prompt, sample_steps: int) -> dict | None:
     """The reference CPU path (single-threaded, as shipped) on a bounded sample."""
     ref = ROOT / "oracle" / "_ref" / "ref_driver"
@@ -204,6 +239,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=256)
     ap.add_argument("--no-gemv-sweep", action="store_true")
+    ap.add_argument("--batch", type=int, default=32, help="configs[4] batch size (0: skip the batched run)")
+    ap.add_argument("--batch-context", type=int, default=4096)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
                     help="run only the counter-run workload (gate_up launches + one copy) and exit")
     args = ap.parse_args()
@@ -315,6 +352,7 @@ def main() -> int:
         dst.free()
 
     sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
+    batched = batched_decode(mmr, model, args.batch, 256, args.batch_context) if args.batch > 0 else None
 
     traffic = None
     tfile = ROOT / "profiles" / "gemv_gate_up_minimind2_traffic.md"
@@ -351,6 +389,7 @@ def main() -> int:
         "kernels": kernels,
         "copy_probe": copy_probe,
         "gemv_sweep": sweep,
+        "batched": batched,
         "launch_mode": "eager (--no-graph)" if args.no_graph else "hipGraph replay",
         "roofline": {"bound": "hbm", "kernel": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",
                      "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),

@@ -182,6 +182,84 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
     }
 }
 
+// Skinny GEMM for few rows of A (batched decode, m <= 16 * BT): one block per
+// 16 rows of W, its kSkinnyWaves waves splitting K into contiguous ranges of
+// 32-wide blocks.  Per 32-k block a lane loads 8 consecutive halves of W row
+// n0 + lane % 16 and 8 fp32 of A row bt * 16 + lane % 16 at k offset
+// 8 * (lane / 16); MFMA s (0..7) takes element s of both, so instruction s
+// covers k = 8 g + s over the four lane groups g.  A wave issues the loads of
+// up to kSkinnyGroup k-blocks before its first MFMA.  The waves' accumulators
+// are summed in LDS in wave order (deterministic), then the residual epilogue.
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyGroup = 4;
+
+template <int BT, bool kResidual>
+__global__ __launch_bounds__(kWave* kSkinnyWaves) void gemm_skinny_kernel(GemmArgs g) {
+  __shared__ __align__(16) float red[kSkinnyWaves][BT][kWave][4];
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int n0 = blockIdx.x * 16;
+  const int nblk = g.k / 32;
+  const int b0 = wave * nblk / kSkinnyWaves, b1 = (wave + 1) * nblk / kSkinnyWaves;
+  const int wrow = min(n0 + lane % 16, g.n - 1);
+  const int koff = 8 * (lane / 16);
+  const __half* wsrc = g.w + static_cast<int64_t>(wrow) * g.k + koff;
+  const float* asrc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt)
+    asrc[bt] = g.a + static_cast<int64_t>(min(bt * 16 + lane % 16, g.m - 1)) * g.lda + koff;
+
+  f32x4 acc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kb = b0; kb < b1; kb += kSkinnyGroup) {
+    uint4 wv[kSkinnyGroup];
+    float4 av[kSkinnyGroup][BT][2];
+#pragma unroll
+    for (int i = 0; i < kSkinnyGroup; ++i) {
+      const int blk = min(kb + i, b1 - 1);  // past the range: reload the last block, masked below
+      wv[i] = *reinterpret_cast<const uint4*>(wsrc + blk * 32);
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) {
+        av[i][bt][0] = *reinterpret_cast<const float4*>(asrc[bt] + blk * 32);
+        av[i][bt][1] = *reinterpret_cast<const float4*>(asrc[bt] + blk * 32 + 4);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kSkinnyGroup; ++i) {
+      if (kb + i < b1) {  // wave-uniform
+        float wf[8];
+        half8_to_float8(wv[i], wf);
+#pragma unroll
+        for (int bt = 0; bt < BT; ++bt) {
+          const float a8[8] = {av[i][bt][0].x, av[i][bt][0].y, av[i][bt][0].z, av[i][bt][0].w,
+                               av[i][bt][1].x, av[i][bt][1].y, av[i][bt][1].z, av[i][bt][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[bt] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[e], a8[e], acc[bt], 0, 0, 0);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt)
+    *reinterpret_cast<f32x4*>(&red[wave][bt][lane][0]) = acc[bt];
+  __syncthreads();
+  // Output fragment of wave-lane l: rows n0 + 4 (l / 16) + r of W, column
+  // (A row) bt * 16 + l % 16.  Threads split the BT * 64 * 4 outputs.
+  for (int o = threadIdx.x; o < BT * kWave * 4; o += kWave * kSkinnyWaves) {
+    const int bt = o / (kWave * 4), l = (o / 4) % kWave, r = o % 4;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSkinnyWaves; ++w) v += red[w][bt][l][r];
+    const int n = n0 + 4 * (l / 16) + r;
+    const int m = bt * 16 + l % 16;
+    if (n < g.n && m < g.m) {
+      const int64_t off = static_cast<int64_t>(m) * g.ldc + n;
+      g.c[off] = kResidual ? g.residual[off] + v : v;
+    }
+  }
+}
+
 // Per (token, head) q/k RMSNorm + RoPE of one row of the fused qkv output,
 // q to `query`, k/v rounded to the cache dtype and written at cache index
 // start + token (decoder_layer.cpp:342-359 per token).  One wave per head;
@@ -446,8 +524,22 @@ hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) 
 
 bool gemm_supported(int m, int n, int k) { return m > 0 && n > 0 && k > 0 && k % 8 == 0; }
 
+template <int BT>
+hipError_t launch_gemm_skinny(const GemmArgs& g, hipStream_t s) {
+  const dim3 grid((g.n + 15) / 16);
+  if (g.residual) {
+    gemm_skinny_kernel<BT, true><<<grid, kWave * kSkinnyWaves, 0, s>>>(g);
+  } else {
+    gemm_skinny_kernel<BT, false><<<grid, kWave * kSkinnyWaves, 0, s>>>(g);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < g.n) return hipErrorInvalidValue;
+  // Few rows (batched decode): stream W with one block per 16 rows of W.
+  if (g.m <= 32 && g.k % 32 == 0 && g.k >= 32 * kSkinnyWaves)
+    return g.m <= 16 ? launch_gemm_skinny<1>(g, s) : launch_gemm_skinny<2>(g, s);
   // The largest tile that still gives every CU a block (256 CUs), else the
   // smallest tile.
   auto blocks = [&](int bm, int bn) { return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn); };
