@@ -37,7 +37,9 @@ inline float normal_at(uint64_t seed, uint64_t i, double std) {
   return static_cast<float>(std * z);
 }
 
-std::vector<float> read_tensor(std::ifstream& in, const std::string& expected, int64_t count) {
+// One tensor record: u64 name length, name, u64 element count, payload of
+// `count` little-endian fp32 (MMRTW001) or IEEE fp16 (MMRTH001) values.
+std::vector<float> read_tensor(std::ifstream& in, const std::string& expected, int64_t count, bool half) {
   uint64_t len = 0;
   in.read(reinterpret_cast<char*>(&len), sizeof(len));
   if (!in || len > 4096) throw std::runtime_error("failed to read " + expected);
@@ -50,8 +52,15 @@ std::vector<float> read_tensor(std::ifstream& in, const std::string& expected, i
   if (!in) throw std::runtime_error("failed to read " + expected);
   if (static_cast<int64_t>(n) != count) throw std::runtime_error(expected + " has invalid size");
   std::vector<float> v(static_cast<size_t>(n));
-  in.read(reinterpret_cast<char*>(v.data()), static_cast<std::streamsize>(n * sizeof(float)));
-  if (!in) throw std::runtime_error("failed to read " + expected);
+  if (half) {
+    std::vector<uint16_t> h(static_cast<size_t>(n));
+    in.read(reinterpret_cast<char*>(h.data()), static_cast<std::streamsize>(n * sizeof(uint16_t)));
+    if (!in) throw std::runtime_error("failed to read " + expected);
+    for (size_t i = 0; i < h.size(); ++i) v[i] = half_to_float(h[i]);
+  } else {
+    in.read(reinterpret_cast<char*>(v.data()), static_cast<std::streamsize>(n * sizeof(float)));
+    if (!in) throw std::runtime_error("failed to read " + expected);
+  }
   return v;
 }
 
@@ -250,11 +259,13 @@ DenseModelWeights read_weights(const MiniMindConfig& c, const std::string& path)
   char magic[8]{};
   in.read(magic, 8);
   if (!in) throw std::runtime_error("failed to read magic");
-  if (std::string(magic, 8) != "MMRTW001") throw std::runtime_error("unsupported runtime weight format");
+  const std::string format(magic, 8);
+  if (format != "MMRTW001" && format != "MMRTH001") throw std::runtime_error("unsupported runtime weight format");
+  const bool half = format == "MMRTH001";
   if (c.use_moe) throw std::runtime_error("the gfx950 runtime implements the dense model only (use_moe=0)");
   const auto order = tensor_order(c);
   std::vector<std::vector<float>> tensors;
-  for (const auto& t : order) tensors.push_back(read_tensor(in, t.name, t.count));
+  for (const auto& t : order) tensors.push_back(read_tensor(in, t.name, t.count, half));
   DenseModelWeights w;
   size_t i = 0;
   w.embed_tokens = std::move(tensors[i++]);

@@ -6,11 +6,13 @@ Greedy token ids must be identical; logits within max|d| / max|ref| <= 2e-3.
 from __future__ import annotations
 
 import os
+import struct
+import sys
 
 import numpy as np
 import pytest
 
-from conftest import load_golden, rel_err
+from conftest import ROOT, load_golden, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -173,3 +175,26 @@ def test_state_reset_and_reuse(gpu):
     assert st.position == 0
     assert [st.forward_next_token(t) for t in g["prompt"]] == first
     assert first[-1] == g["generated"][0]
+
+
+def test_fp16_payload_weights_load_and_match_reference(gpu, tmp_path):
+    # weights.bin with fp16 payloads (MMRTH001, export_minimind_runtime.py
+    # --dtype f16): the runtime loads it and the greedy tokens equal the
+    # reference CPU path's (the golden weights are fp16-representable)
+    sys.path.insert(0, str(ROOT / "minimind-orangepi_amd"))
+    import export_minimind_runtime as ex
+    mmr = gpu
+    g = load_golden("mini")
+    rt = tmp_path / "rt"
+    mmr.write_synthetic_model(rt, mmr.make_config(**g["config"]), g["seed"], g["std"], g["round_fp16"])
+    cfg = ex.CheckpointConfig(**{k: v for k, v in g["config"].items() if k in ex.CheckpointConfig.__dataclass_fields__})
+    half = tmp_path / "half"
+    half.mkdir()
+    (half / "minimind_runtime_config.txt").write_text((rt / "minimind_runtime_config.txt").read_text())
+    with (half / "weights.bin").open("wb") as f:
+        f.write(b"MMRTH001")
+        for name, v in ex.read_runtime_weights(rt / "weights.bin", cfg).items():
+            f.write(struct.pack("<Q", len(name)) + name.encode() + struct.pack("<Q", v.size))
+            f.write(v.astype("<f2").tobytes())
+    m = mmr.Model.load(half)
+    assert m.generate(g["prompt"], g["max_new"]) == g["generated"]
