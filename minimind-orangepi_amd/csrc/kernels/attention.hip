@@ -163,23 +163,34 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   // branch joins, which would serialise these round trips.
   const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
   const bool in0 = lane < D, in1 = lane + kWave < D;
-  float qx0[2], qx1[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int h = min(wave + j * kAttnWaves, R - 1);
-    const float* src = (MODE == kAttnFused ? qkv_row : a.q) + (g * R + h) * D;
-    qx0[j] = src[d0];
-    qx1[j] = src[d1];
-  }
+  // The batched (paged) path may hand the projection over as up to
+  // kAttnMaxQkvParts split-K partials: every part's load is issued (part index
+  // clamped, parts past qkv_parts weighted 0) and the parts summed in order.
+  constexpr int kParts = PAGED ? kAttnMaxQkvParts : 1;
+  float qx0[2] = {0.0f, 0.0f}, qx1[2] = {0.0f, 0.0f};
   float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
   float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+#pragma unroll
+  for (int pt = 0; pt < kParts; ++pt) {
+    const float* row = qkv_row + static_cast<int64_t>(min(pt, a.qkv_parts - 1)) * a.qkv_part_stride;
+    const float wgt = pt < a.qkv_parts ? 1.0f : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = min(wave + j * kAttnWaves, R - 1);
+      const float* src = (MODE == kAttnFused ? row : a.q) + (g * R + h) * D;
+      qx0[j] += wgt * src[d0];
+      qx1[j] += wgt * src[d1];
+    }
+    if constexpr (MODE == kAttnFused) {
+      const float* kraw = row + a.hq * D + g * D;
+      const float* vraw = kraw + a.hkv * D;
+      kx0 += wgt * kraw[d0];
+      vx0 += wgt * vraw[d0];
+      kx1 += wgt * kraw[d1];
+      vx1 += wgt * vraw[d1];
+    }
+  }
   if constexpr (MODE == kAttnFused) {
-    const float* kraw = qkv_row + a.hq * D + g * D;
-    const float* vraw = kraw + a.hkv * D;
-    kx0 = kraw[d0];
-    vx0 = vraw[d0];
-    kx1 = kraw[d1];
-    vx1 = vraw[d1];
     inv_freq = a.inv_freq[min(lane, D / 2 - 1)];
     qw0 = a.q_norm[d0];
     qw1 = a.q_norm[d1];
@@ -534,6 +545,7 @@ size_t attention_partial_floats(int hq, int hkv, int d, int splits) {
 
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream) {
   if (!attention_supported(a.hq, a.hkv, a.d) || a.splits <= 0 || a.batch <= 0) return hipErrorInvalidValue;
+  if (a.qkv_parts < 1 || a.qkv_parts > (a.page_table ? kAttnMaxQkvParts : 1)) return hipErrorInvalidValue;
   if (a.batch > 1 && (a.part_stride < static_cast<int64_t>(attention_partial_floats(a.hq, a.hkv, a.d, a.splits)) ||
                       (mode == kAttnFused && a.qkv_stride <= 0)))
     return hipErrorInvalidValue;

@@ -6,6 +6,8 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <algorithm>
+
 namespace mmr {
 namespace {
 
@@ -73,6 +75,216 @@ __global__ __launch_bounds__(kBatchThreads) void batch_argmax_kernel(const float
   }
 }
 
+// Split-K skinny GEMM (m <= 32 rows of A) on the fp16 matrix cores.
+// Block = 4 waves x 16 rows of W (64 rows) x one K chunk [k0, k0 + 32 NB)
+// (chunks tile K exactly).  The chunk of A is staged once in LDS as two fp16
+// planes: with a power-of-two scale s per row (the row's chunk maximum maps
+// into [2^14, 2^15)), hi = fp16(s a) and lo = fp16(s a - hi), so
+// hi + lo carries ~22 significant bits of s a (fp32 has 24), and W (fp16) is
+// exact.  Per 32-k block, lane l supplies W row n0 + 16 wave + l % 16 and A
+// row 16 bt + l % 16 at the same 8 k positions 8 (l / 16) .. + 7, so one
+// 16x16x32 MFMA per plane covers the block; the products are exact and
+// accumulate in fp32, and the result is multiplied by 1 / s (exact).
+// Output: part[split][m][n], every element written exactly once.
+constexpr int kSplitRows = 64;
+constexpr int kSplitMaxKc = 256;
+constexpr int kSplitMaxM = 32;
+
+using f32x4 = float __attribute__((ext_vector_type(4)));
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
+
+template <int BT, int NB>
+__global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
+  constexpr int KC = 32 * NB;
+  constexpr int kLd = KC + 8;           // halves per LDS row (16-byte aligned rows)
+  constexpr int kRowsPerWave = BT * 4;  // A rows staged by each wave
+  __shared__ __align__(16) _Float16 a_hi[BT * 16][kLd];
+  __shared__ __align__(16) _Float16 a_lo[BT * 16][kLd];
+  __shared__ float row_inv[BT * 16];
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int n0 = blockIdx.x * kSplitRows + wave * 16;
+  const int k0 = blockIdx.y * KC;
+  // W: NB x 8 halves per lane (rows past n clamp to the last row).
+  const int wrow = min(n0 + lane % 16, g.n - 1);
+  const __half* wsrc = g.w + static_cast<int64_t>(wrow) * g.k + k0 + 8 * (lane / 16);
+  uint4 wv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) wv[i] = *reinterpret_cast<const uint4*>(wsrc + 32 * i);
+  // A: wave w stages rows w, w + 4, ...; lane q holds columns 4q .. 4q + 3.
+  float4 av[kRowsPerWave];
+#pragma unroll
+  for (int it = 0; it < kRowsPerWave; ++it) {
+    const int r = wave + 4 * it;
+    av[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (r < g.m && lane < KC / 4)
+      av[it] = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(r) * g.lda + k0 + 4 * lane);
+  }
+#pragma unroll
+  for (int it = 0; it < kRowsPerWave; ++it) {
+    const int r = wave + 4 * it;
+    const float4 v = av[it];
+    const float mx = group_max<kWave>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    int e = 0;
+    frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1); e = 0 for mx = 0
+    e = max(e, -100);
+    const float sc = ldexpf(1.0f, 15 - e);
+    if (lane < KC / 4) {
+      const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+      f16x4 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hi[j] = static_cast<_Float16>(x[j]);
+        lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(hi[j]));
+      }
+      *reinterpret_cast<f16x4*>(&a_hi[r][4 * lane]) = hi;
+      *reinterpret_cast<f16x4*>(&a_lo[r][4 * lane]) = lo;
+    }
+    if (lane == 0) row_inv[r] = ldexpf(1.0f, e - 15);
+  }
+  __syncthreads();
+  f32x4 acc_hi[BT], acc_lo[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    acc_hi[bt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    acc_lo[bt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const f16x8 wh = __builtin_bit_cast(f16x8, wv[i]);
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) {
+      const int ar = bt * 16 + lane % 16, ac = 32 * i + 8 * (lane / 16);
+      const f16x8 ah = *reinterpret_cast<const f16x8*>(&a_hi[ar][ac]);
+      const f16x8 al = *reinterpret_cast<const f16x8*>(&a_lo[ar][ac]);
+      acc_hi[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, ah, acc_hi[bt], 0, 0, 0);
+      acc_lo[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, al, acc_lo[bt], 0, 0, 0);
+    }
+  }
+  // lane holds D[n0 + 4 (lane / 16) + r][16 bt + lane % 16], r = 0..3
+  const int nb = n0 + 4 * (lane / 16);
+  const bool vec = (g.n % 4 == 0) && nb + 3 < g.n;
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    const int m = bt * 16 + lane % 16;
+    if (m >= g.m) continue;
+    const float inv = row_inv[m];
+    float* dst = g.part + (static_cast<int64_t>(blockIdx.y) * g.m + m) * g.n + nb;
+    const float o[4] = {(acc_hi[bt][0] + acc_lo[bt][0]) * inv, (acc_hi[bt][1] + acc_lo[bt][1]) * inv,
+                        (acc_hi[bt][2] + acc_lo[bt][2]) * inv, (acc_hi[bt][3] + acc_lo[bt][3]) * inv};
+    if (vec) {
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (nb + r < g.n) dst[r] = o[r];
+    }
+  }
+}
+
+// Split-K partial sums, read with up to kPartLoads loads in flight per
+// thread before any add: sum over s = s0, s0 + step, ... < splits of
+// part4[s * sstride], in that order.
+constexpr int kPartLoads = 8;
+
+__device__ inline float4 add4(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
+__device__ inline float add4(float a, float b) { return a + b; }
+
+template <typename T>
+__device__ inline T sum_parts4(const T* part4, int64_t sstride, int s0, int step, int splits) {
+  T acc{};
+  for (int base = s0; base < splits; base += step * kPartLoads) {
+    T v[kPartLoads];
+#pragma unroll
+    for (int u = 0; u < kPartLoads; ++u) v[u] = part4[min(base + step * u, splits - 1) * sstride];
+#pragma unroll
+    for (int u = 0; u < kPartLoads; ++u)
+      if (base + step * u < splits) acc = add4(acc, v[u]);
+  }
+  return acc;
+}
+
+// h[b] += sum_s part[s][b], then x[b] = RMSNorm(h[b]) with the layer
+// association x * (scale * w) (decoder_layer.cpp:32-42) or the final one
+// (x * scale) * w (language_model.cpp:24-38).  One block of 1024 threads per
+// row: kResGroups groups of 256 threads each sum every kResGroups-th split of
+// a column chunk (float4 columns), then the groups' sums are added to h in
+// group order.  splits == 0 normalizes h as it is.
+constexpr int kResThreads = 1024;
+constexpr int kResGroups = kResThreads / 256;
+constexpr int kResChunkQuads = 256;
+
+template <bool kFinal>
+__global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float* h, const float* part, int splits,
+                                                                          int batch, int cols, const float* w,
+                                                                          float eps, float* x) {
+  __shared__ float4 red[kResGroups][kResChunkQuads];
+  __shared__ float s_ss[kResThreads / kWave];
+  const int b = blockIdx.x;
+  const int nq = cols / 4;
+  const int grp = threadIdx.x / 256, t = threadIdx.x % 256;
+  float4* h4 = reinterpret_cast<float4*>(h + static_cast<int64_t>(b) * cols);
+  const float4* p4 = reinterpret_cast<const float4*>(part) + static_cast<int64_t>(b) * nq;
+  const int64_t sstride = static_cast<int64_t>(batch) * nq;
+  float ss = 0.0f;
+  for (int c0 = 0; c0 < nq; c0 += kResChunkQuads) {  // block-uniform
+    const int q = c0 + t;
+    if (splits > 0 && q < nq) red[grp][t] = sum_parts4(p4 + q, sstride, grp, kResGroups, splits);
+    __syncthreads();
+    if (grp == 0 && q < nq) {
+      float4 v = h4[q];
+      if (splits > 0) {
+#pragma unroll
+        for (int g2 = 0; g2 < kResGroups; ++g2) v = add4(v, red[g2][t]);
+        h4[q] = v;
+      }
+      ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    __syncthreads();
+  }
+  ss = group_sum<kWave>(ss);
+  if (threadIdx.x % kWave == 0) s_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kResThreads / kWave; ++i) total += s_ss[i];
+  const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
+  float* hr = h + static_cast<int64_t>(b) * cols;
+  float* xr = x + static_cast<int64_t>(b) * cols;
+  for (int i = threadIdx.x; i < cols; i += kResThreads)
+    xr[i] = kFinal ? (hr[i] * scale) * w[i] : hr[i] * (scale * w[i]);
+}
+
+// act[b][i] = silu(sum_s gu[s][b][2i]) * sum_s gu[s][b][2i + 1]
+// (decoder_layer.cpp:175-182 on the interleaved gate/up rows); one float4
+// (two gate/up pairs) per thread.
+__global__ void batch_swiglu_kernel(const float* part, int splits, int batch, int f, float* act) {
+  const int b = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index: act[2i], act[2i + 1]
+  if (2 * i >= f) return;
+  const int64_t sstride = static_cast<int64_t>(batch) * f / 2;
+  const float4 p = sum_parts4(reinterpret_cast<const float4*>(part) + static_cast<int64_t>(b) * f / 2 + i, sstride, 0, 1,
+                              splits);
+  float2 out;
+  out.x = (p.x / (1.0f + expf(-p.x))) * p.y;
+  out.y = (p.z / (1.0f + expf(-p.z))) * p.w;
+  reinterpret_cast<float2*>(act + static_cast<int64_t>(b) * f)[i] = out;
+}
+
+// logits[b][v] = sum_s part[s][b][v] (the batch argmax then reads logits);
+// T = float4 when n is a multiple of 4, else float.
+template <typename T>
+__global__ void batch_sum_parts_kernel(const float* part, int splits, int batch, int n, float* out) {
+  constexpr int kW = sizeof(T) / sizeof(float);
+  const int b = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (kW * i >= n) return;
+  const int64_t row = static_cast<int64_t>(n / kW);
+  reinterpret_cast<T*>(out)[b * row + i] =
+      sum_parts4(reinterpret_cast<const T*>(part) + b * row + i, static_cast<int64_t>(batch) * row, 0, 1, splits);
+}
+
 }  // namespace
 
 hipError_t launch_batch_embed(const __half* embed, const int32_t* seq, int seq_stride, const int32_t* pos, int batch,
@@ -89,6 +301,75 @@ hipError_t launch_batch_argmax(const float* logits, int vocab, int batch, int32_
   if (batch <= 0 || vocab <= 0) return hipErrorInvalidValue;
   batch_argmax_kernel<<<batch, kBatchThreads, 0, stream>>>(logits, vocab, token_out, seq, seq_stride, pos, prompt_len,
                                                            seq_len);
+  return hipGetLastError();
+}
+
+int splitk_chunk(int n, int k) {
+  // The largest chunk (fewest partial sums for the consumer) that tiles K
+  // exactly and still gives at least kSplitMinBlocks blocks; else the chunk
+  // with the most blocks.
+  constexpr int kSplitMinBlocks = 128;
+  if (k <= 0 || k % 32 != 0) return 0;
+  const int nblocks = (n + kSplitRows - 1) / kSplitRows;
+  int kc = 0;
+  for (int nb = kSplitMaxKc / 32; nb >= 1; --nb) {
+    if (k % (32 * nb) != 0) continue;
+    kc = 32 * nb;  // block count grows as the chunk shrinks
+    if (nblocks * (k / kc) >= kSplitMinBlocks) break;
+  }
+  return kc;
+}
+
+namespace {
+template <int BT>
+hipError_t launch_splitk_bt(const SplitKArgs& g, dim3 grid, hipStream_t stream) {
+  switch (g.kc / 32) {
+    case 1: gemm_splitk_kernel<BT, 1><<<grid, 256, 0, stream>>>(g); break;
+    case 2: gemm_splitk_kernel<BT, 2><<<grid, 256, 0, stream>>>(g); break;
+    case 3: gemm_splitk_kernel<BT, 3><<<grid, 256, 0, stream>>>(g); break;
+    case 4: gemm_splitk_kernel<BT, 4><<<grid, 256, 0, stream>>>(g); break;
+    case 5: gemm_splitk_kernel<BT, 5><<<grid, 256, 0, stream>>>(g); break;
+    case 6: gemm_splitk_kernel<BT, 6><<<grid, 256, 0, stream>>>(g); break;
+    case 7: gemm_splitk_kernel<BT, 7><<<grid, 256, 0, stream>>>(g); break;
+    case 8: gemm_splitk_kernel<BT, 8><<<grid, 256, 0, stream>>>(g); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream) {
+  if (g.m <= 0 || g.m > kSplitMaxM || g.n <= 0 || g.k <= 0 || g.kc <= 0 || g.kc % 32 != 0 || g.kc > kSplitMaxKc ||
+      g.k % g.kc != 0 || g.lda < g.k || g.lda % 4 != 0)
+    return hipErrorInvalidValue;
+  const dim3 grid((g.n + kSplitRows - 1) / kSplitRows, g.k / g.kc);
+  return g.m <= 16 ? launch_splitk_bt<1>(g, grid, stream) : launch_splitk_bt<2>(g, grid, stream);
+}
+
+hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,
+                                      float eps, float* x, bool final_norm, hipStream_t stream) {
+  if (batch <= 0 || cols <= 0 || cols % 4 != 0 || splits < 0) return hipErrorInvalidValue;
+  if (final_norm) {
+    batch_residual_norm_kernel<true><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x);
+  } else {
+    batch_residual_norm_kernel<false><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_batch_swiglu(const float* part, int splits, int batch, int f, float* act, hipStream_t stream) {
+  if (batch <= 0 || f <= 0 || f % 2 != 0 || splits <= 0) return hipErrorInvalidValue;
+  batch_swiglu_kernel<<<dim3((f / 2 + 255) / 256, batch), 256, 0, stream>>>(part, splits, batch, f, act);
+  return hipGetLastError();
+}
+
+hipError_t launch_batch_sum_parts(const float* part, int splits, int batch, int n, float* out, hipStream_t stream) {
+  if (batch <= 0 || n <= 0 || splits <= 0) return hipErrorInvalidValue;
+  if (n % 4 == 0) {
+    batch_sum_parts_kernel<float4><<<dim3((n / 4 + 255) / 256, batch), 256, 0, stream>>>(part, splits, batch, n, out);
+  } else {
+    batch_sum_parts_kernel<float><<<dim3((n + 255) / 256, batch), 256, 0, stream>>>(part, splits, batch, n, out);
+  }
   return hipGetLastError();
 }
 

@@ -127,6 +127,11 @@ struct AttnArgs {
   int batch = 1;
   int64_t qkv_stride = 0;
   int64_t part_stride = 0;
+  // Fused mode: the projection may arrive as qkv_parts split-K partials,
+  // partial p of sequence b at qkv + p * qkv_part_stride + b * qkv_stride
+  // (summed in order; 1 = a plain row).
+  int qkv_parts = 1;
+  int64_t qkv_part_stride = 0;
   // Paged cache (fused mode): kcache / vcache are page pools
   // [page][Hkv][kKvPage][D]; page_table[b * pages_per_seq + t / kKvPage] is
   // the page of sequence b's token t; rows = pages_per_seq * kKvPage.
@@ -136,6 +141,7 @@ struct AttnArgs {
 constexpr int kKvPage = 64;  // tokens per KV page (a multiple of every attention tile)
 
 constexpr int kAttnMaxGroup = 8;  // Hq / Hkv supported
+constexpr int kAttnMaxQkvParts = 8;
 size_t attention_partial_floats(int hq, int hkv, int d, int splits);
 int attention_tile_tokens(int d);
 int64_t attention_cache_rows(int64_t capacity, int d);
@@ -232,6 +238,29 @@ hipError_t launch_batch_embed(const __half* embed, const int32_t* seq, int seq_s
 hipError_t launch_batch_argmax(const float* logits, int vocab, int batch, int32_t* token_out, int32_t* seq,
                                int seq_stride, int32_t* pos, const int32_t* prompt_len, int seq_len,
                                hipStream_t stream);
+
+// Split-K projection for few rows (batched decode): part[s][m][n] =
+// sum over k in [s kc, (s + 1) kc) of a[m][k] * w[n][k]; consumers sum the
+// splits in order.  m <= 32, k % 32 == 0, kc a multiple of 32 <= 256.
+struct SplitKArgs {
+  const float* a = nullptr;
+  int lda = 0;
+  const __half* w = nullptr;
+  float* part = nullptr;
+  int m = 0, n = 0, k = 0;
+  int kc = 0;
+};
+// K chunk (a multiple of 32 that divides k, at most 256; 0 when k is not a
+// multiple of 32); splits = k / kc.
+int splitk_chunk(int n, int k);
+hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream);
+// h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]).
+hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,
+                                      float eps, float* x, bool final_norm, hipStream_t stream);
+// act[b][i] = silu(sum_s part[s][b][2i]) * sum_s part[s][b][2i + 1].
+hipError_t launch_batch_swiglu(const float* part, int splits, int batch, int f, float* act, hipStream_t stream);
+// out[b][i] = sum_s part[s][b][i].
+hipError_t launch_batch_sum_parts(const float* part, int splits, int batch, int n, float* out, hipStream_t stream);
 
 // ------------------------------------------------------------- support ----
 hipError_t launch_rms_norm_rows(const float* in, const float* w, float eps, int rows, int cols, float* out,

@@ -5,13 +5,14 @@
 // (language_model.h:22-25); each sequence of a batch computes exactly what
 // LanguageModel::forward_next_token computes for it alone
 // (language_model.cpp:310-333, decoder_layer.cpp:312-407), with the batch's
-// projections as GEMMs of B rows on the fp32 matrix cores.  Step kernels:
-//   embed rows of seq[b][pos[b]]
-//   per layer: RMSNorm rows -> QKV GEMM -> paged split attention (q/k norm,
-//              RoPE at pos[b], K/V append) -> combine -> O GEMM (+residual)
-//              -> RMSNorm rows -> gate_up GEMM -> SwiGLU rows -> down GEMM
-//              (+residual)
-//   final RMSNorm rows -> lm_head GEMM -> per-sequence argmax + bookkeeping
+// projections as split-K GEMMs of B rows on the fp32 matrix cores, whose
+// partial sums the next kernel adds in split order.  Step kernels:
+//   embed rows of seq[b][pos[b]] -> input RMSNorm rows
+//   per layer: QKV split-K -> paged split attention (sums the QKV partials;
+//              q/k norm, RoPE at pos[b], K/V append) -> combine -> O split-K
+//              -> residual add + post RMSNorm -> gate_up split-K -> SwiGLU
+//              (sums partials) -> down split-K -> residual add + next RMSNorm
+//   lm_head split-K -> logits -> per-sequence argmax + bookkeeping
 // captured once per attention split count into a hipGraph.
 //
 // KV cache: per layer a pool of 64-token pages [page][Hkv][64][d]; sequence
@@ -55,6 +56,7 @@ struct BatchDeviceState {
   float* logits = nullptr;  // [batch][V]
   float* part = nullptr;    // attention partials, part_stride floats per sequence
   int64_t part_stride = 0;
+  float* proj = nullptr;    // projection split-K partials [splits][batch][n] (one GEMM at a time)
   int32_t* staging = nullptr;  // pinned host
   int64_t staging_len = 0;
   hipStream_t stream = nullptr;
@@ -79,7 +81,9 @@ void* BatchState::stream() const { return device ? static_cast<void*>(device->st
 
 namespace {
 
-// Attention splits per sequence: about four 64-token tiles per block, capped.
+// Attention splits per sequence: about four 64-token tiles per block, capped
+// (one or two tiles per block measured slower at 4096 keys: more partials for
+// the combine and more blocks paying the fixed per-block chain).
 constexpr int kBatchMaxSplits = 64;
 
 int batch_splits(int64_t n_keys, int tile) {
@@ -89,19 +93,46 @@ int batch_splits(int64_t n_keys, int tile) {
   return s;
 }
 
-void gemm_rows(const BatchDeviceState& s, const float* a, int lda, const __half* w, int n, int k, float* out,
-               bool residual) {
+// K chunk of a projection's split-K launch (0: dense fallback, k not a
+// multiple of 32); QKV partials are consumed by the attention prologue, which
+// takes at most kAttnMaxQkvParts of them.
+int proj_chunk(int n, int k, int max_parts) {
+  int kc = mmr::splitk_chunk(n, k);
+  if (kc == 0 || max_parts <= 0 || k / kc <= max_parts) return kc;
+  for (kc = 32; kc <= 256; kc += 32)  // the smallest chunk that tiles K in max_parts pieces
+    if (k % kc == 0 && k / kc <= max_parts) return kc;
+  return 0;
+}
+
+// out_parts[s][b][n] = partial products of x (batch rows, stride k) with W
+// [n][k]; returns the number of splits (1 for the dense fallback).
+int project(const BatchDeviceState& s, const float* x, const __half* w, int n, int k, int max_parts) {
+  const int B = static_cast<int>(s.batch);
+  const int kc = B <= 32 ? proj_chunk(n, k, max_parts) : 0;
+  if (kc > 0) {
+    mmr::SplitKArgs g;
+    g.a = x;
+    g.lda = k;
+    g.w = w;
+    g.part = s.proj;
+    g.m = B;
+    g.n = n;
+    g.k = k;
+    g.kc = kc;
+    check_hip(mmr::launch_gemm_splitk(g, s.stream), "batch split-K gemm");
+    return (k + kc - 1) / kc;
+  }
   mmr::GemmArgs g;
-  g.a = a;
-  g.lda = lda;
+  g.a = x;
+  g.lda = k;
   g.w = w;
-  g.residual = residual ? out : nullptr;
-  g.c = out;
+  g.c = s.proj;
   g.ldc = n;
-  g.m = static_cast<int>(s.batch);
+  g.m = B;
   g.n = n;
   g.k = k;
   check_hip(mmr::launch_gemm(g, s.stream), "batch gemm");
+  return 1;
 }
 
 void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
@@ -113,16 +144,21 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
   const int qkv_w = (Hq + 2 * Hkv) * D;
   const int B = static_cast<int>(s.batch);
   const int seq_stride = static_cast<int>(s.capacity + 1);
+  const size_t L = m.layers.size();
   check_hip(mmr::launch_batch_embed(m.embed, s.seq, seq_stride, s.pos, B, V, H, s.h, s.stream), "batch embed");
-  for (size_t l = 0; l < m.layers.size(); ++l) {
-    const LayerDev& L = m.layers[l];
-    check_hip(mmr::launch_rms_norm_rows(s.h, L.input_norm, c.rms_norm_eps, B, H, s.x, s.stream), "batch norm");
-    gemm_rows(s, s.x, H, L.qkv, qkv_w, H, s.qkv, false);
+  check_hip(mmr::launch_batch_residual_norm(s.h, nullptr, 0, B, H, m.layers[0].input_norm, c.rms_norm_eps, s.x, false,
+                                            s.stream),
+            "batch input norm");
+  for (size_t l = 0; l < L; ++l) {
+    const LayerDev& Ld = m.layers[l];
+    const int qkv_parts = project(s, s.x, Ld.qkv, qkv_w, H, mmr::kAttnMaxQkvParts);
     mmr::AttnArgs t;
-    t.qkv = s.qkv;
+    t.qkv = s.proj;
     t.qkv_stride = qkv_w;
-    t.q_norm = L.q_norm;
-    t.k_norm = L.k_norm;
+    t.qkv_parts = qkv_parts;
+    t.qkv_part_stride = static_cast<int64_t>(B) * qkv_w;
+    t.q_norm = Ld.q_norm;
+    t.k_norm = Ld.k_norm;
     t.eps = c.rms_norm_eps;
     t.inv_freq = m.inv_freq;
     t.pos = s.pos;
@@ -143,18 +179,42 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
     check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "batch attention");
     check_hip(mmr::launch_attention_combine(s.part, Hq, Hkv, D, splits, s.attn, s.stream, B, s.part_stride),
               "batch attention combine");
-    gemm_rows(s, s.attn, Hq * D, L.o, H, Hq * D, s.h, true);
-    check_hip(mmr::launch_rms_norm_rows(s.h, L.post_norm, c.rms_norm_eps, B, H, s.x, s.stream), "batch post norm");
-    gemm_rows(s, s.x, H, L.gate_up, 2 * F, H, s.gu, false);
-    check_hip(mmr::launch_swiglu_pairs(s.gu, static_cast<int64_t>(B) * F, s.act, s.stream), "batch swiglu");
-    gemm_rows(s, s.act, F, L.down, H, F, s.h, true);
+    const int o_parts = project(s, s.attn, Ld.o, H, Hq * D, 0);
+    check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, o_parts, B, H, Ld.post_norm, c.rms_norm_eps, s.x, false,
+                                              s.stream),
+              "batch residual + post norm");
+    const int gu_parts = project(s, s.x, Ld.gate_up, 2 * F, H, 0);
+    check_hip(mmr::launch_batch_swiglu(s.proj, gu_parts, B, F, s.act, s.stream), "batch swiglu");
+    const int down_parts = project(s, s.act, Ld.down, H, F, 0);
+    const bool last = l + 1 == L;
+    check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, down_parts, B, H,
+                                              last ? m.final_norm : m.layers[l + 1].input_norm, c.rms_norm_eps, s.x,
+                                              last, s.stream),
+              "batch residual + norm");
   }
-  check_hip(mmr::launch_rms_norm_rows(s.h, m.final_norm, c.rms_norm_eps, B, H, s.x, s.stream, true),
-            "batch final norm");
-  gemm_rows(s, s.x, H, m.lm_head, V, H, s.logits, false);
+  const int lm_parts = project(s, s.x, m.lm_head, V, H, 0);
+  check_hip(mmr::launch_batch_sum_parts(s.proj, lm_parts, B, V, s.logits, s.stream), "batch logits");
   check_hip(mmr::launch_batch_argmax(s.logits, V, B, s.token_out, s.seq, seq_stride, s.pos, s.prompt_len,
                                      seq_stride, s.stream),
             "batch argmax");
+}
+
+// Floats of the projection partial buffer: the largest splits * batch * n of
+// the step's projections.
+int64_t proj_floats(const MiniMindConfig& c, int64_t batch) {
+  const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
+  const int qkv_w = static_cast<int>((c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim);
+  const int F = static_cast<int>(c.intermediate_size), V = static_cast<int>(c.vocab_size);
+  const int qd = static_cast<int>(c.num_attention_heads) * D;
+  const struct { int n, k, max_parts; } shapes[] = {
+      {qkv_w, H, mmr::kAttnMaxQkvParts}, {H, qd, 0}, {2 * F, H, 0}, {H, F, 0}, {V, H, 0}};
+  int64_t most = 0;
+  for (const auto& sh : shapes) {
+    const int kc = batch <= 32 ? proj_chunk(sh.n, sh.k, sh.max_parts) : 0;
+    const int64_t parts = kc > 0 ? (sh.k + kc - 1) / kc : 1;
+    most = std::max<int64_t>(most, parts * batch * sh.n);
+  }
+  return most;
 }
 
 hipGraphExec_t capture_batch_step(BatchDeviceState& s, int splits) {
@@ -214,6 +274,8 @@ BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCa
   ar.plan(batch * F * 4);
   ar.plan(batch * V * 4);
   ar.plan(batch * s->part_stride * 4);
+  const int64_t proj = proj_floats(c, batch);
+  ar.plan(proj * 4);
   ar.allocate();
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
     s->kpool.push_back(ar.take<char>(pool_bytes));
@@ -235,6 +297,7 @@ BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCa
   s->act = ar.take<float>(batch * F);
   s->logits = ar.take<float>(batch * V);
   s->part = ar.take<float>(batch * s->part_stride);
+  s->proj = ar.take<float>(proj);
   s->staging_len = std::max<int64_t>(pages, batch * (capacity + 1)) + 4 * batch + 8;
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), s->staging_len * sizeof(int32_t),
                           hipHostMallocDefault),
