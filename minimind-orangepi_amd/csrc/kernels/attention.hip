@@ -27,6 +27,8 @@
 //      tile write the neutral partial (-inf, 0, 0).
 // No block waits for another: the log-sum-exp combine runs in the consumer
 // (the O-projection GEMV prologue, or attention_combine_kernel).
+#include <type_traits>
+
 #include "attention_common.h"
 #include "device_common.h"
 #include "kernels.h"
@@ -98,14 +100,28 @@ template <int D, bool PAGED>
 struct KvRows {
   const int32_t* pages = nullptr;
   int64_t head_base = 0;
-  int hkv = 0, g = 0;
-  __device__ __forceinline__ int64_t row(int t) const {
+  int hkv = 0, g = 0, n_pages = 0;
+  // Page holding token t (its index clamped into the page table, so a
+  // lookahead past the context stays in range); 0 for the contiguous cache.
+  // The table is read-only here and the index uniform: read through the
+  // constant address space, the lookup is a scalar-cache load whose wait
+  // (lgkmcnt) never covers the vector K/V loads in flight.
+  __device__ __forceinline__ int page_of(int t) const {
     if constexpr (PAGED) {
-      return ((static_cast<int64_t>(pages[t / kKvPage]) * hkv + g) * kKvPage + t % kKvPage) * D;
+      using ConstTable = const __attribute__((address_space(4))) int32_t;
+      return ((ConstTable*)pages)[min(t / kKvPage, n_pages - 1)];
+    } else {
+      return 0;
+    }
+  }
+  __device__ __forceinline__ int64_t row_at(int page, int t) const {
+    if constexpr (PAGED) {
+      return ((static_cast<int64_t>(page) * hkv + g) * kKvPage + t % kKvPage) * D;
     } else {
       return head_base + static_cast<int64_t>(t) * D;
     }
   }
+  __device__ __forceinline__ int64_t row(int t) const { return row_at(page_of(t), t); }
 };
 
 template <typename KV, int D, int MODE, bool PAGED>
@@ -141,6 +157,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   kv_rows.head_base = static_cast<int64_t>(g) * a.rows * D;
   kv_rows.hkv = a.hkv;
   kv_rows.g = g;
+  kv_rows.n_pages = a.pages_per_seq;
   float* part = a.part + static_cast<int64_t>(b) * a.part_stride;
   const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
 
@@ -158,6 +175,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
     vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
   }
+  // Page of the block's second tile, looked up one tile ahead of its fetch.
+  int next_page = kv_rows.page_of((split + S) * TT);
   // Loads are unconditional (indices clamped into range, values masked
   // afterwards): a predicated load makes the compiler wait for it before the
   // branch joins, which would serialise these round trips.
@@ -282,23 +301,32 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     }
 
     const float sqrt_d = sqrtf(static_cast<float>(D));
-    for (int tile = split; tile < n_tiles; tile += S) {
+    // Fetch tile `tile`'s K/V chunks into the registers (rows clamped into
+    // the context, all loads issued before any is consumed).
+    auto fetch_tile = [&](int tile, int page) {
       const int t0 = tile * TT;
       const int rows = min(TT, n_keys - t0);
-      // ---- stage K/V through LDS (first tile: the speculative registers) ----
-      if (!(tile == split && spec)) {
-        // Later tiles (or an unaligned capacity): fetch the tile into the same
-        // registers, all loads issued before any is consumed.
-        const int64_t tile_base = kv_rows.row(t0);
+      const int64_t tile_base = kv_rows.row_at(page, t0);
 #pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-          const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
-          const int r = min((c * CH) / D, rows - 1);
-          const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
-          kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
-          vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
-        }
+      for (int i = 0; i < kPerThread; ++i) {
+        const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+        const int r = min((c * CH) / D, rows - 1);
+        const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
+        kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
+        vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
       }
+    };
+    // The first tile comes from the speculative registers when they hold it.
+    if (!spec) fetch_tile(split, kv_rows.page_of(split * TT));
+    // One tile: stage K/V, scores + online softmax, P.V; with the prefetch
+    // variant, the next tile of this block is fetched meanwhile.
+    auto tile_step = [&](int tile, auto prefetch) {
+      const int t0 = tile * TT;
+      const int rows = min(TT, n_keys - t0);
+      // Page of the tile after next, for the prefetch in the next step
+      // (issued now, so its latency hides behind this tile's).
+      int page_after = 0;
+      if constexpr (decltype(prefetch)::value) page_after = kv_rows.page_of((tile + 2 * S) * TT);
       // Rows past the context are zero-filled: P.V runs over the whole tile
       // with zero probabilities there, and 0 * (stale LDS) could be NaN.
 #pragma unroll
@@ -325,6 +353,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
           k_s[r][i] = knew_s[i];
           v_s[r][i] = vnew_s[i];
         }
+      }
+      // The registers are free again: the next tile's loads overlap this
+      // tile's scores and P.V (a compile-time choice: a guarded load would
+      // make the compiler wait for it where the branches join).
+      if constexpr (decltype(prefetch)::value) {
+        fetch_tile(tile + S, next_page);
+        next_page = page_after;
       }
       __syncthreads();
 
@@ -397,7 +432,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
         }
       }
       __syncthreads();
-    }
+    };
+    int tile = split;
+    for (; tile + S < n_tiles; tile += S) tile_step(tile, std::true_type{});
+    if (tile < n_tiles) tile_step(tile, std::false_type{});
   }
 
   // ---- partial (m, l, o[d]) per head; neutral when the split had no tile ----

@@ -83,13 +83,16 @@ namespace {
 
 // Attention splits per sequence: about four 64-token tiles per block, capped
 // (one or two tiles per block measured slower at 4096 keys: more partials for
-// the combine and more blocks paying the fixed per-block chain).
+// the combine and more blocks paying the fixed per-block chain), and raised
+// while the context has the tiles until the launch has about one block per CU.
 constexpr int kBatchMaxSplits = 64;
+constexpr int64_t kBatchAttnBlocks = 256;
 
-int batch_splits(int64_t n_keys, int tile) {
+int batch_splits(int64_t n_keys, int tile, int64_t seq_heads) {
   const int64_t tiles = (n_keys + tile - 1) / tile;
   int s = 1;
   while (s < kBatchMaxSplits && s * 4 < tiles) s *= 2;
+  while (s < kBatchMaxSplits && 2 * s <= tiles && seq_heads * s < kBatchAttnBlocks) s *= 2;
   return s;
 }
 
@@ -320,7 +323,8 @@ BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCa
 void LanguageModel::launch_batch_step(BatchState& state) const {
   BatchDeviceState& s = *state.device;
   if (state.steps >= s.capacity) throw std::length_error("KV cache capacity exhausted");
-  const int splits = batch_splits(state.steps + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  const int splits = batch_splits(state.steps + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)),
+                                  s.batch * config_.num_key_value_heads);
   if (s.use_graphs) {
     auto it = s.graphs.find(splits);
     if (it == s.graphs.end()) it = s.graphs.emplace(splits, capture_batch_step(s, splits)).first;
