@@ -2,7 +2,7 @@
 """Decode throughput of the MiniMind2 gfx950 runtime.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f32|f16] [--no-cpu-baseline]
-                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--batch 32]
+                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--no-attention-sweep] [--batch 32]
                     [--batch-context 4096] [--traffic-probe N]
 
 Workload: MiniMind2 dense (hidden 768, 16 layers, 8/2 heads, d 96, FFN 2048,
@@ -17,6 +17,9 @@ The same line carries
     `--kernel-reps` times over the 16 layers' weights, timed with HIP events on
     the stream it runs on; achieved = algorithmic bytes / average duration;
   * kernels: the same measurement for every kernel of the step;
+  * gemv_sweep / attention_sweep: BASELINE configs[1] GEMV shapes and
+    configs[2] attention contexts alone through the C ABI, MALL-resident and
+    HBM-streaming;
   * batched: BASELINE configs[4], 32 sequences with 256-token prompts decoded
     in lockstep to 4096 positions over a paged fp16 KV cache (aggregate tok/s,
     p50 / p90 step latency);
@@ -136,6 +139,54 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
     return out
 
 
+ATTN_CONTEXTS = (128, 1024, 4096, 8192)
+
+
+def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
+    """decode attention over T cached tokens plus the new
+    one (T + 1 keys), 8 q / 2 kv heads, d 96, fp16 K/V ~ N(0, 1), through the
+    C ABI (mmr_attention_from_cache: split kernel + log-sum-exp combine, split
+    count chosen by the library).  `resident`: every launch reads the same
+    cache (MALL/L2-resident after the first); `hbm` (T >= 4096): launches
+    rotate over caches totalling >= 640 MiB.  GB/s = algorithmic bytes
+    (K + V of T + 1 tokens, fp32 q in and out) / mean launch time."""
+    hq, hkv, d = 8, 2, 96
+    rng = np.random.default_rng(11)
+    q = mmr.DeviceArray.from_numpy(rng.standard_normal(hq * d).astype(np.float32))
+    o = mmr.DeviceArray(hq * d, np.float32)
+    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 0), np.uint8)
+    out = {}
+    for T in ATTN_CONTEXTS:
+        n = T + 1
+        alg = 2 * hkv * d * 2 * n + 2 * hq * d * 4
+        caches = [mmr.KvCache(hkv, d, n, mmr.KV_F16)]
+        rows = caches[0].rows
+        caches[0].upload(rng.standard_normal((hkv, rows, d)).astype(np.float16),
+                         rng.standard_normal((hkv, rows, d)).astype(np.float16))
+        res = {"keys": n, "bytes": alg}
+        labels = [("resident", 1)]
+        if T >= 4096:
+            labels.append(("hbm", -(-(640 << 20) // (2 * hkv * rows * d * 2))))
+        for label, copies in labels:
+            while len(caches) < copies:
+                caches.append(mmr.KvCache(hkv, d, n, mmr.KV_F16))  # zero-filled
+            for i in range(copies):
+                mmr.attention_from_cache(q, caches[i], n, hq, hkv, d, o, ws, stream=stream)
+            ev[0].record(stream)
+            for i in range(reps):
+                mmr.attention_from_cache(q, caches[i % copies], n, hq, hkv, d, o, ws, stream=stream)
+            ev[1].record(stream)
+            stream.synchronize()
+            us = ev[0].elapsed_ms(ev[1]) * 1e3 / reps
+            res[label] = {"avg_us": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
+                          "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "caches": copies}
+        log(f"attention T={T}: " + " | ".join(f"{k} {res[k]['avg_us']:.2f} us {res[k]['gbs']:.0f} GB/s"
+                                              for k, _ in labels))
+        out[str(T)] = res
+        del caches
+    return out
+
+
 def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
     """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: the dominant
     kernel alone -- gate_up GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU
@@ -239,6 +290,7 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=256)
     ap.add_argument("--no-gemv-sweep", action="store_true")
+    ap.add_argument("--no-attention-sweep", action="store_true")
     ap.add_argument("--batch", type=int, default=32, help="configs[4] batch size (0: skip the batched run)")
     ap.add_argument("--batch-context", type=int, default=4096)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
@@ -352,6 +404,7 @@ def main() -> int:
         dst.free()
 
     sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
+    attn_sweep = None if args.no_attention_sweep else attention_sweep(mmr, mmr.Stream(stream), ev)
     batched = batched_decode(mmr, model, args.batch, 256, args.batch_context) if args.batch > 0 else None
 
     traffic = None
@@ -389,6 +442,7 @@ def main() -> int:
         "kernels": kernels,
         "copy_probe": copy_probe,
         "gemv_sweep": sweep,
+        "attention_sweep": attn_sweep,
         "batched": batched,
         "launch_mode": "eager (--no-graph)" if args.no_graph else "hipGraph replay",
         "roofline": {"bound": "hbm", "kernel": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",

@@ -467,28 +467,88 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   }
 }
 
-// Log-sum-exp combine of the split partials: one block of 128 threads per
-// query head, thread = dimension; fixed split order, so deterministic.  The
-// O-projection prologue (kProAttnCombine) performs the same operations in the
-// same order, so both paths give identical bits.
-__global__ __launch_bounds__(128) void attention_combine_kernel(const float* part, int hq, int hkv, int d, int splits,
-                                                                 int64_t part_stride, float* out) {
+// Log-sum-exp combine of the split partials: one block of 1024 threads per
+// query head (grid.y: sequence of a batch).  Thread t holds the (m, l) of
+// splits t, t + 1024, ... (at most kCombineKernelMaxSplits in all); block
+// reductions give M = max m and L = sum_s l_s exp(m_s - M); the weights
+// exp(m_s - M) go to LDS, and eight groups of 128 threads (thread = dimension)
+// each sum e_s o_s over every eighth split with eight loads in flight; the
+// groups' sums are added in group order.  Every order is fixed, so the result
+// is deterministic.  (The O-projection prologue, kProAttnCombine, computes
+// the same quantity for up to kCombineMaxSplits splits.)
+constexpr int kCombineThreads = 1024;
+constexpr int kCombineGroups = kCombineThreads / 128;
+constexpr int kCombinePerThread = 4;
+constexpr int kCombineKernelMaxSplits = kCombineThreads * kCombinePerThread;
+
+// Sum over the block (all threads active) in a fixed order.
+template <typename Op>
+__device__ __forceinline__ float combine_block_reduce(float v, Op op, float* scratch) {
+  v = group_reduce<kWave>(v, op);
+  __syncthreads();  // scratch may still be read from a previous reduction
+  if (threadIdx.x % kWave == 0) scratch[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float r = scratch[0];
+#pragma unroll
+  for (int w = 1; w < kCombineThreads / kWave; ++w) r = op(r, scratch[w]);
+  return r;
+}
+
+__global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(const float* part, int hq, int hkv, int d,
+                                                                             int splits, int64_t part_stride,
+                                                                             float* out) {
+  __shared__ float s_w[kCombineKernelMaxSplits];
+  __shared__ float s_red[kCombineGroups][128];
+  __shared__ float s_scratch[kCombineThreads / kWave];
   const int qh = blockIdx.x;
   part += static_cast<int64_t>(blockIdx.y) * part_stride;  // sequence of a batch
   out += static_cast<int64_t>(blockIdx.y) * hq * d;
   const int R = hq / hkv;
   const int g = qh / R, h = qh % R;
-  float M = -INFINITY;
-  for (int s = 0; s < splits; ++s) M = fmaxf(M, part[attn_ml_offset(g, s, h, splits, R, d, hkv)]);
-  float L = 0.0f, o = 0.0f;
-  const int dim = threadIdx.x;
-  for (int s = 0; s < splits; ++s) {
-    const float* ml = part + attn_ml_offset(g, s, h, splits, R, d, hkv);
-    const float w = expf(ml[0] - M);
-    L = fmaf(ml[1], w, L);
-    if (dim < d) o = fmaf(part[attn_o_offset(g, s, h, splits, R, d) + dim], w, o);
+  const int tid = threadIdx.x;
+  float2 ml[kCombinePerThread];
+#pragma unroll
+  for (int j = 0; j < kCombinePerThread; ++j) {
+    const int sp = min(tid + j * kCombineThreads, splits - 1);
+    ml[j] = *reinterpret_cast<const float2*>(part + attn_ml_offset(g, sp, h, splits, R, d, hkv));
   }
-  if (dim < d) out[qh * d + dim] = o * (1.0f / L);
+  float m_loc = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kCombinePerThread; ++j) m_loc = fmaxf(m_loc, ml[j].x);  // clamped repeats: max unchanged
+  const float M = combine_block_reduce(m_loc, OpMax{}, s_scratch);
+  float l_loc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kCombinePerThread; ++j) {
+    const int sp = tid + j * kCombineThreads;
+    if (sp < splits) {
+      const float e = expf(ml[j].x - M);
+      s_w[sp] = e;
+      l_loc = fmaf(ml[j].y, e, l_loc);
+    }
+  }
+  const float L = combine_block_reduce(l_loc, OpSum{}, s_scratch);  // its barriers also publish s_w
+  const int grp = tid / 128, dim = tid % 128;
+  const int dd = min(dim, d - 1);
+  float o = 0.0f;
+  for (int base = grp; base < splits; base += kCombineGroups * 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = part[attn_o_offset(g, min(base + kCombineGroups * u, splits - 1), h, splits, R, d) + dd];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int sp = base + kCombineGroups * u;
+      if (sp < splits) o = fmaf(v[u], s_w[sp], o);
+    }
+  }
+  s_red[grp][dim] = o;
+  __syncthreads();
+  if (grp == 0 && dim < d) {
+    float x = s_red[0][dim];
+#pragma unroll
+    for (int gi = 1; gi < kCombineGroups; ++gi) x += s_red[gi][dim];
+    out[qh * d + dim] = x * (1.0f / L);
+  }
 }
 
 // Standalone post-process (reference K2): one wave per head.
@@ -592,8 +652,10 @@ hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStr
 
 hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
                                     hipStream_t stream, int batch, int64_t part_stride) {
-  if (!attention_supported(hq, hkv, d) || splits <= 0 || batch <= 0) return hipErrorInvalidValue;
-  attention_combine_kernel<<<dim3(hq, batch), 128, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+  if (!attention_supported(hq, hkv, d) || d > 128 || splits <= 0 || splits > kCombineKernelMaxSplits || batch <= 0)
+    return hipErrorInvalidValue;
+  attention_combine_kernel<<<dim3(hq, batch), kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
+                                                                            out);
   return hipGetLastError();
 }
 
