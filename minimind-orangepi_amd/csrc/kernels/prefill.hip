@@ -23,6 +23,8 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <type_traits>
+
 namespace mmr {
 namespace {
 
@@ -323,43 +325,81 @@ __global__ void swiglu_pairs_kernel(const float* gu, int64_t n, float* out) {
 // over the cache (keys 0 .. position of each query, decoder_layer.cpp:184-234
 // per token), on the fp32 matrix cores.
 //
-// Block = (16 queries, KV group g), one wave per query head of the group, so
-// each 64-key tile of K and V is staged in LDS once for all of them (K
-// row-major, V transposed).  Per 16-key sub-tile a wave forms S^T = K Q^T
-// (v_mfma_f32_16x16x4f32, D/16 slices x 4): lane l holds S^T[key 4(l/16)+i]
-// [query l%16].  That is exactly the B-operand layout of O^T += V^T P^T, so the
-// probabilities never move between lanes; only the per-query tile maximum
-// needs the four 16-lane rows (two xor shuffles).  Online softmax per query:
-// scores are dot / sqrt(d) (a division, as the reference), masked above the
-// query's position; the running sum l stays per lane and is reduced once at
-// the end.
+// Block = (16 queries, one query head): 8 waves, wave w takes the 16-key tiles
+// w, w + 8, ... of the block's causal range (two waves per SIMD, so one wave's
+// vector work overlaps the other's matrix-core work), each with its own LDS stage (K and
+// V row-major, loaded row-contiguously: consecutive lanes read consecutive 16
+// bytes of one row) and its own online-softmax state, and fetches its next
+// tile into registers while it computes the current one.  Per 16-key sub-tile
+// a wave forms S^T = K Q^T (v_mfma_f32_16x16x4f32, D/16 slices x 4): lane l
+// holds S^T[key 4(l/16)+i][query l%16], exactly the B-operand layout of
+// O^T += V^T P^T (A = V^T: lane l reads V[key 4(l/16)+i][16j + l%16], four
+// conflict-free LDS words), so the probabilities never move between lanes;
+// only the per-query tile maximum needs the four 16-lane rows (two xor
+// shuffles).
+// Scores are dot / sqrt(d) (a division, as the reference), masked above the
+// query's position.  A wave may see tiles where a query has no key yet: its
+// state stays (-inf, 0, 0) until one arrives.  At the end the waves' (m, l, O)
+// merge in LDS (log-sum-exp, wave order): the per-query wave weights and 1/L
+// are computed once, then each output is a dot product over the waves.
 constexpr int kPrefillQueries = 16;
-constexpr int kPrefillKeys = 64;
+constexpr int kPrefillKeys = 16;  // keys per wave tile (one matrix-core sub-tile)
+constexpr int kPrefillWaves = 8;
 
-// NW waves per block (4 for groups of up to 4 query heads, else 8); waves past
-// the group size only help staging.
-template <typename KV, int D, int NW>
-__global__ __launch_bounds__(kWave* NW) void prefill_attention_kernel(PrefillAttnArgs a) {
-  constexpr int NT = kWave * NW;
-  constexpr int LDK = D + 4;               // K rows: 16-byte fragment reads hit distinct banks
-  constexpr int LDV = kPrefillKeys + 4;    // V^T rows
-  constexpr int CH = 16 / static_cast<int>(sizeof(KV));
-  constexpr int kChunks = kPrefillKeys * D / CH;
-  constexpr int kPer = (kChunks + NT - 1) / NT;
-  constexpr int DT = D / 16;               // 16-wide slices of the head dimension
-  __shared__ __align__(16) float k_s[kPrefillKeys][LDK];
-  __shared__ __align__(16) float vt_s[D][LDV];
+template <typename KV, int D>
+struct PrefillTileRegs {
+  static constexpr int CH = 16 / static_cast<int>(sizeof(KV));
+  static constexpr int kChunks = kPrefillKeys * D / CH;  // 16-byte chunks of K (or V) per tile
+  static constexpr int kPer = (kChunks + kWave - 1) / kWave;
+  uint4 k[kPer], v[kPer];
+};
+
+template <typename KV, int D>
+__global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel(PrefillAttnArgs a) {
+  using Regs = PrefillTileRegs<KV, D>;
+  constexpr int CH = Regs::CH;
+  constexpr int kChunks = Regs::kChunks;
+  constexpr int kPer = Regs::kPer;
+  constexpr int KT = kPrefillKeys;
+  constexpr int LD = D + 4;    // K and V rows: 16-byte K fragment reads and the 4-row V reads hit distinct banks
+  constexpr int DT = D / 16;   // 16-wide slices of the head dimension
+  constexpr int kRowChunks = D / CH;
+  constexpr int kStageFloats = 2 * KT * LD;
+  constexpr int kMergeLd = kPrefillQueries + 1;  // merge rows padded: conflict-free dimension-major reads
+  // Per-wave stage; after the key loop the same memory holds the merge inputs.
+  __shared__ __align__(16) float stage[kPrefillWaves][kStageFloats];
+  static_assert(kPrefillWaves * kStageFloats >= kPrefillWaves * (3 * kPrefillQueries + D * kMergeLd), "merge must fit");
   const int R = a.hq / a.hkv;
-  const int g = blockIdx.y;
+  const int h = blockIdx.y;
+  const int g = h / R;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const int h = g * R + min(wave, R - 1);  // waves past the group load a valid row and never store
   const int q0 = blockIdx.x * kPrefillQueries;
   const int qi = lane % 16, kq = lane / 16;  // query column, k slot
   const int qrow = min(q0 + qi, a.tokens - 1);
   const int qpos = a.start + q0 + qi;
   const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.rows * D;
   const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
+  float* k_s = stage[wave];            // [KT][LD]
+  float* v_s = stage[wave] + KT * LD;  // [KT][LD]
+
+  const int last_key = a.start + min(q0 + kPrefillQueries, a.tokens) - 1;  // the block's last query position
+  const int n_tiles = last_key / KT + 1;
+  // chunk c: key c / kRowChunks, dims (c % kRowChunks) * CH ..: consecutive
+  // lanes read consecutive 16 bytes of a row.
+  auto fetch = [&](int tile, Regs& r) {
+    const int t0 = tile * KT;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = min(lane + i * kWave, kChunks - 1);
+      const int key = min(t0 + c / kRowChunks, last_key);  // rows past the last key are masked
+      const int64_t off = static_cast<int64_t>(key) * D + (c % kRowChunks) * CH;
+      r.k[i] = *reinterpret_cast<const uint4*>(kbase + off);
+      r.v[i] = *reinterpret_cast<const uint4*>(vbase + off);
+    }
+  };
+  Regs regs;
+  fetch(min(wave, n_tiles - 1), regs);  // unconditional; a wave with no tile never reads it
 
   // Q^T fragments: dims 16j + 4 kq + {0..3} of query qi.
   float4 qf[DT];
@@ -373,105 +413,131 @@ __global__ __launch_bounds__(kWave* NW) void prefill_attention_kernel(PrefillAtt
   float m_run = -INFINITY, l_part = 0.0f;
   const float sqrt_d = sqrtf(static_cast<float>(D));
 
-  const int last_key = a.start + min(q0 + kPrefillQueries, a.tokens) - 1;  // the block's last query position
-  const int n_tiles = last_key / kPrefillKeys + 1;
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int t0 = tile * kPrefillKeys;
-    // chunk c: key c % 64, dims (c / 64) * CH ..: consecutive lanes take
-    // consecutive keys, so the transposed V writes are conflict-free.  All of
-    // a thread's loads are issued before the first LDS write.
-    uint4 kc[kPer], vc[kPer];
+  auto step = [&](int tile, auto prefetch) {
+    const int t0 = tile * KT;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = min(static_cast<int>(threadIdx.x) + i * NT, kChunks - 1);
-      const int r = c % kPrefillKeys, col = (c / kPrefillKeys) * CH;
-      const int key = min(t0 + r, last_key);  // rows past the last key are masked
-      const int64_t off = static_cast<int64_t>(key) * D + col;
-      kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
-      vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
-    }
-    __syncthreads();  // previous tile consumed by every wave
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = static_cast<int>(threadIdx.x) + i * NT;
+      const int c = lane + i * kWave;
       if (c < kChunks) {
-        const int r = c % kPrefillKeys, col = (c / kPrefillKeys) * CH;
+        const int r = c / kRowChunks, col = (c % kRowChunks) * CH;
         float kf[CH], vf[CH];
-        chunk_to_float_n<KV>(kc[i], kf);
-        chunk_to_float_n<KV>(vc[i], vf);
+        chunk_to_float_n<KV>(regs.k[i], kf);
+        chunk_to_float_n<KV>(regs.v[i], vf);
 #pragma unroll
-        for (int e = 0; e < CH; e += 4)
-          *reinterpret_cast<float4*>(&k_s[r][col + e]) = make_float4(kf[e], kf[e + 1], kf[e + 2], kf[e + 3]);
-#pragma unroll
-        for (int e = 0; e < CH; ++e) vt_s[col + e][r] = vf[e];
-      }
-    }
-    __syncthreads();
-    if (wave < R) {
-      // S^T for the four 16-key sub-tiles.
-      f32x4 st[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int j = 0; j < DT; ++j) {
-          const float4 kf = *reinterpret_cast<const float4*>(&k_s[kt * 16 + qi][16 * j + 4 * kq]);
-          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[j].x, st[kt], 0, 0, 0);
-          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[j].y, st[kt], 0, 0, 0);
-          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[j].z, st[kt], 0, 0, 0);
-          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[j].w, st[kt], 0, 0, 0);
+        for (int e = 0; e < CH; e += 4) {
+          *reinterpret_cast<float4*>(&k_s[r * LD + col + e]) = make_float4(kf[e], kf[e + 1], kf[e + 2], kf[e + 3]);
+          *reinterpret_cast<float4*>(&v_s[r * LD + col + e]) = make_float4(vf[e], vf[e + 1], vf[e + 2], vf[e + 3]);
         }
       }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = t0 + kt * 16 + 4 * kq + i;
-          const float sc = st[kt][i] / sqrt_d;  // decoder_layer.cpp:213
-          st[kt][i] = key <= qpos ? sc : -INFINITY;
-          mx = fmaxf(mx, st[kt][i]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      // Every query sees key 0 in tile 0, so m_new is finite from then on.
-      const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
-      l_part *= alpha;
-#pragma unroll
-      for (int j = 0; j < DT; ++j) ot[j] *= alpha;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          st[kt][i] = expf(st[kt][i] - m_new);  // 0 for masked keys
-          l_part += st[kt][i];
-        }
-      m_run = m_new;
-      // O^T += V^T P^T over the 64 keys.
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int j = 0; j < DT; ++j) {
-          const float4 vf = *reinterpret_cast<const float4*>(&vt_s[16 * j + qi][kt * 16 + 4 * kq]);
-          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.x, st[kt][0], ot[j], 0, 0, 0);
-          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.y, st[kt][1], ot[j], 0, 0, 0);
-          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.z, st[kt][2], ot[j], 0, 0, 0);
-          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf.w, st[kt][3], ot[j], 0, 0, 0);
-        }
     }
+    // The registers are free: the wave's next tile loads overlap this tile's
+    // work (a compile-time choice; a guarded load would be waited for where the
+    // branches join).
+    if constexpr (decltype(prefetch)::value) fetch(tile + kPrefillWaves, regs);
+    // The stage is private to this wave, and a wave's LDS operations complete
+    // in order: waiting for the writes is enough before other lanes read them.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    f32x4 st[KT / 16];
+#pragma unroll
+    for (int kt = 0; kt < KT / 16; ++kt) {
+      st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const float4 kf = *reinterpret_cast<const float4*>(&k_s[(kt * 16 + qi) * LD + 16 * j + 4 * kq]);
+        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[j].x, st[kt], 0, 0, 0);
+        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[j].y, st[kt], 0, 0, 0);
+        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[j].z, st[kt], 0, 0, 0);
+        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[j].w, st[kt], 0, 0, 0);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < KT / 16; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = t0 + kt * 16 + 4 * kq + i;
+        const float sc = st[kt][i] / sqrt_d;  // decoder_layer.cpp:213
+        st[kt][i] = key <= qpos ? sc : -INFINITY;
+        mx = fmaxf(mx, st[kt][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    // No key of this query seen yet (m_new = -inf): everything stays zero.
+    const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+    l_part *= alpha;
+#pragma unroll
+    for (int j = 0; j < DT; ++j) ot[j] *= alpha;
+#pragma unroll
+    for (int kt = 0; kt < KT / 16; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st[kt][i] = st[kt][i] == -INFINITY ? 0.0f : expf(st[kt][i] - m_new);
+        l_part += st[kt][i];
+      }
+    m_run = m_new;
+    // O^T += V^T P^T over the tile's keys.
+#pragma unroll
+    for (int kt = 0; kt < KT / 16; ++kt)
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        const float* vcol = &v_s[(kt * 16 + 4 * kq) * LD + 16 * j + qi];
+        const float v0 = vcol[0], v1 = vcol[LD], v2 = vcol[2 * LD], v3 = vcol[3 * LD];
+        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0, st[kt][0], ot[j], 0, 0, 0);
+        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1, st[kt][1], ot[j], 0, 0, 0);
+        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v2, st[kt][2], ot[j], 0, 0, 0);
+        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v3, st[kt][3], ot[j], 0, 0, 0);
+      }
+    // Reads of this stage finish before the next tile's writes (in-order LDS).
+  };
+  int tile = wave;
+  for (; tile + kPrefillWaves < n_tiles; tile += kPrefillWaves) step(tile, std::true_type{});
+  if (tile < n_tiles) step(tile, std::false_type{});
+
+  // ---- merge the four waves: (m, l) per query, O^T fragments ----
+  float l = l_part + __shfl_xor(l_part, 16);
+  l += __shfl_xor(l, 32);
+  __syncthreads();  // every wave is done with its stage
+  float* mrg = &stage[0][0];  // [wave][16] m, [wave][16] l, [wave][D][kMergeLd] o
+  float* m_sh = mrg;
+  float* l_sh = mrg + kPrefillWaves * kPrefillQueries;
+  float* o_sh = mrg + 2 * kPrefillWaves * kPrefillQueries;
+  if (kq == 0) {
+    m_sh[wave * kPrefillQueries + qi] = m_run;
+    l_sh[wave * kPrefillQueries + qi] = l;
   }
-  if (wave < R) {
-    float l = l_part + __shfl_xor(l_part, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
-    if (q0 + qi < a.tokens) {
-      float* dst = a.out + static_cast<int64_t>(q0 + qi) * a.out_stride + h * D;
 #pragma unroll
-      for (int j = 0; j < DT; ++j)
+  for (int j = 0; j < DT; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[16 * j + 4 * kq + i] = ot[j][i] * inv;
+    for (int i = 0; i < 4; ++i) o_sh[(wave * D + 16 * j + 4 * kq + i) * kMergeLd + qi] = ot[j][i];
+  __syncthreads();
+  // Per query: the waves' weights e_w = exp(m_w - M) / L (M finite: wave 0
+  // holds key 0 of every query), in place of m.
+  if (threadIdx.x < kPrefillQueries) {
+    const int q = threadIdx.x;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kPrefillWaves; ++w) M = fmaxf(M, m_sh[w * kPrefillQueries + q]);
+    float e[kPrefillWaves];
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kPrefillWaves; ++w) {
+      const float mw = m_sh[w * kPrefillQueries + q];
+      e[w] = mw == -INFINITY ? 0.0f : expf(mw - M);
+      L = fmaf(l_sh[w * kPrefillQueries + q], e[w], L);
     }
+    const float inv = 1.0f / L;
+#pragma unroll
+    for (int w = 0; w < kPrefillWaves; ++w) m_sh[w * kPrefillQueries + q] = e[w] * inv;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < kPrefillQueries * D; idx += kWave * kPrefillWaves) {
+    const int q = idx / D, dim = idx % D;
+    if (q0 + q >= a.tokens) continue;
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kPrefillWaves; ++w) o = fmaf(o_sh[(w * D + dim) * kMergeLd + q], m_sh[w * kPrefillQueries + q], o);
+    a.out[static_cast<int64_t>(q0 + q) * a.out_stride + h * D + dim] = o;
   }
 }
 
@@ -500,24 +566,19 @@ hipError_t launch_qkv_rows_kv(const QkvRowsArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <typename KV, int NW>
-hipError_t launch_prefill_attention_nw(const PrefillAttnArgs& a, hipStream_t s) {
-  const dim3 grid((a.tokens + kPrefillQueries - 1) / kPrefillQueries, a.hkv);
-  const dim3 block(kWave * NW);
+template <typename KV>
+hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) {
+  const dim3 grid((a.tokens + kPrefillQueries - 1) / kPrefillQueries, a.hq);
+  const dim3 block(kWave * kPrefillWaves);
   switch (a.d) {
-    case 16: prefill_attention_kernel<KV, 16, NW><<<grid, block, 0, s>>>(a); break;
-    case 32: prefill_attention_kernel<KV, 32, NW><<<grid, block, 0, s>>>(a); break;
-    case 64: prefill_attention_kernel<KV, 64, NW><<<grid, block, 0, s>>>(a); break;
-    case 96: prefill_attention_kernel<KV, 96, NW><<<grid, block, 0, s>>>(a); break;
-    case 128: prefill_attention_kernel<KV, 128, NW><<<grid, block, 0, s>>>(a); break;
+    case 16: prefill_attention_kernel<KV, 16><<<grid, block, 0, s>>>(a); break;
+    case 32: prefill_attention_kernel<KV, 32><<<grid, block, 0, s>>>(a); break;
+    case 64: prefill_attention_kernel<KV, 64><<<grid, block, 0, s>>>(a); break;
+    case 96: prefill_attention_kernel<KV, 96><<<grid, block, 0, s>>>(a); break;
+    case 128: prefill_attention_kernel<KV, 128><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
-}
-
-template <typename KV>
-hipError_t launch_prefill_attention_kv(const PrefillAttnArgs& a, hipStream_t s) {
-  return a.hq / a.hkv <= 4 ? launch_prefill_attention_nw<KV, 4>(a, s) : launch_prefill_attention_nw<KV, 8>(a, s);
 }
 
 }  // namespace
