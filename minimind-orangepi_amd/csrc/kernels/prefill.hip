@@ -1,6 +1,7 @@
 // prefill.hip -- prompt (prefill) kernels for gfx950: fp16-weight GEMM on the
-// fp32 matrix cores, per-row q/k norm + RoPE + KV-cache write, interleaved
-// SwiGLU rows, and causal attention over the cache.
+// fp16 matrix cores (hi/lo split of the fp32 activations), per-row q/k norm +
+// RoPE + KV-cache write, interleaved SwiGLU rows, and causal attention over
+// the cache on the fp32 matrix cores.
 //
 // Replaces the reference's device prefill layer (run_dense_prefill_layer_device,
 // decoder_layer.cpp:661-734): device_matmul / device_matmul_add with batch =
@@ -12,14 +13,13 @@
 // the reference runs on the CPU for a prompt (language_model.cpp:384-386).
 //
 // GEMM: C[m][n] (+)= sum_k A[m][k] * W[n][k], A fp32 row-major, W fp16
-// row-major (the decode GEMVs' weights), fp32 accumulation.  The contraction
-// runs on v_mfma_f32_16x16x4f32 with A in fp32 and W widened to fp32 in LDS,
-// so no operand is rounded below the CPU path's fp32.  A 256-thread block
-// computes a BM x BN tile with 2 x 2 waves; K advances 32 at a time through
-// LDS rows padded to 36 floats, which makes the 16-byte fragment reads of a
-// wave hit 64 distinct banks.  Within a 16-wide K slice, MFMA instruction s
-// takes k = 4 * (lane / 16) + s from each lane, so every lane fetches its four
-// k values with one 16-byte LDS read.
+// row-major (the decode GEMVs' weights), fp32 accumulation.  W is exact in
+// fp16; each K tile of A is split into hi + lo fp16 planes under a
+// power-of-two row scale, which keeps ~22 significant bits (fp32 has 24), so
+// the products on v_mfma_f32_16x16x32_f16 are as exact as the CPU path's.
+// A 256-thread block computes a BM x BN tile with 2 x 2 waves; K advances 128
+// at a time through LDS rows padded to 136 halves, which makes the 16-byte
+// fragment reads of 16 lanes hit 64 distinct banks.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -46,12 +46,16 @@ __device__ __forceinline__ void chunk_to_float_n<float>(const uint4& c, float* f
 }
 
 constexpr int kGemmThreads = 256;
-constexpr int kGemmBK = 128;  // K per LDS tile: the next tile's loads overlap 64-128 MFMAs per wave
-constexpr int kGemmLDK = kGemmBK + 4;
+constexpr int kGemmBK = 128;           // K per LDS tile: the next tile's loads overlap this tile's MFMAs
+constexpr int kGemmLDH = kGemmBK + 8;  // halves per LDS row (16-byte aligned, conflict-free fragment reads)
+
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 
 // Per-thread staging registers of one K tile: BM x BK fp32 of A as float4s,
 // BN x BK fp16 of W as 8-half chunks; thread t takes chunks t, t + 256, ...
-// so consecutive lanes read consecutive 16-byte pieces of a row.
+// so consecutive lanes read consecutive 16-byte pieces of a row (32 lanes per
+// A row, 16 per W row).
 template <int BM, int BN>
 struct GemmStage {
   static constexpr int kA = BM * kGemmBK / 4 / kGemmThreads;
@@ -80,31 +84,59 @@ struct GemmStage {
     }
   }
 
-  __device__ __forceinline__ void store(float (*As)[kGemmLDK], float (*Bs)[kGemmLDK], int tid) const {
+  // A -> two fp16 planes with a power-of-two scale per row of the tile:
+  // s = 2^(15 - e) for the row's max |a| = f 2^e (f in [1/2, 1)), hi =
+  // fp16(s a), lo = fp16(s a - hi) (the subtraction is exact), inv[r] = 1/s.
+  // The 32 lanes holding a row reduce its maximum together.
+  __device__ __forceinline__ void store(_Float16 (*Ah)[kGemmLDH], _Float16 (*Al)[kGemmLDH], float* inv,
+                                        _Float16 (*Bs)[kGemmLDH], int tid) const {
 #pragma unroll
     for (int i = 0; i < kA; ++i) {
       const int idx = tid + i * kGemmThreads;
       const int r = idx / (kGemmBK / 4), q = idx % (kGemmBK / 4);
-      *reinterpret_cast<float4*>(&As[r][q * 4]) = a[i];
+      const float4 v = a[i];
+      const float mx = group_max<32>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+      int e = 0;
+      frexpf(mx, &e);  // e = 0 for a zero row
+      e = max(e, -100);
+      const float sc = ldexpf(1.0f, 15 - e);
+      const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+      f16x4 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hi[j] = static_cast<_Float16>(x[j]);
+        lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(hi[j]));
+      }
+      *reinterpret_cast<f16x4*>(&Ah[r][q * 4]) = hi;
+      *reinterpret_cast<f16x4*>(&Al[r][q * 4]) = lo;
+      if (q == 0) inv[r] = ldexpf(1.0f, e - 15);
     }
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
       const int idx = tid + i * kGemmThreads;
       const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
-      float f[8];
-      half8_to_float8(b[i], f);
-      *reinterpret_cast<float4*>(&Bs[r][q * 8]) = make_float4(f[0], f[1], f[2], f[3]);
-      *reinterpret_cast<float4*>(&Bs[r][q * 8 + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+      *reinterpret_cast<uint4*>(&Bs[r][q * 8]) = b[i];
     }
   }
 };
 
+// C[m][n] (+)= sum_k A[m][k] W[n][k] for a BM x BN tile per block of 4 waves
+// (2 x 2, each BM/2 x BN/2 of 16 x 16 fragments), on the fp16 matrix cores.
+// Per K tile: MFMA v_mfma_f32_16x16x32_f16 over the hi and lo planes of A
+// (lane l supplies A row l % 16 and W row l % 16 at the same 8 k positions
+// 8 (l / 16) ..), the products are exact and summed in fp32, then the tile's
+// sum is scaled by the row's 1/s (exact) into the accumulator.  W is exact in
+// fp16; hi + lo carries ~22 significant bits of each activation.  The LDS
+// footprint (~52 KB for 64 x 64) lets two or three blocks share a CU, which
+// hides one block's tile-load wait behind another's work.
 template <int BM, int BN, bool kResidual>
 __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
   static_assert(GemmStage<BM, BN>::kA >= 1 && GemmStage<BM, BN>::kB >= 1, "tile too small for the block");
-  __shared__ __align__(16) float As[BM][kGemmLDK];
-  __shared__ __align__(16) float Bs[BN][kGemmLDK];
+  __shared__ __align__(16) _Float16 Ah[BM][kGemmLDH];
+  __shared__ __align__(16) _Float16 Al[BM][kGemmLDH];
+  __shared__ __align__(16) _Float16 Bs[BN][kGemmLDH];
+  __shared__ __align__(16) float inv_s[BM];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
@@ -120,34 +152,48 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   GemmStage<BM, BN> stage;
   const int nk = (g.k + kGemmBK - 1) / kGemmBK;
   stage.load(g, m0, n0, 0, tid);
-  stage.store(As, Bs, tid);
+  stage.store(Ah, Al, inv_s, Bs, tid);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     // The next tile's loads are in flight during this tile's MFMAs; on the
     // last tile they reload it (unconditional, so the values stay in registers).
     stage.load(g, m0, n0, min(kt + 1, nk - 1) * kGemmBK, tid);
+    f32x4 part[TM][TN];
 #pragma unroll
-    for (int kb = 0; kb < kGemmBK; kb += 16) {
-      const int kk = kb + 4 * (lane / 16);
-      float4 af[TM], bf[TN];
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const float4*>(&As[wm * (BM / 2) + i * 16 + lane % 16][kk]);
+      for (int j = 0; j < TN; ++j) part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const float4*>(&Bs[wn * (BN / 2) + j * 16 + lane % 16][kk]);
+    for (int kb = 0; kb < kGemmBK; kb += 32) {
+      const int kk = kb + 8 * (lane / 16);
+      f16x8 ah[TM], al[TM], bw[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        ah[i] = *reinterpret_cast<const f16x8*>(&Ah[wm * (BM / 2) + i * 16 + lane % 16][kk]);
+        al[i] = *reinterpret_cast<const f16x8*>(&Al[wm * (BM / 2) + i * 16 + lane % 16][kk]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const f16x8*>(&Bs[wn * (BN / 2) + j * 16 + lane % 16][kk]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], part[i][j], 0, 0, 0);
         }
     }
+    // Output rows of lane: 4 (lane / 16) + r of each 16-row fragment.
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const float4 sv = *reinterpret_cast<const float4*>(&inv_s[wm * (BM / 2) + i * 16 + 4 * (lane / 16)]);
+      const float sr[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(part[i][j][r], sr[r], acc[i][j][r]);
+    }
     __syncthreads();
-    stage.store(As, Bs, tid);
+    stage.store(Ah, Al, inv_s, Bs, tid);
     __syncthreads();
   }
 
