@@ -181,8 +181,15 @@ struct GemmArgs {
   float* c = nullptr;
   int ldc = 0;
   int m = 0, n = 0, k = 0;
+  // Split-K: k_splits > 1 writes k_splits partial products (no residual),
+  // split z to c + z * split_stride, over its contiguous range of K tiles.
+  int k_splits = 1;
+  int64_t split_stride = 0;
 };
 bool gemm_supported(int m, int n, int k);
+// Split count launch_gemm accepts and uses well for this shape: about four
+// 128-wide K tiles per split; 1 where the few-rows path applies.
+int gemm_k_splits(int m, int n, int k);
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Rows of the fused qkv projection for tokens at positions start ..
@@ -205,9 +212,6 @@ struct QkvRowsArgs {
   int query_stride = 0;
 };
 hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream);
-
-// out[i] = silu(gate_up[2i]) * gate_up[2i + 1] for i < n (interleaved rows).
-hipError_t launch_swiglu_pairs(const float* gate_up, int64_t n, float* out, hipStream_t stream);
 
 // Causal attention of query rows at positions start .. start + tokens - 1
 // over cache keys 0 .. each query's position.

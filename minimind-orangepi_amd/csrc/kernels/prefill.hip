@@ -23,6 +23,7 @@
 #include "device_common.h"
 #include "kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace mmr {
@@ -149,15 +150,20 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  GemmStage<BM, BN> stage;
+  // Split z (grid z) takes K tiles [kt0, kt1); an empty range writes zeros.
   const int nk = (g.k + kGemmBK - 1) / kGemmBK;
-  stage.load(g, m0, n0, 0, tid);
+  const int per = (nk + static_cast<int>(gridDim.z) - 1) / static_cast<int>(gridDim.z);
+  const int kt0 = static_cast<int>(blockIdx.z) * per, kt1 = min(kt0 + per, nk);
+  float* out = g.c + static_cast<int64_t>(blockIdx.z) * g.split_stride;
+
+  GemmStage<BM, BN> stage;
+  stage.load(g, m0, n0, kt0 * kGemmBK, tid);  // past k: clamped loads, zeroed
   stage.store(Ah, Al, inv_s, Bs, tid);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
+  for (int kt = kt0; kt < kt1; ++kt) {
     // The next tile's loads are in flight during this tile's MFMAs; on the
     // last tile they reload it (unconditional, so the values stay in registers).
-    stage.load(g, m0, n0, min(kt + 1, nk - 1) * kGemmBK, tid);
+    stage.load(g, m0, n0, min(kt + 1, kt1 - 1) * kGemmBK, tid);
     f32x4 part[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
         const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
         if (row < g.m && col < g.n) {
           const float v = acc[i][j][r];
-          g.c[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
+          out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
         }
       }
     }
@@ -356,15 +362,6 @@ __global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
       vdst[i] = from_float<KV>(vsrc[i]);
     }
   }
-}
-
-// out[t][i] = silu(gu[t][2i]) * gu[t][2i + 1] (decoder_layer.cpp:175-182 on
-// the interleaved gate/up rows of the runtime's fused weight).
-__global__ void swiglu_pairs_kernel(const float* gu, int64_t n, float* out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float2 p = reinterpret_cast<const float2*>(gu)[i];
-  out[i] = (p.x / (1.0f + expf(-p.x))) * p.y;
 }
 
 // Causal attention of `tokens` queries at positions start .. start + tokens - 1
@@ -589,7 +586,7 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
 
 template <int BM, int BN>
 hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
-  const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM);
+  const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.k_splits);
   if (g.residual) {
     gemm_f16w_kernel<BM, BN, true><<<grid, kGemmThreads, 0, s>>>(g);
   } else {
@@ -642,11 +639,30 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, hipStream_t s) {
   return hipGetLastError();
 }
 
+namespace {
+bool use_skinny(int m, int k) { return m <= 32 && k % 32 == 0 && k >= 32 * kSkinnyWaves; }
+}  // namespace
+
+int gemm_k_splits(int m, int n, int k) {
+  if (!gemm_supported(m, n, k) || use_skinny(m, k)) return 1;
+  // Tiles as launch_gemm picks them; at 512 or more (two blocks per CU) the
+  // partial-sum traffic costs more than the shorter K loop saves (measured:
+  // gate_up 512 x 4096 x 768 26.5 -> 30.6 us with 2 splits; o 14 -> 11 us and
+  // down 30 -> 23 us with 2 and 4).
+  auto blocks = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+  const int64_t tiles = blocks(64, 64) >= 256 ? blocks(64, 64) : blocks(32, 64) >= 256 ? blocks(32, 64) : blocks(32, 32);
+  if (tiles >= 512) return 1;
+  const int nk = (k + kGemmBK - 1) / kGemmBK;
+  return std::max(1, std::min(8, (nk + 3) / 4));
+}
+
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < g.n) return hipErrorInvalidValue;
+  if (g.k_splits < 1 || (g.k_splits > 1 && (g.residual || g.split_stride < static_cast<int64_t>(g.m) * g.ldc ||
+                                            g.k_splits > gemm_k_splits(g.m, g.n, g.k))))
+    return hipErrorInvalidValue;
   // Few rows (batched decode): stream W with one block per 16 rows of W.
-  if (g.m <= 32 && g.k % 32 == 0 && g.k >= 32 * kSkinnyWaves)
-    return g.m <= 16 ? launch_gemm_skinny<1>(g, s) : launch_gemm_skinny<2>(g, s);
+  if (use_skinny(g.m, g.k)) return g.m <= 16 ? launch_gemm_skinny<1>(g, s) : launch_gemm_skinny<2>(g, s);
   // The largest tile that still gives every CU a block (256 CUs), else the
   // smallest tile.
   auto blocks = [&](int bm, int bn) { return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn); };
@@ -658,12 +674,6 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
 hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream) {
   if (!attention_supported(a.hq, a.hkv, a.d) || a.tokens <= 0) return hipErrorInvalidValue;
   return kv == kKvF16 ? launch_qkv_rows_kv<__half>(a, stream) : launch_qkv_rows_kv<float>(a, stream);
-}
-
-hipError_t launch_swiglu_pairs(const float* gate_up, int64_t n, float* out, hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  swiglu_pairs_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, stream>>>(gate_up, n, out);
-  return hipGetLastError();
 }
 
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, KvDtype kv, hipStream_t stream) {

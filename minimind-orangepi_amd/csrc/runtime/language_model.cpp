@@ -59,7 +59,7 @@ struct DeviceState {
   float* pf_qkv = nullptr;  // [chunk][(Hq + 2 Hkv) d]
   float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
   float* pf_attn = nullptr; // [chunk][Hq d]
-  float* pf_gu = nullptr;   // [chunk][2F] interleaved gate/up
+  float* pf_part = nullptr; // split-K partials of the O, gate_up or down GEMM: [splits][chunk][N]
   float* pf_act = nullptr;  // [chunk][F]
   bool prefill_tokenwise = false;  // prefill through the decode step instead of the GEMM path
   hipStream_t stream = nullptr;
@@ -284,13 +284,21 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   if (const char* pc = std::getenv("MMR_PREFILL_CHUNK")) chunk = std::max<int64_t>(1, std::atoll(pc));
   s->pf_chunk = s->prefill_tokenwise ? 0 : std::min<int64_t>(capacity, chunk);
   const int64_t C = s->pf_chunk;
+  // Largest split-K partial set of a chunk (the split count depends on the
+  // row count only through the few-rows path, where it is 1).
+  int64_t part_f = 0;
   if (C > 0) {
+    const int ci = static_cast<int>(C);
+    const int64_t shapes[3][2] = {{H, Hq * D}, {2 * F, H}, {H, F}};
+    for (const auto& sh : shapes)
+      part_f = std::max<int64_t>(
+          part_f, int64_t{mmr::gemm_k_splits(ci, static_cast<int>(sh[0]), static_cast<int>(sh[1]))} * C * sh[0]);
     ar.plan(C * H * 4);
     ar.plan(C * H * 4);
     ar.plan(C * qkv_w * 4);
     ar.plan(C * Hq * D * 4);
     ar.plan(C * Hq * D * 4);
-    ar.plan(C * 2 * F * 4);
+    ar.plan(part_f * 4);
     ar.plan(C * F * 4);
   }
   ar.allocate();
@@ -318,7 +326,7 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     s->pf_qkv = ar.take<float>(C * qkv_w);
     s->pf_q = ar.take<float>(C * Hq * D);
     s->pf_attn = ar.take<float>(C * Hq * D);
-    s->pf_gu = ar.take<float>(C * 2 * F);
+    s->pf_part = ar.take<float>(part_f);
     s->pf_act = ar.take<float>(C * F);
   }
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
@@ -497,12 +505,14 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
   const int rows = static_cast<int>(n);
   check_hip(mmr::launch_embedding_gather(m.embed, s.seq + start, rows, V, H, s.pf_h, s.err, s.stream),
             "prefill embedding");
-  auto gemm = [&](const float* a, int lda, const __half* w, int N, int K, float* out, bool residual) {
+  // Dense GEMM into out (QKV), or split-K partial products into pf_part
+  // (returns the split count) for the O / gate_up / down projections, whose
+  // consumers add the partials: residual add + RMSNorm, or SwiGLU.
+  auto gemm_dense = [&](const float* a, int lda, const __half* w, int N, int K, float* out) {
     mmr::GemmArgs g;
     g.a = a;
     g.lda = lda;
     g.w = w;
-    g.residual = residual ? out : nullptr;
     g.c = out;
     g.ldc = N;
     g.m = rows;
@@ -510,16 +520,34 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     g.k = K;
     check_hip(mmr::launch_gemm(g, s.stream), "prefill gemm");
   };
-  for (size_t l = 0; l < m.layers.size(); ++l) {
-    const LayerDev& L = m.layers[l];
-    check_hip(mmr::launch_rms_norm_rows(s.pf_h, L.input_norm, c.rms_norm_eps, rows, H, s.pf_x, s.stream),
-              "prefill input norm");
-    gemm(s.pf_x, H, L.qkv, qkv_w, H, s.pf_qkv, false);
+  auto gemm_parts = [&](const float* a, int lda, const __half* w, int N, int K) {
+    mmr::GemmArgs g;
+    g.a = a;
+    g.lda = lda;
+    g.w = w;
+    g.c = s.pf_part;
+    g.ldc = N;
+    g.m = rows;
+    g.n = N;
+    g.k = K;
+    g.k_splits = mmr::gemm_k_splits(rows, N, K);
+    g.split_stride = static_cast<int64_t>(rows) * N;
+    check_hip(mmr::launch_gemm(g, s.stream), "prefill split-K gemm");
+    return g.k_splits;
+  };
+  const size_t L = m.layers.size();
+  // Layer 0's input norm; later layers get theirs from the previous layer's
+  // residual consumer.
+  check_hip(mmr::launch_rms_norm_rows(s.pf_h, m.layers[0].input_norm, c.rms_norm_eps, rows, H, s.pf_x, s.stream),
+            "prefill input norm");
+  for (size_t l = 0; l < L; ++l) {
+    const LayerDev& Ld = m.layers[l];
+    gemm_dense(s.pf_x, H, Ld.qkv, qkv_w, H, s.pf_qkv);
     mmr::QkvRowsArgs q;
     q.qkv = s.pf_qkv;
     q.qkv_stride = qkv_w;
-    q.q_norm = L.q_norm;
-    q.k_norm = L.k_norm;
+    q.q_norm = Ld.q_norm;
+    q.k_norm = Ld.k_norm;
     q.eps = c.rms_norm_eps;
     q.inv_freq = m.inv_freq;
     q.start = static_cast<int>(start);
@@ -547,12 +575,20 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     at.out = s.pf_attn;
     at.out_stride = Hq * D;
     check_hip(mmr::launch_prefill_attention(at, s.kv, s.stream), "prefill attention");
-    gemm(s.pf_attn, Hq * D, L.o, H, Hq * D, s.pf_h, true);
-    check_hip(mmr::launch_rms_norm_rows(s.pf_h, L.post_norm, c.rms_norm_eps, rows, H, s.pf_x, s.stream),
-              "prefill post norm");
-    gemm(s.pf_x, H, L.gate_up, 2 * F, H, s.pf_gu, false);
-    check_hip(mmr::launch_swiglu_pairs(s.pf_gu, static_cast<int64_t>(rows) * F, s.pf_act, s.stream), "prefill swiglu");
-    gemm(s.pf_act, F, L.down, H, F, s.pf_h, true);
+    const int so = gemm_parts(s.pf_attn, Hq * D, Ld.o, H, Hq * D);
+    check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, s.pf_x,
+                                              false, s.stream),
+              "prefill residual + post norm");
+    const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H);
+    check_hip(mmr::launch_batch_swiglu(s.pf_part, sg, rows, F, s.pf_act, s.stream), "prefill swiglu");
+    const int sd = gemm_parts(s.pf_act, F, Ld.down, H, F);
+    // The next layer's input norm (after the last layer: the final norm, whose
+    // rows are not used; the head normalises the last row itself).
+    const bool last = l + 1 == L;
+    check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, sd, rows, H,
+                                              last ? m.final_norm : m.layers[l + 1].input_norm, c.rms_norm_eps,
+                                              s.pf_x, last, s.stream),
+              "prefill residual + norm");
   }
 }
 
