@@ -94,11 +94,21 @@ using f32x4 = float __attribute__((ext_vector_type(4)));
 using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
 using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 
-template <int BT, int NB>
+// SwiGLU input staging: at most kSwiGluParts gate_up partials, read with
+// clamped indices and summed in split order (as batch_swiglu_kernel does).
+constexpr int kSwiGluParts = 4;
+
+template <int BT, int NB, bool kSwiGlu>
 __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   constexpr int KC = 32 * NB;
   constexpr int kLd = KC + 8;           // halves per LDS row (16-byte aligned rows)
-  constexpr int kRowsPerWave = BT * 4;  // A rows staged by each wave
+  constexpr int kRowsPerWave = BT * 4;  // A rows staged by each wave: w, w + 4, ...
+  constexpr int QR = KC / 4;            // float4 quads per A row
+  // Rows per pass: short rows share a wave (QR consecutive lanes per row).
+  constexpr int kRpp0 = kWave % QR == 0 ? kWave / QR : 1;
+  constexpr int RPP = kRpp0 < kRowsPerWave ? kRpp0 : kRowsPerWave;
+  constexpr int kPasses = kRowsPerWave / RPP;
+  constexpr int GW = RPP > 1 ? QR : kWave;  // lanes reducing one row's maximum
   __shared__ __align__(16) _Float16 a_hi[BT * 16][kLd];
   __shared__ __align__(16) _Float16 a_lo[BT * 16][kLd];
   __shared__ float row_inv[BT * 16];
@@ -112,25 +122,67 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   uint4 wv[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) wv[i] = *reinterpret_cast<const uint4*>(wsrc + 32 * i);
-  // A: wave w stages rows w, w + 4, ...; lane q holds columns 4q .. 4q + 3.
-  float4 av[kRowsPerWave];
+  // A: pass p, lane -> row wave + 4 (p RPP + lane / QR), columns 4 (lane % QR) ..
+  const int sub = lane / QR, q = lane % QR;
+  const bool lane_on = lane < RPP * QR;
+  float4 av[kPasses];
+  if constexpr (kSwiGlu) {
+    // All partial loads first: two float4 (four gate/up pairs) per part.
+    float4 pv[kPasses][kSwiGluParts][2];
+    const int64_t part_stride = static_cast<int64_t>(g.m) * 2 * g.k;
 #pragma unroll
-  for (int it = 0; it < kRowsPerWave; ++it) {
-    const int r = wave + 4 * it;
-    av[it] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (r < g.m && lane < KC / 4)
-      av[it] = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(r) * g.lda + k0 + 4 * lane);
+    for (int p = 0; p < kPasses; ++p) {
+      const int r = wave + 4 * (p * RPP + sub);
+      const bool on = lane_on && r < g.m;
+      const float* row = g.gu + static_cast<int64_t>(on ? r : 0) * 2 * g.k + 2 * (k0 + 4 * (on ? q : 0));
+#pragma unroll
+      for (int s = 0; s < kSwiGluParts; ++s) {
+        const float* src = row + min(s, g.gu_splits - 1) * part_stride;
+        pv[p][s][0] = *reinterpret_cast<const float4*>(src);
+        pv[p][s][1] = *reinterpret_cast<const float4*>(src + 4);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      float gs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, us[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < kSwiGluParts; ++s) {
+        if (s < g.gu_splits) {
+          gs[0] += pv[p][s][0].x;
+          us[0] += pv[p][s][0].y;
+          gs[1] += pv[p][s][0].z;
+          us[1] += pv[p][s][0].w;
+          gs[2] += pv[p][s][1].x;
+          us[2] += pv[p][s][1].y;
+          gs[3] += pv[p][s][1].z;
+          us[3] += pv[p][s][1].w;
+        }
+      }
+      const int r = wave + 4 * (p * RPP + sub);
+      float x[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = (gs[j] / (1.0f + expf(-gs[j]))) * us[j];  // decoder_layer.cpp:175-182
+      av[p] = (lane_on && r < g.m) ? make_float4(x[0], x[1], x[2], x[3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int r = wave + 4 * (p * RPP + sub);
+      av[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (lane_on && r < g.m)
+        av[p] = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(r) * g.lda + k0 + 4 * q);
+    }
   }
 #pragma unroll
-  for (int it = 0; it < kRowsPerWave; ++it) {
-    const int r = wave + 4 * it;
-    const float4 v = av[it];
-    const float mx = group_max<kWave>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  for (int p = 0; p < kPasses; ++p) {
+    const int r = wave + 4 * (p * RPP + sub);
+    const float4 v = av[p];
+    const float mx = group_max<GW>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     int e = 0;
     frexpf(mx, &e);  // mx = f 2^e, f in [0.5, 1); e = 0 for mx = 0
     e = max(e, -100);
     const float sc = ldexpf(1.0f, 15 - e);
-    if (lane < KC / 4) {
+    if (lane_on) {
       const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
       f16x4 hi, lo;
 #pragma unroll
@@ -138,10 +190,10 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
         hi[j] = static_cast<_Float16>(x[j]);
         lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(hi[j]));
       }
-      *reinterpret_cast<f16x4*>(&a_hi[r][4 * lane]) = hi;
-      *reinterpret_cast<f16x4*>(&a_lo[r][4 * lane]) = lo;
+      *reinterpret_cast<f16x4*>(&a_hi[r][4 * q]) = hi;
+      *reinterpret_cast<f16x4*>(&a_lo[r][4 * q]) = lo;
+      if (q == 0) row_inv[r] = ldexpf(1.0f, e - 15);
     }
-    if (lane == 0) row_inv[r] = ldexpf(1.0f, e - 15);
   }
   __syncthreads();
   f32x4 acc_hi[BT], acc_lo[BT];
@@ -321,29 +373,61 @@ int splitk_chunk(int n, int k) {
 }
 
 namespace {
-template <int BT>
+// Staging passes of gemm_splitk_kernel (rows per wave / rows per pass).
+constexpr int splitk_passes(int bt, int nb) {
+  const int qr = 8 * nb, rows = 4 * bt;
+  const int rpp0 = kWave % qr == 0 ? kWave / qr : 1;
+  return rows / (rpp0 < rows ? rpp0 : rows);
+}
+// The SwiGLU staging holds passes x kSwiGluParts x 2 float4 per lane.
+constexpr int kSwiGluMaxPasses = 4;
+}  // namespace
+
+bool splitk_swiglu_supported(int m, int kc, int gu_splits) {
+  if (gu_splits < 1 || gu_splits > kSwiGluParts || m < 1 || m > kSplitMaxM || kc < 32 || kc % 32 != 0 ||
+      kc > kSplitMaxKc)
+    return false;
+  return splitk_passes(m <= 16 ? 1 : 2, kc / 32) <= kSwiGluMaxPasses;
+}
+
+namespace {
+template <int BT, int NB, bool kSwiGlu>
+hipError_t launch_splitk_nb(const SplitKArgs& g, dim3 grid, hipStream_t stream) {
+  if constexpr (kSwiGlu && splitk_passes(BT, NB) > kSwiGluMaxPasses) {
+    return hipErrorInvalidValue;  // rejected by splitk_swiglu_supported; not instantiated
+  } else {
+    gemm_splitk_kernel<BT, NB, kSwiGlu><<<grid, 256, 0, stream>>>(g);
+    return hipGetLastError();
+  }
+}
+
+template <int BT, bool kSwiGlu>
 hipError_t launch_splitk_bt(const SplitKArgs& g, dim3 grid, hipStream_t stream) {
   switch (g.kc / 32) {
-    case 1: gemm_splitk_kernel<BT, 1><<<grid, 256, 0, stream>>>(g); break;
-    case 2: gemm_splitk_kernel<BT, 2><<<grid, 256, 0, stream>>>(g); break;
-    case 3: gemm_splitk_kernel<BT, 3><<<grid, 256, 0, stream>>>(g); break;
-    case 4: gemm_splitk_kernel<BT, 4><<<grid, 256, 0, stream>>>(g); break;
-    case 5: gemm_splitk_kernel<BT, 5><<<grid, 256, 0, stream>>>(g); break;
-    case 6: gemm_splitk_kernel<BT, 6><<<grid, 256, 0, stream>>>(g); break;
-    case 7: gemm_splitk_kernel<BT, 7><<<grid, 256, 0, stream>>>(g); break;
-    case 8: gemm_splitk_kernel<BT, 8><<<grid, 256, 0, stream>>>(g); break;
+    case 1: return launch_splitk_nb<BT, 1, kSwiGlu>(g, grid, stream);
+    case 2: return launch_splitk_nb<BT, 2, kSwiGlu>(g, grid, stream);
+    case 3: return launch_splitk_nb<BT, 3, kSwiGlu>(g, grid, stream);
+    case 4: return launch_splitk_nb<BT, 4, kSwiGlu>(g, grid, stream);
+    case 5: return launch_splitk_nb<BT, 5, kSwiGlu>(g, grid, stream);
+    case 6: return launch_splitk_nb<BT, 6, kSwiGlu>(g, grid, stream);
+    case 7: return launch_splitk_nb<BT, 7, kSwiGlu>(g, grid, stream);
+    case 8: return launch_splitk_nb<BT, 8, kSwiGlu>(g, grid, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 }  // namespace
 
 hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream) {
   if (g.m <= 0 || g.m > kSplitMaxM || g.n <= 0 || g.k <= 0 || g.kc <= 0 || g.kc % 32 != 0 || g.kc > kSplitMaxKc ||
-      g.k % g.kc != 0 || g.lda < g.k || g.lda % 4 != 0)
+      g.k % g.kc != 0)
     return hipErrorInvalidValue;
   const dim3 grid((g.n + kSplitRows - 1) / kSplitRows, g.k / g.kc);
-  return g.m <= 16 ? launch_splitk_bt<1>(g, grid, stream) : launch_splitk_bt<2>(g, grid, stream);
+  if (g.gu) {
+    if (!splitk_swiglu_supported(g.m, g.kc, g.gu_splits)) return hipErrorInvalidValue;
+    return g.m <= 16 ? launch_splitk_bt<1, true>(g, grid, stream) : launch_splitk_bt<2, true>(g, grid, stream);
+  }
+  if (g.lda < g.k || g.lda % 4 != 0) return hipErrorInvalidValue;
+  return g.m <= 16 ? launch_splitk_bt<1, false>(g, grid, stream) : launch_splitk_bt<2, false>(g, grid, stream);
 }
 
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,

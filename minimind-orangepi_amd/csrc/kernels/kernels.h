@@ -253,10 +253,18 @@ struct SplitKArgs {
   float* part = nullptr;
   int m = 0, n = 0, k = 0;
   int kc = 0;
+  // SwiGLU input: when gu is set, A[r][j] = silu(g) * u with g, u the sums (in
+  // split order) of gu[s][r][2j] and gu[s][r][2j + 1] over s < gu_splits
+  // (the gate_up partials, [gu_splits][m][2k]); a and lda are unused.
+  const float* gu = nullptr;
+  int gu_splits = 0;
 };
 // K chunk (a multiple of 32 that divides k, at most 256; 0 when k is not a
 // multiple of 32); splits = k / kc.
 int splitk_chunk(int n, int k);
+// Whether launch_gemm_splitk takes SwiGLU input for m rows, chunk kc and
+// gu_splits gate_up partials (the staging loads must fit in registers).
+bool splitk_swiglu_supported(int m, int kc, int gu_splits);
 hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream);
 // h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]).
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,

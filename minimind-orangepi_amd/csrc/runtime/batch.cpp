@@ -10,8 +10,9 @@
 //   embed rows of seq[b][pos[b]] -> input RMSNorm rows
 //   per layer: QKV split-K -> paged split attention (sums the QKV partials;
 //              q/k norm, RoPE at pos[b], K/V append) -> combine -> O split-K
-//              -> residual add + post RMSNorm -> gate_up split-K -> SwiGLU
-//              (sums partials) -> down split-K -> residual add + next RMSNorm
+//              -> residual add + post RMSNorm -> gate_up split-K -> down
+//              split-K whose staging sums the gate_up partials and applies
+//              SwiGLU -> residual add + next RMSNorm
 //   lm_head split-K -> logits -> per-sequence argmax + bookkeeping
 // captured once per attention split count into a hipGraph.
 //
@@ -57,6 +58,7 @@ struct BatchDeviceState {
   float* part = nullptr;    // attention partials, part_stride floats per sequence
   int64_t part_stride = 0;
   float* proj = nullptr;    // projection split-K partials [splits][batch][n] (one GEMM at a time)
+  float* proj_gu = nullptr; // gate_up partials, read by the down projection's staging
   int32_t* staging = nullptr;  // pinned host
   int64_t staging_len = 0;
   hipStream_t stream = nullptr;
@@ -111,7 +113,9 @@ int proj_chunk(int n, int k, int max_parts) {
 
 // out_parts[s][b][n] = partial products of x (batch rows, stride k) with W
 // [n][k]; returns the number of splits (1 for the dense fallback).
-int project(const BatchDeviceState& s, const float* x, const __half* w, int n, int k, int max_parts) {
+int project(const BatchDeviceState& s, const float* x, const __half* w, int n, int k, int max_parts,
+            float* out = nullptr) {
+  if (!out) out = s.proj;
   const int B = static_cast<int>(s.batch);
   const int kc = B <= 32 ? proj_chunk(n, k, max_parts) : 0;
   if (kc > 0) {
@@ -119,7 +123,7 @@ int project(const BatchDeviceState& s, const float* x, const __half* w, int n, i
     g.a = x;
     g.lda = k;
     g.w = w;
-    g.part = s.proj;
+    g.part = out;
     g.m = B;
     g.n = n;
     g.k = k;
@@ -131,13 +135,36 @@ int project(const BatchDeviceState& s, const float* x, const __half* w, int n, i
   g.a = x;
   g.lda = k;
   g.w = w;
-  g.c = s.proj;
+  g.c = out;
   g.ldc = n;
   g.m = B;
   g.n = n;
   g.k = k;
   check_hip(mmr::launch_gemm(g, s.stream), "batch gemm");
   return 1;
+}
+
+// The down projection of SwiGLU(gate_up partials): the split-K staging sums
+// the partials and applies SwiGLU itself where its registers allow, else the
+// SwiGLU kernel writes act first.
+int project_swiglu(const BatchDeviceState& s, const float* gu, int gu_parts, const __half* w, int n, int f) {
+  const int B = static_cast<int>(s.batch);
+  const int kc = B <= 32 ? proj_chunk(n, f, 0) : 0;
+  if (kc > 0 && mmr::splitk_swiglu_supported(B, kc, gu_parts)) {
+    mmr::SplitKArgs g;
+    g.gu = gu;
+    g.gu_splits = gu_parts;
+    g.w = w;
+    g.part = s.proj;
+    g.m = B;
+    g.n = n;
+    g.k = f;
+    g.kc = kc;
+    check_hip(mmr::launch_gemm_splitk(g, s.stream), "batch split-K gemm (SwiGLU input)");
+    return f / kc;
+  }
+  check_hip(mmr::launch_batch_swiglu(gu, gu_parts, B, f, s.act, s.stream), "batch swiglu");
+  return project(s, s.act, w, n, f, 0);
 }
 
 void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
@@ -188,9 +215,8 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
     check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, o_parts, B, H, Ld.post_norm, c.rms_norm_eps, s.x, false,
                                               s.stream),
               "batch residual + post norm");
-    const int gu_parts = project(s, s.x, Ld.gate_up, 2 * F, H, 0);
-    check_hip(mmr::launch_batch_swiglu(s.proj, gu_parts, B, F, s.act, s.stream), "batch swiglu");
-    const int down_parts = project(s, s.act, Ld.down, H, F, 0);
+    const int gu_parts = project(s, s.x, Ld.gate_up, 2 * F, H, 0, s.proj_gu);
+    const int down_parts = project_swiglu(s, s.proj_gu, gu_parts, Ld.down, H, F);
     const bool last = l + 1 == L;
     check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, down_parts, B, H,
                                               last ? m.final_norm : m.layers[l + 1].input_norm, c.rms_norm_eps, s.x,
@@ -204,6 +230,13 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
             "batch argmax");
 }
 
+// Floats of one projection's partial set: splits * batch * n.
+int64_t parts_floats(int n, int k, int max_parts, int64_t batch) {
+  const int kc = batch <= 32 ? proj_chunk(n, k, max_parts) : 0;
+  const int64_t parts = kc > 0 ? (k + kc - 1) / kc : 1;
+  return parts * batch * n;
+}
+
 // Floats of the projection partial buffer: the largest splits * batch * n of
 // the step's projections.
 int64_t proj_floats(const MiniMindConfig& c, int64_t batch) {
@@ -214,11 +247,7 @@ int64_t proj_floats(const MiniMindConfig& c, int64_t batch) {
   const struct { int n, k, max_parts; } shapes[] = {
       {qkv_w, H, mmr::kAttnMaxQkvParts}, {H, qd, 0}, {2 * F, H, 0}, {H, F, 0}, {V, H, 0}};
   int64_t most = 0;
-  for (const auto& sh : shapes) {
-    const int kc = batch <= 32 ? proj_chunk(sh.n, sh.k, sh.max_parts) : 0;
-    const int64_t parts = kc > 0 ? (sh.k + kc - 1) / kc : 1;
-    most = std::max<int64_t>(most, parts * batch * sh.n);
-  }
+  for (const auto& sh : shapes) most = std::max(most, parts_floats(sh.n, sh.k, sh.max_parts, batch));
   return most;
 }
 
@@ -281,6 +310,9 @@ BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCa
   ar.plan(batch * s->part_stride * 4);
   const int64_t proj = proj_floats(c, batch);
   ar.plan(proj * 4);
+  const int64_t proj_gu = parts_floats(static_cast<int>(2 * c.intermediate_size), static_cast<int>(c.hidden_size), 0,
+                                       batch);
+  ar.plan(proj_gu * 4);
   ar.allocate();
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
     s->kpool.push_back(ar.take<char>(pool_bytes));
@@ -303,6 +335,7 @@ BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCa
   s->logits = ar.take<float>(batch * V);
   s->part = ar.take<float>(batch * s->part_stride);
   s->proj = ar.take<float>(proj);
+  s->proj_gu = ar.take<float>(proj_gu);
   s->staging_len = std::max<int64_t>(pages, batch * (capacity + 1)) + 4 * batch + 8;
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), s->staging_len * sizeof(int32_t),
                           hipHostMallocDefault),
