@@ -3,6 +3,7 @@
 // language_model.h:22-25).  The projections of a batched step run on the
 // prefill GEMM (M = batch) and the attention on the split kernel with a
 // paged cache; these kernels cover the per-sequence token handling.
+#include "attention_common.h"
 #include "device_common.h"
 #include "kernels.h"
 
@@ -94,12 +95,17 @@ using f32x4 = float __attribute__((ext_vector_type(4)));
 using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
 using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 
-// SwiGLU input staging: at most kSwiGluParts gate_up partials, read with
-// clamped indices and summed in split order (as batch_swiglu_kernel does).
+// A staging modes: plain rows; SwiGLU of the gate_up partials (at most
+// kSwiGluParts, read with clamped indices and summed in split order, as
+// batch_swiglu_kernel does); the attention output merged from at most 4 or 8
+// split partials (log-sum-exp in split order).
+constexpr int kAPlain = 0, kASwiGlu = 1, kACombine4 = 2, kACombine8 = 3;
 constexpr int kSwiGluParts = 4;
 
-template <int BT, int NB, bool kSwiGlu>
+template <int BT, int NB, int kAMode>
 __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
+  constexpr bool kSwiGlu = kAMode == kASwiGlu;
+  constexpr int kCombine = kAMode == kACombine4 ? 4 : kAMode == kACombine8 ? 8 : 0;
   constexpr int KC = 32 * NB;
   constexpr int kLd = KC + 8;           // halves per LDS row (16-byte aligned rows)
   constexpr int kRowsPerWave = BT * 4;  // A rows staged by each wave: w, w + 4, ...
@@ -163,6 +169,52 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) x[j] = (gs[j] / (1.0f + expf(-gs[j]))) * us[j];  // decoder_layer.cpp:175-182
       av[p] = (lane_on && r < g.m) ? make_float4(x[0], x[1], x[2], x[3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  } else if constexpr (kCombine > 0) {
+    // This lane's quad lies in one head (d is a multiple of 4): head kk / d,
+    // dims kk % d .. + 3.  All split loads first, then the merge.
+    const int R = g.hq / g.hkv;
+    const int kk = k0 + 4 * q;
+    const int head = kk / g.d, dd = kk % g.d;
+    const int gq = head / R, hr = head % R;
+    const int S = g.attn_splits;
+    float2 ml[kPasses][kCombine];
+    float4 ov[kPasses][kCombine];
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int r = wave + 4 * (p * RPP + sub);
+      const bool on = lane_on && r < g.m;
+      const float* base = g.attn_part + static_cast<int64_t>(on ? r : 0) * g.attn_part_stride;
+#pragma unroll
+      for (int sp = 0; sp < kCombine; ++sp) {
+        const int sc = min(sp, S - 1);
+        ml[p][sp] = *reinterpret_cast<const float2*>(base + attn_ml_offset(gq, sc, hr, S, R, g.d, g.hkv));
+        ov[p][sp] = *reinterpret_cast<const float4*>(base + attn_o_offset(gq, sc, hr, S, R, g.d) + dd);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int sp = 0; sp < kCombine; ++sp)
+        if (sp < S) M = fmaxf(M, ml[p][sp].x);
+      float L = 0.0f;
+      float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int sp = 0; sp < kCombine; ++sp) {
+        if (sp < S) {
+          const float e = expf(ml[p][sp].x - M);
+          L = fmaf(ml[p][sp].y, e, L);
+          o.x = fmaf(ov[p][sp].x, e, o.x);
+          o.y = fmaf(ov[p][sp].y, e, o.y);
+          o.z = fmaf(ov[p][sp].z, e, o.z);
+          o.w = fmaf(ov[p][sp].w, e, o.w);
+        }
+      }
+      const float inv = 1.0f / L;
+      const int r = wave + 4 * (p * RPP + sub);
+      av[p] = (lane_on && r < g.m) ? make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv)
+                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   } else {
 #pragma unroll
@@ -379,8 +431,15 @@ constexpr int splitk_passes(int bt, int nb) {
   const int rpp0 = kWave % qr == 0 ? kWave / qr : 1;
   return rows / (rpp0 < rows ? rpp0 : rows);
 }
-// The SwiGLU staging holds passes x kSwiGluParts x 2 float4 per lane.
+// The SwiGLU staging holds passes x kSwiGluParts x 2 float4 per lane, the
+// combine staging passes x (4 or 8) x (float4 + float2).
 constexpr int kSwiGluMaxPasses = 4;
+constexpr int kCombineMaxSlots = 16;  // passes x splits held
+constexpr bool splitk_mode_fits(int bt, int nb, int mode) {
+  return mode == kAPlain ? true
+         : mode == kASwiGlu ? splitk_passes(bt, nb) <= kSwiGluMaxPasses
+                            : splitk_passes(bt, nb) * (mode == kACombine4 ? 4 : 8) <= kCombineMaxSlots;
+}
 }  // namespace
 
 bool splitk_swiglu_supported(int m, int kc, int gu_splits) {
@@ -390,30 +449,42 @@ bool splitk_swiglu_supported(int m, int kc, int gu_splits) {
   return splitk_passes(m <= 16 ? 1 : 2, kc / 32) <= kSwiGluMaxPasses;
 }
 
+bool splitk_combine_supported(int m, int kc, int attn_splits, int d) {
+  if (attn_splits < 1 || attn_splits > 8 || m < 1 || m > kSplitMaxM || kc < 32 || kc % 32 != 0 ||
+      kc > kSplitMaxKc || d <= 0 || d % 4 != 0)
+    return false;
+  return splitk_passes(m <= 16 ? 1 : 2, kc / 32) * (attn_splits <= 4 ? 4 : 8) <= kCombineMaxSlots;
+}
+
 namespace {
-template <int BT, int NB, bool kSwiGlu>
+template <int BT, int NB, int kAMode>
 hipError_t launch_splitk_nb(const SplitKArgs& g, dim3 grid, hipStream_t stream) {
-  if constexpr (kSwiGlu && splitk_passes(BT, NB) > kSwiGluMaxPasses) {
-    return hipErrorInvalidValue;  // rejected by splitk_swiglu_supported; not instantiated
+  if constexpr (!splitk_mode_fits(BT, NB, kAMode)) {
+    return hipErrorInvalidValue;  // rejected by the *_supported checks; not instantiated
   } else {
-    gemm_splitk_kernel<BT, NB, kSwiGlu><<<grid, 256, 0, stream>>>(g);
+    gemm_splitk_kernel<BT, NB, kAMode><<<grid, 256, 0, stream>>>(g);
     return hipGetLastError();
   }
 }
 
-template <int BT, bool kSwiGlu>
+template <int BT, int kAMode>
 hipError_t launch_splitk_bt(const SplitKArgs& g, dim3 grid, hipStream_t stream) {
   switch (g.kc / 32) {
-    case 1: return launch_splitk_nb<BT, 1, kSwiGlu>(g, grid, stream);
-    case 2: return launch_splitk_nb<BT, 2, kSwiGlu>(g, grid, stream);
-    case 3: return launch_splitk_nb<BT, 3, kSwiGlu>(g, grid, stream);
-    case 4: return launch_splitk_nb<BT, 4, kSwiGlu>(g, grid, stream);
-    case 5: return launch_splitk_nb<BT, 5, kSwiGlu>(g, grid, stream);
-    case 6: return launch_splitk_nb<BT, 6, kSwiGlu>(g, grid, stream);
-    case 7: return launch_splitk_nb<BT, 7, kSwiGlu>(g, grid, stream);
-    case 8: return launch_splitk_nb<BT, 8, kSwiGlu>(g, grid, stream);
+    case 1: return launch_splitk_nb<BT, 1, kAMode>(g, grid, stream);
+    case 2: return launch_splitk_nb<BT, 2, kAMode>(g, grid, stream);
+    case 3: return launch_splitk_nb<BT, 3, kAMode>(g, grid, stream);
+    case 4: return launch_splitk_nb<BT, 4, kAMode>(g, grid, stream);
+    case 5: return launch_splitk_nb<BT, 5, kAMode>(g, grid, stream);
+    case 6: return launch_splitk_nb<BT, 6, kAMode>(g, grid, stream);
+    case 7: return launch_splitk_nb<BT, 7, kAMode>(g, grid, stream);
+    case 8: return launch_splitk_nb<BT, 8, kAMode>(g, grid, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <int kAMode>
+hipError_t launch_splitk_mode(const SplitKArgs& g, dim3 grid, hipStream_t stream) {
+  return g.m <= 16 ? launch_splitk_bt<1, kAMode>(g, grid, stream) : launch_splitk_bt<2, kAMode>(g, grid, stream);
 }
 }  // namespace
 
@@ -422,12 +493,19 @@ hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream) {
       g.k % g.kc != 0)
     return hipErrorInvalidValue;
   const dim3 grid((g.n + kSplitRows - 1) / kSplitRows, g.k / g.kc);
+  if (g.attn_part) {
+    if (!splitk_combine_supported(g.m, g.kc, g.attn_splits, g.d) || g.hkv <= 0 || g.hq % g.hkv != 0 ||
+        g.k != g.hq * g.d)
+      return hipErrorInvalidValue;
+    return g.attn_splits <= 4 ? launch_splitk_mode<kACombine4>(g, grid, stream)
+                              : launch_splitk_mode<kACombine8>(g, grid, stream);
+  }
   if (g.gu) {
     if (!splitk_swiglu_supported(g.m, g.kc, g.gu_splits)) return hipErrorInvalidValue;
-    return g.m <= 16 ? launch_splitk_bt<1, true>(g, grid, stream) : launch_splitk_bt<2, true>(g, grid, stream);
+    return launch_splitk_mode<kASwiGlu>(g, grid, stream);
   }
   if (g.lda < g.k || g.lda % 4 != 0) return hipErrorInvalidValue;
-  return g.m <= 16 ? launch_splitk_bt<1, false>(g, grid, stream) : launch_splitk_bt<2, false>(g, grid, stream);
+  return launch_splitk_mode<kAPlain>(g, grid, stream);
 }
 
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,

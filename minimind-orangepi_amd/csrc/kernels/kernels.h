@@ -258,6 +258,14 @@ struct SplitKArgs {
   // (the gate_up partials, [gu_splits][m][2k]); a and lda are unused.
   const float* gu = nullptr;
   int gu_splits = 0;
+  // Attention-combine input: when attn_part is set, row r of A is sequence
+  // r's attention output merged from its split partials (the layout of
+  // attn_o_offset / attn_ml_offset, attn_splits splits, attn_part_stride
+  // floats per sequence); a, lda and gu are unused.
+  const float* attn_part = nullptr;
+  int attn_splits = 0;
+  int64_t attn_part_stride = 0;
+  int hq = 0, hkv = 0, d = 0;
 };
 // K chunk (a multiple of 32 that divides k, at most 256; 0 when k is not a
 // multiple of 32); splits = k / kc.
@@ -265,6 +273,9 @@ int splitk_chunk(int n, int k);
 // Whether launch_gemm_splitk takes SwiGLU input for m rows, chunk kc and
 // gu_splits gate_up partials (the staging loads must fit in registers).
 bool splitk_swiglu_supported(int m, int kc, int gu_splits);
+// Whether launch_gemm_splitk takes attention-combine input for m rows, chunk
+// kc, attn_splits splits and head_dim d.
+bool splitk_combine_supported(int m, int kc, int attn_splits, int d);
 hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream);
 // h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]).
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,

@@ -9,8 +9,9 @@
 // partial sums the next kernel adds in split order.  Step kernels:
 //   embed rows of seq[b][pos[b]] -> input RMSNorm rows
 //   per layer: QKV split-K -> paged split attention (sums the QKV partials;
-//              q/k norm, RoPE at pos[b], K/V append) -> combine -> O split-K
-//              -> residual add + post RMSNorm -> gate_up split-K -> down
+//              q/k norm, RoPE at pos[b], K/V append) -> O split-K whose
+//              staging merges the attention splits -> residual add + post
+//              RMSNorm -> gate_up split-K -> down
 //              split-K whose staging sums the gate_up partials and applies
 //              SwiGLU -> residual add + next RMSNorm
 //   lm_head split-K -> logits -> per-sequence argmax + bookkeeping
@@ -144,6 +145,35 @@ int project(const BatchDeviceState& s, const float* x, const __half* w, int n, i
   return 1;
 }
 
+// The O projection of the attention output: the split-K staging merges the
+// attention split partials itself where its registers allow (up to 8 splits),
+// else the combine kernel writes attn first.
+int project_combine(const BatchDeviceState& s, int splits, const __half* w, int n, int hq, int hkv, int d) {
+  const int B = static_cast<int>(s.batch);
+  const int k = hq * d;
+  const int kc = B <= 32 ? proj_chunk(n, k, 0) : 0;
+  if (kc > 0 && mmr::splitk_combine_supported(B, kc, splits, d)) {
+    mmr::SplitKArgs g;
+    g.attn_part = s.part;
+    g.attn_splits = splits;
+    g.attn_part_stride = s.part_stride;
+    g.hq = hq;
+    g.hkv = hkv;
+    g.d = d;
+    g.w = w;
+    g.part = s.proj;
+    g.m = B;
+    g.n = n;
+    g.k = k;
+    g.kc = kc;
+    check_hip(mmr::launch_gemm_splitk(g, s.stream), "batch split-K gemm (attention-combine input)");
+    return k / kc;
+  }
+  check_hip(mmr::launch_attention_combine(s.part, hq, hkv, d, splits, s.attn, s.stream, B, s.part_stride),
+            "batch attention combine");
+  return project(s, s.attn, w, n, k, 0);
+}
+
 // The down projection of SwiGLU(gate_up partials): the split-K staging sums
 // the partials and applies SwiGLU itself where its registers allow, else the
 // SwiGLU kernel writes act first.
@@ -209,9 +239,7 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
     t.page_table = s.page_table;
     t.pages_per_seq = static_cast<int>(s.pages_per_seq);
     check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "batch attention");
-    check_hip(mmr::launch_attention_combine(s.part, Hq, Hkv, D, splits, s.attn, s.stream, B, s.part_stride),
-              "batch attention combine");
-    const int o_parts = project(s, s.attn, Ld.o, H, Hq * D, 0);
+    const int o_parts = project_combine(s, splits, Ld.o, H, Hq, Hkv, D);
     check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, o_parts, B, H, Ld.post_norm, c.rms_norm_eps, s.x, false,
                                               s.stream),
               "batch residual + post norm");

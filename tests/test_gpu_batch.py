@@ -4,8 +4,8 @@ the token ids the single-sequence path produces for it alone (which equal the
 reference CPU path), with logits within the bound.
 
 Bound: max |batch - single| / max |single| <= 1e-4 for logits (the batch runs
-its projections as GEMMs on the fp32 matrix cores, the single path as GEMVs);
-token ids exact.
+its projections as split-K GEMMs on the fp16 matrix cores with a hi/lo split
+of the fp32 activations, the single path as GEMVs); token ids exact.
 """
 from __future__ import annotations
 
@@ -53,6 +53,29 @@ def test_batch_matches_single_sequences(gpu, kv):
         ref_seq, ref_logits = single_sequence(mmr, m, p, last, cap, kvd)
         got = bs.read_sequence(b, 0, last + 1)
         np.testing.assert_array_equal(got, ref_seq, err_msg=f"sequence {b}")
+        assert rel_err(bs.read_logits(b), ref_logits) < 1e-4, b
+
+
+def test_batch_long_context_split_paths(gpu):
+    # positions up to 1150: the attention split count per sequence steps
+    # through 1, 2, 4, 8 and 16, so the O projection's staging merges 1-4 and
+    # 5-8 split partials itself and hands 16 to the combine kernel
+    mmr = gpu
+    print("[case] batch mini long context", flush=True)
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    rng = np.random.default_rng(5)
+    lengths = [20, 3]
+    prompts = [[int(t) for t in rng.integers(0, g["config"]["vocab_size"], n)] for n in lengths]
+    cap, steps = 1200, 1130
+    bs = m.make_batch_state(len(prompts), cap, mmr.KV_F16)
+    bs.prefill(prompts)
+    bs.decode(steps)
+    bs.synchronize()
+    last = max(lengths) + steps
+    for b, p in enumerate(prompts):
+        ref_seq, ref_logits = single_sequence(mmr, m, p, last, cap, mmr.KV_F16)
+        np.testing.assert_array_equal(bs.read_sequence(b, 0, last + 1), ref_seq, err_msg=f"sequence {b}")
         assert rel_err(bs.read_logits(b), ref_logits) < 1e-4, b
 
 
