@@ -76,6 +76,80 @@ __global__ __launch_bounds__(kBatchThreads) void batch_argmax_kernel(const float
   }
 }
 
+// Head of the batched step: logits[b] = sum_s part[s][b] (split order, at
+// most kHeadParts partials, all loads issued first), then the first-index
+// argmax and the same bookkeeping as batch_argmax_kernel.  One block of
+// kHeadThreads per sequence, kHeadPer logits per thread per pass.
+constexpr int kHeadThreads = 1024;
+constexpr int kHeadPer = 8;
+constexpr int kHeadParts = 4;
+
+__global__ __launch_bounds__(kHeadThreads) void batch_head_kernel(const float* part, int splits, int batch, int vocab,
+                                                                  float* logits, int32_t* token_out, int32_t* seq,
+                                                                  int seq_stride, int32_t* pos,
+                                                                  const int32_t* prompt_len, int seq_len) {
+  __shared__ float s_val[kHeadThreads / kWave];
+  __shared__ int s_idx[kHeadThreads / kWave];
+  const int b = blockIdx.x;
+  const int64_t sstride = static_cast<int64_t>(batch) * vocab;
+  const float* src = part + static_cast<int64_t>(b) * vocab;
+  float* row = logits + static_cast<int64_t>(b) * vocab;
+  float best = -INFINITY;
+  int best_i = 0x7fffffff;
+  for (int base = 0; base < vocab; base += kHeadThreads * kHeadPer) {  // block-uniform
+    float pv[kHeadPer][kHeadParts];
+#pragma unroll
+    for (int e = 0; e < kHeadPer; ++e) {
+      const int i = min(base + static_cast<int>(threadIdx.x) + e * kHeadThreads, vocab - 1);
+#pragma unroll
+      for (int sp = 0; sp < kHeadParts; ++sp) pv[e][sp] = src[min(sp, splits - 1) * sstride + i];
+    }
+#pragma unroll
+    for (int e = 0; e < kHeadPer; ++e) {
+      const int i = base + static_cast<int>(threadIdx.x) + e * kHeadThreads;
+      float v = 0.0f;
+#pragma unroll
+      for (int sp = 0; sp < kHeadParts; ++sp)
+        if (sp < splits) v += pv[e][sp];
+      if (i < vocab) {
+        row[i] = v;
+        if (argmax_better(v, i, best, best_i)) {
+          best = v;
+          best_i = i;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(best_i, off);
+    if (argmax_better(ov, oi, best, best_i)) {
+      best = ov;
+      best_i = oi;
+    }
+  }
+  if (threadIdx.x % kWave == 0) {
+    s_val[threadIdx.x / kWave] = best;
+    s_idx[threadIdx.x / kWave] = best_i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kHeadThreads / kWave; ++w)
+      if (argmax_better(s_val[w], s_idx[w], best, best_i)) {
+        best = s_val[w];
+        best_i = s_idx[w];
+      }
+    const int next = best_i < vocab ? best_i : 0;
+    if (token_out) token_out[b] = next;
+    if (pos) {
+      const int p = pos[b];
+      if (p + 1 < seq_len && p + 1 >= prompt_len[b]) seq[static_cast<int64_t>(b) * seq_stride + p + 1] = next;
+      pos[b] = p + 1;
+    }
+  }
+}
+
 // Split-K skinny GEMM (m <= 32 rows of A) on the fp16 matrix cores.
 // Block = 4 waves x 16 rows of W (64 rows) x one K chunk [k0, k0 + 32 NB)
 // (chunks tile K exactly).  The chunk of A is staged once in LDS as two fp16
@@ -396,6 +470,20 @@ hipError_t launch_batch_embed(const __half* embed, const int32_t* seq, int seq_s
   if (batch <= 0 || hidden <= 0) return hipErrorInvalidValue;
   const dim3 grid((hidden + kBatchThreads - 1) / kBatchThreads, batch);
   batch_embed_kernel<<<grid, kBatchThreads, 0, stream>>>(embed, seq, seq_stride, pos, vocab, hidden, h);
+  return hipGetLastError();
+}
+
+hipError_t launch_batch_head(const float* part, int splits, int vocab, int batch, float* logits, int32_t* token_out,
+                             int32_t* seq, int seq_stride, int32_t* pos, const int32_t* prompt_len, int seq_len,
+                             hipStream_t stream) {
+  if (batch <= 0 || vocab <= 0 || splits < 1) return hipErrorInvalidValue;
+  if (splits > kHeadParts) {
+    const hipError_t e = launch_batch_sum_parts(part, splits, batch, vocab, logits, stream);
+    if (e != hipSuccess) return e;
+    return launch_batch_argmax(logits, vocab, batch, token_out, seq, seq_stride, pos, prompt_len, seq_len, stream);
+  }
+  batch_head_kernel<<<batch, kHeadThreads, 0, stream>>>(part, splits, batch, vocab, logits, token_out, seq, seq_stride,
+                                                       pos, prompt_len, seq_len);
   return hipGetLastError();
 }
 

@@ -284,6 +284,11 @@ hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, i
 hipError_t launch_batch_swiglu(const float* part, int splits, int batch, int f, float* act, hipStream_t stream);
 // out[b][i] = sum_s part[s][b][i].
 hipError_t launch_batch_sum_parts(const float* part, int splits, int batch, int n, float* out, hipStream_t stream);
+// logits[b] = sum_s part[s][b] (lm_head split-K partials), then the batch
+// argmax with its bookkeeping (one kernel for up to 4 partials).
+hipError_t launch_batch_head(const float* part, int splits, int vocab, int batch, float* logits, int32_t* token_out,
+                             int32_t* seq, int seq_stride, int32_t* pos, const int32_t* prompt_len, int seq_len,
+                             hipStream_t stream);
 
 // ------------------------------------------------------------- support ----
 hipError_t launch_rms_norm_rows(const float* in, const float* w, float eps, int rows, int cols, float* out,

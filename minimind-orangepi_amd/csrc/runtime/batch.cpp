@@ -14,7 +14,8 @@
 //              RMSNorm -> gate_up split-K -> down
 //              split-K whose staging sums the gate_up partials and applies
 //              SwiGLU -> residual add + next RMSNorm
-//   lm_head split-K -> logits -> per-sequence argmax + bookkeeping
+//   lm_head split-K -> logits (sums the partials) + per-sequence argmax +
+//   bookkeeping
 // captured once per attention split count into a hipGraph.
 //
 // KV cache: per layer a pool of 64-token pages [page][Hkv][64][d]; sequence
@@ -252,10 +253,9 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
               "batch residual + norm");
   }
   const int lm_parts = project(s, s.x, m.lm_head, V, H, 0);
-  check_hip(mmr::launch_batch_sum_parts(s.proj, lm_parts, B, V, s.logits, s.stream), "batch logits");
-  check_hip(mmr::launch_batch_argmax(s.logits, V, B, s.token_out, s.seq, seq_stride, s.pos, s.prompt_len,
-                                     seq_stride, s.stream),
-            "batch argmax");
+  check_hip(mmr::launch_batch_head(s.proj, lm_parts, V, B, s.logits, s.token_out, s.seq, seq_stride, s.pos,
+                                   s.prompt_len, seq_stride, s.stream),
+            "batch logits + argmax");
 }
 
 // Floats of one projection's partial set: splits * batch * n.
