@@ -88,10 +88,17 @@ void require_size(const std::vector<float>& v, int64_t expected, const std::stri
   if (static_cast<int64_t>(v.size()) != expected) throw std::invalid_argument(name + " has invalid size");
 }
 
+// Up to kPrologueTiles tiles the step keeps 16 splits (two tiles for some
+// blocks, the next one prefetched), so the O-projection prologue merges them
+// and no combine kernel runs; beyond, one tile per split.  Measured per step
+// (MiniMind2, f32 KV): 1024 keys 386 -> 368 us with the 16-split cap, 2048 keys
+// 391 us with one tile per split against 405 us capped.
+constexpr int64_t kPrologueTiles = 24;
+
 int choose_splits(int64_t n_keys, int tile) {
   const int64_t n_tiles = (n_keys + tile - 1) / tile;
   for (int s : kSplitBuckets)
-    if (s >= n_tiles) return s;
+    if (s >= n_tiles || (n_tiles <= kPrologueTiles && s >= mmr::kCombineMaxSplits)) return s;
   return kMaxSplits;
 }
 
