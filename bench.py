@@ -2,7 +2,7 @@
 """Decode throughput of the MiniMind2 gfx950 runtime.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f32|f16] [--no-cpu-baseline]
-                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--no-attention-sweep] [--batch 32]
+                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--no-attention-sweep] [--no-context-sweep] [--batch 32]
                     [--batch-context 4096] [--traffic-probe N]
 
 Workload: MiniMind2 dense (hidden 768, 16 layers, 8/2 heads, d 96, FFN 2048,
@@ -20,6 +20,8 @@ The same line carries
   * gemv_sweep / attention_sweep: BASELINE configs[1] GEMV shapes and
     configs[2] attention contexts alone through the C ABI, MALL-resident and
     HBM-streaming;
+  * decode_context_sweep: the whole decode step at the configs[2] context
+    lengths (1024 / 4096 / 8192 tokens);
   * batched: BASELINE configs[4], 32 sequences with 256-token prompts decoded
     in lockstep to 4096 positions over a paged fp16 KV cache (aggregate tok/s,
     p50 / p90 step latency);
@@ -187,6 +189,33 @@ def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
     return out
 
 
+DECODE_CONTEXTS = (1024, 4096, 8192)
+
+
+def decode_context_sweep(mmr, model, kv, steps: int = 64) -> dict:
+    """The batch-1 decode step at the configs[2] context lengths: a prompt of T
+    uniform tokens (chunked GEMM prefill), 8 warm steps, then `steps` timed
+    hipGraph-replayed steps (HIP events on the decode stream)."""
+    rng = np.random.default_rng(12)
+    out = {}
+    for T in DECODE_CONTEXTS:
+        prompt = [int(t) for t in rng.integers(0, MINIMIND2["vocab_size"], T)]
+        st = model.make_state(T + steps + 16, kv)
+        st.enqueue_prefill(prompt)
+        st.enqueue_decode(8)
+        st.synchronize()
+        ev = [mmr.Event() for _ in range(2)]
+        ev[0].record(st.stream)
+        st.enqueue_decode(steps)
+        ev[1].record(st.stream)
+        st.synchronize()
+        ms = ev[0].elapsed_ms(ev[1])
+        out[str(T)] = {"us_per_step": round(ms * 1e3 / steps, 1), "tok_s": round(steps / (ms * 1e-3), 1)}
+        log(f"decode at context {T}: {out[str(T)]['us_per_step']} us/step, {out[str(T)]['tok_s']} tok/s")
+        del st
+    return out
+
+
 def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
     """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: the dominant
     kernel alone -- gate_up GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU
@@ -291,6 +320,7 @@ def main() -> int:
     ap.add_argument("--copy-probe-mib", type=int, default=256)
     ap.add_argument("--no-gemv-sweep", action="store_true")
     ap.add_argument("--no-attention-sweep", action="store_true")
+    ap.add_argument("--no-context-sweep", action="store_true")
     ap.add_argument("--batch", type=int, default=32, help="configs[4] batch size (0: skip the batched run)")
     ap.add_argument("--batch-context", type=int, default=4096)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
@@ -405,6 +435,7 @@ def main() -> int:
 
     sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
     attn_sweep = None if args.no_attention_sweep else attention_sweep(mmr, mmr.Stream(stream), ev)
+    ctx_sweep = None if args.no_context_sweep else decode_context_sweep(mmr, model, kv)
     batched = batched_decode(mmr, model, args.batch, 256, args.batch_context) if args.batch > 0 else None
 
     traffic = None
@@ -444,6 +475,7 @@ def main() -> int:
         "copy_probe": copy_probe,
         "gemv_sweep": sweep,
         "attention_sweep": attn_sweep,
+        "decode_context_sweep": ctx_sweep,
         "batched": batched,
         "launch_mode": "eager (--no-graph)" if args.no_graph else "hipGraph replay",
         "roofline": {"bound": "hbm", "kernel": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",
