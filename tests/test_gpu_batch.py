@@ -79,6 +79,30 @@ def test_batch_long_context_split_paths(gpu):
         assert rel_err(bs.read_logits(b), ref_logits) < 1e-4, b
 
 
+@pytest.mark.parametrize("batch", [17, 40])
+def test_batch_sizes_across_gemm_paths(gpu, batch):
+    # 17 rows: the split-K GEMMs' second 16-row tile is partly filled; 40 rows
+    # (over 32): the projections fall back to the dense GEMM, whose single
+    # "partial" the consumers add, with the separate combine and SwiGLU kernels
+    mmr = gpu
+    print(f"[case] batch mini B={batch}", flush=True)
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    rng = np.random.default_rng(batch)
+    lengths = [int(n) for n in rng.integers(1, 40, batch)]
+    prompts = [[int(t) for t in rng.integers(0, g["config"]["vocab_size"], n)] for n in lengths]
+    cap, steps = 96, 50
+    bs = m.make_batch_state(batch, cap, mmr.KV_F16)
+    bs.prefill(prompts)
+    bs.decode(steps)
+    bs.synchronize()
+    last = max(lengths) + steps
+    for b in (0, batch // 2, batch - 1):
+        ref_seq, ref_logits = single_sequence(mmr, m, prompts[b], last, cap, mmr.KV_F16)
+        np.testing.assert_array_equal(bs.read_sequence(b, 0, last + 1), ref_seq, err_msg=f"sequence {b}")
+        assert rel_err(bs.read_logits(b), ref_logits) < 1e-4, b
+
+
 def test_batch_reproduces_reference_golden(gpu):
     # MiniMind2 (configs[3] weights): sequence 0 holds the cfg3_short prompt,
     # whose greedy continuation is the reference CPU path's golden output
