@@ -198,6 +198,10 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 struct QkvRowsArgs {
   const float* qkv = nullptr;  // [tokens][qkv_stride]
   int qkv_stride = 0;
+  // Split-K partials of the projection: qkv holds qkv_parts (<= kQkvRowsMaxParts)
+  // sets qkv_part_stride floats apart, added in split order.
+  int qkv_parts = 1;
+  int64_t qkv_part_stride = 0;
   const float* q_norm = nullptr;
   const float* k_norm = nullptr;
   float eps = 0.0f;
@@ -211,6 +215,7 @@ struct QkvRowsArgs {
   float* query = nullptr;  // [tokens][query_stride]
   int query_stride = 0;
 };
+constexpr int kQkvRowsMaxParts = 4;
 hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream);
 
 // Causal attention of query rows at positions start .. start + tokens - 1

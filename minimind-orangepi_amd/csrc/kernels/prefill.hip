@@ -330,7 +330,19 @@ __global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
   const float* src = row + (is_q ? head * D : a.hq * D + head * D);
   const float* w = is_q ? a.q_norm : a.k_norm;
   const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
-  float x0 = src[d0], x1 = src[d1];
+  // Sum of the projection's split partials at p[i] (clamped loads, all issued
+  // before the adds, added in split order).
+  auto part_sum = [&](const float* p, int i) {
+    float v[kQkvRowsMaxParts];
+#pragma unroll
+    for (int sp = 0; sp < kQkvRowsMaxParts; ++sp) v[sp] = p[min(sp, a.qkv_parts - 1) * a.qkv_part_stride + i];
+    float x = v[0];
+#pragma unroll
+    for (int sp = 1; sp < kQkvRowsMaxParts; ++sp)
+      if (sp < a.qkv_parts) x += v[sp];
+    return x;
+  };
+  float x0 = part_sum(src, d0), x1 = part_sum(src, d1);
   const float w0 = w[d0], w1 = w[d1];
   const float f = a.inv_freq[min(lane, D / 2 - 1)];
   x0 = lane < D ? x0 : 0.0f;
@@ -359,7 +371,7 @@ __global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
     KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
     for (int i = lane; i < D; i += kWave) {
       kdst[i] = from_float<KV>(x_s[i]);
-      vdst[i] = from_float<KV>(vsrc[i]);
+      vdst[i] = from_float<KV>(part_sum(vsrc, i));
     }
   }
 }
@@ -641,19 +653,34 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, hipStream_t s) {
 
 namespace {
 bool use_skinny(int m, int k) { return m <= 32 && k % 32 == 0 && k >= 32 * kSkinnyWaves; }
+
+// Tiling of a launch_gemm call: the largest tile whose smallest split count
+// reaches kGemmTargetBlocks blocks (1.5 per CU) while every split keeps at
+// least two K tiles; else the smallest tile with as many splits as that
+// allows.  Measured at M = 512: qkv 1152 x 768 15.3 -> 12.6 us (64 x 64, 3
+// splits), o 768 x 768 12.8 -> 9.8 us (32 x 64, 2), down 768 x 2048
+// 21.1 -> 18.8 us (64 x 64, 4), gate_up 4096 x 768 24.9 us unsplit.
+struct GemmTiling {
+  int bm = 32, bn = 32, splits = 1;
+};
+constexpr int64_t kGemmTargetBlocks = 384;
+
+GemmTiling choose_gemm_tiling(int m, int n, int k) {
+  const int nk = (k + kGemmBK - 1) / kGemmBK;
+  const int max_splits = std::max(1, std::min(8, nk / 2));
+  const int tiles[3][2] = {{64, 64}, {32, 64}, {32, 32}};
+  for (const auto& t : tiles) {
+    const int64_t blocks = static_cast<int64_t>((m + t[0] - 1) / t[0]) * ((n + t[1] - 1) / t[1]);
+    const int64_t need = (kGemmTargetBlocks + blocks - 1) / blocks;
+    if (need <= max_splits) return {t[0], t[1], static_cast<int>(need)};
+  }
+  return {32, 32, max_splits};
+}
 }  // namespace
 
 int gemm_k_splits(int m, int n, int k) {
   if (!gemm_supported(m, n, k) || use_skinny(m, k)) return 1;
-  // Tiles as launch_gemm picks them; at 512 or more (two blocks per CU) the
-  // partial-sum traffic costs more than the shorter K loop saves (measured:
-  // gate_up 512 x 4096 x 768 26.5 -> 30.6 us with 2 splits; o 14 -> 11 us and
-  // down 30 -> 23 us with 2 and 4).
-  auto blocks = [&](int bm, int bn) { return static_cast<int64_t>((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
-  const int64_t tiles = blocks(64, 64) >= 256 ? blocks(64, 64) : blocks(32, 64) >= 256 ? blocks(32, 64) : blocks(32, 32);
-  if (tiles >= 512) return 1;
-  const int nk = (k + kGemmBK - 1) / kGemmBK;
-  return std::max(1, std::min(8, (nk + 3) / 4));
+  return choose_gemm_tiling(m, n, k).splits;
 }
 
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
@@ -663,16 +690,27 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
     return hipErrorInvalidValue;
   // Few rows (batched decode): stream W with one block per 16 rows of W.
   if (use_skinny(g.m, g.k)) return g.m <= 16 ? launch_gemm_skinny<1>(g, s) : launch_gemm_skinny<2>(g, s);
-  // The largest tile that still gives every CU a block (256 CUs), else the
-  // smallest tile.
-  auto blocks = [&](int bm, int bn) { return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn); };
+  // Split-K calls with the chooser's split count take its tile.
+  const GemmTiling t = choose_gemm_tiling(g.m, g.n, g.k);
+  if (g.k_splits > 1 && g.k_splits == t.splits) {
+    if (t.bm == 64) return launch_gemm_tile<64, 64>(g, s);
+    if (t.bn == 64) return launch_gemm_tile<32, 64>(g, s);
+    return launch_gemm_tile<32, 32>(g, s);
+  }
+  // Otherwise the largest tile that still gives every CU a block (256 CUs,
+  // counting the K splits), else the smallest tile.
+  auto blocks = [&](int bm, int bn) {
+    return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn) * g.k_splits;
+  };
   if (blocks(64, 64) >= 256) return launch_gemm_tile<64, 64>(g, s);
   if (blocks(32, 64) >= 256) return launch_gemm_tile<32, 64>(g, s);
   return launch_gemm_tile<32, 32>(g, s);
 }
 
 hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream) {
-  if (!attention_supported(a.hq, a.hkv, a.d) || a.tokens <= 0) return hipErrorInvalidValue;
+  if (!attention_supported(a.hq, a.hkv, a.d) || a.tokens <= 0 || a.qkv_parts < 1 ||
+      a.qkv_parts > kQkvRowsMaxParts || (a.qkv_parts > 1 && a.qkv_part_stride < int64_t{a.tokens} * a.qkv_stride))
+    return hipErrorInvalidValue;
   return kv == kKvF16 ? launch_qkv_rows_kv<__half>(a, stream) : launch_qkv_rows_kv<float>(a, stream);
 }
 

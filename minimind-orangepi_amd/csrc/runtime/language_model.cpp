@@ -56,10 +56,9 @@ struct DeviceState {
   int64_t pf_chunk = 0;
   float* pf_h = nullptr;    // [chunk][H] residual stream
   float* pf_x = nullptr;    // [chunk][H] normalised rows
-  float* pf_qkv = nullptr;  // [chunk][(Hq + 2 Hkv) d]
   float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
   float* pf_attn = nullptr; // [chunk][Hq d]
-  float* pf_part = nullptr; // split-K partials of the O, gate_up or down GEMM: [splits][chunk][N]
+  float* pf_part = nullptr; // split-K partials of one GEMM (QKV, O, gate_up or down): [splits][chunk][N]
   float* pf_act = nullptr;  // [chunk][F]
   bool prefill_tokenwise = false;  // prefill through the decode step instead of the GEMM path
   hipStream_t stream = nullptr;
@@ -296,13 +295,12 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   int64_t part_f = 0;
   if (C > 0) {
     const int ci = static_cast<int>(C);
-    const int64_t shapes[3][2] = {{H, Hq * D}, {2 * F, H}, {H, F}};
+    const int64_t shapes[4][2] = {{qkv_w, H}, {H, Hq * D}, {2 * F, H}, {H, F}};
     for (const auto& sh : shapes)
       part_f = std::max<int64_t>(
           part_f, int64_t{mmr::gemm_k_splits(ci, static_cast<int>(sh[0]), static_cast<int>(sh[1]))} * C * sh[0]);
     ar.plan(C * H * 4);
     ar.plan(C * H * 4);
-    ar.plan(C * qkv_w * 4);
     ar.plan(C * Hq * D * 4);
     ar.plan(C * Hq * D * 4);
     ar.plan(part_f * 4);
@@ -330,7 +328,6 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   if (C > 0) {
     s->pf_h = ar.take<float>(C * H);
     s->pf_x = ar.take<float>(C * H);
-    s->pf_qkv = ar.take<float>(C * qkv_w);
     s->pf_q = ar.take<float>(C * Hq * D);
     s->pf_attn = ar.take<float>(C * Hq * D);
     s->pf_part = ar.take<float>(part_f);
@@ -512,22 +509,10 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
   const int rows = static_cast<int>(n);
   check_hip(mmr::launch_embedding_gather(m.embed, s.seq + start, rows, V, H, s.pf_h, s.err, s.stream),
             "prefill embedding");
-  // Dense GEMM into out (QKV), or split-K partial products into pf_part
-  // (returns the split count) for the O / gate_up / down projections, whose
-  // consumers add the partials: residual add + RMSNorm, or SwiGLU.
-  auto gemm_dense = [&](const float* a, int lda, const __half* w, int N, int K, float* out) {
-    mmr::GemmArgs g;
-    g.a = a;
-    g.lda = lda;
-    g.w = w;
-    g.c = out;
-    g.ldc = N;
-    g.m = rows;
-    g.n = N;
-    g.k = K;
-    check_hip(mmr::launch_gemm(g, s.stream), "prefill gemm");
-  };
-  auto gemm_parts = [&](const float* a, int lda, const __half* w, int N, int K) {
+  // Split-K partial products into pf_part (at most max_splits; returns the
+  // split count, 1 = the dense product); the consumers add the partials:
+  // q/k norm + RoPE + KV write, residual add + RMSNorm, or SwiGLU.
+  auto gemm_parts = [&](const float* a, int lda, const __half* w, int N, int K, int max_splits) {
     mmr::GemmArgs g;
     g.a = a;
     g.lda = lda;
@@ -537,11 +522,12 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     g.m = rows;
     g.n = N;
     g.k = K;
-    g.k_splits = mmr::gemm_k_splits(rows, N, K);
+    g.k_splits = std::min(mmr::gemm_k_splits(rows, N, K), max_splits);
     g.split_stride = static_cast<int64_t>(rows) * N;
-    check_hip(mmr::launch_gemm(g, s.stream), "prefill split-K gemm");
+    check_hip(mmr::launch_gemm(g, s.stream), "prefill gemm");
     return g.k_splits;
   };
+  constexpr int kAnySplits = 1 << 30;
   const size_t L = m.layers.size();
   // Layer 0's input norm; later layers get theirs from the previous layer's
   // residual consumer.
@@ -549,10 +535,12 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
             "prefill input norm");
   for (size_t l = 0; l < L; ++l) {
     const LayerDev& Ld = m.layers[l];
-    gemm_dense(s.pf_x, H, Ld.qkv, qkv_w, H, s.pf_qkv);
+    const int sq = gemm_parts(s.pf_x, H, Ld.qkv, qkv_w, H, mmr::kQkvRowsMaxParts);
     mmr::QkvRowsArgs q;
-    q.qkv = s.pf_qkv;
+    q.qkv = s.pf_part;
     q.qkv_stride = qkv_w;
+    q.qkv_parts = sq;
+    q.qkv_part_stride = static_cast<int64_t>(rows) * qkv_w;
     q.q_norm = Ld.q_norm;
     q.k_norm = Ld.k_norm;
     q.eps = c.rms_norm_eps;
@@ -582,13 +570,13 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     at.out = s.pf_attn;
     at.out_stride = Hq * D;
     check_hip(mmr::launch_prefill_attention(at, s.kv, s.stream), "prefill attention");
-    const int so = gemm_parts(s.pf_attn, Hq * D, Ld.o, H, Hq * D);
+    const int so = gemm_parts(s.pf_attn, Hq * D, Ld.o, H, Hq * D, kAnySplits);
     check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, s.pf_x,
                                               false, s.stream),
               "prefill residual + post norm");
-    const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H);
+    const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H, kAnySplits);
     check_hip(mmr::launch_batch_swiglu(s.pf_part, sg, rows, F, s.pf_act, s.stream), "prefill swiglu");
-    const int sd = gemm_parts(s.pf_act, F, Ld.down, H, F);
+    const int sd = gemm_parts(s.pf_act, F, Ld.down, H, F, kAnySplits);
     // The next layer's input norm (after the last layer: the final norm, whose
     // rows are not used; the head normalises the last row itself).
     const bool last = l + 1 == L;
