@@ -185,11 +185,16 @@ struct GemmArgs {
   // split z to c + z * split_stride, over its contiguous range of K tiles.
   int k_splits = 1;
   int64_t split_stride = 0;
+  // SwiGLU epilogue over interleaved gate/up columns: c receives
+  // act[m][n / 2] (row stride ldc); needs k_splits == 1 and no residual.
+  bool swiglu = false;
 };
 bool gemm_supported(int m, int n, int k);
 // Split count launch_gemm accepts and uses well for this shape: about four
 // 128-wide K tiles per split; 1 where the few-rows path applies.
 int gemm_k_splits(int m, int n, int k);
+// Whether launch_gemm takes the SwiGLU epilogue for this shape (unsplit tiles).
+bool gemm_swiglu_supported(int m, int n, int k);
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Rows of the fused qkv projection for tokens at positions start ..

@@ -130,8 +130,14 @@ struct GemmStage {
 // fp16; hi + lo carries ~22 significant bits of each activation.  The LDS
 // footprint (~52 KB for 64 x 64) lets two or three blocks share a CU, which
 // hides one block's tile-load wait behind another's work.
-template <int BM, int BN, bool kResidual>
+// Epilogues of gemm_f16w_kernel: store C; add the residual; SwiGLU over the
+// interleaved gate/up columns (2i, 2i + 1) -> act[m][i] (decoder_layer.cpp:
+// 175-182), the pair meeting through one lane exchange.
+constexpr int kGemmEpiStore = 0, kGemmEpiResidual = 1, kGemmEpiSwiGlu = 2;
+
+template <int BM, int BN, int kEpi>
 __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
+  constexpr bool kResidual = kEpi == kGemmEpiResidual;
   constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
   static_assert(GemmStage<BM, BN>::kA >= 1 && GemmStage<BM, BN>::kB >= 1, "tile too small for the block");
   __shared__ __align__(16) _Float16 Ah[BM][kGemmLDH];
@@ -228,8 +234,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
-        if (row < g.m && col < g.n) {
-          const float v = acc[i][j][r];
+        const float v = acc[i][j][r];
+        if constexpr (kEpi == kGemmEpiSwiGlu) {
+          // Even lanes hold gate column 2i, their odd neighbours up column 2i + 1.
+          const float u = __shfl_xor(v, 1);
+          if ((lane & 1) == 0 && row < g.m && col < g.n)
+            out[static_cast<int64_t>(row) * g.ldc + col / 2] = (v / (1.0f + expf(-v))) * u;
+        } else if (row < g.m && col < g.n) {
           out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
         }
       }
@@ -599,10 +610,12 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
 template <int BM, int BN>
 hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
   const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.k_splits);
-  if (g.residual) {
-    gemm_f16w_kernel<BM, BN, true><<<grid, kGemmThreads, 0, s>>>(g);
+  if (g.swiglu) {
+    gemm_f16w_kernel<BM, BN, kGemmEpiSwiGlu><<<grid, kGemmThreads, 0, s>>>(g);
+  } else if (g.residual) {
+    gemm_f16w_kernel<BM, BN, kGemmEpiResidual><<<grid, kGemmThreads, 0, s>>>(g);
   } else {
-    gemm_f16w_kernel<BM, BN, false><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiStore><<<grid, kGemmThreads, 0, s>>>(g);
   }
   return hipGetLastError();
 }
@@ -683,8 +696,15 @@ int gemm_k_splits(int m, int n, int k) {
   return choose_gemm_tiling(m, n, k).splits;
 }
 
+bool gemm_swiglu_supported(int m, int n, int k) {
+  return gemm_supported(m, n, k) && !use_skinny(m, k) && n % 2 == 0 && choose_gemm_tiling(m, n, k).splits == 1;
+}
+
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
-  if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < g.n) return hipErrorInvalidValue;
+  if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < (g.swiglu ? g.n / 2 : g.n))
+    return hipErrorInvalidValue;
+  if (g.swiglu && (g.k_splits != 1 || g.residual || !gemm_swiglu_supported(g.m, g.n, g.k)))
+    return hipErrorInvalidValue;
   if (g.k_splits < 1 || (g.k_splits > 1 && (g.residual || g.split_stride < static_cast<int64_t>(g.m) * g.ldc ||
                                             g.k_splits > gemm_k_splits(g.m, g.n, g.k))))
     return hipErrorInvalidValue;

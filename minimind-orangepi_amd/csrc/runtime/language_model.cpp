@@ -574,8 +574,22 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, s.pf_x,
                                               false, s.stream),
               "prefill residual + post norm");
-    const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H, kAnySplits);
-    check_hip(mmr::launch_batch_swiglu(s.pf_part, sg, rows, F, s.pf_act, s.stream), "prefill swiglu");
+    if (mmr::gemm_swiglu_supported(rows, 2 * F, H)) {  // SwiGLU in the gate_up epilogue
+      mmr::GemmArgs g;
+      g.a = s.pf_x;
+      g.lda = H;
+      g.w = Ld.gate_up;
+      g.c = s.pf_act;
+      g.ldc = F;
+      g.m = rows;
+      g.n = 2 * F;
+      g.k = H;
+      g.swiglu = true;
+      check_hip(mmr::launch_gemm(g, s.stream), "prefill gate_up + SwiGLU");
+    } else {
+      const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H, kAnySplits);
+      check_hip(mmr::launch_batch_swiglu(s.pf_part, sg, rows, F, s.pf_act, s.stream), "prefill swiglu");
+    }
     const int sd = gemm_parts(s.pf_act, F, Ld.down, H, F, kAnySplits);
     // The next layer's input norm (after the last layer: the final norm, whose
     // rows are not used; the head normalises the last row itself).
