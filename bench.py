@@ -433,6 +433,20 @@ def main() -> int:
         src.free()
         dst.free()
 
+    # Prefill alone, repeated on the reset state (its decode results were read
+    # above): the median of 8 runs, since one run varies by a few percent.
+    pf = []
+    for _ in range(8):
+        state.reset()
+        mmr.synchronize()
+        ev[0].record(stream)
+        state.enqueue_prefill(prompt)
+        ev[1].record(stream)
+        state.synchronize()
+        pf.append(ev[0].elapsed_ms(ev[1]))
+    prefill_tok_s = PROMPT_LEN / (float(np.median(pf)) / 1e3)
+    log(f"prefill: median of 8 runs {np.median(pf):.3f} ms -> {prefill_tok_s:.1f} tok/s")
+
     sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
     attn_sweep = None if args.no_attention_sweep else attention_sweep(mmr, mmr.Stream(stream), ev)
     ctx_sweep = None if args.no_context_sweep else decode_context_sweep(mmr, model, kv)
