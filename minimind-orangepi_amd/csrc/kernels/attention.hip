@@ -18,9 +18,11 @@
 // q/k/v and the RoPE frequencies are all issued before the device position
 // arrives; RoPE angles are float(pos) * inv_freq with inv_freq from the host
 // (the reference formula) and cos/sin evaluated on the device.
-//   1. q RMSNorm + RoPE into LDS; the block holding the new token also
+//   1. q RMSNorm + RoPE in registers (a wave per head, a lane per RoPE
+//      pair), then into LDS; the block holding the new token also
 //      normalises/rotates its k, rounds k and v to the cache dtype and appends
-//      them (fused mode);
+//      them (fused mode).  The first tile's staging barrier is the only one
+//      before the scores;
 //   2. per tile: scores q.k / sqrt(d) with one lane per token, online softmax
 //      with one wave per query head, P.V with one lane per dimension pair;
 //   3. the block writes its (max, sum, o[d]) partial per head; splits with no
@@ -53,29 +55,20 @@ __device__ __forceinline__ void chunk_to_float<float>(const uint4& c, float* dst
   dst[3] = __uint_as_float(c.w);
 }
 
-// Per-head RMSNorm (decoder_layer.cpp:32-42, x * (scale * w)) of values held
-// as (x0 at dim lane, x1 at dim lane + 64; zero outside d) with gains
-// (w0, w1) at the same dims, into dst; executed by one wave.
+// One head in registers, one wave: lane i < d/2 holds the RoPE pair
+// (x0 = x[i], x1 = x[i + d/2]) and the gains at the same dims (lanes past d/2
+// hold zeros).  Per-head RMSNorm (decoder_layer.cpp:32-42, x * (scale * w)),
+// then rotate-half RoPE with the pair's (cos, sin) (decoder_layer.cpp:139-152),
+// in place; no LDS and no barrier.
 template <int D>
-__device__ __forceinline__ void wave_rms_norm_regs(float x0, float x1, float w0, float w1, float eps, float* dst,
-                                                   int lane) {
+__device__ __forceinline__ void wave_norm_rope_pair(float& x0, float& x1, float w0, float w1, float eps, float c,
+                                                    float s) {
   const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
   const float scale = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-  if (lane < D) dst[lane] = x0 * (scale * w0);
-  if (lane + kWave < D) dst[lane + kWave] = x1 * (scale * w1);
-}
-
-// Rotate-half RoPE in place on one head in LDS (decoder_layer.cpp:139-152);
-// lane i < d/2 holds (cos, sin) of pair i.
-template <int D>
-__device__ __forceinline__ void wave_rope(float* x, float c, float s, int lane) {
-  constexpr int kHalf = D / 2;
-  if (lane < kHalf) {
-    const float first = x[lane];
-    const float second = x[lane + kHalf];
-    x[lane] = first * c - second * s;
-    x[lane + kHalf] = second * c + first * s;
-  }
+  const float first = x0 * (scale * w0);
+  const float second = x1 * (scale * w1);
+  x0 = first * c - second * s;
+  x1 = second * c + first * s;
 }
 
 __device__ __forceinline__ void pv_fma(float2& acc, float p, const float2& v) {
@@ -140,8 +133,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   __shared__ __align__(16) float p_s[TT][kAttnMaxGroup];  // token-major: one 16-byte read per 4 heads
   __shared__ float alpha_s[kAttnMaxGroup];
   static_assert(kPvGroups * kAttnMaxGroup * D <= TT * LD, "P.V reduction must fit in k_s");
-  __shared__ float knew_s[D];
-  __shared__ float vnew_s[D];
+  static_assert(D / 2 <= kWave, "a wave holds one head as d/2 RoPE pairs");
 
   const int split = blockIdx.x;
   const int g = blockIdx.y;
@@ -179,9 +171,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   int next_page = kv_rows.page_of((split + S) * TT);
   // Loads are unconditional (indices clamped into range, values masked
   // afterwards): a predicated load makes the compiler wait for it before the
-  // branch joins, which would serialise these round trips.
-  const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
-  const bool in0 = lane < D, in1 = lane + kWave < D;
+  // branch joins, which would serialise these round trips.  Lane i < d/2
+  // holds dims (i, i + d/2), the pair RoPE rotates together.
+  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
+  const bool in_pair = lane < D / 2;
   // The batched (paged) path may hand the projection over as up to
   // kAttnMaxQkvParts split-K partials: every part's load is issued (part index
   // clamped, parts past qkv_parts weighted 0) and the parts summed in order.
@@ -218,13 +211,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    qx0[j] = in0 ? qx0[j] : 0.0f;
-    qx1[j] = in1 ? qx1[j] : 0.0f;
+    qx0[j] = in_pair ? qx0[j] : 0.0f;
+    qx1[j] = in_pair ? qx1[j] : 0.0f;
   }
-  kx0 = in0 ? kx0 : 0.0f;
-  vx0 = in0 ? vx0 : 0.0f;
-  kx1 = in1 ? kx1 : 0.0f;
-  vx1 = in1 ? vx1 : 0.0f;
+  kx0 = in_pair ? kx0 : 0.0f;
+  vx0 = in_pair ? vx0 : 0.0f;
+  kx1 = in_pair ? kx1 : 0.0f;
+  vx1 = in_pair ? vx1 : 0.0f;
 
   // ---- 2. extent of the context ----
   int n_keys;
@@ -248,56 +241,44 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   for (int h = 0; h < kAttnMaxGroup; ++h) pacc[h] = make_float2(0.0f, 0.0f);
 
   if (split < n_tiles) {
-    // ---- 3. queries (and the new key/value), RoPE angle from the position ----
+    // ---- 3. queries (and the new key/value), RoPE angle from the position,
+    // all in registers; the first tile's staging barrier publishes q_s ----
     float rc = 1.0f, rs = 0.0f;
     if constexpr (MODE == kAttnFused) {
-      if (lane < D / 2) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
+      if (in_pair) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int h = wave + j * kAttnWaves;
       if (h < R) {
-        if constexpr (MODE == kAttnFused) {
-          wave_rms_norm_regs<D>(qx0[j], qx1[j], qw0, qw1, a.eps, q_s[h], lane);
-        } else {
-          if (lane < D) q_s[h][lane] = qx0[j];
-          if (lane + kWave < D) q_s[h][lane + kWave] = qx1[j];
+        if constexpr (MODE == kAttnFused) wave_norm_rope_pair<D>(qx0[j], qx1[j], qw0, qw1, a.eps, rc, rs);
+        if (in_pair) {
+          q_s[h][d0] = qx0[j];
+          q_s[h][d1] = qx1[j];
         }
       }
     }
     // The new token sits in tile p / TT; only the block owning that tile
-    // appends it.
+    // appends it, from its last wave, which also places the token's row in
+    // that tile's LDS stage.  k and v are rounded to the cache dtype once, so
+    // this step and later steps see the same key/value.
     const bool owns_new = (MODE == kAttnFused) && ((p / TT) % S == split);
     if (owns_new && wave == kAttnWaves - 1) {
-      wave_rms_norm_regs<D>(kx0, kx1, kw0, kw1, a.eps, knew_s, lane);
-      if (lane < D) vnew_s[lane] = vx0;
-      if (lane + kWave < D) vnew_s[lane + kWave] = vx1;
-    }
-    __syncthreads();
-    if constexpr (MODE == kAttnFused) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int h = wave + j * kAttnWaves;
-        if (h < R) wave_rope<D>(q_s[h], rc, rs, lane);
-      }
-      if (owns_new && wave == kAttnWaves - 1) wave_rope<D>(knew_s, rc, rs, lane);
-      // The rounding below reads elements other lanes rotated: barrier first.
-      __syncthreads();
-      if (owns_new && wave == kAttnWaves - 1) {
-        // Round to the cache dtype once, so this step and later steps see the
-        // same key/value.
+      wave_norm_rope_pair<D>(kx0, kx1, kw0, kw1, a.eps, rc, rs);
+      const KV k0 = from_float<KV>(kx0), k1 = from_float<KV>(kx1);
+      const KV v0 = from_float<KV>(vx0), v1 = from_float<KV>(vx1);
+      if (in_pair) {
         KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
         KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
-        for (int i = lane; i < D; i += kWave) {
-          const KV kq = from_float<KV>(knew_s[i]);
-          const KV vq = from_float<KV>(vnew_s[i]);
-          kdst[i] = kq;
-          vdst[i] = vq;
-          knew_s[i] = to_float<KV>(kq);
-          vnew_s[i] = to_float<KV>(vq);
-        }
+        kdst[d0] = k0;
+        kdst[d1] = k1;
+        vdst[d0] = v0;
+        vdst[d1] = v1;
       }
-      __syncthreads();
+      kx0 = to_float<KV>(k0);
+      kx1 = to_float<KV>(k1);
+      vx0 = to_float<KV>(v0);
+      vx1 = to_float<KV>(v1);
     }
 
     const float sqrt_d = sqrtf(static_cast<float>(D));
@@ -347,12 +328,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
           }
         }
       }
-      if (MODE == kAttnFused && p >= t0 && p < t0 + rows) {
+      if (MODE == kAttnFused && p >= t0 && p < t0 + rows && wave == kAttnWaves - 1 && in_pair) {
         const int r = p - t0;
-        for (int i = threadIdx.x; i < D; i += kAttnThreads) {
-          k_s[r][i] = knew_s[i];
-          v_s[r][i] = vnew_s[i];
-        }
+        k_s[r][d0] = kx0;
+        k_s[r][d1] = kx1;
+        v_s[r][d0] = vx0;
+        v_s[r][d1] = vx1;
       }
       // The registers are free again: the next tile's loads overlap this
       // tile's scores and P.V (a compile-time choice: a guarded load would
@@ -551,35 +532,36 @@ __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(cons
   }
 }
 
-// Standalone post-process (reference K2): one wave per head.
+// Standalone post-process (reference K2): one wave per head, lane i < d/2
+// holding the RoPE pair (i, i + d/2).
 template <typename KV, int D>
 __global__ __launch_bounds__(kWave) void qkv_postprocess_kernel(QkvPostArgs a) {
-  __shared__ float x_s[D];
+  static_assert(D / 2 <= kWave, "a wave holds one head as d/2 RoPE pairs");
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const bool is_q = b < a.hq;
   const int head = is_q ? b : b - a.hq;
   const float* src = a.qkv + (is_q ? head * D : a.hq * D + head * D);
   const float* w = is_q ? a.q_norm : a.k_norm;
-  const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
-  const float x0 = lane < D ? src[d0] : 0.0f;
-  const float x1 = lane + kWave < D ? src[d1] : 0.0f;
-  wave_rms_norm_regs<D>(x0, x1, w[d0], w[d1], a.eps, x_s, lane);
+  const bool in_pair = lane < D / 2;
+  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
+  float x0 = in_pair ? src[d0] : 0.0f;
+  float x1 = in_pair ? src[d1] : 0.0f;
   float rc = 1.0f, rs = 0.0f;
-  if (lane < D / 2) sincosf(static_cast<float>(a.position) * a.inv_freq[lane], &rs, &rc);
-  __syncthreads();
-  wave_rope<D>(x_s, rc, rs, lane);
-  __syncthreads();
+  if (in_pair) sincosf(static_cast<float>(a.position) * a.inv_freq[d0], &rs, &rc);
+  wave_norm_rope_pair<D>(x0, x1, w[d0], w[d1], a.eps, rc, rs);
+  if (!in_pair) return;
   if (is_q) {
-    for (int i = lane; i < D; i += kWave) a.query_out[head * D + i] = x_s[i];
+    a.query_out[head * D + d0] = x0;
+    a.query_out[head * D + d1] = x1;
   } else {
     const float* vsrc = a.qkv + a.hq * D + a.hkv * D + head * D;
     KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.rows + a.index) * D;
     KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + a.index) * D;
-    for (int i = lane; i < D; i += kWave) {
-      kdst[i] = from_float<KV>(x_s[i]);
-      vdst[i] = from_float<KV>(vsrc[i]);
-    }
+    kdst[d0] = from_float<KV>(x0);
+    kdst[d1] = from_float<KV>(x1);
+    vdst[d0] = from_float<KV>(vsrc[d0]);
+    vdst[d1] = from_float<KV>(vsrc[d1]);
   }
 }
 

@@ -34,7 +34,7 @@ __global__ __launch_bounds__(kGemvBlock) void argmax_finalize_kernel(ArgmaxFinal
   r_val[threadIdx.x] = bv;
   r_idx[threadIdx.x] = bi;
   __syncthreads();
-  for (int off = kGemvBlock / 2; off > 0; off >>= 1) {
+  for (unsigned off = kGemvBlock / 2; off > 0; off >>= 1) {
     if (threadIdx.x < off && argmax_better(r_val[threadIdx.x + off], r_idx[threadIdx.x + off], r_val[threadIdx.x],
                                            r_idx[threadIdx.x])) {
       r_val[threadIdx.x] = r_val[threadIdx.x + off];
