@@ -71,6 +71,11 @@ __device__ __forceinline__ void wave_norm_rope_pair(float& x0, float& x1, float 
   x1 = second * c + first * s;
 }
 
+// Lane `src` of v, as a wave-uniform value (src a compile-time constant).
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
 __device__ __forceinline__ void pv_fma(float2& acc, float p, const float2& v) {
   acc.x = fmaf(p, v.x, acc.x);
   acc.y = fmaf(p, v.y, acc.y);
@@ -448,6 +453,272 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   }
 }
 
+// attention_head_kernel, splits * hq blocks, 256 threads: the contiguous-cache
+// (single-sequence) variant.  Block (s, h) serves query head h of KV group
+// g = h / R over the tiles s, s + splits, ...  The R blocks of a group stage
+// the same K/V tile: a single-sequence step has few tiles, and four times the
+// blocks spreads the scores and P.V over four times the CUs.  Inside the
+// block, wave w owns tokens [w, w + 1) * TT / 4 of each tile with its own
+// online softmax; the waves' (m, l, o) merge at the end.
+//  * scores: the kLanesPerTok adjacent lanes of a token each sum an
+//    interleaved share of the dims (16-byte columns c * kLanesPerTok + share),
+//    then add across the share with DPP;
+//  * P.V: one lane per dimension pair over the wave's tokens, the
+//    probabilities read out of the scoring lanes.
+// Writes the same (m, l, o[d]) split partials as attention_split_kernel.
+template <typename KV, int D, int MODE>
+__global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a) {
+  constexpr int TT = attn_tile_tokens<D>();
+  constexpr int LD = D + 4;
+  constexpr int CH = 16 / static_cast<int>(sizeof(KV));
+  constexpr int kChunks = TT * D / CH;
+  constexpr int kPerThread = (kChunks + kAttnThreads - 1) / kAttnThreads;
+  constexpr int kPairs = D / 2;
+  constexpr int kTokPerWave = TT / kAttnWaves;
+  constexpr int kLanesPerTok = kWave / kTokPerWave;
+  constexpr int kQuadsPerLane = D / 4 / kLanesPerTok;
+  static_assert(TT % kAttnWaves == 0 && kWave % kTokPerWave == 0, "a wave holds whole tokens");
+  static_assert((D / 4) % kLanesPerTok == 0, "the dims split evenly over a token's lanes");
+  static_assert(D / 2 <= kWave, "a wave holds one head as d/2 RoPE pairs");
+  __shared__ __align__(16) float q_s[D];
+  __shared__ __align__(16) float k_s[TT][LD];
+  __shared__ __align__(16) float v_s[TT][LD];
+  __shared__ __align__(16) float red_o[kAttnWaves][D];
+  __shared__ float red_m[kAttnWaves], red_l[kAttnWaves];
+
+  const int R = a.hq / a.hkv;
+  const int S = a.splits;
+  // Block -> (split, group, head): the R head-blocks of one (split, group)
+  // unit take ids 8 apart, so the round-robin dispatch over the 8 XCDs puts
+  // them on one XCD and their K/V tile is read from HBM into one L2.  (A
+  // last partial group of 8 units keeps its blocks together less tightly.)
+  const int units = S * a.hkv;
+  const int full = units / 8 * 8;
+  const int id = blockIdx.x;
+  int unit, r;
+  if (id < full * R) {
+    const int w = id % (8 * R);
+    unit = id / (8 * R) * 8 + w % 8;
+    r = w / 8;
+  } else {
+    const int tail = units - full, w = id - full * R;
+    unit = full + w % tail;
+    r = w / tail;
+  }
+  const int split = unit / a.hkv;
+  const int g = unit % a.hkv;
+  const int h = g * R + r;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const KV* kbase = reinterpret_cast<const KV*>(a.kcache);
+  const KV* vbase = reinterpret_cast<const KV*>(a.vcache);
+  KvRows<D, false> kv_rows;
+  kv_rows.head_base = static_cast<int64_t>(g) * a.rows * D;
+
+  // ---- 1. independent loads, issued before the position is known ----
+  int p = -1;
+  if constexpr (MODE == kAttnFused) p = a.pos[0];
+  uint4 kc[kPerThread], vc[kPerThread];
+  const int t_spec = split * TT;
+  const bool spec = t_spec + TT <= a.rows;
+  const int64_t t_load = kv_rows.row(spec ? t_spec : 0);
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+    kc[i] = *reinterpret_cast<const uint4*>(kbase + t_load + c * CH);
+    vc[i] = *reinterpret_cast<const uint4*>(vbase + t_load + c * CH);
+  }
+  // Lane i < d/2 holds dims (i, i + d/2), the pair RoPE rotates together.
+  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
+  const bool in_pair = lane < D / 2;
+  const float* qsrc = (MODE == kAttnFused ? a.qkv : a.q) + h * D;
+  float qx0 = in_pair ? qsrc[d0] : 0.0f, qx1 = in_pair ? qsrc[d1] : 0.0f;
+  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
+  float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+  if constexpr (MODE == kAttnFused) {
+    const float* kraw = a.qkv + a.hq * D + g * D;
+    const float* vraw = kraw + a.hkv * D;
+    kx0 = in_pair ? kraw[d0] : 0.0f;
+    kx1 = in_pair ? kraw[d1] : 0.0f;
+    vx0 = in_pair ? vraw[d0] : 0.0f;
+    vx1 = in_pair ? vraw[d1] : 0.0f;
+    inv_freq = a.inv_freq[d0];
+    qw0 = a.q_norm[d0];
+    qw1 = a.q_norm[d1];
+    kw0 = a.k_norm[d0];
+    kw1 = a.k_norm[d1];
+  }
+
+  // ---- 2. extent of the context ----
+  int n_keys;
+  if constexpr (MODE == kAttnFused) {
+    const bool ok = p >= 0 && p < a.capacity;
+    if (!ok && threadIdx.x == 0 && split == 0 && h == 0) *a.err = 1;  // vector store, once
+    n_keys = ok ? p + 1 : 0;
+  } else {
+    n_keys = a.tokens < a.capacity ? a.tokens : a.capacity;
+  }
+  const int n_tiles = (n_keys + TT - 1) / TT;
+
+  // The wave's running softmax state and P.V sums (lane i < d/2: dims 2i, 2i + 1).
+  float m_run = -INFINITY, l_run = 0.0f;
+  float2 pacc = make_float2(0.0f, 0.0f);
+  const int pv_pair = min(lane, kPairs - 1);
+  const int tok = wave * kTokPerWave + lane / kLanesPerTok;  // scoring token within the tile
+  const int share = lane % kLanesPerTok;  // which interleaved share of the dims
+
+  if (split < n_tiles) {
+    // ---- 3. q (wave 0) and the new key/value (wave 1), in registers ----
+    float rc = 1.0f, rs = 0.0f;
+    if constexpr (MODE == kAttnFused) {
+      if (in_pair) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
+    }
+    if (wave == 0) {
+      if constexpr (MODE == kAttnFused) wave_norm_rope_pair<D>(qx0, qx1, qw0, qw1, a.eps, rc, rs);
+      if (in_pair) {
+        q_s[d0] = qx0;
+        q_s[d1] = qx1;
+      }
+    }
+    // The block owning tile p / TT places the new token's row in its stage;
+    // the first block of the group also appends it to the cache.  k and v
+    // are rounded to the cache dtype once, so this step and later steps see
+    // the same key/value.
+    const bool owns_new = (MODE == kAttnFused) && ((p / TT) % S == split);
+    if (owns_new && wave == 1) {
+      wave_norm_rope_pair<D>(kx0, kx1, kw0, kw1, a.eps, rc, rs);
+      const KV k0 = from_float<KV>(kx0), k1 = from_float<KV>(kx1);
+      const KV v0 = from_float<KV>(vx0), v1 = from_float<KV>(vx1);
+      if (in_pair && r == 0) {
+        KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
+        KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
+        kdst[d0] = k0;
+        kdst[d1] = k1;
+        vdst[d0] = v0;
+        vdst[d1] = v1;
+      }
+      kx0 = to_float<KV>(k0);
+      kx1 = to_float<KV>(k1);
+      vx0 = to_float<KV>(v0);
+      vx1 = to_float<KV>(v1);
+    }
+
+    const float sqrt_d = sqrtf(static_cast<float>(D));
+    auto fetch_tile = [&](int tile) {
+      const int t0 = tile * TT;
+      const int rows = min(TT, n_keys - t0);
+      const int64_t tile_base = kv_rows.row(t0);
+#pragma unroll
+      for (int i = 0; i < kPerThread; ++i) {
+        const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+        const int r = min((c * CH) / D, rows - 1);
+        const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
+        kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
+        vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+      }
+    };
+    if (!spec) fetch_tile(split);
+    auto tile_step = [&](int tile, auto prefetch) {
+      const int t0 = tile * TT;
+      const int rows = min(TT, n_keys - t0);
+      // Rows past the context are zero-filled (0 * stale LDS could be NaN).
+#pragma unroll
+      for (int i = 0; i < kPerThread; ++i) {
+        const int c = threadIdx.x + i * kAttnThreads;
+        const int r = (c * CH) / D;
+        const int col = (c * CH) % D;
+        if (c < kChunks && !(MODE == kAttnFused && t0 + r == p)) {
+          if (r < rows) {
+            chunk_to_float<KV>(kc[i], &k_s[r][col]);
+            chunk_to_float<KV>(vc[i], &v_s[r][col]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+              k_s[r][col + e] = 0.0f;
+              v_s[r][col + e] = 0.0f;
+            }
+          }
+        }
+      }
+      if (MODE == kAttnFused && p >= t0 && p < t0 + rows && wave == 1 && in_pair) {
+        const int r = p - t0;
+        k_s[r][d0] = kx0;
+        k_s[r][d1] = kx1;
+        v_s[r][d0] = vx0;
+        v_s[r][d1] = vx1;
+      }
+      if constexpr (decltype(prefetch)::value) fetch_tile(tile + S);
+      __syncthreads();
+
+      // ---- scores of the wave's tokens ----
+      float dot = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kQuadsPerLane; ++c) {
+        const int col = 4 * (c * kLanesPerTok + share);
+        const float4 k4 = *reinterpret_cast<const float4*>(&k_s[tok][col]);
+        const float4 q4 = *reinterpret_cast<const float4*>(&q_s[col]);
+        dot = fmaf(q4.x, k4.x, dot);
+        dot = fmaf(q4.y, k4.y, dot);
+        dot = fmaf(q4.z, k4.z, dot);
+        dot = fmaf(q4.w, k4.w, dot);
+      }
+      dot = group_sum<kLanesPerTok>(dot);
+      const bool live = tok < rows;
+      const float sc = live ? dot / sqrt_d : -INFINITY;  // decoder_layer.cpp:213 divides by sqrt(d)
+      // ---- the wave's online softmax (a wave may have no live token yet) ----
+      const float m_new = fmaxf(m_run, group_max<kWave>(sc));
+      const float alpha = m_new == -INFINITY ? 1.0f : expf(m_run - m_new);
+      const float pv = live ? expf(sc - m_new) : 0.0f;
+      l_run = l_run * alpha + group_sum<kWave>(share == 0 ? pv : 0.0f);
+      m_run = m_new;
+      // ---- P.V over the wave's tokens ----
+      float2 acc = make_float2(pacc.x * alpha, pacc.y * alpha);
+#pragma unroll
+      for (int t = 0; t < kTokPerWave; ++t) {
+        const float pt = lane_value(pv, t * kLanesPerTok);
+        const float2 v = *reinterpret_cast<const float2*>(&v_s[wave * kTokPerWave + t][2 * pv_pair]);
+        acc.x = fmaf(pt, v.x, acc.x);
+        acc.y = fmaf(pt, v.y, acc.y);
+      }
+      pacc = acc;
+      // The next tile's staging overwrites k_s / v_s: every wave must be done.
+      if constexpr (decltype(prefetch)::value) __syncthreads();
+    };
+    int tile = split;
+    for (; tile + S < n_tiles; tile += S) tile_step(tile, std::true_type{});
+    if (tile < n_tiles) tile_step(tile, std::false_type{});
+  }
+
+  // ---- merge the waves' (m, l, o) in wave order; neutral when the split had
+  // no tile ----
+  if (lane < kPairs) *reinterpret_cast<float2*>(&red_o[wave][2 * lane]) = pacc;
+  if (lane == 0) {
+    red_m[wave] = m_run;
+    red_l[wave] = l_run;
+  }
+  __syncthreads();
+  float M = red_m[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w]);
+  float e[kAttnWaves];
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; ++w) e[w] = M == -INFINITY ? 0.0f : expf(red_m[w] - M);
+  for (int idx = threadIdx.x; idx < D; idx += kAttnThreads) {
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) o = fmaf(e[w], red_o[w][idx], o);
+    a.part[attn_o_offset(g, split, r, S, R, D) + idx] = o;
+  }
+  if (threadIdx.x == 0) {
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) L = fmaf(e[w], red_l[w], L);
+    float* dst = a.part + attn_ml_offset(g, split, r, S, R, D, a.hkv);
+    dst[0] = M;
+    dst[1] = L;
+  }
+}
+
 // Log-sum-exp combine of the split partials: one block of 1024 threads per
 // query head (grid.y: sequence of a batch).  Thread t holds the (m, l) of
 // splits t, t + 1024, ... (at most kCombineKernelMaxSplits in all); block
@@ -565,16 +836,29 @@ __global__ __launch_bounds__(kWave) void qkv_postprocess_kernel(QkvPostArgs a) {
   }
 }
 
+// The per-head kernel re-stages each K/V tile once per query head of the
+// group; past this many blocks (long contexts, many splits) one block per
+// (split, group) serving every head of the group is faster.
+constexpr int kHeadKernelMaxBlocks = 512;
+
 template <typename KV, int D>
 hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
-  const dim3 grid(a.splits, a.hkv, a.batch), block(kAttnThreads);
+  const dim3 block(kAttnThreads);
+  const dim3 group_grid(a.splits, a.hkv, a.batch);
   if (a.page_table) {
     if (mode != kAttnFused) return hipErrorInvalidValue;
-    attention_split_kernel<KV, D, kAttnFused, true><<<grid, block, 0, s>>>(a);
+    attention_split_kernel<KV, D, kAttnFused, true><<<group_grid, block, 0, s>>>(a);
+  } else if (static_cast<int64_t>(a.splits) * a.hq <= kHeadKernelMaxBlocks) {
+    const dim3 head_grid(a.splits * a.hq);
+    if (mode == kAttnFused) {
+      attention_head_kernel<KV, D, kAttnFused><<<head_grid, block, 0, s>>>(a);
+    } else {
+      attention_head_kernel<KV, D, kAttnFromCache><<<head_grid, block, 0, s>>>(a);
+    }
   } else if (mode == kAttnFused) {
-    attention_split_kernel<KV, D, kAttnFused, false><<<grid, block, 0, s>>>(a);
+    attention_split_kernel<KV, D, kAttnFused, false><<<group_grid, block, 0, s>>>(a);
   } else {
-    attention_split_kernel<KV, D, kAttnFromCache, false><<<grid, block, 0, s>>>(a);
+    attention_split_kernel<KV, D, kAttnFromCache, false><<<group_grid, block, 0, s>>>(a);
   }
   return hipGetLastError();
 }
@@ -626,6 +910,7 @@ size_t attention_partial_floats(int hq, int hkv, int d, int splits) {
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream) {
   if (!attention_supported(a.hq, a.hkv, a.d) || a.splits <= 0 || a.batch <= 0) return hipErrorInvalidValue;
   if (a.qkv_parts < 1 || a.qkv_parts > (a.page_table ? kAttnMaxQkvParts : 1)) return hipErrorInvalidValue;
+  if (!a.page_table && a.batch != 1) return hipErrorInvalidValue;  // the contiguous cache holds one sequence
   if (a.batch > 1 && (a.part_stride < static_cast<int64_t>(attention_partial_floats(a.hq, a.hkv, a.d, a.splits)) ||
                       (mode == kAttnFused && a.qkv_stride <= 0)))
     return hipErrorInvalidValue;
