@@ -1,14 +1,17 @@
 #!/usr/bin/env python3
 """Decode throughput of the MiniMind2 gfx950 runtime.
 
-    python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f32|f16] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f16|f32] [--no-other-kv] [--no-cpu-baseline]
                     [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--no-attention-sweep] [--no-context-sweep] [--batch 32]
                     [--batch-context 4096] [--traffic-probe N]
 
 Workload: MiniMind2 dense (hidden 768, 16 layers, 8/2 heads, d 96, FFN 2048,
 vocab 6400), fp16 weights drawn N(0, 0.02) from seed 0, a 512-token uniform
 prompt from seed 1, then `--steps` greedy decode steps replayed from the
-captured hipGraph with the token fed forward on the device.  A "step" is one
+captured hipGraph with the token fed forward on the device.  The KV cache is
+fp16 by default, as the reference's device cache (CustomAttentionCache,
+ascend_custom_ops.cpp:59-65,126-139); `other_kv_cache` records the same decode
+with the other dtype (fp32, the reference CPU path's).  A "step" is one
 decode step (one token); `value` is decode tok/s = steps / time of the steps,
 measured with HIP events on the decode stream between two device syncs.
 
@@ -192,6 +195,34 @@ def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
 DECODE_CONTEXTS = (1024, 4096, 8192)
 
 
+def other_kv_decode(mmr, model, prompt, steps: int, kv_name: str) -> dict:
+    """The same decode with the other KV cache dtype (one warm and one timed
+    run): the value line uses --kv, this records the alternative's rate and
+    whether its tokens also equal the reference CPU path's."""
+    kv = mmr.KV_F16 if kv_name == "f16" else mmr.KV_F32
+    st = model.make_state(PROMPT_LEN + steps + 8, kv)
+    ev = [mmr.Event() for _ in range(2)]
+    for _ in range(2):
+        st.reset()
+        st.enqueue_prefill(prompt)
+        ev[0].record(st.stream)
+        st.enqueue_decode(steps)
+        ev[1].record(st.stream)
+        st.synchronize()
+    ms = ev[0].elapsed_ms(ev[1])
+    generated = st.read_sequence(PROMPT_LEN, steps + 1).tolist()
+    golden = ROOT / "tests" / "golden" / "cfg3.json"
+    match = None
+    if golden.exists():
+        ref = json.loads(golden.read_text())["generated"]
+        n = min(len(ref), len(generated))
+        match = bool(generated[:n] == ref[:n])
+    st.free()
+    log(f"decode with {kv_name} KV: {steps / (ms / 1e3):.1f} tok/s, tokens match reference: {match}")
+    return {"kv_cache": kv_name, "tok_s": round(steps / (ms / 1e3), 1), "ms_per_step": round(ms / steps, 5),
+            "tokens_match_reference": match}
+
+
 def decode_context_sweep(mmr, model, kv, steps: int = 64) -> dict:
     """The batch-1 decode step at the configs[2] context lengths: a prompt of T
     uniform tokens (chunked GEMM prefill), 8 warm steps, then `steps` timed
@@ -312,7 +343,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--kv", choices=["f32", "f16"], default="f32")
+    ap.add_argument("--kv", choices=["f32", "f16"], default="f16")
+    ap.add_argument("--no-other-kv", action="store_true", help="skip the decode with the other KV cache dtype")
     ap.add_argument("--kernel-reps", type=int, default=320)
     ap.add_argument("--cpu-sample-steps", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -406,7 +438,8 @@ def main() -> int:
         b = kernel_bytes(MINIMIND2, name, n_keys, kv_bytes)
         kernels[name] = {"avg_us": round(avg_us, 3), "bytes": b, "gbs": round(b / (avg_us * 1e-6) / 1e9, 1)}
         if name == "attention":
-            kernels[name]["splits_note"] = "split kernel only; the combine runs in the o-projection prologue"
+            kernels[name]["splits_note"] = ("attention kernel only (one block per query head and split at this "
+                                            "context); the split combine runs in the o-projection prologue")
         log(f"kernel {name:9s} {avg_us:8.3f} us  {kernels[name]['gbs']:8.1f} GB/s")
     per_step_us = sum(kernels[n]["avg_us"] for n in names[:5]) * MINIMIND2["num_hidden_layers"] + \
         kernels["lm_head"]["avg_us"] + kernels["finalize"]["avg_us"]
@@ -450,6 +483,8 @@ def main() -> int:
     sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
     attn_sweep = None if args.no_attention_sweep else attention_sweep(mmr, mmr.Stream(stream), ev)
     ctx_sweep = None if args.no_context_sweep else decode_context_sweep(mmr, model, kv)
+    other_kv = None if args.no_other_kv else other_kv_decode(mmr, model, prompt, args.steps,
+                                                             "f32" if args.kv == "f16" else "f16")
     batched = batched_decode(mmr, model, args.batch, 256, args.batch_context) if args.batch > 0 else None
 
     traffic = None
@@ -490,6 +525,7 @@ def main() -> int:
         "gemv_sweep": sweep,
         "attention_sweep": attn_sweep,
         "decode_context_sweep": ctx_sweep,
+        "other_kv_cache": other_kv,
         "batched": batched,
         "launch_mode": "eager (--no-graph)" if args.no_graph else "hipGraph replay",
         "roofline": {"bound": "hbm", "kernel": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",
