@@ -28,6 +28,9 @@ The same line carries
   * batched: BASELINE configs[4], 32 sequences with 256-token prompts decoded
     in lockstep to 4096 positions over a paged fp16 KV cache (aggregate tok/s,
     p50 / p90 step latency);
+  * launch_floor: per-kernel time of a hipGraph chain of 80 trivial kernels
+    (empty, and one dependent load + store), the latency every kernel of the
+    82-kernel step pays before it moves a byte;
   * copy_probe: a device-to-device copy of --copy-probe-mib MiB (HIP's blit
     kernel), the achievable-bandwidth yardstick and the calibration dispatch
     of the FETCH_SIZE / WRITE_SIZE counter runs;
@@ -447,6 +450,12 @@ def main() -> int:
         kernels["lm_head"]["bytes"]
     dom = "gate_up"
     ach = kernels[dom]["gbs"]
+    # The chain's per-kernel floor: trivial kernels replayed from a hipGraph.
+    floor = {"kernels_in_chain": 80, "blocks": 256,
+             "empty_us": round(mmr.launch_floor_us(80, 256, False, 20), 3),
+             "load_store_us": round(mmr.launch_floor_us(80, 256, True, 20), 3)}
+    log(f"launch floor: empty {floor['empty_us']:.3f} us, dependent load + store {floor['load_store_us']:.3f} us "
+        f"per kernel (graph chain of 80)")
 
     copy_probe = None
     if args.copy_probe_mib > 0:
@@ -524,6 +533,7 @@ def main() -> int:
         "copy_probe": copy_probe,
         "gemv_sweep": sweep,
         "attention_sweep": attn_sweep,
+        "launch_floor": floor,
         "decode_context_sweep": ctx_sweep,
         "other_kv_cache": other_kv,
         "batched": batched,

@@ -77,6 +77,11 @@ int mmr_event_create(void** event);
 int mmr_event_destroy(void* event);
 int mmr_event_record(void* event, mmr_stream_t stream);
 int mmr_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Measurement aid with no counterpart in the reference: the per-kernel time of
+ * a hipGraph chain of `kernels` trivial launches of `blocks` x 256 threads
+ * (load_store 0: empty kernels; 1: each loads one float its predecessor
+ * wrote and stores one), replayed `reps` times.  Synchronous. */
+int mmr_launch_floor_us(int kernels, int blocks, int load_store, int reps, float* us_per_kernel);
 /* float_to_half / half_to_float (ascend_matmul.h:14-15), but IEEE
  * round-to-nearest-even instead of the reference's ties-away rounding. */
 int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n);

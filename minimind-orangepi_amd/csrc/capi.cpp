@@ -218,6 +218,13 @@ int mmr_event_elapsed_ms(void* start, void* stop, float* ms) {
         "hipEventElapsedTime");
   });
 }
+int mmr_launch_floor_us(int kernels, int blocks, int load_store, int reps, float* us_per_kernel) {
+  return guarded([&] {
+    require(us_per_kernel, "null us_per_kernel");
+    require(kernels > 0 && kernels <= 4096 && blocks > 0 && blocks <= 65536 && reps > 0, "probe size out of range");
+    hip(mmr::measure_launch_floor(kernels, blocks, load_store != 0, reps, us_per_kernel), "launch floor probe");
+  });
+}
 int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n) {
   return guarded([&] {
     require(src && dst, "null buffer");

@@ -308,4 +308,9 @@ hipError_t launch_swiglu_rows(const float* gate_up, int rows, int cols, float* o
 hipError_t launch_embedding_gather(const __half* table, const int32_t* ids, int tokens, int vocab, int hidden,
                                    float* out, int32_t* err, hipStream_t stream);
 
+// Per-kernel time of a hipGraph chain of `kernels` trivial launches of
+// `blocks` x 256 threads (empty, or one dependent load + store), replayed
+// `reps` times on a private stream (probe.hip).
+hipError_t measure_launch_floor(int kernels, int blocks, bool load_store, int reps, float* us_per_kernel);
+
 }  // namespace mmr

@@ -82,6 +82,7 @@ _SIGS = {
     "mmr_last_error": ([], C.c_char_p),
     "mmr_version": ([], C.c_int),
     "mmr_device_count": ([C.POINTER(C.c_int)], C.c_int),
+    "mmr_launch_floor_us": ([C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)], C.c_int),
     "mmr_malloc": ([C.POINTER(VP), SZ], C.c_int),
     "mmr_free": ([VP], C.c_int),
     "mmr_memcpy_h2d": ([VP, VP, SZ], C.c_int),
@@ -177,6 +178,13 @@ def check(code: int) -> None:
 
 def _ptr(a: np.ndarray) -> int:
     return a.ctypes.data
+
+
+def launch_floor_us(kernels: int = 80, blocks: int = 256, load_store: bool = True, reps: int = 20) -> float:
+    """Per-kernel time of a hipGraph chain of trivial kernels (mmr_launch_floor_us)."""
+    us = C.c_float()
+    check(_lib.mmr_launch_floor_us(kernels, blocks, int(load_store), reps, C.byref(us)))
+    return float(us.value)
 
 
 def device_count() -> int:

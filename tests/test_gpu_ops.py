@@ -260,3 +260,13 @@ def test_support_ops(gpu, oracle):
     e = de.numpy().reshape(4, 16)
     np.testing.assert_array_equal(e[:3], table[[3, 0, 9]].astype(np.float32))
     assert not e[3].any() and int(derr.numpy()[0]) == 1
+
+
+def test_launch_floor_probe(gpu):
+    # the bench's per-kernel floor: both chains run and report a plausible time
+    mmr = gpu
+    empty = mmr.launch_floor_us(16, 64, False, 4)
+    dep = mmr.launch_floor_us(16, 64, True, 4)
+    assert 0.1 < empty < 100.0 and 0.1 < dep < 100.0
+    with pytest.raises(mmr.InvalidArgument):
+        mmr.launch_floor_us(0, 64, True, 4)
