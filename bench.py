@@ -17,8 +17,9 @@ measured with HIP events on the decode stream between two device syncs.
 
 The same line carries
   * roofline: the dominant kernel (gate_up GEMV + SwiGLU) launched alone
-    `--kernel-reps` times over the 16 layers' weights, timed with HIP events on
-    the stream it runs on; achieved = algorithmic bytes / average duration;
+    `--kernel-reps` times over the 16 layers' weights as one hipGraph chain
+    (eager launches with --no-graph), timed with HIP events on the stream it
+    runs on; achieved = algorithmic bytes / average time per launch;
   * kernels: the same measurement for every kernel of the step;
   * gemv_sweep / attention_sweep: BASELINE configs[1] GEMV shapes and
     configs[2] attention contexts alone through the C ABI, MALL-resident and
@@ -431,13 +432,9 @@ def main() -> int:
     state.enqueue_decode(args.steps - 1)
     state.synchronize()
     for kid, name in enumerate(names):
-        state.launch_step_kernel(kid, 0, 32)  # warm
-        mmr.synchronize()
-        ev[0].record(stream)
-        state.launch_step_kernel(kid, 0, args.kernel_reps)
-        ev[1].record(stream)
-        state.synchronize()
-        avg_us = ev[0].elapsed_ms(ev[1]) * 1e3 / args.kernel_reps
+        # kernel_reps launches as one hipGraph chain (eager with --no-graph),
+        # timed with HIP events on the decode stream
+        avg_us = state.time_step_kernel(kid, 0, args.kernel_reps)
         b = kernel_bytes(MINIMIND2, name, n_keys, kv_bytes)
         kernels[name] = {"avg_us": round(avg_us, 3), "bytes": b, "gbs": round(b / (avg_us * 1e-6) / 1e9, 1)}
         if name == "attention":

@@ -271,6 +271,13 @@ int mmr_batch_read_logits(const mmr_model* model, mmr_batch_state* state, int64_
  * bookkeeping).  For timing
  * with events recorded on the state's stream; overwrites scratch buffers. */
 int mmr_launch_step_kernel(const mmr_model* model, mmr_state* state, int kernel, int64_t layer, int64_t count);
+/* Average time per launch in us of `count` back-to-back launches of one step
+ * kernel (numbering as above), from HIP events on the state's stream: the
+ * launches are captured into one hipGraph and replayed (eager launches after
+ * 32 warm ones when the state runs without graphs, MMR_NO_GRAPH).
+ * Synchronous; overwrites scratch buffers. */
+int mmr_time_step_kernel(const mmr_model* model, mmr_state* state, int kernel, int64_t layer, int64_t count,
+                         double* avg_us);
 
 #ifdef __cplusplus
 }

@@ -884,4 +884,12 @@ int mmr_launch_step_kernel(const mmr_model* model, mmr_state* state, int kernel,
   });
 }
 
+int mmr_time_step_kernel(const mmr_model* model, mmr_state* state, int kernel, int64_t layer, int64_t count,
+                         double* avg_us) {
+  return guarded([&] {
+    require(model && state && avg_us, "null argument");
+    *avg_us = model->lm->time_kernel(state->st, kernel, layer, count);
+  });
+}
+
 }  // extern "C"

@@ -717,6 +717,54 @@ void LanguageModel::enqueue_kernel(DecoderState& state, int kernel, int64_t laye
     ::minimind::model::enqueue_kernel(s, kernel, static_cast<size_t>((layer + i) % L), splits, false);
 }
 
+double LanguageModel::time_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const {
+  DeviceState& s = *state.device;
+  if (count <= 0) throw std::invalid_argument("count must be positive");
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipGraphExec_t exec = nullptr;
+  auto release = [&] {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+  };
+  try {
+    check_hip(hipEventCreate(&e0), "hipEventCreate");
+    check_hip(hipEventCreate(&e1), "hipEventCreate");
+    if (s.use_graphs) {
+      hipGraph_t graph = nullptr;
+      check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        enqueue_kernel(state, kernel, layer, count);
+      } catch (...) {
+        (void)hipStreamEndCapture(s.stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+      }
+      check_hip(hipStreamEndCapture(s.stream, &graph), "hipStreamEndCapture");
+      const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      check_hip(st, "hipGraphInstantiate");
+      check_hip(hipGraphLaunch(exec, s.stream), "hipGraphLaunch");  // warm
+      check_hip(hipEventRecord(e0, s.stream), "hipEventRecord");
+      check_hip(hipGraphLaunch(exec, s.stream), "hipGraphLaunch");
+    } else {
+      enqueue_kernel(state, kernel, layer, 32);  // warm
+      check_hip(hipEventRecord(e0, s.stream), "hipEventRecord");
+      enqueue_kernel(state, kernel, layer, count);
+    }
+    check_hip(hipEventRecord(e1, s.stream), "hipEventRecord");
+    check_hip(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.0f;
+    check_hip(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    release();
+    return static_cast<double>(ms) * 1e3 / static_cast<double>(count);
+  } catch (...) {
+    (void)hipStreamSynchronize(s.stream);
+    release();
+    throw;
+  }
+}
+
 std::vector<int32_t> LanguageModel::read_sequence(DecoderState& state, int64_t first, int64_t count) const {
   DeviceState& s = *state.device;
   if (first < 0 || count < 0 || first + count > s.capacity + 1) throw std::out_of_range("sequence range");

@@ -112,6 +112,12 @@ class LanguageModel {
   // cycling over layers from `layer`.  Used to time single kernels;
   // overwrites scratch buffers.
   void enqueue_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const;
+  // Average time per launch (us) of `count` back-to-back launches of one step
+  // kernel, from HIP events on the state's stream.  With graphs enabled the
+  // launches are captured into one hipGraph (a dependent chain, as in the
+  // step) and replayed once after a warm replay, so host launch overhead never
+  // paces them; otherwise they are launched eagerly after 32 warm launches.
+  double time_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const;
   // Reset position to 0 (the cache contents are overwritten as it refills).
   void reset_state(DecoderState& state) const;
 

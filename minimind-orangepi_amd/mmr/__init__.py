@@ -147,6 +147,7 @@ _SIGS = {
     "mmr_read_sequence": ([VP, VP, I64, I64, VP], C.c_int),
     "mmr_read_logits": ([VP, VP, VP], C.c_int),
     "mmr_launch_step_kernel": ([VP, VP, C.c_int, I64, I64], C.c_int),
+    "mmr_time_step_kernel": ([VP, VP, C.c_int, I64, I64, C.POINTER(C.c_double)], C.c_int),
     "mmr_batch_state_create": ([VP, I64, I64, C.c_int, C.POINTER(VP)], C.c_int),
     "mmr_batch_state_free": ([VP], C.c_int),
     "mmr_batch_state_info": ([VP, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64)], C.c_int),
@@ -615,6 +616,12 @@ class State:
 
     def launch_step_kernel(self, kernel: int, layer: int, count: int) -> None:
         check(_lib.mmr_launch_step_kernel(self.model.handle, self.handle, kernel, layer, count))
+
+    def time_step_kernel(self, kernel: int, layer: int, count: int) -> float:
+        """Average us per launch of `count` back-to-back launches (mmr_time_step_kernel)."""
+        us = C.c_double()
+        check(_lib.mmr_time_step_kernel(self.model.handle, self.handle, kernel, layer, count, C.byref(us)))
+        return float(us.value)
 
     def free(self) -> None:
         if self.handle:
