@@ -105,7 +105,8 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
     mmr_matvec_argmax_f16), each timed over rotated weight copies: `mall` keeps
     the rotation at <= 160 MiB (resident in the 256 MB Infinity Cache), `hbm`
     at >= 640 MiB (every launch streams from HBM).  GB/s = algorithmic bytes
-    (W fp16 + x fp32 + y fp32, or the int32 token for argmax) / mean launch time."""
+    (W fp16 + x fp32 + y fp32, or the int32 token for argmax) / mean launch time
+    of `reps` launches replayed as one hipGraph chain."""
     lib = mmr.lib()
     out = {}
     rng = np.random.default_rng(7)
@@ -133,11 +134,16 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
 
             for i in range(copies):
                 launch(i)
+            # the reps launches as one graph chain: host launch cost never paces them
+            with mmr.Graph(stream) as graph:
+                for i in range(reps):
+                    launch(i)
+            graph.launch()
             ev[0].record(stream)
-            for i in range(reps):
-                launch(i)
+            graph.launch()
             ev[1].record(stream)
             stream.synchronize()
+            graph.free()
             us = ev[0].elapsed_ms(ev[1]) * 1e3 / reps
             res[label] = {"avg_us": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
                           "rotation_mib": round(copies * wbytes / 2**20, 1)}
@@ -154,11 +160,12 @@ ATTN_CONTEXTS = (128, 1024, 4096, 8192)
 def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
     """decode attention over T cached tokens plus the new
     one (T + 1 keys), 8 q / 2 kv heads, d 96, fp16 K/V ~ N(0, 1), through the
-    C ABI (mmr_attention_from_cache: split kernel + log-sum-exp combine, split
+    C ABI (mmr_attention_from_cache: attention kernel + log-sum-exp combine, split
     count chosen by the library).  `resident`: every launch reads the same
     cache (MALL/L2-resident after the first); `hbm` (T >= 4096): launches
     rotate over caches totalling >= 640 MiB.  GB/s = algorithmic bytes
-    (K + V of T + 1 tokens, fp32 q in and out) / mean launch time."""
+    (K + V of T + 1 tokens, fp32 q in and out) / mean time per call of `reps`
+    calls replayed as one hipGraph chain."""
     hq, hkv, d = 8, 2, 96
     rng = np.random.default_rng(11)
     q = mmr.DeviceArray.from_numpy(rng.standard_normal(hq * d).astype(np.float32))
@@ -181,11 +188,16 @@ def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
                 caches.append(mmr.KvCache(hkv, d, n, mmr.KV_F16))  # zero-filled
             for i in range(copies):
                 mmr.attention_from_cache(q, caches[i], n, hq, hkv, d, o, ws, stream=stream)
+            # the reps calls as one graph chain: host launch cost never paces them
+            with mmr.Graph(stream) as graph:
+                for i in range(reps):
+                    mmr.attention_from_cache(q, caches[i % copies], n, hq, hkv, d, o, ws, stream=stream)
+            graph.launch()
             ev[0].record(stream)
-            for i in range(reps):
-                mmr.attention_from_cache(q, caches[i % copies], n, hq, hkv, d, o, ws, stream=stream)
+            graph.launch()
             ev[1].record(stream)
             stream.synchronize()
+            graph.free()
             us = ev[0].elapsed_ms(ev[1]) * 1e3 / reps
             res[label] = {"avg_us": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
                           "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "caches": copies}

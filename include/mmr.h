@@ -77,6 +77,14 @@ int mmr_event_create(void** event);
 int mmr_event_destroy(void* event);
 int mmr_event_record(void* event, mmr_stream_t stream);
 int mmr_event_elapsed_ms(void* start, void* stop, float* ms);
+/* Stream capture into a replayable hipGraph (no counterpart in the reference,
+ * whose device path launches every op from the host): everything enqueued on
+ * `stream` between begin and end (which must not allocate or synchronize)
+ * becomes one executable graph, replayed by mmr_graph_launch on any stream. */
+int mmr_graph_capture_begin(mmr_stream_t stream);
+int mmr_graph_capture_end(mmr_stream_t stream, void** graph);
+int mmr_graph_launch(void* graph, mmr_stream_t stream);
+int mmr_graph_destroy(void* graph);
 /* Measurement aid with no counterpart in the reference: the per-kernel time of
  * a hipGraph chain of `kernels` trivial launches of `blocks` x 256 threads
  * (load_store 0: empty kernels; 1: each loads one float its predecessor

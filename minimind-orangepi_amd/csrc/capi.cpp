@@ -218,6 +218,36 @@ int mmr_event_elapsed_ms(void* start, void* stop, float* ms) {
         "hipEventElapsedTime");
   });
 }
+int mmr_graph_capture_begin(mmr_stream_t stream) {
+  return guarded([&] {
+    require(stream, "graph capture needs a created stream");
+    hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  });
+}
+int mmr_graph_capture_end(mmr_stream_t stream, void** graph) {
+  return guarded([&] {
+    require(stream && graph, "null argument");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    hip(hipStreamEndCapture(as_stream(stream), &g), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t st = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    hip(st, "hipGraphInstantiate");
+    *graph = exec;
+  });
+}
+int mmr_graph_launch(void* graph, mmr_stream_t stream) {
+  return guarded([&] {
+    require(graph, "null graph");
+    hip(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), as_stream(stream)), "hipGraphLaunch");
+  });
+}
+int mmr_graph_destroy(void* graph) {
+  return guarded([&] {
+    if (graph) hip(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)), "hipGraphExecDestroy");
+  });
+}
 int mmr_launch_floor_us(int kernels, int blocks, int load_store, int reps, float* us_per_kernel) {
   return guarded([&] {
     require(us_per_kernel, "null us_per_kernel");

@@ -83,6 +83,10 @@ _SIGS = {
     "mmr_version": ([], C.c_int),
     "mmr_device_count": ([C.POINTER(C.c_int)], C.c_int),
     "mmr_launch_floor_us": ([C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)], C.c_int),
+    "mmr_graph_capture_begin": ([VP], C.c_int),
+    "mmr_graph_capture_end": ([VP, C.POINTER(VP)], C.c_int),
+    "mmr_graph_launch": ([VP, VP], C.c_int),
+    "mmr_graph_destroy": ([VP], C.c_int),
     "mmr_malloc": ([C.POINTER(VP), SZ], C.c_int),
     "mmr_free": ([VP], C.c_int),
     "mmr_memcpy_h2d": ([VP, VP, SZ], C.c_int),
@@ -266,6 +270,40 @@ class Stream:
                 _lib.mmr_stream_destroy(self.handle)
             except Exception:
                 pass
+
+
+class Graph:
+    """A hipGraph captured from everything enqueued on `stream` inside the
+    `with` block (mmr_graph_capture_begin / _end), replayed by launch()."""
+
+    def __init__(self, stream: Stream):
+        self.stream = stream
+        self.handle = None
+
+    def __enter__(self) -> "Graph":
+        check(_lib.mmr_graph_capture_begin(self.stream.handle))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        h = VP()
+        rc = _lib.mmr_graph_capture_end(self.stream.handle, C.byref(h))
+        if exc_type is None:
+            check(rc)
+            self.handle = h.value
+
+    def launch(self, stream: Stream | None = None) -> None:
+        check(_lib.mmr_graph_launch(self.handle, (stream or self.stream).handle))
+
+    def free(self) -> None:
+        if self.handle:
+            _lib.mmr_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Event:

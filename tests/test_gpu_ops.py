@@ -270,3 +270,27 @@ def test_launch_floor_probe(gpu):
     assert 0.1 < empty < 100.0 and 0.1 < dep < 100.0
     with pytest.raises(mmr.InvalidArgument):
         mmr.launch_floor_us(0, 64, True, 4)
+
+
+def test_graph_capture_replays_the_captured_calls(gpu, oracle):
+    # mmr.Graph: calls enqueued inside the block are captured, not run; each
+    # replay runs them again and matches the eager result.
+    mmr = gpu
+    rng = np.random.default_rng(5)
+    w, w32 = f16_weights(rng, 768, 768)
+    x = rng.standard_normal(768).astype(np.float32)
+    dw, dx = mmr.DeviceArray.from_numpy(w.view(np.uint16)), mmr.DeviceArray.from_numpy(x)
+    y_eager, y_graph = mmr.DeviceArray(768, np.float32), mmr.DeviceArray(768, np.float32, zero=True)
+    stream = mmr.Stream()
+    mmr.matvec_f16(dw, 768, 768, dx, y_eager, stream=stream)
+    with mmr.Graph(stream) as graph:
+        mmr.matvec_f16(dw, 768, 768, dx, y_graph, stream=stream)
+    stream.synchronize()
+    assert not y_graph.numpy().any()  # captured, not executed
+    for _ in range(3):
+        graph.launch()
+        stream.synchronize()
+        np.testing.assert_array_equal(y_graph.numpy(), y_eager.numpy())
+        y_graph.upload(np.zeros(768, np.float32))
+    graph.free()
+    assert rel_err(y_eager.numpy(), oracle.matvec(w32, x)) < TOL
