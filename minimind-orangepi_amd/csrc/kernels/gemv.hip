@@ -17,10 +17,12 @@ int round_cpl(int needed) {
 namespace {
 
 // One block reduces the per-block argmax partials; thread 0 does the step
-// bookkeeping.
+// bookkeeping.  (max, lowest index) is associative and commutative, so the
+// lane exchanges and the wave order cannot change the result.
 __global__ __launch_bounds__(kGemvBlock) void argmax_finalize_kernel(ArgmaxFinalizeArgs a) {
-  __shared__ float r_val[kGemvBlock];
-  __shared__ int r_idx[kGemvBlock];
+  constexpr int kWaves = kGemvBlock / kWave;
+  __shared__ float w_val[kWaves];
+  __shared__ int w_idx[kWaves];
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int b = threadIdx.x; b < a.parts; b += kGemvBlock) {
@@ -31,19 +33,27 @@ __global__ __launch_bounds__(kGemvBlock) void argmax_finalize_kernel(ArgmaxFinal
       bi = i;
     }
   }
-  r_val[threadIdx.x] = bv;
-  r_idx[threadIdx.x] = bi;
-  __syncthreads();
-  for (unsigned off = kGemvBlock / 2; off > 0; off >>= 1) {
-    if (threadIdx.x < off && argmax_better(r_val[threadIdx.x + off], r_idx[threadIdx.x + off], r_val[threadIdx.x],
-                                           r_idx[threadIdx.x])) {
-      r_val[threadIdx.x] = r_val[threadIdx.x + off];
-      r_idx[threadIdx.x] = r_idx[threadIdx.x + off];
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off);
+    const int oi = __shfl_xor(bi, off);
+    if (argmax_better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
     }
-    __syncthreads();
   }
+  if (threadIdx.x % kWave == 0) {
+    w_val[threadIdx.x / kWave] = bv;
+    w_idx[threadIdx.x / kWave] = bi;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const int32_t next = r_idx[0];
+    for (int w = 1; w < kWaves; ++w)
+      if (argmax_better(w_val[w], w_idx[w], bv, bi)) {
+        bv = w_val[w];
+        bi = w_idx[w];
+      }
+    const int32_t next = bi;
     if (a.token_out) *a.token_out = next;
     if (a.pos) {
       const int32_t p = *a.pos;
@@ -70,7 +80,9 @@ bool gemv_plan(int rows, int k, GemvEpilogue epi, int lanes_per_row, int rows_pe
   if (g == 0) g = kchunks >= 96 ? 64 : (kchunks >= 48 ? 32 : 16);
   if (g != 16 && g != 32 && g != 64) return false;
   int rpg = rows_per_group;
-  if (rpg == 0) rpg = (epi == kEpiSwiGlu) ? 2 : 1;
+  // Two rows per group for SwiGLU (the gate/up pair) and argmax (half the
+  // partials for the finalize), one otherwise.
+  if (rpg == 0) rpg = (epi == kEpiSwiGlu || epi == kEpiArgmax) ? 2 : 1;
   if (rpg != 1 && rpg != 2 && rpg != 4) return false;
   if (epi == kEpiSwiGlu && (rpg % 2 != 0 || rows % 2 != 0)) return false;
   const int cpl = round_cpl((kchunks + g - 1) / g);

@@ -234,7 +234,7 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
                       static_cast<int>(H) / 8 >= 48 ? 32 : 0, 0, &dm->plan_gu))
     throw std::invalid_argument("unsupported GEMV shape for gate_up_proj");
   dm->plan_down = plan_or_throw(static_cast<int>(H), static_cast<int>(F), mmr::kEpiResidual, "down_proj");
-  if (!mmr::gemv_plan(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, 0, 2, &dm->plan_lm))
+  if (!mmr::gemv_plan(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, 0, 0, &dm->plan_lm))
     throw std::invalid_argument("unsupported GEMV shape for lm_head");
   dm->gemm_prefill = mmr::gemm_supported(1, static_cast<int>(qs + 2 * kvs), static_cast<int>(H)) &&
                      mmr::gemm_supported(1, static_cast<int>(H), static_cast<int>(qs)) &&
