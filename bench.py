@@ -266,7 +266,8 @@ def decode_context_sweep(mmr, model, kv, steps: int = 64) -> dict:
 def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
     """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: the dominant
     kernel alone -- gate_up GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU
-    epilogue, the decode step's automatic launch plan) through the C ABI over a
+    epilogue, the decode step's launch plan: 32-lane groups, two rows per
+    group) through the C ABI over a
     16-copy weight rotation like the 16 layers of the step -- then one
     device-to-device copy of `copy_mib` MiB, the calibration dispatch whose
     bytes are known."""
@@ -281,7 +282,7 @@ def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
     lib = mmr.lib()
     for i in range(launches):
         mmr.check(lib.mmr_matvec_f16_ex(w.ptr + (i % layers) * wbytes, 2 * F, H, x.ptr, g.ptr, 1e-5, mmr.PRO_RMSNORM,
-                                        mmr.EPI_SWIGLU, None, y.ptr, 0, 0, stream.handle))
+                                        mmr.EPI_SWIGLU, None, y.ptr, 32, 2, stream.handle))
     stream.synchronize()
     n = copy_mib << 20
     src, dst = mmr.DeviceArray(n, np.uint8, zero=True), mmr.DeviceArray(n, np.uint8)
