@@ -393,10 +393,10 @@ constexpr int kResThreads = 1024;
 constexpr int kResGroups = kResThreads / 256;
 constexpr int kResChunkQuads = 256;
 
-template <bool kFinal>
+template <bool kFinal, bool kSplit>
 __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float* h, const float* part, int splits,
                                                                           int batch, int cols, const float* w,
-                                                                          float eps, float* x) {
+                                                                          float eps, float* x, SplitPlanes sp) {
   __shared__ float4 red[kResGroups][kResChunkQuads];
   __shared__ float s_ss[kResThreads / kWave];
   const int b = blockIdx.x;
@@ -429,9 +429,48 @@ __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float*
   for (int i = 0; i < kResThreads / kWave; ++i) total += s_ss[i];
   const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
   float* hr = h + static_cast<int64_t>(b) * cols;
-  float* xr = x + static_cast<int64_t>(b) * cols;
-  for (int i = threadIdx.x; i < cols; i += kResThreads)
-    xr[i] = kFinal ? (hr[i] * scale) * w[i] : hr[i] * (scale * w[i]);
+  if (x) {
+    float* xr = x + static_cast<int64_t>(b) * cols;
+    for (int i = threadIdx.x; i < cols; i += kResThreads)
+      xr[i] = kFinal ? (hr[i] * scale) * w[i] : hr[i] * (scale * w[i]);
+  }
+  if constexpr (kSplit) {
+    // Thread = 4 consecutive columns; the 32 threads of a 128-wide chunk
+    // reduce its max together (whole chunks per pass: 1024 threads = 32
+    // chunks), then write the planes as GemmStage would split them.
+    const int nchunks = (cols + kSplitChunk - 1) / kSplitChunk;
+    for (int q0 = 0; q0 < nchunks * (kSplitChunk / 4); q0 += kResThreads) {  // block-uniform
+      const int q = q0 + static_cast<int>(threadIdx.x);
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (4 * q < cols) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * q + e;
+          v[e] = kFinal ? (hr[i] * scale) * w[i] : hr[i] * (scale * w[i]);
+        }
+      }
+      const float mx = group_max<32>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+      if (4 * q < cols) {
+        int e2 = 0;
+        frexpf(mx, &e2);  // e2 = 0 for a zero chunk
+        e2 = max(e2, -100);
+        const float sc = ldexpf(1.0f, 15 - e2);
+        uint16_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float xs = v[e] * sc;
+          const _Float16 hh = static_cast<_Float16>(xs);
+          const _Float16 ll = static_cast<_Float16>(xs - static_cast<float>(hh));
+          __builtin_memcpy(&hi[e], &hh, 2);
+          __builtin_memcpy(&lo[e], &ll, 2);
+        }
+        const int64_t off = static_cast<int64_t>(b) * cols + 4 * q;
+        *reinterpret_cast<uint2*>(sp.hi + off) = make_uint2(hi[0] | (uint32_t{hi[1]} << 16), hi[2] | (uint32_t{hi[3]} << 16));
+        *reinterpret_cast<uint2*>(sp.lo + off) = make_uint2(lo[0] | (uint32_t{lo[1]} << 16), lo[2] | (uint32_t{lo[3]} << 16));
+        if (q % (kSplitChunk / 4) == 0) sp.inv[static_cast<int64_t>(b) * nchunks + q / (kSplitChunk / 4)] = ldexpf(1.0f, e2 - 15);
+      }
+    }
+  }
 }
 
 // act[b][i] = silu(sum_s gu[s][b][2i]) * sum_s gu[s][b][2i + 1]
@@ -597,12 +636,22 @@ hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream) {
 }
 
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,
-                                      float eps, float* x, bool final_norm, hipStream_t stream) {
+                                      float eps, float* x, bool final_norm, hipStream_t stream,
+                                      const SplitPlanes* split) {
   if (batch <= 0 || cols <= 0 || cols % 4 != 0 || splits < 0) return hipErrorInvalidValue;
+  if (split && (!split->hi || !split->lo || !split->inv)) return hipErrorInvalidValue;
+  if (!x && !split) return hipErrorInvalidValue;
+  const SplitPlanes sp = split ? *split : SplitPlanes{};
   if (final_norm) {
-    batch_residual_norm_kernel<true><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x);
+    if (split) {
+      batch_residual_norm_kernel<true, true><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+    } else {
+      batch_residual_norm_kernel<true, false><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+    }
+  } else if (split) {
+    batch_residual_norm_kernel<false, true><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
   } else {
-    batch_residual_norm_kernel<false><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x);
+    batch_residual_norm_kernel<false, false><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
   }
   return hipGetLastError();
 }

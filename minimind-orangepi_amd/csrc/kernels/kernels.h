@@ -188,6 +188,12 @@ struct GemmArgs {
   // SwiGLU epilogue over interleaved gate/up columns: c receives
   // act[m][n / 2] (row stride ldc); needs k_splits == 1 and no residual.
   bool swiglu = false;
+  // A given pre-split instead of `a` (see SplitPlanes): fp16 bit planes hi and
+  // lo [m][lda] and inv [m][ceil(k / 128)].  The product is bit-identical to
+  // the fp32 path's, which splits the same way per block.
+  const uint16_t* a_hi = nullptr;
+  const uint16_t* a_lo = nullptr;
+  const float* a_inv = nullptr;
 };
 bool gemm_supported(int m, int n, int k);
 // Split count launch_gemm accepts and uses well for this shape: about four
@@ -195,6 +201,9 @@ bool gemm_supported(int m, int n, int k);
 int gemm_k_splits(int m, int n, int k);
 // Whether launch_gemm takes the SwiGLU epilogue for this shape (unsplit tiles).
 bool gemm_swiglu_supported(int m, int n, int k);
+// Whether launch_gemm takes pre-split A (a_hi / a_lo / a_inv) for this shape
+// (the tiled path; the few-rows path reads fp32 A).
+bool gemm_presplit_supported(int m, int n, int k);
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Rows of the fused qkv projection for tokens at positions start ..
@@ -287,9 +296,20 @@ bool splitk_swiglu_supported(int m, int kc, int gu_splits);
 // kc, attn_splits splits and head_dim d.
 bool splitk_combine_supported(int m, int kc, int attn_splits, int d);
 hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream);
-// h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]).
+// A [rows][cols] as the GEMM's fp16 matrix cores take it: per row and
+// 128-wide column chunk a power-of-two scale s (the chunk's max |a| mapped
+// into [2^14, 2^15)), hi = fp16(s a), lo = fp16(s a - hi), inv = 1 / s.
+struct SplitPlanes {
+  uint16_t* hi = nullptr;  // [rows][cols] fp16 bits
+  uint16_t* lo = nullptr;
+  float* inv = nullptr;    // [rows][ceil(cols / 128)]
+};
+constexpr int kSplitChunk = 128;
+// h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]); x may be
+// null when `split` receives the normalised rows instead (or as well).
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,
-                                      float eps, float* x, bool final_norm, hipStream_t stream);
+                                      float eps, float* x, bool final_norm, hipStream_t stream,
+                                      const SplitPlanes* split = nullptr);
 // act[b][i] = silu(sum_s part[s][b][2i]) * sum_s part[s][b][2i + 1].
 hipError_t launch_batch_swiglu(const float* part, int splits, int batch, int f, float* act, hipStream_t stream);
 // out[b][i] = sum_s part[s][b][i].

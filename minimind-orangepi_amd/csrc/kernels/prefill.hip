@@ -57,22 +57,44 @@ using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 // BN x BK fp16 of W as 8-half chunks; thread t takes chunks t, t + 256, ...
 // so consecutive lanes read consecutive 16-byte pieces of a row (32 lanes per
 // A row, 16 per W row).
-template <int BM, int BN>
+template <int BM, int BN, bool kPreSplit = false>
 struct GemmStage {
   static constexpr int kA = BM * kGemmBK / 4 / kGemmThreads;
   static constexpr int kB = BN * kGemmBK / 8 / kGemmThreads;
-  float4 a[kA];
+  // Pre-split A: 16-byte chunks (8 halves) of each plane per thread.
+  static constexpr int kP = kPreSplit ? BM * kGemmBK / 8 / kGemmThreads : 1;
+  float4 a[kPreSplit ? 1 : kA];
+  uint4 ph[kP], pl[kP];
+  float pinv = 0.0f;
   uint4 b[kB];
 
   __device__ __forceinline__ void load(const GemmArgs& g, int m0, int n0, int k0, int tid) {
+    if constexpr (kPreSplit) {
+      static_assert(kP >= 1 && BM <= kGemmThreads, "tile too small for the block");
 #pragma unroll
-    for (int i = 0; i < kA; ++i) {
-      const int idx = tid + i * kGemmThreads;
-      const int r = idx / (kGemmBK / 4), q = idx % (kGemmBK / 4);
-      const int row = min(m0 + r, g.m - 1);  // clamped: in bounds, never stored
-      const int kc = k0 + q * 4;               // past k (last, partial tile): clamped load, zeroed
-      const float4 v = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(row) * g.lda + min(kc, g.k - 4));
-      a[i] = kc < g.k ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int i = 0; i < kP; ++i) {
+        const int idx = tid + i * kGemmThreads;
+        const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
+        const int row = min(m0 + r, g.m - 1);  // clamped: in bounds, never stored
+        const int kc = k0 + q * 8;               // past k (last, partial tile): clamped load, zeroed
+        const int64_t off = static_cast<int64_t>(row) * g.lda + min(kc, g.k - 8);
+        const uint4 vh = *reinterpret_cast<const uint4*>(g.a_hi + off);
+        const uint4 vl = *reinterpret_cast<const uint4*>(g.a_lo + off);
+        ph[i] = kc < g.k ? vh : make_uint4(0u, 0u, 0u, 0u);
+        pl[i] = kc < g.k ? vl : make_uint4(0u, 0u, 0u, 0u);
+      }
+      const int nkc = (g.k + kGemmBK - 1) / kGemmBK;
+      pinv = g.a_inv[static_cast<int64_t>(min(m0 + min(tid, BM - 1), g.m - 1)) * nkc + k0 / kGemmBK];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kA; ++i) {
+        const int idx = tid + i * kGemmThreads;
+        const int r = idx / (kGemmBK / 4), q = idx % (kGemmBK / 4);
+        const int row = min(m0 + r, g.m - 1);  // clamped: in bounds, never stored
+        const int kc = k0 + q * 4;               // past k (last, partial tile): clamped load, zeroed
+        const float4 v = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(row) * g.lda + min(kc, g.k - 4));
+        a[i] = kc < g.k ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
@@ -91,8 +113,18 @@ struct GemmStage {
   // The 32 lanes holding a row reduce its maximum together.
   __device__ __forceinline__ void store(_Float16 (*Ah)[kGemmLDH], _Float16 (*Al)[kGemmLDH], float* inv,
                                         _Float16 (*Bs)[kGemmLDH], int tid) const {
+    if constexpr (kPreSplit) {
 #pragma unroll
-    for (int i = 0; i < kA; ++i) {
+      for (int i = 0; i < kP; ++i) {
+        const int idx = tid + i * kGemmThreads;
+        const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
+        *reinterpret_cast<uint4*>(&Ah[r][q * 8]) = ph[i];
+        *reinterpret_cast<uint4*>(&Al[r][q * 8]) = pl[i];
+      }
+      if (tid < BM) inv[tid] = pinv;
+    }
+#pragma unroll
+    for (int i = 0; i < (kPreSplit ? 0 : kA); ++i) {
       const int idx = tid + i * kGemmThreads;
       const int r = idx / (kGemmBK / 4), q = idx % (kGemmBK / 4);
       const float4 v = a[i];
@@ -135,7 +167,7 @@ struct GemmStage {
 // 175-182), the pair meeting through one lane exchange.
 constexpr int kGemmEpiStore = 0, kGemmEpiResidual = 1, kGemmEpiSwiGlu = 2;
 
-template <int BM, int BN, int kEpi>
+template <int BM, int BN, int kEpi, bool kPreSplit>
 __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   constexpr bool kResidual = kEpi == kGemmEpiResidual;
   constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
@@ -162,7 +194,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   const int kt0 = static_cast<int>(blockIdx.z) * per, kt1 = min(kt0 + per, nk);
   float* out = g.c + static_cast<int64_t>(blockIdx.z) * g.split_stride;
 
-  GemmStage<BM, BN> stage;
+  GemmStage<BM, BN, kPreSplit> stage;
   stage.load(g, m0, n0, kt0 * kGemmBK, tid);  // past k: clamped loads, zeroed
   stage.store(Ah, Al, inv_s, Bs, tid);
   __syncthreads();
@@ -607,15 +639,24 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
   }
 }
 
-template <int BM, int BN>
-hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
+template <int BM, int BN, bool kPreSplit>
+void launch_gemm_tile_epi(const GemmArgs& g, hipStream_t s) {
   const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.k_splits);
   if (g.swiglu) {
-    gemm_f16w_kernel<BM, BN, kGemmEpiSwiGlu><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiSwiGlu, kPreSplit><<<grid, kGemmThreads, 0, s>>>(g);
   } else if (g.residual) {
-    gemm_f16w_kernel<BM, BN, kGemmEpiResidual><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiResidual, kPreSplit><<<grid, kGemmThreads, 0, s>>>(g);
   } else {
-    gemm_f16w_kernel<BM, BN, kGemmEpiStore><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiStore, kPreSplit><<<grid, kGemmThreads, 0, s>>>(g);
+  }
+}
+
+template <int BM, int BN>
+hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
+  if (g.a_hi) {
+    launch_gemm_tile_epi<BM, BN, true>(g, s);
+  } else {
+    launch_gemm_tile_epi<BM, BN, false>(g, s);
   }
   return hipGetLastError();
 }
@@ -703,6 +744,8 @@ int gemm_k_splits(int m, int n, int k) {
   return choose_gemm_tiling(m, n, k).splits;
 }
 
+bool gemm_presplit_supported(int m, int n, int k) { return gemm_supported(m, n, k) && !use_skinny(m, k); }
+
 bool gemm_swiglu_supported(int m, int n, int k) {
   return gemm_supported(m, n, k) && !use_skinny(m, k) && n % 2 == 0 && choose_gemm_tiling(m, n, k).splits == 1;
 }
@@ -710,6 +753,9 @@ bool gemm_swiglu_supported(int m, int n, int k) {
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < (g.swiglu ? g.n / 2 : g.n))
     return hipErrorInvalidValue;
+  // Pre-split A: all three planes, 16-byte rows, and the tiled path.
+  if (g.a_hi && (!g.a_lo || !g.a_inv || g.lda % 8 != 0 || use_skinny(g.m, g.k))) return hipErrorInvalidValue;
+  if (!g.a_hi && !g.a) return hipErrorInvalidValue;
   if (g.swiglu && (g.k_splits != 1 || g.residual || !gemm_swiglu_supported(g.m, g.n, g.k)))
     return hipErrorInvalidValue;
   if (g.k_splits < 1 || (g.k_splits > 1 && (g.residual || g.split_stride < static_cast<int64_t>(g.m) * g.ldc ||

@@ -56,6 +56,9 @@ struct DeviceState {
   int64_t pf_chunk = 0;
   float* pf_h = nullptr;    // [chunk][H] residual stream
   float* pf_x = nullptr;    // [chunk][H] normalised rows
+  // The normalised rows pre-split for the GEMMs (hi / lo fp16 planes and
+  // per-128-column scales), written by the norm kernels beside or instead of pf_x.
+  mmr::SplitPlanes pf_xs;
   float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
   float* pf_attn = nullptr; // [chunk][Hq d]
   float* pf_part = nullptr; // split-K partials of one GEMM (QKV, O, gate_up or down): [splits][chunk][N]
@@ -312,6 +315,9 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     ar.plan(C * Hq * D * 4);
     ar.plan(part_f * 4);
     ar.plan(C * F * 4);
+    ar.plan(C * H * 2);
+    ar.plan(C * H * 2);
+    ar.plan(C * ((H + mmr::kSplitChunk - 1) / mmr::kSplitChunk) * 4);
   }
   ar.allocate();
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
@@ -339,6 +345,9 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     s->pf_attn = ar.take<float>(C * Hq * D);
     s->pf_part = ar.take<float>(part_f);
     s->pf_act = ar.take<float>(C * F);
+    s->pf_xs.hi = ar.take<uint16_t>(C * H);
+    s->pf_xs.lo = ar.take<uint16_t>(C * H);
+    s->pf_xs.inv = ar.take<float>(C * ((H + mmr::kSplitChunk - 1) / mmr::kSplitChunk));
   }
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
                           hipHostMallocDefault),
@@ -519,9 +528,29 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
   // Split-K partial products into pf_part (at most max_splits; returns the
   // split count, 1 = the dense product); the consumers add the partials:
   // q/k norm + RoPE + KV write, residual add + RMSNorm, or SwiGLU.
+  // The normalised rows go to the QKV and gate_up GEMMs pre-split when the
+  // tiled path takes them (all but the few-rows path): the GEMM blocks then
+  // stage the planes instead of each splitting the same rows again.
+  const bool presplit = mmr::gemm_presplit_supported(rows, qkv_w, H) && mmr::gemm_presplit_supported(rows, 2 * F, H);
+  const mmr::SplitPlanes* xs = presplit ? &s.pf_xs : nullptr;
+  float* const xf = presplit ? nullptr : s.pf_x;  // fp32 normalised rows, when the GEMMs read those
+  auto use_x = [&](mmr::GemmArgs& g) {
+    if (presplit) {
+      g.a = nullptr;
+      g.a_hi = s.pf_xs.hi;
+      g.a_lo = s.pf_xs.lo;
+      g.a_inv = s.pf_xs.inv;
+    } else {
+      g.a = s.pf_x;
+    }
+  };
   auto gemm_parts = [&](const float* a, int lda, const __half* w, int N, int K, int max_splits) {
     mmr::GemmArgs g;
-    g.a = a;
+    if (a == s.pf_x) {
+      use_x(g);
+    } else {
+      g.a = a;
+    }
     g.lda = lda;
     g.w = w;
     g.c = s.pf_part;
@@ -538,7 +567,8 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
   const size_t L = m.layers.size();
   // Layer 0's input norm; later layers get theirs from the previous layer's
   // residual consumer.
-  check_hip(mmr::launch_rms_norm_rows(s.pf_h, m.layers[0].input_norm, c.rms_norm_eps, rows, H, s.pf_x, s.stream),
+  check_hip(mmr::launch_batch_residual_norm(s.pf_h, nullptr, 0, rows, H, m.layers[0].input_norm, c.rms_norm_eps, xf,
+                                            false, s.stream, xs),
             "prefill input norm");
   for (size_t l = 0; l < L; ++l) {
     const LayerDev& Ld = m.layers[l];
@@ -578,12 +608,12 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     at.out_stride = Hq * D;
     check_hip(mmr::launch_prefill_attention(at, s.kv, s.stream), "prefill attention");
     const int so = gemm_parts(s.pf_attn, Hq * D, Ld.o, H, Hq * D, kAnySplits);
-    check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, s.pf_x,
-                                              false, s.stream),
+    check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, xf,
+                                              false, s.stream, xs),
               "prefill residual + post norm");
     if (mmr::gemm_swiglu_supported(rows, 2 * F, H)) {  // SwiGLU in the gate_up epilogue
       mmr::GemmArgs g;
-      g.a = s.pf_x;
+      use_x(g);
       g.lda = H;
       g.w = Ld.gate_up;
       g.c = s.pf_act;
@@ -601,9 +631,10 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     // The next layer's input norm (after the last layer: the final norm, whose
     // rows are not used; the head normalises the last row itself).
     const bool last = l + 1 == L;
+    // The final norm's rows are not split (nothing multiplies them).
     check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, sd, rows, H,
                                               last ? m.final_norm : m.layers[l + 1].input_norm, c.rms_norm_eps,
-                                              s.pf_x, last, s.stream),
+                                              last ? s.pf_x : xf, last, s.stream, last ? nullptr : xs),
               "prefill residual + norm");
   }
 }
