@@ -435,9 +435,8 @@ __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float*
       xr[i] = kFinal ? (hr[i] * scale) * w[i] : hr[i] * (scale * w[i]);
   }
   if constexpr (kSplit) {
-    // Thread = 4 consecutive columns; the 32 threads of a 128-wide chunk
-    // reduce its max together (whole chunks per pass: 1024 threads = 32
-    // chunks), then write the planes as GemmStage would split them.
+    // Thread = 4 consecutive columns; the threads of a chunk reduce its max
+    // together (whole chunks per pass), then write the planes.
     const int nchunks = (cols + kSplitChunk - 1) / kSplitChunk;
     for (int q0 = 0; q0 < nchunks * (kSplitChunk / 4); q0 += kResThreads) {  // block-uniform
       const int q = q0 + static_cast<int>(threadIdx.x);
@@ -449,7 +448,8 @@ __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float*
           v[e] = kFinal ? (hr[i] * scale) * w[i] : hr[i] * (scale * w[i]);
         }
       }
-      const float mx = group_max<32>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+      const float mx =
+          group_max<kSplitChunk / 4>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
       if (4 * q < cols) {
         int e2 = 0;
         frexpf(mx, &e2);  // e2 = 0 for a zero chunk

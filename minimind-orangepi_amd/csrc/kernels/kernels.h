@@ -173,6 +173,22 @@ hipError_t launch_qkv_postprocess(const QkvPostArgs& a, KvDtype kv, hipStream_t 
 // C[m][n] = (residual[m][n] +) sum_k A[m][k] * W[n][k]: A fp32 (row stride
 // lda), W fp16 row-major [n][k], C fp32 (row stride ldc); residual may alias
 // C.  fp32 matrix cores, fp32 accumulation.  k % 8 == 0, lda % 4 == 0.
+// A [rows][cols] as the GEMM's fp16 matrix cores take it: per row and
+// `chunk`-wide column chunk a power-of-two scale s (the chunk's max |a|
+// mapped into [2^14, 2^15)), hi = fp16(s a), lo = fp16(s a - hi), inv = 1 / s.
+// Written once by the kernel producing A, staged by every GEMM block.
+// kSplitChunk (one scale per GEMM K tile) is staged as is; kSplitChunkFine
+// suits producers that see 32 columns at a time (attention heads, the SwiGLU
+// epilogue) and is brought to one scale per K tile while staging.
+constexpr int kSplitChunk = 128;
+constexpr int kSplitChunkFine = 32;
+struct SplitPlanes {
+  uint16_t* hi = nullptr;  // [rows][row stride] fp16 bits, cols used
+  uint16_t* lo = nullptr;
+  float* inv = nullptr;    // [rows][ceil(cols / chunk)], dense
+  int chunk = kSplitChunk;
+};
+
 struct GemmArgs {
   const float* a = nullptr;
   int lda = 0;
@@ -188,12 +204,17 @@ struct GemmArgs {
   // SwiGLU epilogue over interleaved gate/up columns: c receives
   // act[m][n / 2] (row stride ldc); needs k_splits == 1 and no residual.
   bool swiglu = false;
-  // A given pre-split instead of `a` (see SplitPlanes): fp16 bit planes hi and
-  // lo [m][lda] and inv [m][ceil(k / 128)].  The product is bit-identical to
-  // the fp32 path's, which splits the same way per block.
+  // A given pre-split instead of `a` (SplitPlanes): fp16 bit planes hi and lo
+  // [m][lda] and inv [m][ceil(k / a_chunk)]; a_chunk kSplitChunkFine only
+  // for the plain store (no residual, no SwiGLU).
   const uint16_t* a_hi = nullptr;
   const uint16_t* a_lo = nullptr;
   const float* a_inv = nullptr;
+  int a_chunk = kSplitChunk;
+  // SwiGLU epilogue only: act as SplitPlanes instead of into c (c unused),
+  // with kSplitChunkFine chunks (planes [m][ldc], inv [m][n / 2 / 32]);
+  // needs the tiling gemm_swiglu_split_supported accepts.
+  SplitPlanes act_split;
 };
 bool gemm_supported(int m, int n, int k);
 // Split count launch_gemm accepts and uses well for this shape: about four
@@ -204,6 +225,10 @@ bool gemm_swiglu_supported(int m, int n, int k);
 // Whether launch_gemm takes pre-split A (a_hi / a_lo / a_inv) for this shape
 // (the tiled path; the few-rows path reads fp32 A).
 bool gemm_presplit_supported(int m, int n, int k);
+// Whether the SwiGLU epilogue can write act pre-split (act_split) for this
+// shape: 64 x 128 tiles (a block holds 64 whole act columns of its rows) and
+// n a multiple of 64.
+bool gemm_swiglu_split_supported(int m, int n, int k);
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Rows of the fused qkv projection for tokens at positions start ..
@@ -243,8 +268,11 @@ struct PrefillAttnArgs {
   int start = 0;
   int tokens = 0;
   int hq = 0, hkv = 0, d = 0;
-  float* out = nullptr;  // [tokens][out_stride]
+  float* out = nullptr;  // [tokens][out_stride]; may be null when out_split is set
   int out_stride = 0;
+  // Optional: the output also as SplitPlanes with kSplitChunkFine chunks,
+  // planes [tokens][out_stride], inv [tokens][hq d / 32]; needs d % 32 == 0.
+  SplitPlanes out_split;
 };
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, KvDtype kv, hipStream_t stream);
 
@@ -296,15 +324,6 @@ bool splitk_swiglu_supported(int m, int kc, int gu_splits);
 // kc, attn_splits splits and head_dim d.
 bool splitk_combine_supported(int m, int kc, int attn_splits, int d);
 hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream);
-// A [rows][cols] as the GEMM's fp16 matrix cores take it: per row and
-// 128-wide column chunk a power-of-two scale s (the chunk's max |a| mapped
-// into [2^14, 2^15)), hi = fp16(s a), lo = fp16(s a - hi), inv = 1 / s.
-struct SplitPlanes {
-  uint16_t* hi = nullptr;  // [rows][cols] fp16 bits
-  uint16_t* lo = nullptr;
-  float* inv = nullptr;    // [rows][ceil(cols / 128)]
-};
-constexpr int kSplitChunk = 128;
 // h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]); x may be
 // null when `split` receives the normalised rows instead (or as well).
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,

@@ -57,20 +57,29 @@ using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 // BN x BK fp16 of W as 8-half chunks; thread t takes chunks t, t + 256, ...
 // so consecutive lanes read consecutive 16-byte pieces of a row (32 lanes per
 // A row, 16 per W row).
-template <int BM, int BN, bool kPreSplit = false>
+// How a GEMM block gets A: fp32 rows it splits itself (kSplitNone); planes
+// pre-split per 128 columns, one scale per row and K tile (kSplitTile); planes
+// pre-split per 32 columns, brought to one scale per row and K tile while
+// staging (kSplitFine).
+constexpr int kSplitNone = 0, kSplitTile = 1, kSplitFine = 2;
+
+template <int BM, int BN, int kMode = kSplitNone>
 struct GemmStage {
+  static constexpr bool kPreSplit = kMode != kSplitNone;
   static constexpr int kA = BM * kGemmBK / 4 / kGemmThreads;
   static constexpr int kB = BN * kGemmBK / 8 / kGemmThreads;
   // Pre-split A: 16-byte chunks (8 halves) of each plane per thread.
   static constexpr int kP = kPreSplit ? BM * kGemmBK / 8 / kGemmThreads : 1;
   float4 a[kPreSplit ? 1 : kA];
   uint4 ph[kP], pl[kP];
-  float pinv = 0.0f;
+  // kSplitTile: row tid's scale; kSplitFine: the scale of each chunk's 32 columns.
+  float pinv[kMode == kSplitFine ? kP : 1];
   uint4 b[kB];
 
   __device__ __forceinline__ void load(const GemmArgs& g, int m0, int n0, int k0, int tid) {
     if constexpr (kPreSplit) {
       static_assert(kP >= 1 && BM <= kGemmThreads, "tile too small for the block");
+      static_assert(kGemmBK == kSplitChunk && kGemmBK % kSplitChunkFine == 0, "scale layout");
 #pragma unroll
       for (int i = 0; i < kP; ++i) {
         const int idx = tid + i * kGemmThreads;
@@ -83,8 +92,19 @@ struct GemmStage {
         ph[i] = kc < g.k ? vh : make_uint4(0u, 0u, 0u, 0u);
         pl[i] = kc < g.k ? vl : make_uint4(0u, 0u, 0u, 0u);
       }
-      const int nkc = (g.k + kGemmBK - 1) / kGemmBK;
-      pinv = g.a_inv[static_cast<int64_t>(min(m0 + min(tid, BM - 1), g.m - 1)) * nkc + k0 / kGemmBK];
+      if constexpr (kMode == kSplitTile) {
+        const int nkc = (g.k + kGemmBK - 1) / kGemmBK;
+        pinv[0] = g.a_inv[static_cast<int64_t>(min(m0 + min(tid, BM - 1), g.m - 1)) * nkc + k0 / kGemmBK];
+      } else {
+        const int nkc = (g.k + kSplitChunkFine - 1) / kSplitChunkFine;
+#pragma unroll
+        for (int i = 0; i < kP; ++i) {
+          const int idx = tid + i * kGemmThreads;
+          const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
+          const int c = min((k0 + q * 8) / kSplitChunkFine, nkc - 1);  // past k: any scale, the planes are zero
+          pinv[i] = g.a_inv[static_cast<int64_t>(min(m0 + r, g.m - 1)) * nkc + c];
+        }
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < kA; ++i) {
@@ -113,7 +133,7 @@ struct GemmStage {
   // The 32 lanes holding a row reduce its maximum together.
   __device__ __forceinline__ void store(_Float16 (*Ah)[kGemmLDH], _Float16 (*Al)[kGemmLDH], float* inv,
                                         _Float16 (*Bs)[kGemmLDH], int tid) const {
-    if constexpr (kPreSplit) {
+    if constexpr (kMode == kSplitTile) {
 #pragma unroll
       for (int i = 0; i < kP; ++i) {
         const int idx = tid + i * kGemmThreads;
@@ -121,7 +141,30 @@ struct GemmStage {
         *reinterpret_cast<uint4*>(&Ah[r][q * 8]) = ph[i];
         *reinterpret_cast<uint4*>(&Al[r][q * 8]) = pl[i];
       }
-      if (tid < BM) inv[tid] = pinv;
+      if (tid < BM) inv[tid] = pinv[0];
+    } else if constexpr (kMode == kSplitFine) {
+      // The 16 lanes holding a row's tile take its largest chunk scale as the
+      // tile's, and multiply their chunk by the power of two between the two
+      // (exact but for results below fp16's normal range, i.e. below 2^-29 of
+      // the tile's largest value: far under fp32 accumulation's rounding).
+#pragma unroll
+      for (int i = 0; i < kP; ++i) {
+        const int idx = tid + i * kGemmThreads;
+        const int r = idx / (kGemmBK / 8), q = idx % (kGemmBK / 8);
+        const float tinv = group_max<kGemmBK / 8>(pinv[i]);
+        int ec = 0, et = 0;
+        frexpf(pinv[i], &ec);
+        frexpf(tinv, &et);
+        const _Float16 ratio = static_cast<_Float16>(ldexpf(1.0f, ec - et));  // 2^-d, 0 below 2^-24
+        f16x8 vh, vl;
+        __builtin_memcpy(&vh, &ph[i], 16);
+        __builtin_memcpy(&vl, &pl[i], 16);
+        vh *= ratio;
+        vl *= ratio;
+        *reinterpret_cast<f16x8*>(&Ah[r][q * 8]) = vh;
+        *reinterpret_cast<f16x8*>(&Al[r][q * 8]) = vl;
+        if (q == 0) inv[r] = tinv;
+      }
     }
 #pragma unroll
     for (int i = 0; i < (kPreSplit ? 0 : kA); ++i) {
@@ -166,9 +209,10 @@ struct GemmStage {
 // interleaved gate/up columns (2i, 2i + 1) -> act[m][i] (decoder_layer.cpp:
 // 175-182), the pair meeting through one lane exchange.
 constexpr int kGemmEpiStore = 0, kGemmEpiResidual = 1, kGemmEpiSwiGlu = 2;
+constexpr int kActLd = 64 + 4;  // floats per row of the act tile in LDS (64 x 128 tiles)
 
-template <int BM, int BN, int kEpi, bool kPreSplit>
-__global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
+template <int BM, int BN, int kEpi, int kMode>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_f16w_kernel(GemmArgs g) {
   constexpr bool kResidual = kEpi == kGemmEpiResidual;
   constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
   static_assert(GemmStage<BM, BN>::kA >= 1 && GemmStage<BM, BN>::kB >= 1, "tile too small for the block");
@@ -194,7 +238,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
   const int kt0 = static_cast<int>(blockIdx.z) * per, kt1 = min(kt0 + per, nk);
   float* out = g.c + static_cast<int64_t>(blockIdx.z) * g.split_stride;
 
-  GemmStage<BM, BN, kPreSplit> stage;
+  GemmStage<BM, BN, kMode> stage;
   stage.load(g, m0, n0, kt0 * kGemmBK, tid);  // past k: clamped loads, zeroed
   stage.store(Ah, Al, inv_s, Bs, tid);
   __syncthreads();
@@ -258,25 +302,89 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f16w_kernel(GemmArgs g) {
         }
       }
   }
+  // SwiGLU: even lanes hold gate column 2i, their odd neighbours up column
+  // 2i + 1 (one DPP exchange).
+  auto swiglu_act = [](float v) {
+    const float u = dpp_move<dpp::kQuadXor1>(v);
+    return (v / (1.0f + expf(-v))) * u;
+  };
+  bool act_to_lds = false;
+  if constexpr (kEpi == kGemmEpiSwiGlu && BN == 128) act_to_lds = g.act_split.hi != nullptr;
+  if (act_to_lds) {
+    // act tile for the pre-split writer below: [BM][BN / 2] (padded) over the
+    // W staging buffer, which the K loop no longer reads.  Rows past m hold
+    // values of clamped rows; the writer skips them.
+    float* act_s = reinterpret_cast<float*>(&Bs[0][0]);
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
-        const float v = acc[i][j][r];
-        if constexpr (kEpi == kGemmEpiSwiGlu) {
-          // Even lanes hold gate column 2i, their odd neighbours up column 2i + 1.
-          const float u = __shfl_xor(v, 1);
-          if ((lane & 1) == 0 && row < g.m && col < g.n)
-            out[static_cast<int64_t>(row) * g.ldc + col / 2] = (v / (1.0f + expf(-v))) * u;
-        } else if (row < g.m && col < g.n) {
-          out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
+        for (int r = 0; r < 4; ++r) {
+          const float act = swiglu_act(acc[i][j][r]);
+          if ((lane & 1) == 0)
+            act_s[(wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r) * kActLd + (wn * (BN / 2) + j * 16 + lane % 16) / 2] =
+                act;
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
+          const float v = acc[i][j][r];
+          if constexpr (kEpi == kGemmEpiSwiGlu) {
+            const float act = swiglu_act(v);
+            if ((lane & 1) == 0 && row < g.m && col < g.n) out[static_cast<int64_t>(row) * g.ldc + col / 2] = act;
+          } else if (row < g.m && col < g.n) {
+            out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
+          }
+        }
+      }
+  }
+  if constexpr (kEpi == kGemmEpiSwiGlu && BN == 128) {
+    if (act_to_lds) {
+      // act pre-split per 32 columns (the down GEMM's A): thread = 4
+      // consecutive columns of one row, the 8 threads of a chunk reduce its
+      // max together, then write 8-byte runs of both planes.
+      static_assert(BM * kActLd * 4 <= BN * kGemmLDH * 2, "act tile exceeds the W buffer");
+      __syncthreads();
+      const float* act_s = reinterpret_cast<const float*>(&Bs[0][0]);
+      const int nkc = g.n / 2 / kSplitChunkFine;
+#pragma unroll
+      for (int p = 0; p < BM * (BN / 2) / 4 / kGemmThreads; ++p) {
+        const int idx = tid + p * kGemmThreads;
+        const int r = idx / (BN / 8), c4 = idx % (BN / 8);
+        const int row = m0 + r, col = n0 / 2 + c4 * 4;
+        const bool ok = row < g.m && col < g.n / 2;
+        const float4 v = ok ? *reinterpret_cast<const float4*>(&act_s[r * kActLd + c4 * 4])
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float mx =
+            group_max<kSplitChunkFine / 4>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        int e = 0;
+        frexpf(mx, &e);  // e = 0 for a zero chunk
+        e = max(e, -100);
+        const float sc = ldexpf(1.0f, 15 - e);
+        const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+        f16x4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hi[j] = static_cast<_Float16>(x[j]);
+          lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(hi[j]));
+        }
+        if (ok) {
+          const int64_t off = static_cast<int64_t>(row) * g.ldc + col;
+          *reinterpret_cast<f16x4*>(g.act_split.hi + off) = hi;
+          *reinterpret_cast<f16x4*>(g.act_split.lo + off) = lo;
+          if (c4 % (kSplitChunkFine / 4) == 0)
+            g.act_split.inv[static_cast<int64_t>(row) * nkc + col / kSplitChunkFine] = ldexpf(1.0f, e - 15);
         }
       }
     }
+  }
 }
 
 // Skinny GEMM for few rows of A (batched decode, m <= 16 * BT): one block per
@@ -629,34 +737,60 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
     for (int w = 0; w < kPrefillWaves; ++w) m_sh[w * kPrefillQueries + q] = e[w] * inv;
   }
   __syncthreads();
+  // Every thread runs the same trip count (16 D is a multiple of the block
+  // for d % 32 == 0), so the 32-lane chunk reductions below see whole waves.
   for (int idx = threadIdx.x; idx < kPrefillQueries * D; idx += kWave * kPrefillWaves) {
     const int q = idx / D, dim = idx % D;
-    if (q0 + q >= a.tokens) continue;
+    const bool valid = q0 + q < a.tokens;
     float o = 0.0f;
 #pragma unroll
     for (int w = 0; w < kPrefillWaves; ++w) o = fmaf(o_sh[(w * D + dim) * kMergeLd + q], m_sh[w * kPrefillQueries + q], o);
-    a.out[static_cast<int64_t>(q0 + q) * a.out_stride + h * D + dim] = o;
+    const int64_t off = static_cast<int64_t>(q0 + q) * a.out_stride + h * D + dim;
+    if (a.out && valid) a.out[off] = o;
+    if constexpr (D % kSplitChunkFine == 0) {
+      if (a.out_split.hi) {
+        // 32 consecutive dims of one query per chunk (the lanes of a half wave).
+        const float mx = group_max<kSplitChunkFine>(valid ? fabsf(o) : 0.0f);
+        int e = 0;
+        frexpf(mx, &e);  // e = 0 for a zero chunk
+        e = max(e, -100);
+        if (valid) {
+          const float xs = o * ldexpf(1.0f, 15 - e);
+          const _Float16 hh = static_cast<_Float16>(xs);
+          const _Float16 ll = static_cast<_Float16>(xs - static_cast<float>(hh));
+          __builtin_memcpy(a.out_split.hi + off, &hh, 2);
+          __builtin_memcpy(a.out_split.lo + off, &ll, 2);
+          if (dim % kSplitChunkFine == 0)
+            a.out_split.inv[static_cast<int64_t>(q0 + q) * (a.hq * D / kSplitChunkFine) + (h * D + dim) / kSplitChunkFine] =
+                ldexpf(1.0f, e - 15);
+        }
+      }
+    }
   }
 }
 
-template <int BM, int BN, bool kPreSplit>
+template <int BM, int BN, int kMode>
 void launch_gemm_tile_epi(const GemmArgs& g, hipStream_t s) {
   const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.k_splits);
   if (g.swiglu) {
-    gemm_f16w_kernel<BM, BN, kGemmEpiSwiGlu, kPreSplit><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiSwiGlu, kMode><<<grid, kGemmThreads, 0, s>>>(g);
   } else if (g.residual) {
-    gemm_f16w_kernel<BM, BN, kGemmEpiResidual, kPreSplit><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiResidual, kMode><<<grid, kGemmThreads, 0, s>>>(g);
   } else {
-    gemm_f16w_kernel<BM, BN, kGemmEpiStore, kPreSplit><<<grid, kGemmThreads, 0, s>>>(g);
+    gemm_f16w_kernel<BM, BN, kGemmEpiStore, kMode><<<grid, kGemmThreads, 0, s>>>(g);
   }
 }
 
 template <int BM, int BN>
 hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
-  if (g.a_hi) {
-    launch_gemm_tile_epi<BM, BN, true>(g, s);
+  if (!g.a_hi) {
+    launch_gemm_tile_epi<BM, BN, kSplitNone>(g, s);
+  } else if (g.a_chunk == kSplitChunk) {
+    launch_gemm_tile_epi<BM, BN, kSplitTile>(g, s);
   } else {
-    launch_gemm_tile_epi<BM, BN, false>(g, s);
+    // Fine planes feed the split-K partial products (O, down) only.
+    const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.k_splits);
+    gemm_f16w_kernel<BM, BN, kGemmEpiStore, kSplitFine><<<grid, kGemmThreads, 0, s>>>(g);
   }
   return hipGetLastError();
 }
@@ -746,6 +880,10 @@ int gemm_k_splits(int m, int n, int k) {
 
 bool gemm_presplit_supported(int m, int n, int k) { return gemm_supported(m, n, k) && !use_skinny(m, k); }
 
+bool gemm_swiglu_split_supported(int m, int n, int k) {
+  return gemm_swiglu_supported(m, n, k) && n % (2 * kSplitChunkFine) == 0 && choose_gemm_tiling(m, n, k).bn == 128;
+}
+
 bool gemm_swiglu_supported(int m, int n, int k) {
   return gemm_supported(m, n, k) && !use_skinny(m, k) && n % 2 == 0 && choose_gemm_tiling(m, n, k).splits == 1;
 }
@@ -753,9 +891,19 @@ bool gemm_swiglu_supported(int m, int n, int k) {
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
   if (!gemm_supported(g.m, g.n, g.k) || g.lda % 4 != 0 || g.lda < g.k || g.ldc < (g.swiglu ? g.n / 2 : g.n))
     return hipErrorInvalidValue;
-  // Pre-split A: all three planes, 16-byte rows, and the tiled path.
-  if (g.a_hi && (!g.a_lo || !g.a_inv || g.lda % 8 != 0 || use_skinny(g.m, g.k))) return hipErrorInvalidValue;
+  // Pre-split A: all three planes, 16-byte rows, and the tiled path; fine
+  // (32-column) scales only for the plain store.
+  if (g.a_hi && (!g.a_lo || !g.a_inv || g.lda % 8 != 0 || use_skinny(g.m, g.k) ||
+                 (g.a_chunk != kSplitChunk && g.a_chunk != kSplitChunkFine) ||
+                 (g.a_chunk == kSplitChunkFine && (g.swiglu || g.residual))))
+    return hipErrorInvalidValue;
   if (!g.a_hi && !g.a) return hipErrorInvalidValue;
+  // act pre-split: the SwiGLU epilogue on 64 x 128 tiles, all three planes,
+  // 8-byte rows.
+  if (g.act_split.hi && (!g.swiglu || !g.act_split.lo || !g.act_split.inv || g.ldc % 4 != 0 ||
+                         !gemm_swiglu_split_supported(g.m, g.n, g.k)))
+    return hipErrorInvalidValue;
+  if (!g.c && !g.act_split.hi) return hipErrorInvalidValue;
   if (g.swiglu && (g.k_splits != 1 || g.residual || !gemm_swiglu_supported(g.m, g.n, g.k)))
     return hipErrorInvalidValue;
   if (g.k_splits < 1 || (g.k_splits > 1 && (g.residual || g.split_stride < static_cast<int64_t>(g.m) * g.ldc ||
@@ -791,6 +939,10 @@ hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream)
 
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, KvDtype kv, hipStream_t stream) {
   if (!attention_supported(a.hq, a.hkv, a.d) || a.tokens <= 0 || a.start < 0) return hipErrorInvalidValue;
+  if (!a.out && !a.out_split.hi) return hipErrorInvalidValue;
+  if (a.out_split.hi && (!a.out_split.lo || !a.out_split.inv || a.out_split.chunk != kSplitChunkFine ||
+                         a.d % kSplitChunkFine != 0))
+    return hipErrorInvalidValue;
   return kv == kKvF16 ? launch_prefill_attention_kv<__half>(a, stream)
                       : launch_prefill_attention_kv<float>(a, stream);
 }

@@ -56,9 +56,11 @@ struct DeviceState {
   int64_t pf_chunk = 0;
   float* pf_h = nullptr;    // [chunk][H] residual stream
   float* pf_x = nullptr;    // [chunk][H] normalised rows
-  // The normalised rows pre-split for the GEMMs (hi / lo fp16 planes and
-  // per-128-column scales), written by the norm kernels beside or instead of pf_x.
-  mmr::SplitPlanes pf_xs;
+  // GEMM inputs pre-split (hi / lo fp16 planes and power-of-two scales): the
+  // normalised rows (per 128 columns, written by the norm kernels instead of
+  // pf_x), the attention output (per 32, instead of pf_attn) and act (per 32,
+  // written by the gate_up epilogue instead of pf_act).
+  mmr::SplitPlanes pf_xs, pf_attn_s, pf_act_s;
   float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
   float* pf_attn = nullptr; // [chunk][Hq d]
   float* pf_part = nullptr; // split-K partials of one GEMM (QKV, O, gate_up or down): [splits][chunk][N]
@@ -318,6 +320,12 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     ar.plan(C * H * 2);
     ar.plan(C * H * 2);
     ar.plan(C * ((H + mmr::kSplitChunk - 1) / mmr::kSplitChunk) * 4);
+    ar.plan(C * Hq * D * 2);
+    ar.plan(C * Hq * D * 2);
+    ar.plan(C * ((Hq * D + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine) * 4);
+    ar.plan(C * F * 2);
+    ar.plan(C * F * 2);
+    ar.plan(C * ((F + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine) * 4);
   }
   ar.allocate();
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
@@ -348,6 +356,14 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     s->pf_xs.hi = ar.take<uint16_t>(C * H);
     s->pf_xs.lo = ar.take<uint16_t>(C * H);
     s->pf_xs.inv = ar.take<float>(C * ((H + mmr::kSplitChunk - 1) / mmr::kSplitChunk));
+    s->pf_attn_s.hi = ar.take<uint16_t>(C * Hq * D);
+    s->pf_attn_s.lo = ar.take<uint16_t>(C * Hq * D);
+    s->pf_attn_s.inv = ar.take<float>(C * ((Hq * D + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine));
+    s->pf_attn_s.chunk = mmr::kSplitChunkFine;
+    s->pf_act_s.hi = ar.take<uint16_t>(C * F);
+    s->pf_act_s.lo = ar.take<uint16_t>(C * F);
+    s->pf_act_s.inv = ar.take<float>(C * ((F + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine));
+    s->pf_act_s.chunk = mmr::kSplitChunkFine;
   }
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
                           hipHostMallocDefault),
@@ -534,12 +550,21 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
   const bool presplit = mmr::gemm_presplit_supported(rows, qkv_w, H) && mmr::gemm_presplit_supported(rows, 2 * F, H);
   const mmr::SplitPlanes* xs = presplit ? &s.pf_xs : nullptr;
   float* const xf = presplit ? nullptr : s.pf_x;  // fp32 normalised rows, when the GEMMs read those
+  // Likewise the attention output (written split by the attention kernel)
+  // for the O GEMM, and act (written split by the gate_up SwiGLU epilogue)
+  // for the down GEMM.
+  const bool attn_split = D % mmr::kSplitChunkFine == 0 && mmr::gemm_presplit_supported(rows, H, Hq * D);
+  const bool act_split = mmr::gemm_swiglu_split_supported(rows, 2 * F, H) && mmr::gemm_presplit_supported(rows, H, F);
+  auto use_planes = [](mmr::GemmArgs& g, const mmr::SplitPlanes& p) {
+    g.a = nullptr;
+    g.a_hi = p.hi;
+    g.a_lo = p.lo;
+    g.a_inv = p.inv;
+    g.a_chunk = p.chunk;
+  };
   auto use_x = [&](mmr::GemmArgs& g) {
     if (presplit) {
-      g.a = nullptr;
-      g.a_hi = s.pf_xs.hi;
-      g.a_lo = s.pf_xs.lo;
-      g.a_inv = s.pf_xs.inv;
+      use_planes(g, s.pf_xs);
     } else {
       g.a = s.pf_x;
     }
@@ -548,6 +573,10 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     mmr::GemmArgs g;
     if (a == s.pf_x) {
       use_x(g);
+    } else if (a == s.pf_attn && attn_split) {
+      use_planes(g, s.pf_attn_s);
+    } else if (a == s.pf_act && act_split) {
+      use_planes(g, s.pf_act_s);
     } else {
       g.a = a;
     }
@@ -604,8 +633,9 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     at.hq = Hq;
     at.hkv = Hkv;
     at.d = D;
-    at.out = s.pf_attn;
+    at.out = attn_split ? nullptr : s.pf_attn;
     at.out_stride = Hq * D;
+    if (attn_split) at.out_split = s.pf_attn_s;
     check_hip(mmr::launch_prefill_attention(at, s.kv, s.stream), "prefill attention");
     const int so = gemm_parts(s.pf_attn, Hq * D, Ld.o, H, Hq * D, kAnySplits);
     check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, xf,
@@ -616,7 +646,8 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
       use_x(g);
       g.lda = H;
       g.w = Ld.gate_up;
-      g.c = s.pf_act;
+      g.c = act_split ? nullptr : s.pf_act;
+      if (act_split) g.act_split = s.pf_act_s;
       g.ldc = F;
       g.m = rows;
       g.n = 2 * F;
