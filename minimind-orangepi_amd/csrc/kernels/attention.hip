@@ -719,19 +719,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   }
 }
 
-// Log-sum-exp combine of the split partials: one block of 1024 threads per
-// query head (grid.y: sequence of a batch).  Thread t holds the (m, l) of
-// splits t, t + 1024, ... (at most kCombineKernelMaxSplits in all); block
-// reductions give M = max m and L = sum_s l_s exp(m_s - M); the weights
-// exp(m_s - M) go to LDS, and eight groups of 128 threads (thread = dimension)
-// each sum e_s o_s over every eighth split with eight loads in flight; the
-// groups' sums are added in group order.  Every order is fixed, so the result
-// is deterministic.  (The O-projection prologue, kProAttnCombine, computes
-// the same quantity for up to kCombineMaxSplits splits.)
-constexpr int kCombineThreads = 1024;
-constexpr int kCombineGroups = kCombineThreads / 128;
-constexpr int kCombinePerThread = 4;
-constexpr int kCombineKernelMaxSplits = kCombineThreads * kCombinePerThread;
+// Log-sum-exp combine of the split partials: one block of 256 threads per
+// (query head, 32-dimension slice) (grid.y: sequence of a batch).  Thread t
+// holds the (m, l) of splits t, t + 256, ... (at most kCombineKernelMaxSplits
+// in all); block reductions give M = max m and L = sum_s l_s exp(m_s - M);
+// the weights exp(m_s - M) go to LDS, and eight groups of 32 threads (thread
+// = dimension) each sum e_s o_s over every eighth split.  The first eight o
+// values of every thread are loaded with the (m, l), so one memory round trip
+// serves up to 64 splits.  The groups' sums are added in group order.  Every
+// order is fixed, so the result is deterministic.  (The O-projection
+// prologue, kProAttnCombine, computes the same quantity for up to
+// kCombineMaxSplits splits.)
+constexpr int kCombineThreads = 256;
+constexpr int kCombineSlice = 32;                                   // dimensions per block
+constexpr int kCombineGroups = kCombineThreads / kCombineSlice;     // split groups
+constexpr int kCombineUnroll = 8;                                   // o loads in flight per thread
+constexpr int kCombineKernelMaxSplits = 4096;
+constexpr int kCombinePerThread = kCombineKernelMaxSplits / kCombineThreads;
 
 // Sum over the block (all threads active) in a fixed order.
 template <typename Op>
@@ -750,14 +754,25 @@ __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(cons
                                                                              int splits, int64_t part_stride,
                                                                              float* out) {
   __shared__ float s_w[kCombineKernelMaxSplits];
-  __shared__ float s_red[kCombineGroups][128];
+  __shared__ float s_red[kCombineGroups][kCombineSlice];
   __shared__ float s_scratch[kCombineThreads / kWave];
-  const int qh = blockIdx.x;
+  const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
+  const int qh = blockIdx.x / nslice, slice = blockIdx.x % nslice;
   part += static_cast<int64_t>(blockIdx.y) * part_stride;  // sequence of a batch
   out += static_cast<int64_t>(blockIdx.y) * hq * d;
   const int R = hq / hkv;
   const int g = qh / R, h = qh % R;
   const int tid = threadIdx.x;
+  const int grp = tid / kCombineSlice, dim = slice * kCombineSlice + tid % kCombineSlice;
+  const int dd = min(dim, d - 1);
+  // This thread's first kCombineUnroll o values (clamped: in bounds, weighted
+  // only below `splits`), issued together with the (m, l) loads.
+  float v[kCombineUnroll];
+#pragma unroll
+  for (int u = 0; u < kCombineUnroll; ++u)
+    v[u] = part[attn_o_offset(g, min(grp + kCombineGroups * u, splits - 1), h, splits, R, d) + dd];
+  // Unconditional, clamped (m, l) loads: past `splits` they repeat the last
+  // split's (one cache line per wave), and no branch holds the loads back.
   float2 ml[kCombinePerThread];
 #pragma unroll
   for (int j = 0; j < kCombinePerThread; ++j) {
@@ -779,26 +794,28 @@ __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(cons
     }
   }
   const float L = combine_block_reduce(l_loc, OpSum{}, s_scratch);  // its barriers also publish s_w
-  const int grp = tid / 128, dim = tid % 128;
-  const int dd = min(dim, d - 1);
   float o = 0.0f;
-  for (int base = grp; base < splits; base += kCombineGroups * 8) {
-    float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+  for (int u = 0; u < kCombineUnroll; ++u) {
+    const int sp = grp + kCombineGroups * u;
+    if (sp < splits) o = fmaf(v[u], s_w[sp], o);
+  }
+  for (int base = grp + kCombineGroups * kCombineUnroll; base < splits; base += kCombineGroups * kCombineUnroll) {
+#pragma unroll
+    for (int u = 0; u < kCombineUnroll; ++u)
       v[u] = part[attn_o_offset(g, min(base + kCombineGroups * u, splits - 1), h, splits, R, d) + dd];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kCombineUnroll; ++u) {
       const int sp = base + kCombineGroups * u;
       if (sp < splits) o = fmaf(v[u], s_w[sp], o);
     }
   }
-  s_red[grp][dim] = o;
+  s_red[grp][tid % kCombineSlice] = o;
   __syncthreads();
   if (grp == 0 && dim < d) {
-    float x = s_red[0][dim];
+    float x = s_red[0][tid];
 #pragma unroll
-    for (int gi = 1; gi < kCombineGroups; ++gi) x += s_red[gi][dim];
+    for (int gi = 1; gi < kCombineGroups; ++gi) x += s_red[gi][tid];
     out[qh * d + dim] = x * (1.0f / L);
   }
 }
@@ -921,8 +938,9 @@ hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, i
                                     hipStream_t stream, int batch, int64_t part_stride) {
   if (!attention_supported(hq, hkv, d) || d > 128 || splits <= 0 || splits > kCombineKernelMaxSplits || batch <= 0)
     return hipErrorInvalidValue;
-  attention_combine_kernel<<<dim3(hq, batch), kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
-                                                                            out);
+  const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
+  attention_combine_kernel<<<dim3(hq * nslice, batch), kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits,
+                                                                                     part_stride, out);
   return hipGetLastError();
 }
 
