@@ -363,7 +363,7 @@ def main() -> int:
     ap.add_argument("--kv", choices=["f32", "f16"], default="f16")
     ap.add_argument("--no-other-kv", action="store_true", help="skip the decode with the other KV cache dtype")
     ap.add_argument("--kernel-reps", type=int, default=320)
-    ap.add_argument("--cpu-sample-steps", type=int, default=48)
+    ap.add_argument("--cpu-sample-steps", type=int, default=320)  # ~13 s of one core
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=256)
