@@ -51,6 +51,7 @@ constexpr int kGemmBK = 128;           // K per LDS tile: the next tile's loads 
 constexpr int kGemmLDH = kGemmBK + 8;  // halves per LDS row (16-byte aligned, conflict-free fragment reads)
 
 using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 
 // Per-thread staging registers of one K tile: BM x BK fp32 of A as float4s,
@@ -588,6 +589,13 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
   const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
   float* k_s = stage[wave];            // [KT][LD]
   float* v_s = stage[wave] + KT * LD;  // [KT][LD]
+  // fp16 cache (d % 32 == 0): K and V stay fp16 in the stage and both
+  // products run on the fp16 matrix cores, with q and p split hi + lo.
+  constexpr bool kF16 = std::is_same<KV, __half>::value && D % 32 == 0;
+  constexpr int LDH = D + 8;  // halves per fp16 stage row: 16-byte aligned, 13 x 16 bytes for d 96
+  static_assert(!kF16 || 2 * KT * LDH * 2 <= kStageFloats * 4, "fp16 stage must fit");
+  _Float16* kh_s = reinterpret_cast<_Float16*>(stage[wave]);  // [KT][LDH]
+  _Float16* vh_s = kh_s + KT * LDH;                            // [KT][LDH]
 
   const int last_key = a.start + min(q0 + kPrefillQueries, a.tokens) - 1;  // the block's last query position
   const int n_tiles = last_key / KT + 1;
@@ -607,11 +615,30 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
   Regs regs;
   fetch(min(wave, n_tiles - 1), regs);  // unconditional; a wave with no tile never reads it
 
-  // Q^T fragments: dims 16j + 4 kq + {0..3} of query qi.
-  float4 qf[DT];
+  // Q^T fragments: dims 16j + 4 kq + {0..3} of query qi (fp32), or dims
+  // 32j + 8 kq + {0..7} split into fp16 hi + lo (fp16 path).
+  float4 qf[kF16 ? 1 : DT];
+  uint4 qh[kF16 ? D / 32 : 1], ql[kF16 ? D / 32 : 1];  // f16x8 bits
   const float* qsrc = a.query + static_cast<int64_t>(qrow) * a.query_stride + h * D;
+  if constexpr (kF16) {
 #pragma unroll
-  for (int j = 0; j < DT; ++j) qf[j] = *reinterpret_cast<const float4*>(qsrc + 16 * j + 4 * kq);
+    for (int j = 0; j < D / 32; ++j) {
+      const float4 x0 = *reinterpret_cast<const float4*>(qsrc + 32 * j + 8 * kq);
+      const float4 x1 = *reinterpret_cast<const float4*>(qsrc + 32 * j + 8 * kq + 4);
+      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      f16x8 hv, lv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hv[e] = static_cast<_Float16>(x[e]);
+        lv[e] = static_cast<_Float16>(x[e] - static_cast<float>(hv[e]));
+      }
+      qh[j] = __builtin_bit_cast(uint4, hv);
+      ql[j] = __builtin_bit_cast(uint4, lv);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < DT; ++j) qf[j] = *reinterpret_cast<const float4*>(qsrc + 16 * j + 4 * kq);
+  }
 
   f32x4 ot[DT];  // O^T[d = 16 dt + 4 kq + i][query qi]
 #pragma unroll
@@ -624,7 +651,13 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = lane + i * kWave;
-      if (c < kChunks) {
+      if (kF16 && c < kChunks) {
+        const int r = c / kRowChunks, col = (c % kRowChunks) * CH;
+        // Component-wise (a whole-struct copy would keep regs in scratch).
+        const uint4 kc = regs.k[i], vc = regs.v[i];
+        *reinterpret_cast<u32x4*>(&kh_s[r * LDH + col]) = u32x4{kc.x, kc.y, kc.z, kc.w};
+        *reinterpret_cast<u32x4*>(&vh_s[r * LDH + col]) = u32x4{vc.x, vc.y, vc.z, vc.w};
+      } else if (c < kChunks) {
         const int r = c / kRowChunks, col = (c % kRowChunks) * CH;
         float kf[CH], vf[CH];
         chunk_to_float_n<KV>(regs.k[i], kf);
@@ -647,13 +680,23 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
 #pragma unroll
     for (int kt = 0; kt < KT / 16; ++kt) {
       st[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (kF16) {
+        // A = K (key qi, dims 32j + 8 kq ..), B = Q^T: 32 dims per product.
 #pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        const float4 kf = *reinterpret_cast<const float4*>(&k_s[(kt * 16 + qi) * LD + 16 * j + 4 * kq]);
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[j].x, st[kt], 0, 0, 0);
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[j].y, st[kt], 0, 0, 0);
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[j].z, st[kt], 0, 0, 0);
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[j].w, st[kt], 0, 0, 0);
+        for (int j = 0; j < D / 32; ++j) {
+          const f16x8 kf = *reinterpret_cast<const f16x8*>(&kh_s[(kt * 16 + qi) * LDH + 32 * j + 8 * kq]);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, __builtin_bit_cast(f16x8, qh[j]), st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, __builtin_bit_cast(f16x8, ql[j]), st[kt], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+          const float4 kf = *reinterpret_cast<const float4*>(&k_s[(kt * 16 + qi) * LD + 16 * j + 4 * kq]);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.x, qf[j].x, st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.y, qf[j].y, st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.z, qf[j].z, st[kt], 0, 0, 0);
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf.w, qf[j].w, st[kt], 0, 0, 0);
+        }
       }
     }
     float mx = -INFINITY;
@@ -682,18 +725,39 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
         l_part += st[kt][i];
       }
     m_run = m_new;
-    // O^T += V^T P^T over the tile's keys.
+    // O^T += V^T P^T over the tile's keys.  fp16 path: one 16x16x16 product
+    // per (slice, plane): lane l supplies keys 4 kq + {0..3}, which are the
+    // rows of S^T it holds, so p goes in as is (split hi + lo).
+    if constexpr (kF16) {
 #pragma unroll
-    for (int kt = 0; kt < KT / 16; ++kt)
+      for (int kt = 0; kt < KT / 16; ++kt) {
+        f16x4 ph, pl;
 #pragma unroll
-      for (int j = 0; j < DT; ++j) {
-        const float* vcol = &v_s[(kt * 16 + 4 * kq) * LD + 16 * j + qi];
-        const float v0 = vcol[0], v1 = vcol[LD], v2 = vcol[2 * LD], v3 = vcol[3 * LD];
-        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0, st[kt][0], ot[j], 0, 0, 0);
-        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1, st[kt][1], ot[j], 0, 0, 0);
-        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v2, st[kt][2], ot[j], 0, 0, 0);
-        ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v3, st[kt][3], ot[j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          ph[i] = static_cast<_Float16>(st[kt][i]);
+          pl[i] = static_cast<_Float16>(st[kt][i] - static_cast<float>(ph[i]));
+        }
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+          const _Float16* vcol = &vh_s[(kt * 16 + 4 * kq) * LDH + 16 * j + qi];
+          const f16x4 va = {vcol[0], vcol[LDH], vcol[2 * LDH], vcol[3 * LDH]};
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, ot[j], 0, 0, 0);
+        }
       }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < KT / 16; ++kt)
+#pragma unroll
+        for (int j = 0; j < DT; ++j) {
+          const float* vcol = &v_s[(kt * 16 + 4 * kq) * LD + 16 * j + qi];
+          const float v0 = vcol[0], v1 = vcol[LD], v2 = vcol[2 * LD], v3 = vcol[3 * LD];
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0, st[kt][0], ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1, st[kt][1], ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v2, st[kt][2], ot[j], 0, 0, 0);
+          ot[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(v3, st[kt][3], ot[j], 0, 0, 0);
+        }
+    }
     // Reads of this stage finish before the next tile's writes (in-order LDS).
   };
   int tile = wave;
