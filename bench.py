@@ -533,8 +533,8 @@ def main() -> int:
                    "prompt_tokens": PROMPT_LEN, "decode_steps": args.steps, "kv_cache": args.kv,
                    "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 1),
-        "prefill_mode": "chunked batched kernels (fp16-MFMA GEMMs with hi/lo fp32 activations, fp32-MFMA causal "
-                        "attention), 512-token chunks",
+        "prefill_mode": "chunked batched kernels (fp16-MFMA GEMMs with hi/lo fp32 activations, fp16-MFMA causal "
+                        "attention with hi/lo q and p for the fp16 KV cache), 512-token chunks",
         "tokens_match_reference": parity,
         "step_bytes": step_bytes,
         "step_gbs": round(step_bytes / (decode_ms / args.steps * 1e-3) / 1e9, 1),

@@ -182,8 +182,8 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
  * (ascend_matmul.h:102-107) and cube_matmul (ascend_matmul.h:122-126).
  * y[b][r] = sum_c W[r*cols + c] * x[b][c] (+ residual[b][r]); W fp16
  * row-major [rows][cols], x [batch][cols], y/residual [batch][rows] fp32;
- * fp32 matrix cores with fp32 accumulation.  cols % 8 == 0; residual may
- * alias y. */
+ * fp16 matrix cores on x split into hi + lo fp16 planes (W is exact in
+ * fp16), fp32 accumulation.  cols % 8 == 0; residual may alias y. */
 int mmr_matmul_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, int64_t batch,
                    const float* residual, float* y, mmr_stream_t stream);
 /* Rows of the fused qkv projection for positions start_position ..

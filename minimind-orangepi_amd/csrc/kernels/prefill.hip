@@ -1,7 +1,8 @@
 // prefill.hip -- prompt (prefill) kernels for gfx950: fp16-weight GEMM on the
 // fp16 matrix cores (hi/lo split of the fp32 activations), per-row q/k norm +
 // RoPE + KV-cache write, interleaved SwiGLU rows, and causal attention over
-// the cache on the fp32 matrix cores.
+// the cache on the matrix cores (fp16 with hi/lo q and p for an fp16 cache,
+// fp32 for an fp32 cache).
 //
 // Replaces the reference's device prefill layer (run_dense_prefill_layer_device,
 // decoder_layer.cpp:661-734): device_matmul / device_matmul_add with batch =
@@ -530,7 +531,8 @@ __global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
 
 // Causal attention of `tokens` queries at positions start .. start + tokens - 1
 // over the cache (keys 0 .. position of each query, decoder_layer.cpp:184-234
-// per token), on the fp32 matrix cores.
+// per token), on the fp32 matrix cores (fp32 cache) or the fp16 ones (fp16
+// cache, below).
 //
 // Block = (16 queries, one query head): 8 waves, wave w takes the 16-key tiles
 // w, w + 8, ... of the block's causal range (two waves per SIMD, so one wave's
