@@ -130,12 +130,12 @@ def test_attention_from_cache_matches_oracle(gpu, oracle, kv, tokens):
     cache = mmr.KvCache(hkv, d, cap, mmr.KV_F16 if kv == "f16" else mmr.KV_F32)
     cache.upload(cache_layout(k, tokens, hkv, d, cache.rows), cache_layout(v, tokens, hkv, d, cache.rows))
     dq, out = mmr.DeviceArray.from_numpy(q), mmr.DeviceArray(hq * d, np.float32)
-    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 512), np.uint8)
+    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 4096), np.uint8)
     ref = oracle.attention_step(q, k, v, tokens, hq, hkv, d)
     mmr.attention_from_cache(dq, cache, tokens, hq, hkv, d, out, ws)
     got = out.numpy()
     assert rel_err(got, ref) < TOL
-    for splits in (1, 3, 7, 512):  # any split count gives the same result
+    for splits in (1, 3, 7, 65, 512, 4096):  # any split count (up to the limit) gives the same result
         mmr.attention_from_cache(dq, cache, tokens, hq, hkv, d, out, ws, splits=splits)
         assert rel_err(out.numpy(), got) < 1e-5
 

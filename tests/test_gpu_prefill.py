@@ -93,7 +93,7 @@ def test_prefill_qkv_rows_match_per_token_postprocess(gpu, oracle, d, start):
 
 
 @pytest.mark.parametrize("kv", ["f16", "f32"])
-@pytest.mark.parametrize("d", [64, 96, 128])
+@pytest.mark.parametrize("d", [32, 64, 96, 128])
 @pytest.mark.parametrize("start,T", [(0, 1), (0, 16), (0, 17), (0, 100), (70, 33), (130, 64)])
 def test_prefill_attention_matches_oracle(gpu, oracle, kv, d, start, T):
     mmr = gpu
