@@ -725,15 +725,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
 // in all); block reductions give M = max m and L = sum_s l_s exp(m_s - M);
 // the weights exp(m_s - M) go to LDS, and eight groups of 32 threads (thread
 // = dimension) each sum e_s o_s over every eighth split.  The first eight o
-// values of every thread are loaded with the (m, l), so one memory round trip
-// serves up to 64 splits.  The groups' sums are added in group order.  Every
+// values of every thread (sixteen above 64 splits) are loaded with the (m, l),
+// so one memory round trip serves up to 128 splits.  The groups' sums are added in group order.  Every
 // order is fixed, so the result is deterministic.  (The O-projection
 // prologue, kProAttnCombine, computes the same quantity for up to
 // kCombineMaxSplits splits.)
 constexpr int kCombineThreads = 256;
 constexpr int kCombineSlice = 32;                                   // dimensions per block
 constexpr int kCombineGroups = kCombineThreads / kCombineSlice;     // split groups
-constexpr int kCombineUnroll = 8;                                   // o loads in flight per thread
 constexpr int kCombineKernelMaxSplits = 4096;
 constexpr int kCombinePerThread = kCombineKernelMaxSplits / kCombineThreads;
 
@@ -750,6 +749,8 @@ __device__ __forceinline__ float combine_block_reduce(float v, Op op, float* scr
   return r;
 }
 
+// kCombineUnroll: o loads in flight per thread (8, or 16 above 64 splits).
+template <int kCombineUnroll>
 __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(const float* part, int hq, int hkv, int d,
                                                                              int splits, int64_t part_stride,
                                                                              float* out) {
@@ -939,8 +940,12 @@ hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, i
   if (!attention_supported(hq, hkv, d) || d > 128 || splits <= 0 || splits > kCombineKernelMaxSplits || batch <= 0)
     return hipErrorInvalidValue;
   const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
-  attention_combine_kernel<<<dim3(hq * nslice, batch), kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits,
-                                                                                     part_stride, out);
+  const dim3 grid(hq * nslice, batch);
+  if (splits > 8 * kCombineGroups) {
+    attention_combine_kernel<16><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+  } else {
+    attention_combine_kernel<8><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+  }
   return hipGetLastError();
 }
 
