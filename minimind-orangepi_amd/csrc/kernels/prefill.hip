@@ -469,18 +469,28 @@ __global__ __launch_bounds__(kWave* kSkinnyWaves) void gemm_skinny_kernel(GemmAr
 
 // Per (token, head) q/k RMSNorm + RoPE of one row of the fused qkv output,
 // q to `query`, k/v rounded to the cache dtype and written at cache index
-// start + token (decoder_layer.cpp:342-359 per token).  One wave per head;
-// grid (hq + hkv, tokens).
+// start + token (decoder_layer.cpp:342-359 per token).  One wave per (head,
+// token); a block holds kQkvRowsTokens consecutive tokens of one head, grid
+// (hq + hkv, ceil(tokens / kQkvRowsTokens)).
+constexpr int kQkvRowsTokens = 4;
 template <typename KV, int D>
-__global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
-  __shared__ float x_s[D];
+__global__ __launch_bounds__(kWave* kQkvRowsTokens) void qkv_rows_kernel(QkvRowsArgs a) {
+  __shared__ float x_all[kQkvRowsTokens][D];
   const int b = blockIdx.x;
-  const int t = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  // Wave = one token of the block's kQkvRowsTokens; past the last token the
+  // wave works on a clamped row (every wave reaches the barriers) and stores
+  // nothing.
+  const int t_raw = blockIdx.y * kQkvRowsTokens + wave;
+  const bool live = t_raw < a.tokens;
+  const int t = min(t_raw, a.tokens - 1);
+  float* x_s = x_all[wave];
   const bool is_q = b < a.hq;
   const int head = is_q ? b : b - a.hq;
   const float* row = a.qkv + static_cast<int64_t>(t) * a.qkv_stride;
   const float* src = row + (is_q ? head * D : a.hq * D + head * D);
+  const float* vsrc = row + a.hq * D + a.hkv * D + head * D;
   const float* w = is_q ? a.q_norm : a.k_norm;
   const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
   // Sum of the projection's split partials at p[i] (clamped loads, all issued
@@ -496,6 +506,8 @@ __global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
     return x;
   };
   float x0 = part_sum(src, d0), x1 = part_sum(src, d1);
+  // V rows of a KV head are loaded with the K rows (a query block's copy is unused).
+  const float v0 = part_sum(is_q ? src : vsrc, d0), v1 = part_sum(is_q ? src : vsrc, d1);
   const float w0 = w[d0], w1 = w[d1];
   const float f = a.inv_freq[min(lane, D / 2 - 1)];
   x0 = lane < D ? x0 : 0.0f;
@@ -515,16 +527,20 @@ __global__ __launch_bounds__(kWave) void qkv_rows_kernel(QkvRowsArgs a) {
     x_s[lane + D / 2] = second * rc + first * rs;
   }
   __syncthreads();
+  if (!live) return;
   if (is_q) {
     float* dst = a.query + static_cast<int64_t>(t) * a.query_stride + head * D;
     for (int i = lane; i < D; i += kWave) dst[i] = x_s[i];
   } else {
-    const float* vsrc = row + a.hq * D + a.hkv * D + head * D;
     KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
     KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
-    for (int i = lane; i < D; i += kWave) {
-      kdst[i] = from_float<KV>(x_s[i]);
-      vdst[i] = from_float<KV>(part_sum(vsrc, i));
+    if (lane < D) {
+      kdst[lane] = from_float<KV>(x_s[lane]);
+      vdst[lane] = from_float<KV>(v0);
+    }
+    if (lane + kWave < D) {
+      kdst[lane + kWave] = from_float<KV>(x_s[lane + kWave]);
+      vdst[lane + kWave] = from_float<KV>(v1);
     }
   }
 }
@@ -863,13 +879,14 @@ hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
 
 template <typename KV>
 hipError_t launch_qkv_rows_kv(const QkvRowsArgs& a, hipStream_t s) {
-  const dim3 grid(a.hq + a.hkv, a.tokens);
+  const dim3 grid(a.hq + a.hkv, (a.tokens + kQkvRowsTokens - 1) / kQkvRowsTokens);
+  const dim3 block(kWave * kQkvRowsTokens);
   switch (a.d) {
-    case 16: qkv_rows_kernel<KV, 16><<<grid, kWave, 0, s>>>(a); break;
-    case 32: qkv_rows_kernel<KV, 32><<<grid, kWave, 0, s>>>(a); break;
-    case 64: qkv_rows_kernel<KV, 64><<<grid, kWave, 0, s>>>(a); break;
-    case 96: qkv_rows_kernel<KV, 96><<<grid, kWave, 0, s>>>(a); break;
-    case 128: qkv_rows_kernel<KV, 128><<<grid, kWave, 0, s>>>(a); break;
+    case 16: qkv_rows_kernel<KV, 16><<<grid, block, 0, s>>>(a); break;
+    case 32: qkv_rows_kernel<KV, 32><<<grid, block, 0, s>>>(a); break;
+    case 64: qkv_rows_kernel<KV, 64><<<grid, block, 0, s>>>(a); break;
+    case 96: qkv_rows_kernel<KV, 96><<<grid, block, 0, s>>>(a); break;
+    case 128: qkv_rows_kernel<KV, 128><<<grid, block, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
