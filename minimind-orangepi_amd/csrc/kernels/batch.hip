@@ -8,6 +8,7 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mmr {
 namespace {
@@ -385,18 +386,20 @@ __device__ inline T sum_parts4(const T* part4, int64_t sstride, int s0, int step
 
 // h[b] += sum_s part[s][b], then x[b] = RMSNorm(h[b]) with the layer
 // association x * (scale * w) (decoder_layer.cpp:32-42) or the final one
-// (x * scale) * w (language_model.cpp:24-38).  One block of 1024 threads per
-// row: kResGroups groups of 256 threads each sum every kResGroups-th split of
-// a column chunk (float4 columns), then the groups' sums are added to h in
-// group order.  splits == 0 normalizes h as it is.
-constexpr int kResThreads = 1024;
-constexpr int kResGroups = kResThreads / 256;
+// (x * scale) * w (language_model.cpp:24-38).  One block of kResThreads per
+// row: kResThreads / 256 groups of 256 threads each sum every group-count-th
+// split of a column chunk (float4 columns), then the groups' sums are added
+// to h in group order.  splits == 0 normalizes h as it is.
+// kResThreads: 1024 for a few rows (batched decode: more loads in flight per
+// row), 256 for many (prefill: one group adds the splits in order).
 constexpr int kResChunkQuads = 256;
+constexpr int kResManyRows = 64;
 
-template <bool kFinal, bool kSplit>
+template <bool kFinal, bool kSplit, int kResThreads>
 __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float* h, const float* part, int splits,
                                                                           int batch, int cols, const float* w,
                                                                           float eps, float* x, SplitPlanes sp) {
+  constexpr int kResGroups = kResThreads / 256;
   __shared__ float4 red[kResGroups][kResChunkQuads];
   __shared__ float s_ss[kResThreads / kWave];
   const int b = blockIdx.x;
@@ -642,16 +645,24 @@ hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, i
   if (split && (!split->hi || !split->lo || !split->inv)) return hipErrorInvalidValue;
   if (!x && !split) return hipErrorInvalidValue;
   const SplitPlanes sp = split ? *split : SplitPlanes{};
-  if (final_norm) {
-    if (split) {
-      batch_residual_norm_kernel<true, true><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+  auto run = [&](auto threads) {
+    constexpr int T = decltype(threads)::value;
+    if (final_norm) {
+      if (split) {
+        batch_residual_norm_kernel<true, true, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+      } else {
+        batch_residual_norm_kernel<true, false, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+      }
+    } else if (split) {
+      batch_residual_norm_kernel<false, true, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
     } else {
-      batch_residual_norm_kernel<true, false><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+      batch_residual_norm_kernel<false, false, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
     }
-  } else if (split) {
-    batch_residual_norm_kernel<false, true><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+  };
+  if (batch >= kResManyRows) {
+    run(std::integral_constant<int, 256>{});
   } else {
-    batch_residual_norm_kernel<false, false><<<batch, kResThreads, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+    run(std::integral_constant<int, 1024>{});
   }
   return hipGetLastError();
 }
