@@ -211,7 +211,6 @@ struct GemmStage {
 // interleaved gate/up columns (2i, 2i + 1) -> act[m][i] (decoder_layer.cpp:
 // 175-182), the pair meeting through one lane exchange.
 constexpr int kGemmEpiStore = 0, kGemmEpiResidual = 1, kGemmEpiSwiGlu = 2;
-constexpr int kActLd = 64 + 4;  // floats per row of the act tile in LDS (64 x 128 tiles)
 
 template <int BM, int BN, int kEpi, int kMode>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_f16w_kernel(GemmArgs g) {
@@ -311,7 +310,9 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     return (v / (1.0f + expf(-v))) * u;
   };
   bool act_to_lds = false;
-  if constexpr (kEpi == kGemmEpiSwiGlu && BN == 128) act_to_lds = g.act_split.hi != nullptr;
+  constexpr bool kActSplit = kEpi == kGemmEpiSwiGlu && (BN == 128 || BN == 64);  // whole 32-column act chunks
+  constexpr int kActLd = BN / 2 + 4;  // floats per row of the act tile in LDS
+  if constexpr (kActSplit) act_to_lds = g.act_split.hi != nullptr;
   if (act_to_lds) {
     // act tile for the pre-split writer below: [BM][BN / 2] (padded) over the
     // W staging buffer, which the K loop no longer reads.  Rows past m hold
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
         }
       }
   }
-  if constexpr (kEpi == kGemmEpiSwiGlu && BN == 128) {
+  if constexpr (kActSplit) {
     if (act_to_lds) {
       // act pre-split per 32 columns (the down GEMM's A): thread = 4
       // consecutive columns of one row, the 8 threads of a chunk reduce its
@@ -939,11 +940,14 @@ constexpr int64_t kGemmTargetBlocks = 384;
 GemmTiling choose_gemm_tiling(int m, int n, int k) {
   const int nk = (k + kGemmBK - 1) / kGemmBK;
   const int max_splits = std::max(1, std::min(8, nk / 2));
-  // 64 x 128 (A split once per 128 columns instead of 64) when it gives every
-  // CU a block unsplit, or reaches the target within the split limit:
-  // gate_up 26.3 -> 24.0 us, down 18.6 -> 17.2 us (8 splits) at M = 512.
+  // Unsplit: 64 x 128 when that gives every CU two blocks, else 64 x 64 when
+  // that does (A arrives pre-split, so the narrower tile costs only A
+  // re-reads, and the second block per CU hides the first's tile loads:
+  // gate_up at M = 512 19.6 -> 17.9 us).  Else 64 x 128 split when that
+  // reaches the target within the split limit (down at M = 512, 8 splits).
   const int64_t wide = static_cast<int64_t>((m + 63) / 64) * ((n + 127) / 128);
-  if (wide >= 256) return {64, 128, 1};
+  if (wide >= 512) return {64, 128, 1};
+  if (2 * wide >= 512) return {64, 64, 1};
   if ((kGemmTargetBlocks + wide - 1) / wide <= max_splits)
     return {64, 128, static_cast<int>((kGemmTargetBlocks + wide - 1) / wide)};
   const int tiles[3][2] = {{64, 64}, {32, 64}, {32, 32}};
@@ -964,7 +968,8 @@ int gemm_k_splits(int m, int n, int k) {
 bool gemm_presplit_supported(int m, int n, int k) { return gemm_supported(m, n, k) && !use_skinny(m, k); }
 
 bool gemm_swiglu_split_supported(int m, int n, int k) {
-  return gemm_swiglu_supported(m, n, k) && n % (2 * kSplitChunkFine) == 0 && choose_gemm_tiling(m, n, k).bn == 128;
+  const GemmTiling t = choose_gemm_tiling(m, n, k);
+  return gemm_swiglu_supported(m, n, k) && n % (2 * kSplitChunkFine) == 0 && (t.bn == 128 || t.bn == 64);
 }
 
 bool gemm_swiglu_supported(int m, int n, int k) {
@@ -994,9 +999,9 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
     return hipErrorInvalidValue;
   // Few rows (batched decode): stream W with one block per 16 rows of W.
   if (use_skinny(g.m, g.k)) return g.m <= 16 ? launch_gemm_skinny<1>(g, s) : launch_gemm_skinny<2>(g, s);
-  // Split-K calls with the chooser's split count take its tile.
+  // Calls with the chooser's split count take its tile.
   const GemmTiling t = choose_gemm_tiling(g.m, g.n, g.k);
-  if (g.k_splits > 1 && g.k_splits == t.splits) {
+  if (g.k_splits == t.splits) {
     if (t.bn == 128) return launch_gemm_tile<64, 128>(g, s);
     if (t.bm == 64) return launch_gemm_tile<64, 64>(g, s);
     if (t.bn == 64) return launch_gemm_tile<32, 64>(g, s);
