@@ -943,13 +943,12 @@ GemmTiling choose_gemm_tiling(int m, int n, int k) {
   // Unsplit: 64 x 128 when that gives every CU two blocks, else 64 x 64 when
   // that does (A arrives pre-split, so the narrower tile costs only A
   // re-reads, and the second block per CU hides the first's tile loads:
-  // gate_up at M = 512 19.6 -> 17.9 us).  Else 64 x 128 split when that
-  // reaches the target within the split limit (down at M = 512, 8 splits).
+  // gate_up at M = 512 19.6 -> 17.9 us).  Else the largest tile whose
+  // smallest split count reaches the target (down at M = 512: 64 x 64 with 4
+  // splits, as fast as 64 x 128 with 8 and half the partials to add).
   const int64_t wide = static_cast<int64_t>((m + 63) / 64) * ((n + 127) / 128);
   if (wide >= 512) return {64, 128, 1};
   if (2 * wide >= 512) return {64, 64, 1};
-  if ((kGemmTargetBlocks + wide - 1) / wide <= max_splits)
-    return {64, 128, static_cast<int>((kGemmTargetBlocks + wide - 1) / wide)};
   const int tiles[3][2] = {{64, 64}, {32, 64}, {32, 32}};
   for (const auto& t : tiles) {
     const int64_t blocks = static_cast<int64_t>((m + t[0] - 1) / t[0]) * ((n + t[1] - 1) / t[1]);
