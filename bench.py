@@ -96,6 +96,21 @@ def kernel_bytes(c: dict, kernel: str, n_keys: int, kv_bytes: int) -> int:
     raise KeyError(kernel)
 
 
+KERNEL_LABELS = {
+    "qkv": "gemv qkv (1152x768 fp16, RMSNorm prologue)",
+    "attention": "decode attention (q/k norm + RoPE + KV append + split partials, 8/2 heads, d 96, fp16 KV)",
+    "o": "gemv o (768x768 fp16, split combine prologue, residual epilogue)",
+    "gate_up": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",
+    "down": "gemv down (768x2048 fp16, residual epilogue)",
+    "lm_head": "gemv lm_head (6400x768 fp16, final RMSNorm prologue, argmax partials)",
+    "finalize": "argmax finalize",
+}
+# Committed FETCH_SIZE / WRITE_SIZE summaries (bench.py --traffic-probe) per kernel.
+TRAFFIC_FILES = {
+    "gate_up": "profiles/gemv_gate_up_minimind2_traffic.md",
+    "attention": "profiles/attention_minimind2_768keys_traffic.md",
+}
+
 GEMV_SHAPES = [("qkv", 1152, 768), ("o", 768, 768), ("gate_up", 4096, 768), ("down", 768, 2048),
                ("lm_head_argmax", 6400, 768)]
 
@@ -263,33 +278,51 @@ def decode_context_sweep(mmr, model, kv, steps: int = 64) -> dict:
     return out
 
 
-def traffic_probe(mmr, launches: int, copy_mib: int) -> int:
-    """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: the dominant
-    kernel alone -- gate_up GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU
-    epilogue, the decode step's launch plan: 32-lane groups, two rows per
-    group) through the C ABI over a
-    16-copy weight rotation like the 16 layers of the step -- then one
-    device-to-device copy of `copy_mib` MiB, the calibration dispatch whose
-    bytes are known."""
+def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
+    """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: one kernel of the
+    decode step launched alone, eagerly (rocprofv3's counter collection is
+    run on eager dispatches only), then one device-to-device copy of
+    `copy_mib` MiB, the calibration dispatch whose bytes are known.
+
+    gate_up: the GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU epilogue, the
+    step's launch plan: 32-lane groups, two rows per group) through the C ABI
+    over a 16-copy weight rotation like the 16 layers of the step.
+    attention: the step's own attention kernel (q/k norm + RoPE + KV append +
+    attention partials) on the MiniMind2 decode state after the 512-token
+    prompt and 255 steps (768 keys, fp16 KV), cycling over the 16 layers'
+    caches (mmr_launch_step_kernel)."""
     H, F, layers = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"], MINIMIND2["num_hidden_layers"]
     rng = np.random.default_rng(3)
-    wbytes = 2 * F * H * 2
-    w = mmr.DeviceArray(layers * wbytes, np.uint8, zero=True)
-    x = mmr.DeviceArray.from_numpy(rng.standard_normal(H).astype(np.float32))
-    g = mmr.DeviceArray.from_numpy(np.ones(H, np.float32))
-    y = mmr.DeviceArray(F, np.float32)
-    stream = mmr.Stream()
-    lib = mmr.lib()
-    for i in range(launches):
-        mmr.check(lib.mmr_matvec_f16_ex(w.ptr + (i % layers) * wbytes, 2 * F, H, x.ptr, g.ptr, 1e-5, mmr.PRO_RMSNORM,
-                                        mmr.EPI_SWIGLU, None, y.ptr, 32, 2, stream.handle))
-    stream.synchronize()
+    if kernel == "attention":
+        model = mmr.Model.synthetic(mmr.make_config(**MINIMIND2), 0, 0.02, True)
+        st = model.make_state(PROMPT_LEN + 264, mmr.KV_F16)
+        st.enqueue_prefill(mmr.synthesize_prompt(1, PROMPT_LEN, MINIMIND2["vocab_size"]))
+        st.enqueue_decode(255)
+        st.synchronize()
+        n_keys = st.position + 1
+        st.launch_step_kernel(mmr.KERNEL_ATTENTION, 0, launches)
+        stream = mmr.Stream(st.stream)
+        stream.synchronize()
+        alg = kernel_bytes(MINIMIND2, "attention", n_keys, 2)
+    else:
+        wbytes = 2 * F * H * 2
+        w = mmr.DeviceArray(layers * wbytes, np.uint8, zero=True)
+        x = mmr.DeviceArray.from_numpy(rng.standard_normal(H).astype(np.float32))
+        g = mmr.DeviceArray.from_numpy(np.ones(H, np.float32))
+        y = mmr.DeviceArray(F, np.float32)
+        stream = mmr.Stream()
+        lib = mmr.lib()
+        for i in range(launches):
+            mmr.check(lib.mmr_matvec_f16_ex(w.ptr + (i % layers) * wbytes, 2 * F, H, x.ptr, g.ptr, 1e-5,
+                                            mmr.PRO_RMSNORM, mmr.EPI_SWIGLU, None, y.ptr, 32, 2, stream.handle))
+        stream.synchronize()
+        alg = kernel_bytes(MINIMIND2, "gate_up", 0, 0)
     n = copy_mib << 20
     src, dst = mmr.DeviceArray(n, np.uint8, zero=True), mmr.DeviceArray(n, np.uint8)
     dst.copy_from(src, stream)
     stream.synchronize()
-    print(json.dumps({"traffic_probe": {"gate_up_launches": launches, "gate_up_alg_bytes": kernel_bytes(
-        MINIMIND2, "gate_up", 0, 0), "copy_bytes": n}}), flush=True)
+    print(json.dumps({"traffic_probe": {"kernel": kernel, "launches": launches, "alg_bytes": alg,
+                                        "copy_bytes": n}}), flush=True)
     return 0
 
 
@@ -324,34 +357,62 @@ def batched_decode(mmr, model, batch: int, prompt_len: int, context: int) -> dic
     return out
 
 
+def host_cpu() -> dict:
+    """Host CPU model and the cores this process may use (the GPU box's share)."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return {"cpu_model": model, "cores_available": avail, "cores_online": os.cpu_count()}
+
+
 def cpu_baseline(mmr, cfg, prompt, sample_steps: int) -> dict | None:
-    """The reference CPU path (single-threaded, as shipped) on a bounded sample."""
+    """The reference CPU path (oracle/_ref/ref_driver, the unmodified reference
+    sources; single-threaded as shipped) at the GPU line's context: the same
+    512-token prompt fed token by token (the reference's CPU prefill,
+    language_model.cpp:339-341 needs Ascend), then `sample_steps` greedy decode
+    steps timed as bench_decode.cpp:86-113 does, pinned to one core."""
     ref = ROOT / "oracle" / "_ref" / "ref_driver"
     if not ref.exists():
         log("oracle/_ref/ref_driver not built: cpu_baseline omitted")
         return None
+    host = host_cpu()
     with tempfile.TemporaryDirectory() as tmp:
         mmr.write_synthetic_model(tmp, cfg, 0, 0.02, True)
-        short = [int(t) for t in prompt[:8]]
-        cmd = [str(ref), "bench", tmp, ",".join(map(str, short)), str(sample_steps + 1)]
+        cmd = [str(ref), "bench", tmp, ",".join(str(int(t)) for t in prompt), str(sample_steps + 1)]
         try:
             cmd = ["taskset", "-c", str(sorted(os.sched_getaffinity(0))[0])] + cmd
         except (AttributeError, OSError):
             pass
         t0 = time.time()
-        proc = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+        proc = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
         if proc.returncode != 0:
             log(f"ref_driver failed: {proc.stderr.strip()}")
             return None
         out = json.loads(proc.stdout)
-        log(f"cpu baseline: {out['decode_tokens_per_second']:.2f} tok/s ({time.time() - t0:.1f}s)")
+        log(f"cpu baseline: {out['decode_tokens_per_second']:.2f} tok/s decode, prompt "
+            f"{out['prefill_tokens'] / out['prefill_seconds']:.2f} tok/s ({time.time() - t0:.1f}s)")
+    P, n = len(prompt), out["decode_steps"]
     return {
         "value": round(out["decode_tokens_per_second"], 3),
         "unit": "tok/s",
         "cores": 1,
+        "cores_available": host["cores_available"],
+        "cores_online": host["cores_online"],
+        "cpu_model": host["cpu_model"],
         "kind": "reference",
-        "sample": f"MiniMind2 same weights, 8-token prompt fed token by token, then {out['decode_steps']} greedy "
-                  f"decode steps (positions 8..{8 + out['decode_steps']}); reference CPU path, single thread",
+        "prompt_tok_s": round(out["prefill_tokens"] / out["prefill_seconds"], 3),
+        "sample": f"MiniMind2, the GPU line's weights and 512-token prompt, fed token by token "
+                  f"({out['prefill_seconds']:.1f} s), then {n} greedy decode steps at positions {P}..{P + n} "
+                  f"(the GPU line decodes {P}..{P + 256}); reference CPU path, one thread pinned to one core",
     }
 
 
@@ -363,7 +424,7 @@ def main() -> int:
     ap.add_argument("--kv", choices=["f32", "f16"], default="f16")
     ap.add_argument("--no-other-kv", action="store_true", help="skip the decode with the other KV cache dtype")
     ap.add_argument("--kernel-reps", type=int, default=320)
-    ap.add_argument("--cpu-sample-steps", type=int, default=320)  # ~13 s of one core
+    ap.add_argument("--cpu-sample-steps", type=int, default=128)  # ~25 s of one core with the prompt
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=256)
@@ -373,7 +434,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=32, help="configs[4] batch size (0: skip the batched run)")
     ap.add_argument("--batch-context", type=int, default=4096)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
-                    help="run only the counter-run workload (gate_up launches + one copy) and exit")
+                    help="run only the counter-run workload (kernel launches + one copy) and exit")
+    ap.add_argument("--traffic-kernel", choices=["attention", "gate_up"], default="attention")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -386,12 +448,12 @@ def main() -> int:
         print("--steps out of range", file=sys.stderr)
         return 2
 
-    if args.no_graph:
+    if args.no_graph or args.traffic_probe > 0:
         os.environ["MMR_NO_GRAPH"] = "1"  # read when the decode state is created
     import mmr  # noqa: E402  (fails loudly if libmmr.so is not built)
 
     if args.traffic_probe > 0:
-        return traffic_probe(mmr, args.traffic_probe, max(args.copy_probe_mib, 1))
+        return traffic_probe(mmr, args.traffic_probe, max(args.copy_probe_mib, 1), args.traffic_kernel)
 
     if mmr.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
@@ -458,8 +520,13 @@ def main() -> int:
         kernels["lm_head"]["avg_us"] + kernels["finalize"]["avg_us"]
     step_bytes = sum(kernels[n]["bytes"] for n in names[:5]) * MINIMIND2["num_hidden_layers"] + \
         kernels["lm_head"]["bytes"]
-    dom = "gate_up"
-    ach = kernels[dom]["gbs"]
+    # The roofline kernel is the one with the largest share of the step:
+    # time per launch x launches per step (16 for the layer kernels).
+    per_step = {n: kernels[n]["avg_us"] * (MINIMIND2["num_hidden_layers"] if n in names[:5] else 1) for n in names}
+    for n in names:
+        kernels[n]["us_per_step"] = round(per_step[n], 2)
+    dom = max(per_step, key=per_step.get)
+    log(f"dominant kernel: {dom} ({per_step[dom]:.1f} us per step)")
     # The chain's per-kernel floor: trivial kernels replayed from a hipGraph.
     floor = {"kernels_in_chain": 80, "blocks": 256,
              "empty_us": round(mmr.launch_floor_us(80, 256, False, 20), 3),
@@ -506,11 +573,22 @@ def main() -> int:
                                                              "f32" if args.kv == "f16" else "f16")
     batched = batched_decode(mmr, model, args.batch, 256, args.batch_context) if args.batch > 0 else None
 
-    traffic = None
-    tfile = ROOT / "profiles" / "gemv_gate_up_minimind2_traffic.md"
-    if tfile.exists():
-        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", tfile.read_text())
-        traffic = int(m.group(1)) if m else None
+    def roofline_of(name: str) -> dict:
+        """HBM roofline entry of one step kernel; traffic (L2-to-memory bytes
+        per launch) from its committed counter summary, null without one."""
+        traffic, tsrc = None, TRAFFIC_FILES.get(name)
+        if tsrc and (ROOT / tsrc).exists():
+            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", (ROOT / tsrc).read_text())
+            traffic = int(m.group(1)) if m else None
+        ach = kernels[name]["gbs"]
+        return {"bound": "hbm", "kernel": KERNEL_LABELS[name], "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": tsrc if traffic is not None else None,
+                "bytes_per_launch": kernels[name]["bytes"], "avg_us": kernels[name]["avg_us"],
+                "us_per_step": kernels[name]["us_per_step"]}
+
+    roofline = roofline_of(dom)
+    roofline["secondary"] = {n: roofline_of(n) for n in ("gate_up", "attention", "lm_head") if n != dom}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -548,10 +626,7 @@ def main() -> int:
         "other_kv_cache": other_kv,
         "batched": batched,
         "launch_mode": "eager (--no-graph)" if args.no_graph else "hipGraph replay",
-        "roofline": {"bound": "hbm", "kernel": "gemv gate_up+SwiGLU (4096x768 fp16, RMSNorm prologue)",
-                     "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "traffic_source": "profiles/gemv_gate_up_minimind2_traffic.md"
-                     if traffic is not None else None},
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -36,6 +36,7 @@ typedef struct mmr_state mmr_state;
 typedef struct mmr_batch_state mmr_batch_state;
 typedef struct mmr_rope_table mmr_rope_table;
 typedef struct mmr_kv_cache mmr_kv_cache;
+typedef struct mmr_layer_weights mmr_layer_weights;
 
 /* Fields of MiniMindConfig (src/csrc/models/minimind/config.h:21-45) used by
  * the dense path. */
@@ -176,6 +177,33 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
                                const mmr_rope_table* rope, const int32_t* position, mmr_kv_cache* cache,
                                int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, void* workspace,
                                size_t workspace_bytes, int splits, int32_t* error, mmr_stream_t stream);
+
+/* ---- one decoder layer: run_dense_decoder_layer_device (decoder_layer.h:50-80,
+ * decoder_layer.cpp:617-659) and run_dense_decoder_layer (decoder_layer.cpp:312-407)
+ * over a LayerKvCache (decoder_layer.h:40-48).
+ * Layer weights: the reference's DenseLayerWeights members (decoder_layer.h:19-35),
+ * fp32 host arrays, uploaded as fp16 in the runtime's fused layout
+ * (mmr_layer_weights_create), or a view of a loaded model's layer that keeps
+ * the model's weights alive (mmr_model_layer_weights).
+ * mmr_decoder_layer_forward: out = layer(hidden) for the token at device
+ * position *position, which is also the cache row its k/v are appended at;
+ * attention runs over *position + 1 keys (the reference's cache.tokens after
+ * its increment).  hidden/out [hidden_size] fp32 on the device (out may
+ * alias hidden); the cache must match the layer (kv_heads, head_dim); splits
+ * 0 = automatic from the cache capacity.  No allocation, no
+ * synchronisation: the call may be recorded into a hipGraph and replayed
+ * with the position advanced in device memory.  *error (device int32) is
+ * set to 1 when *position is outside the cache or max_position_embeddings. */
+int mmr_layer_weights_create(const mmr_config* config, const float* input_norm, const float* post_attention_norm,
+                             const float* q_norm, const float* k_norm, const float* q_proj, const float* k_proj,
+                             const float* v_proj, const float* o_proj, const float* gate_proj, const float* up_proj,
+                             const float* down_proj, mmr_layer_weights** out);
+int mmr_model_layer_weights(const mmr_model* model, int64_t layer, mmr_layer_weights** out);
+int mmr_layer_weights_destroy(mmr_layer_weights* weights);
+size_t mmr_decoder_layer_workspace_size(const mmr_config* config, int splits);
+int mmr_decoder_layer_forward(const mmr_layer_weights* weights, mmr_kv_cache* cache, const float* hidden,
+                              const int32_t* position, float* out, void* workspace, size_t workspace_bytes,
+                              int splits, int32_t* error, mmr_stream_t stream);
 
 /* ---- prefill (run_dense_prefill_layer_device, decoder_layer.cpp:661-734) ----
  * Batched projection: device_matmul / device_matmul_add with batch = seq_len

@@ -5,6 +5,7 @@
 #include "../../include/mmr.h"
 
 #include "kernels/kernels.h"
+#include "runtime/decoder_layer.h"
 #include "runtime/device.h"
 #include "runtime/language_model.h"
 
@@ -37,6 +38,9 @@ struct mmr_kv_cache {
   DeviceBuffer keys, values;
   int64_t kv_heads = 0, head_dim = 0, capacity = 0, rows = 0;
   int dtype = MMR_KV_F32;
+};
+struct mmr_layer_weights {
+  std::shared_ptr<DeviceLayerWeights> w;
 };
 
 namespace {
@@ -567,6 +571,88 @@ int mmr_prefill_qkv_rows(const float* qkv, const float* q_norm, const float* k_n
     a.query_stride = static_cast<int>(q_heads * head_dim);
     hip(mmr::launch_qkv_rows(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32, as_stream(stream)),
         "qkv rows launch");
+  });
+}
+
+int mmr_layer_weights_create(const mmr_config* config, const float* input_norm, const float* post_attention_norm,
+                             const float* q_norm, const float* k_norm, const float* q_proj, const float* k_proj,
+                             const float* v_proj, const float* o_proj, const float* gate_proj, const float* up_proj,
+                             const float* down_proj, mmr_layer_weights** out) {
+  return guarded([&] {
+    require(config && out, "null argument");
+    require(input_norm && post_attention_norm && q_norm && k_norm && q_proj && k_proj && v_proj && o_proj &&
+                gate_proj && up_proj && down_proj,
+            "null weight array");
+    const MiniMindConfig c = to_cpp(*config);
+    // The config sets how many floats are read from each array: validate it first.
+    const auto errors = validate_config(c);
+    if (!errors.empty()) throw std::invalid_argument("invalid MiniMind config: " + errors.front());
+    const auto dev_errors = validate_device_config(c);
+    if (!dev_errors.empty()) throw std::invalid_argument("unsupported by the gfx950 runtime: " + dev_errors.front());
+    const int64_t H = c.hidden_size, D = c.head_dim, F = c.intermediate_size;
+    const int64_t qs = c.num_attention_heads * D, kvs = c.num_key_value_heads * D;
+    const auto vec = [](const float* p, int64_t n) { return std::vector<float>(p, p + n); };
+    DenseLayerWeights L;
+    L.input_norm = vec(input_norm, H);
+    L.post_attention_norm = vec(post_attention_norm, H);
+    L.q_norm = vec(q_norm, D);
+    L.k_norm = vec(k_norm, D);
+    L.q_proj = vec(q_proj, qs * H);
+    L.k_proj = vec(k_proj, kvs * H);
+    L.v_proj = vec(v_proj, kvs * H);
+    L.o_proj = vec(o_proj, H * qs);
+    L.gate_proj = vec(gate_proj, F * H);
+    L.up_proj = vec(up_proj, F * H);
+    L.down_proj = vec(down_proj, H * F);
+    auto h = std::make_unique<mmr_layer_weights>();
+    h->w = DeviceLayerWeights::upload(c, L);
+    *out = h.release();
+  });
+}
+
+int mmr_model_layer_weights(const mmr_model* model, int64_t layer, mmr_layer_weights** out) {
+  return guarded([&] {
+    require(model && out, "null argument");
+    auto h = std::make_unique<mmr_layer_weights>();
+    h->w = DeviceLayerWeights::view(model->lm->shared_device_model(), layer);
+    *out = h.release();
+  });
+}
+
+int mmr_layer_weights_destroy(mmr_layer_weights* weights) {
+  delete weights;
+  return MMR_OK;
+}
+
+size_t mmr_decoder_layer_workspace_size(const mmr_config* config, int splits) {
+  if (!config || splits < 1 || splits > 4096) return 0;
+  return decoder_layer_workspace_floats(to_cpp(*config), splits) * 4;
+}
+
+int mmr_decoder_layer_forward(const mmr_layer_weights* weights, mmr_kv_cache* cache, const float* hidden,
+                              const int32_t* position, float* out, void* workspace, size_t workspace_bytes,
+                              int splits, int32_t* error, mmr_stream_t stream) {
+  return guarded([&] {
+    require(weights && weights->w && cache && hidden && position && out && workspace && error, "null argument");
+    const MiniMindConfig& c = weights->w->cfg;
+    require(cache->kv_heads == c.num_key_value_heads && cache->head_dim == c.head_dim,
+            "cache shape does not match the layer (kv_heads, head_dim)");
+    if (splits <= 0) splits = auto_splits(cache->capacity, c.head_dim);
+    require(splits <= 4096, "splits too large");
+    require(workspace_bytes >= decoder_layer_workspace_floats(c, splits) * 4, "workspace too small");
+    DecoderLayerIo io;
+    io.hidden = hidden;
+    io.out = out;
+    io.position = position;
+    io.kcache = cache->keys.data();
+    io.vcache = cache->values.data();
+    io.rows = static_cast<int>(cache->rows);
+    io.capacity = static_cast<int>(std::min(cache->capacity, c.max_position_embeddings));
+    io.kv = cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32;
+    io.splits = splits;
+    io.workspace = static_cast<float*>(workspace);
+    io.err = error;
+    enqueue_decoder_layer(*weights->w, io, as_stream(stream));
   });
 }
 

@@ -18,6 +18,7 @@
 #include "language_model.h"
 
 #include "device.h"
+#include "decoder_layer.h"
 #include "device_model.h"
 #include "../kernels/kernels.h"
 
@@ -122,12 +123,6 @@ T* upload(Arena& arena, const void* host, std::size_t count) {
   return dst;
 }
 
-mmr::GemvPlan plan_or_throw(int rows, int k, mmr::GemvEpilogue epi, const char* name) {
-  mmr::GemvPlan p;
-  if (!mmr::gemv_plan(rows, k, epi, 0, 0, &p))
-    throw std::invalid_argument(std::string("unsupported GEMV shape for ") + name);
-  return p;
-}
 
 }  // namespace
 
@@ -158,39 +153,17 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
   require_size(weights.lm_head, V * H, "lm_head");
   if (static_cast<int64_t>(weights.layers.size()) != c.num_hidden_layers)
     throw std::invalid_argument("layer weight count does not match config");
-  for (const auto& L : weights.layers) {
-    require_size(L.input_norm, H, "input_norm");
-    require_size(L.post_attention_norm, H, "post_attention_norm");
-    require_size(L.q_norm, D, "q_norm");
-    require_size(L.k_norm, D, "k_norm");
-    require_size(L.q_proj, qs * H, "q_proj");
-    require_size(L.k_proj, kvs * H, "k_proj");
-    require_size(L.v_proj, kvs * H, "v_proj");
-    require_size(L.o_proj, H * qs, "o_proj");
-    require_size(L.gate_proj, F * H, "gate_proj");
-    require_size(L.up_proj, F * H, "up_proj");
-    require_size(L.down_proj, H * F, "down_proj");
-  }
+  for (const auto& L : weights.layers) check_layer_weights(c, L);
 
   auto dm = std::make_shared<DeviceModel>();
   dm->cfg = c;
   const bool share_head = weights.lm_head == weights.embed_tokens;
   const int64_t half_d = D / 2;
-  const int64_t max_pos = c.max_position_embeddings;
   Arena& ar = dm->arena;
   ar.plan(V * H * 2);
   if (!share_head) ar.plan(V * H * 2);
   ar.plan(H * 4);
-  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
-    ar.plan(H * 4);
-    ar.plan(H * 4);
-    ar.plan(D * 4);
-    ar.plan(D * 4);
-    ar.plan((qs + 2 * kvs) * H * 2);
-    ar.plan(H * qs * 2);
-    ar.plan(2 * F * H * 2);
-    ar.plan(H * F * 2);
-  }
+  for (int64_t l = 0; l < c.num_hidden_layers; ++l) ar.plan(plan_layer_bytes(c));
   ar.plan(half_d * 4);
   ar.allocate();
 
@@ -199,49 +172,21 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
   dm->final_norm = upload<float>(ar, weights.final_norm.data(), H);
   std::size_t wbytes = V * H * 2 * (share_head ? 1 : 2) + H * 4;
   for (const auto& L : weights.layers) {
-    LayerDev d;
-    d.input_norm = upload<float>(ar, L.input_norm.data(), H);
-    d.post_norm = upload<float>(ar, L.post_attention_norm.data(), H);
-    d.q_norm = upload<float>(ar, L.q_norm.data(), D);
-    d.k_norm = upload<float>(ar, L.k_norm.data(), D);
-    std::vector<float> qkv;
-    qkv.reserve((qs + 2 * kvs) * H);
-    qkv.insert(qkv.end(), L.q_proj.begin(), L.q_proj.end());
-    qkv.insert(qkv.end(), L.k_proj.begin(), L.k_proj.end());
-    qkv.insert(qkv.end(), L.v_proj.begin(), L.v_proj.end());
-    d.qkv = upload<__half>(ar, to_half(qkv).data(), qkv.size());
-    d.o = upload<__half>(ar, to_half(L.o_proj).data(), L.o_proj.size());
-    std::vector<uint16_t> gu(static_cast<size_t>(2 * F * H));
-    for (int64_t r = 0; r < F; ++r)
-      for (int64_t k = 0; k < H; ++k) {
-        gu[static_cast<size_t>((2 * r) * H + k)] = float_to_half(L.gate_proj[static_cast<size_t>(r * H + k)]);
-        gu[static_cast<size_t>((2 * r + 1) * H + k)] = float_to_half(L.up_proj[static_cast<size_t>(r * H + k)]);
-      }
-    d.gate_up = upload<__half>(ar, gu.data(), gu.size());
-    d.down = upload<__half>(ar, to_half(L.down_proj).data(), L.down_proj.size());
-    dm->layers.push_back(d);
+    dm->layers.push_back(upload_layer(ar, c, L));
     wbytes += 2 * H * 4 + 2 * D * 4 + ((qs + 2 * kvs) * H + H * qs + 2 * F * H + H * F) * 2;
   }
-  // RoPE frequencies with the reference formula (decoder_layer.cpp:114):
-  // inv_freq = 1 / powf(theta, 2i / d); the kernels evaluate
-  // cos/sin(float(pos) * inv_freq) on the device.
+  // RoPE frequencies with the reference formula (decoder_layer.cpp:114); the
+  // kernels evaluate cos/sin(float(pos) * inv_freq) on the device.
   {
-    std::vector<float> inv(static_cast<size_t>(half_d));
-    for (int64_t i = 0; i < half_d; ++i)
-      inv[static_cast<size_t>(i)] =
-          1.0F / std::pow(c.rope_theta, static_cast<float>(i * 2) / static_cast<float>(D));
+    const std::vector<float> inv = rope_inv_freq(c);
     dm->inv_freq = upload<float>(ar, inv.data(), inv.size());
   }
-  (void)max_pos;
   dm->weight_bytes = wbytes;
-  dm->plan_qkv = plan_or_throw(static_cast<int>(qs + 2 * kvs), static_cast<int>(H), mmr::kEpiStore, "qkv_proj");
-  dm->plan_o = plan_or_throw(static_cast<int>(H), static_cast<int>(qs), mmr::kEpiResidual, "o_proj");
-  // gate_up keeps 32-lane groups: 64 measured slower for this kernel alone and
-  // within noise for the step.
-  if (!mmr::gemv_plan(static_cast<int>(2 * F), static_cast<int>(H), mmr::kEpiSwiGlu,
-                      static_cast<int>(H) / 8 >= 48 ? 32 : 0, 0, &dm->plan_gu))
-    throw std::invalid_argument("unsupported GEMV shape for gate_up_proj");
-  dm->plan_down = plan_or_throw(static_cast<int>(H), static_cast<int>(F), mmr::kEpiResidual, "down_proj");
+  const LayerPlans lp = plan_layer(c);
+  dm->plan_qkv = lp.qkv;
+  dm->plan_o = lp.o;
+  dm->plan_gu = lp.gate_up;
+  dm->plan_down = lp.down;
   if (!mmr::gemv_plan(static_cast<int>(V), static_cast<int>(H), mmr::kEpiArgmax, 0, 0, &dm->plan_lm))
     throw std::invalid_argument("unsupported GEMV shape for lm_head");
   dm->gemm_prefill = mmr::gemm_supported(1, static_cast<int>(qs + 2 * kvs), static_cast<int>(H)) &&

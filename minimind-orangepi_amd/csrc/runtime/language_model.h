@@ -135,6 +135,7 @@ class LanguageModel {
   std::vector<float> read_batch_logits(BatchState& state, int64_t index) const;
 
   const DeviceModel& device_model() const { return *device_; }
+  std::shared_ptr<const DeviceModel> shared_device_model() const { return device_; }
   std::size_t device_weight_bytes() const;
 
  private:

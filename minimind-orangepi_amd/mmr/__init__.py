@@ -118,6 +118,11 @@ _SIGS = {
     "mmr_attention_from_cache": ([VP, VP, I64, I64, I64, I64, VP, VP, SZ, C.c_int, VP], C.c_int),
     "mmr_decode_attention_fused": ([VP, VP, VP, F32, VP, VP, VP, I64, I64, I64, VP, VP, SZ, C.c_int, VP, VP],
                                    C.c_int),
+    "mmr_layer_weights_create": ([C.POINTER(Config)] + [VP] * 11 + [C.POINTER(VP)], C.c_int),
+    "mmr_model_layer_weights": ([VP, I64, C.POINTER(VP)], C.c_int),
+    "mmr_layer_weights_destroy": ([VP], C.c_int),
+    "mmr_decoder_layer_workspace_size": ([C.POINTER(Config), C.c_int], SZ),
+    "mmr_decoder_layer_forward": ([VP, VP, VP, VP, VP, VP, SZ, C.c_int, VP, VP], C.c_int),
     "mmr_matmul_f16": ([VP, I64, I64, VP, I64, VP, VP, VP], C.c_int),
     "mmr_prefill_qkv_rows": ([VP, VP, VP, F32, VP, VP, I64, I64, I64, I64, I64, VP, VP], C.c_int),
     "mmr_prefill_attention": ([VP, VP, I64, I64, I64, I64, I64, VP, VP], C.c_int),
@@ -490,6 +495,52 @@ def swiglu_rows(gate_up, rows, cols, out, stream=None) -> None:
 def embedding_gather(table, ids, tokens, vocab, hidden, out, error=None, stream=None) -> None:
     check(_lib.mmr_embedding_gather(table.ptr, ids.ptr, tokens, vocab, hidden, out.ptr,
                                     error.ptr if error else None, _s(stream)))
+
+
+class LayerWeights:
+    """One decoder layer's device weights (mmr_layer_weights_create from the
+    reference's DenseLayerWeights members, or a view of a model's layer)."""
+
+    NAMES = ("input_norm", "post_attention_norm", "q_norm", "k_norm", "q_proj", "k_proj", "v_proj", "o_proj",
+             "gate_proj", "up_proj", "down_proj")
+
+    def __init__(self, handle: int, config: "Config", owner=None):
+        self.handle = handle
+        self.config = config
+        self._owner = owner  # a Model whose weights a view shares
+
+    @classmethod
+    def create(cls, config: "Config", **arrays) -> "LayerWeights":
+        host = [np.ascontiguousarray(arrays[n], dtype=np.float32) for n in cls.NAMES]
+        h = VP()
+        check(_lib.mmr_layer_weights_create(C.byref(config), *[_ptr(a) for a in host], C.byref(h)))
+        return cls(h.value, config)
+
+    @classmethod
+    def of_model(cls, model: "Model", layer: int) -> "LayerWeights":
+        h = VP()
+        check(_lib.mmr_model_layer_weights(model.handle, layer, C.byref(h)))
+        return cls(h.value, model.config, model)
+
+    def workspace_size(self, splits: int) -> int:
+        return int(_lib.mmr_decoder_layer_workspace_size(C.byref(self.config), splits))
+
+    def forward(self, cache: "KvCache", hidden: DeviceArray, position: DeviceArray, out: DeviceArray,
+                workspace: DeviceArray, splits: int, error: DeviceArray, stream=None) -> None:
+        """mmr_decoder_layer_forward: out = layer(hidden) at device position *position."""
+        check(_lib.mmr_decoder_layer_forward(self.handle, cache.handle, hidden.ptr, position.ptr, out.ptr,
+                                             workspace.ptr, workspace.nbytes, splits, error.ptr, _s(stream)))
+
+    def free(self) -> None:
+        if self.handle:
+            _lib.mmr_layer_weights_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 # ---------------------------------------------------------------- model ----

@@ -529,6 +529,23 @@ static void layer_step(const orc_config* c, const orc_layer* L, orc_kv* kv, floa
   free(mlp);
 }
 
+/* decoder_layer.cpp:312-407 for one layer of the model on its own: hidden is
+ * updated in place, the layer's KV cache in `s` grows by one token.  The same
+ * layer_step the model uses, exposed for the per-layer boundary test. */
+int orc_decoder_layer(const orc_model* m, orc_state* s, int64_t layer, float* hidden, int64_t position) {
+  if (layer < 0 || layer >= m->cfg.num_hidden_layers) return -1;
+  layer_step(&m->cfg, &m->layers[layer], &s->layers[layer], hidden, position);
+  return 0;
+}
+
+/* Keys / values of one layer's cache, [tokens][kv_heads][d]; returns tokens. */
+int64_t orc_state_layer_cache(const orc_state* s, int64_t layer, const float** keys, const float** values) {
+  if (layer < 0 || layer >= s->n_layers) return -1;
+  *keys = s->layers[layer].keys;
+  *values = s->layers[layer].values;
+  return s->layers[layer].tokens;
+}
+
 /* language_model.cpp:297-308 (forward_token) */
 int orc_forward_token(const orc_model* m, orc_state* s, int32_t token, float* logits_out) {
   const orc_config* c = &m->cfg;

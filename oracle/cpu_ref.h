@@ -73,6 +73,13 @@ orc_state* orc_state_new(const orc_model* m);
 void orc_state_free(orc_state* s);
 int64_t orc_state_position(const orc_state* s);
 
+/* decoder_layer.cpp:312-407: one decoder layer of the model, in place on
+ * hidden [hidden_size], appending to that layer's KV cache in `s` (the
+ * state's position is not advanced).  Returns 0, or -1 on a bad layer. */
+int orc_decoder_layer(const orc_model* m, orc_state* s, int64_t layer, float* hidden, int64_t position);
+/* That layer's cache ([tokens][kv_heads][d] keys and values); returns tokens. */
+int64_t orc_state_layer_cache(const orc_state* s, int64_t layer, const float** keys, const float** values);
+
 /* language_model.cpp:297-308 logits of one step; returns 0, or -1 when the token is out of range */
 int orc_forward_token(const orc_model* m, orc_state* s, int32_t token, float* logits_out);
 /* language_model.cpp:310-333 greedy next token; -1 on a bad token */

@@ -61,6 +61,8 @@ def _load() -> C.CDLL:
         "orc_forward_token": ([C.c_void_p, C.c_void_p, C.c_int32, f32p], C.c_int),
         "orc_forward_next_token": ([C.c_void_p, C.c_void_p, C.c_int32], C.c_int32),
         "orc_generate": ([C.c_void_p, i32p, C.c_int64, C.c_int64, i32p, P(C.c_int64), f32p], C.c_int),
+        "orc_decoder_layer": ([C.c_void_p, C.c_void_p, C.c_int64, f32p, C.c_int64], C.c_int),
+        "orc_state_layer_cache": ([C.c_void_p, C.c_int64, P(P(C.c_float)), P(P(C.c_float))], C.c_int64),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(lib, name)
@@ -214,6 +216,26 @@ class OracleState:
         if _lib.orc_forward_token(self.model.handle, self.handle, token, _f(out)) != 0:
             raise IndexError("token id out of vocabulary range")
         return out
+
+    def decoder_layer(self, layer: int, hidden, position: int) -> np.ndarray:
+        """One decoder layer (decoder_layer.cpp:312-407) on a copy of hidden,
+        appending to this state's cache of that layer."""
+        h = f32(hidden).copy()
+        if _lib.orc_decoder_layer(self.model.handle, self.handle, layer, _f(h), position) != 0:
+            raise IndexError("layer out of range")
+        return h
+
+    def layer_cache(self, layer: int):
+        """(keys, values) of one layer, shaped [tokens][kv_heads][d]."""
+        k, v = C.POINTER(C.c_float)(), C.POINTER(C.c_float)()
+        n = int(_lib.orc_state_layer_cache(self.handle, layer, C.byref(k), C.byref(v)))
+        c = self.model.config
+        shape = (n, int(c.num_key_value_heads), int(c.head_dim))
+        if n <= 0:
+            return np.zeros(shape, np.float32), np.zeros(shape, np.float32)
+        size = int(np.prod(shape))
+        return (np.ctypeslib.as_array(k, (size,)).reshape(shape).copy(),
+                np.ctypeslib.as_array(v, (size,)).reshape(shape).copy())
 
     def forward_next_token(self, token: int) -> int:
         nxt = int(_lib.orc_forward_next_token(self.model.handle, self.handle, token))

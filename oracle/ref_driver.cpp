@@ -14,6 +14,9 @@
 //       step, LanguageModel::forward_token for the logits of each generated
 //       token.  Logits of the generated-token indices in logit_steps_csv are
 //       appended to logits_out.bin as float32.
+//   stream <dir> <prompt_csv> <steps> [logits_out.bin] [logit_steps_csv]
+//       Greedy forward_token/argmax_token loop of exactly <steps> tokens with
+//       no EOS stop; per step the top-2 margin and the runner-up id.
 //   loader <dir> <prompt_csv> <max_new>
 //       load_runtime_language_model (runtime_loader.cpp:177-182) + generate.
 //   bench <dir> <prompt_csv> <decode_steps>
@@ -187,6 +190,44 @@ int run_generate(const std::string& dir, const std::vector<int32_t>& prompt, int
   return 0;
 }
 
+// Greedy continuation with no EOS stop (the device loop and the batched step
+// decode a fixed number of steps): forward_token + argmax_token per step, as
+// forward_next_token does (language_model.cpp:310-333).  Per step it records
+// the top-2 margin and the runner-up id, so a GPU run that parts ways at a
+// near-tie can be told apart from a wrong result.
+int run_stream(const std::string& dir, const std::vector<int32_t>& prompt, int64_t steps, const char* logits_path,
+               const std::vector<int32_t>& logit_steps) {
+  LanguageModel model = build_model(dir);
+  auto state = model.make_state();
+  std::vector<float> logits;
+  for (int32_t t : prompt) logits = model.forward_token(t, state);
+  std::vector<int32_t> tokens, runner_up;
+  std::vector<double> margin;
+  std::FILE* lf = logits_path ? std::fopen(logits_path, "wb") : nullptr;
+  for (int64_t i = 0; i < steps; ++i) {
+    const int32_t next = minimind::model::argmax_token(logits);
+    int32_t second = -1;
+    for (int32_t j = 0; j < static_cast<int32_t>(logits.size()); ++j)
+      if (j != next && (second < 0 || logits[j] > logits[second])) second = j;
+    tokens.push_back(next);
+    runner_up.push_back(second);
+    margin.push_back(static_cast<double>(logits[next]) - static_cast<double>(logits[second]));
+    if (lf && std::find(logit_steps.begin(), logit_steps.end(), static_cast<int32_t>(i)) != logit_steps.end())
+      std::fwrite(logits.data(), 4, logits.size(), lf);
+    if (i + 1 < steps) logits = model.forward_token(next, state);
+  }
+  if (lf) std::fclose(lf);
+  std::printf("{");
+  print_tokens("generated", tokens);
+  std::printf(", ");
+  print_tokens("runner_up", runner_up);
+  std::printf(", \"margin\": [");
+  for (size_t i = 0; i < margin.size(); ++i) std::printf("%s%.9g", i ? ", " : "", margin[i]);
+  std::printf("], \"eps\": %.9g, \"theta\": %.9g}\n", static_cast<double>(model.config().rms_norm_eps),
+              static_cast<double>(model.config().rope_theta));
+  return 0;
+}
+
 int run_loader(const std::string& dir, const std::vector<int32_t>& prompt, int64_t max_new) {
   LanguageModel model = minimind::model::load_runtime_language_model(dir);
   const auto generated = model.generate(prompt, max_new);
@@ -236,6 +277,9 @@ int main(int argc, char** argv) {
     if (mode == "generate")
       return run_generate(dir, prompt, n, argc > 5 ? argv[5] : nullptr,
                           argc > 6 ? parse_csv(argv[6]) : std::vector<int32_t>{});
+    if (mode == "stream")
+      return run_stream(dir, prompt, n, argc > 5 ? argv[5] : nullptr,
+                        argc > 6 ? parse_csv(argv[6]) : std::vector<int32_t>{});
     if (mode == "loader") return run_loader(dir, prompt, n);
     if (mode == "bench") return run_bench(dir, prompt, n);
     std::fprintf(stderr, "unknown mode %s\n", mode.c_str());

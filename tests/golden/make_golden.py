@@ -43,6 +43,15 @@ MINIMIND2 = dict(hidden_size=768, num_hidden_layers=16, num_attention_heads=8, n
 MINIMIND2_SMALL = dict(hidden_size=512, num_hidden_layers=8, num_attention_heads=8, num_key_value_heads=2,
                        head_dim=64, intermediate_size=1408, vocab_size=6400, max_position_embeddings=32768,
                        rms_norm_eps=1e-5, rope_theta=1e6, tie_word_embeddings=1)
+# configs[2]'s attention shape (8 query / 2 KV heads, head_dim 96, theta 1e6)
+# in a one-layer model, and a head_dim 128 variant: long-context decode cases
+# the CPU path finishes in about a minute
+ATTN96 = dict(hidden_size=768, num_hidden_layers=1, num_attention_heads=8, num_key_value_heads=2, head_dim=96,
+              intermediate_size=512, vocab_size=512, max_position_embeddings=16384, rms_norm_eps=1e-5,
+              rope_theta=1e6, tie_word_embeddings=0)
+ATTN128 = dict(hidden_size=1024, num_hidden_layers=1, num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+               intermediate_size=512, vocab_size=512, max_position_embeddings=16384, rms_norm_eps=1e-5,
+               rope_theta=1e6, tie_word_embeddings=0)
 MINI = dict(hidden_size=256, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
             intermediate_size=512, vocab_size=512, max_position_embeddings=4096, rms_norm_eps=1e-5, rope_theta=1e4,
             tie_word_embeddings=0)
@@ -64,6 +73,20 @@ CASES = {
     # 512-token prompt, 256 greedy steps
     "cfg3": dict(config=MINIMIND2, seed=0, round_fp16=True, prompt_seed=1, prompt_len=512, max_new=256,
                  logit_steps=[0, 64, 128, 192, 255]),
+    # BASELINE configs[4], sequence 0 of the batch: MiniMind2, 256-token prompt
+    # (seed 1000 + sequence index), greedy to a 4096-token context with no EOS
+    # stop (the batched step decodes a fixed number of steps)
+    "cfg4_seq0": dict(config=MINIMIND2, seed=0, round_fp16=True, prompt_seed=1000, prompt_len=256, max_new=3840,
+                      logit_steps=[0, 1280, 2560, 3839], stream=True),
+    # decode steps whose context crosses 4096 and 8192 keys (d 96) and 2048 keys
+    # (d 128): the split attention with the fused q/k postprocess and the
+    # separate combine kernel
+    "long4k": dict(config=ATTN96, seed=21, round_fp16=True, prompt_seed=22, prompt_len=4090, max_new=16,
+                   logit_steps=list(range(16)), stream=True),
+    "long8k": dict(config=ATTN96, seed=21, round_fp16=True, prompt_seed=23, prompt_len=8185, max_new=16,
+                   logit_steps=list(range(16)), stream=True),
+    "long_d128": dict(config=ATTN128, seed=24, round_fp16=True, prompt_seed=25, prompt_len=2040, max_new=16,
+                      logit_steps=list(range(16)), stream=True),
 }
 
 
@@ -75,9 +98,10 @@ def sha256_file(path: Path) -> str:
     return h.hexdigest()
 
 
-def oracle_replay(model_dir: Path, prompt, max_new: int, steps):
+def oracle_replay(model_dir: Path, prompt, max_new: int, steps, stop_at_eos: bool = True):
     """C restatement, step by step: greedy tokens with generate's EOS rule
-    (language_model.cpp:389-395) and the logits rows at `steps`."""
+    (language_model.cpp:389-395) unless stop_at_eos is False, and the logits
+    rows at `steps`."""
     m = oracle.OracleModel(model_dir)
     eos = int(m.config.eos_token_id)
     st = m.new_state()
@@ -90,7 +114,7 @@ def oracle_replay(model_dir: Path, prompt, max_new: int, steps):
         ids.append(nxt)
         if i in steps:
             rows.append(lg.copy())
-        if nxt == eos or i + 1 == max_new:
+        if (stop_at_eos and nxt == eos) or i + 1 == max_new:
             break
         lg = st.forward_token(nxt)
     return ids, np.array(rows, np.float32).reshape(len(rows), m.vocab)
@@ -115,12 +139,14 @@ def make_case(name: str, spec: dict, workdir: Path) -> dict:
             raise SystemExit(f"{name}: restatement tokens differ from the reference loader run")
     else:
         lpath = workdir / f"{name}_logits.bin"
+        mode = "stream" if spec.get("stream") else "generate"
         with ThreadPoolExecutor(1) as ex:  # reference process and restatement run concurrently
-            fut_ref = ex.submit(oracle.ref_run, "generate", model_dir, prompt, spec["max_new"], lpath, steps)
-            ora_ids, ora_rows = oracle_replay(model_dir, prompt, spec["max_new"], steps)
+            fut_ref = ex.submit(oracle.ref_run, mode, model_dir, prompt, spec["max_new"], lpath, steps)
+            ora_ids, ora_rows = oracle_replay(model_dir, prompt, spec["max_new"], steps,
+                                              stop_at_eos=not spec.get("stream"))
             ref = fut_ref.result()
         logits = np.fromfile(lpath, np.float32).reshape(len(steps), spec["config"]["vocab_size"])
-        if ref["generated"] != ref["replay"]:
+        if mode == "generate" and ref["generated"] != ref["replay"]:
             raise SystemExit(f"{name}: reference generate and forward_token replay disagree")
         if ora_ids != ref["generated"]:
             raise SystemExit(f"{name}: restatement tokens differ from the reference build")
@@ -137,7 +163,9 @@ def make_case(name: str, spec: dict, workdir: Path) -> dict:
         "prompt": prompt,
         "max_new": spec["max_new"],
         "generated": ref["generated"],
+        "stop_at_eos": not spec.get("stream"),
         "margin": ref.get("margin", []),
+        "runner_up": ref.get("runner_up", []),
         "logit_sum": ref.get("logit_sum", []),
         "logit_sumsq": ref.get("logit_sumsq", []),
         "logit_steps": steps,

@@ -50,12 +50,16 @@ def test_generate_and_logits_match_reference(gpu, case):
     assert st.position == len(g["prompt"]) + len(g["generated"]) - 1
 
 
-def test_minimind2_512_prompt_256_steps_device_loop(gpu):
-    # BASELINE configs[3] at full size: 512-token prompt, 256 greedy steps in the hipGraph loop
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+def test_minimind2_512_prompt_256_steps_device_loop(gpu, kv):
+    # BASELINE configs[3] at full size: 512-token prompt, 256 greedy steps in
+    # the hipGraph loop, with an fp32 and with an fp16 KV cache (the latter is
+    # the reference device cache's dtype and the one bench.py times)
     mmr = gpu
+    print(f"[case] cfg3 512 + 256 kv={kv}", flush=True)
     g = load_golden("cfg3")
     m = synth_model(mmr, g)
-    st = m.make_state(len(g["prompt"]) + g["max_new"])
+    st = m.make_state(len(g["prompt"]) + g["max_new"], mmr.KV_F16 if kv == "f16" else mmr.KV_F32)
     st.enqueue_prefill(g["prompt"])
     st.enqueue_decode(g["max_new"] - 1)
     st.synchronize()
