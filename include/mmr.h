@@ -168,6 +168,22 @@ int mmr_attention_from_cache(const float* query, const mmr_kv_cache* cache, int6
                              int64_t kv_heads, int64_t head_dim, float* out, void* workspace, size_t workspace_bytes,
                              int splits, mmr_stream_t stream);
 
+/* No counterpart in the reference: mmr_attention_from_cache without a
+ * workspace argument, for callers that cannot allocate device memory (code
+ * under hipGraph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split partials live in a static device array of the
+ * library, MMR_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends;
+ * a call whose partials (mmr_attention_workspace_size) exceed it fails with
+ * MMR_ERR_INVALID_ARGUMENT.  Allocates nothing; the first call on each GPU
+ * looks up that GPU's copy of the array (make it outside stream capture).
+ * Every call on one GPU shares the array and leaves its contents behind:
+ * calls that overlap on one GPU (several streams or threads) race, so the
+ * caller serialises them. */
+#define MMR_NOALLOC_SCRATCH_BYTES (2u << 20)
+int mmr_attention_from_cache_noalloc(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
+                                     int64_t kv_heads, int64_t head_dim, float* out, int splits,
+                                     mmr_stream_t stream);
+
 /* ---- fused post-process + append + attend (the decode-step form of
  * device_decode_attention, ascend_custom_ops.h:153-161): position read from
  * device memory (*position), k/v appended at that index, attention over

@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -452,34 +453,98 @@ size_t mmr_attention_workspace_size(int64_t q_heads, int64_t kv_heads, int64_t h
   return attention_ws_bytes(q_heads, kv_heads, head_dim, splits);
 }
 
+namespace {
+
+// mmr_attention_from_cache with the split partials in `part` (checked by the
+// callers to hold attention_ws_bytes for `splits`).
+void enqueue_attention_from_cache(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
+                                  int64_t kv_heads, int64_t head_dim, float* out, float* part, int splits,
+                                  mmr_stream_t stream) {
+  mmr::AttnArgs a;
+  a.q = query;
+  a.tokens = static_cast<int>(tokens);
+  a.kcache = cache->keys.data();
+  a.vcache = cache->values.data();
+  a.capacity = static_cast<int>(cache->capacity);
+  a.rows = static_cast<int>(cache->rows);
+  a.hq = static_cast<int>(q_heads);
+  a.hkv = static_cast<int>(kv_heads);
+  a.d = static_cast<int>(head_dim);
+  a.splits = splits;
+  a.part = part;
+  hip(mmr::launch_attention(a, mmr::kAttnFromCache, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
+                            as_stream(stream)),
+      "attention launch");
+  hip(mmr::launch_attention_combine(a.part, a.hq, a.hkv, a.d, splits, out, as_stream(stream)),
+      "attention combine launch");
+}
+
+void check_attention_from_cache(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
+                                int64_t kv_heads, int64_t head_dim, const float* out, int* splits) {
+  require(query && cache && out, "null argument");
+  check_attention_shape(q_heads, kv_heads, head_dim);
+  require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+  require(tokens >= 1 && tokens <= cache->capacity, "tokens must be in [1, capacity]");
+  if (*splits <= 0) *splits = auto_splits(tokens, head_dim);
+  require(*splits <= 4096, "splits too large");
+}
+
+}  // namespace
+
 int mmr_attention_from_cache(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, float* out, void* workspace, size_t workspace_bytes,
                              int splits, mmr_stream_t stream) {
   return guarded([&] {
-    require(query && cache && out && workspace, "null argument");
-    check_attention_shape(q_heads, kv_heads, head_dim);
-    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
-    require(tokens >= 1 && tokens <= cache->capacity, "tokens must be in [1, capacity]");
-    if (splits <= 0) splits = auto_splits(tokens, head_dim);
-    require(splits <= 4096, "splits too large");
+    check_attention_from_cache(query, cache, tokens, q_heads, kv_heads, head_dim, out, &splits);
+    require(workspace != nullptr, "null argument");
     require(workspace_bytes >= attention_ws_bytes(q_heads, kv_heads, head_dim, splits), "workspace too small");
-    mmr::AttnArgs a;
-    a.q = query;
-    a.tokens = static_cast<int>(tokens);
-    a.kcache = cache->keys.data();
-    a.vcache = cache->values.data();
-    a.capacity = static_cast<int>(cache->capacity);
-    a.rows = static_cast<int>(cache->rows);
-    a.hq = static_cast<int>(q_heads);
-    a.hkv = static_cast<int>(kv_heads);
-    a.d = static_cast<int>(head_dim);
-    a.splits = splits;
-    a.part = static_cast<float*>(workspace);
-    hip(mmr::launch_attention(a, mmr::kAttnFromCache, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
-                              as_stream(stream)),
-        "attention launch");
-    hip(mmr::launch_attention_combine(a.part, a.hq, a.hkv, a.d, splits, out, as_stream(stream)),
-        "attention combine launch");
+    enqueue_attention_from_cache(query, cache, tokens, q_heads, kv_heads, head_dim, out,
+                                 static_cast<float*>(workspace), splits, stream);
+  });
+}
+
+// ---- mmr_attention_from_cache_noalloc: the split partials in a static
+// device array instead of a caller workspace.  One copy per GPU, held until
+// the process ends.  In host code `scratch` names a host-side stand-in, never
+// the device copy: every use goes through the address hipGetSymbolAddress
+// returns for the current device, looked up once per device on its first
+// call (under g_scratch_mutex) and kept in g_scratch_ptr.
+static __device__ __align__(256) float scratch[MMR_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+float* device_scratch() {
+  int dev = -1;
+  hip(hipGetDevice(&dev), "hipGetDevice");
+  require(dev >= 0 && dev < kMaxScratchDevices, "device index beyond the static scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    require(p != nullptr, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+int mmr_attention_from_cache_noalloc(const float* query, const mmr_kv_cache* cache, int64_t tokens, int64_t q_heads,
+                                     int64_t kv_heads, int64_t head_dim, float* out, int splits,
+                                     mmr_stream_t stream) {
+  return guarded([&] {
+    check_attention_from_cache(query, cache, tokens, q_heads, kv_heads, head_dim, out, &splits);
+    const size_t need = attention_ws_bytes(q_heads, kv_heads, head_dim, splits);
+    if (need > MMR_NOALLOC_SCRATCH_BYTES)
+      throw std::invalid_argument("split partials need " + std::to_string(need) + " bytes, beyond the " +
+                                  std::to_string(MMR_NOALLOC_SCRATCH_BYTES) +
+                                  "-byte static scratch: use fewer splits or mmr_attention_from_cache");
+    enqueue_attention_from_cache(query, cache, tokens, q_heads, kv_heads, head_dim, out, device_scratch(), splits,
+                                 stream);
   });
 }
 

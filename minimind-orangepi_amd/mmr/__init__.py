@@ -116,6 +116,7 @@ _SIGS = {
     "mmr_decode_qkv_postprocess": ([VP, VP, VP, VP, I64, I64, I64, I64, I64, VP, F32, VP, VP], C.c_int),
     "mmr_attention_workspace_size": ([I64, I64, I64, C.c_int], SZ),
     "mmr_attention_from_cache": ([VP, VP, I64, I64, I64, I64, VP, VP, SZ, C.c_int, VP], C.c_int),
+    "mmr_attention_from_cache_noalloc": ([VP, VP, I64, I64, I64, I64, VP, C.c_int, VP], C.c_int),
     "mmr_decode_attention_fused": ([VP, VP, VP, F32, VP, VP, VP, I64, I64, I64, VP, VP, SZ, C.c_int, VP, VP],
                                    C.c_int),
     "mmr_layer_weights_create": ([C.POINTER(Config)] + [VP] * 11 + [C.POINTER(VP)], C.c_int),
@@ -455,6 +456,16 @@ def attention_from_cache(query, cache: KvCache, tokens, q_heads, kv_heads, head_
                          stream=None) -> None:
     check(_lib.mmr_attention_from_cache(query.ptr, cache.handle, tokens, q_heads, kv_heads, head_dim, out.ptr,
                                         workspace.ptr, workspace.nbytes, splits, _s(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 2 << 20  # MMR_NOALLOC_SCRATCH_BYTES
+
+
+def attention_from_cache_noalloc(query, cache: KvCache, tokens, q_heads, kv_heads, head_dim, out, splits=0,
+                                 stream=None) -> None:
+    """mmr_attention_from_cache with the library's static scratch (allocates nothing)."""
+    check(_lib.mmr_attention_from_cache_noalloc(query.ptr, cache.handle, tokens, q_heads, kv_heads, head_dim, out.ptr,
+                                                splits, _s(stream)))
 
 
 def decode_attention_fused(qkv, q_norm, k_norm, eps, rope: RopeTable, position, cache: KvCache, q_heads, kv_heads,
