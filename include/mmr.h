@@ -269,6 +269,12 @@ int mmr_model_weight_bytes(const mmr_model* model, uint64_t* bytes);
  * runtime_loader.cpp:121-167) with seeded synthetic weights. */
 int mmr_write_synthetic_model(const char* model_dir, const mmr_config* config, uint64_t seed, double std,
                               int round_fp16);
+/* make_toy_language_model (language_model.cpp:415-470): the reference's
+ * built-in toy model (hidden 4, head_dim 2, vocab 8, 16 positions), run on
+ * the small-model step kernel; mmr_write_toy_model writes the same model as a
+ * runtime directory (config + MMRTW001 weights). */
+int mmr_model_create_toy(mmr_model** out);
+int mmr_write_toy_model(const char* model_dir);
 int mmr_synthesize_normals(uint64_t seed, uint64_t first, uint64_t count, double std, int round_fp16, float* out);
 int mmr_synthesize_prompt(uint64_t seed, int64_t count, int64_t vocab, int32_t* out);
 

@@ -6,7 +6,7 @@
 
 Outputs (git-ignored, shipped with the tree to the GPU box):
     minimind-orangepi_amd/lib/libmmr.so
-    minimind-orangepi_amd/bin/bench_decode, bin/minimind_generate
+    minimind-orangepi_amd/bin/bench_decode, bin/minimind_generate, bin/check_prefill_consistency
 """
 from __future__ import annotations
 
@@ -31,7 +31,8 @@ COMMON = ["-std=c++17", "-O3", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{ROOT
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 SOURCES = sorted(CSRC.glob("kernels/*.hip")) + sorted(CSRC.glob("runtime/*.cpp")) + [CSRC / "capi.cpp"]
-TOOLS = {"bench_decode": CSRC / "tools" / "bench_decode.cpp", "minimind_generate": CSRC / "tools" / "minimind_generate.cpp"}
+TOOLS = {name: CSRC / "tools" / f"{name}.cpp"
+         for name in ("bench_decode", "minimind_generate", "check_prefill_consistency")}
 
 
 def _headers() -> list[Path]:

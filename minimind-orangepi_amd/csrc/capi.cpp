@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <filesystem>
 #include <memory>
 #include <mutex>
 #include <stdexcept>
@@ -856,6 +857,25 @@ int mmr_write_synthetic_model(const char* model_dir, const mmr_config* config, u
     const auto errors = validate_config(c);
     if (!errors.empty()) throw std::invalid_argument("invalid MiniMind config: " + errors.front());
     write_synthetic_model(model_dir, c, seed, std, round_fp16 != 0);
+  });
+}
+
+int mmr_model_create_toy(mmr_model** out) {
+  return guarded([&] {
+    require(out, "null out");
+    auto m = std::make_unique<mmr_model>();
+    m->lm = std::make_unique<LanguageModel>(make_toy_language_model());
+    *out = m.release();
+  });
+}
+
+int mmr_write_toy_model(const char* model_dir) {
+  return guarded([&] {
+    require(model_dir, "null argument");
+    const auto cw = toy_model_weights();
+    std::filesystem::create_directories(model_dir);
+    write_config(cw.first, std::string(model_dir) + "/minimind_runtime_config.txt");
+    write_weights(cw.first, cw.second, std::string(model_dir) + "/weights.bin");
   });
 }
 

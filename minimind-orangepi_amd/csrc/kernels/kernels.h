@@ -339,6 +339,48 @@ hipError_t launch_batch_head(const float* part, int splits, int vocab, int batch
                              int32_t* seq, int seq_stride, int32_t* pos, const int32_t* prompt_len, int seq_len,
                              hipStream_t stream);
 
+// -------------------------------------------------------- small models ----
+// A whole decode step in one workgroup (tiny.hip) for models whose shapes the
+// GEMV / attention kernels do not take (the reference's toy model: hidden 4,
+// head_dim 2).  Same step bookkeeping as launch_argmax_finalize.
+struct TinyLayerPtrs {
+  const float* input_norm = nullptr;
+  const float* post_norm = nullptr;
+  const float* q_norm = nullptr;
+  const float* k_norm = nullptr;
+  const __half* qkv = nullptr;      // [(Hq + 2 Hkv) d][H]
+  const __half* o = nullptr;        // [H][Hq d]
+  const __half* gate_up = nullptr;  // [2F][H] interleaved gate/up rows
+  const __half* down = nullptr;     // [H][F]
+  void* kcache = nullptr;           // [Hkv][rows][d]
+  void* vcache = nullptr;
+};
+struct TinyStepArgs {
+  const __half* embed = nullptr;    // [V][H]
+  const __half* lm_head = nullptr;  // [V][H]
+  const float* final_norm = nullptr;
+  const TinyLayerPtrs* layers = nullptr;  // device array [n_layers]
+  int n_layers = 0;
+  const float* inv_freq = nullptr;  // [d/2]
+  int hidden = 0, hq = 0, hkv = 0, d = 0, f = 0, vocab = 0;
+  float eps = 0.0f;
+  int rows = 0;      // cache rows per KV head
+  int capacity = 0;  // usable positions
+  int32_t* seq = nullptr;
+  int32_t* pos = nullptr;
+  const int32_t* prompt_len = nullptr;
+  int seq_len = 0;
+  int32_t* err = nullptr;
+  int32_t* token_out = nullptr;
+  float* logits = nullptr;  // [V]
+};
+constexpr int kTinyMaxWidth = 1024;   // hidden and (Hq + 2 Hkv) d
+constexpr int kTinyMaxFfn = 2048;
+constexpr int kTinyMaxHeadDim = 128;  // even
+constexpr int kTinyMaxContext = 2048; // positions of one state
+bool tiny_step_supported(int hidden, int hq, int hkv, int d, int f, int vocab, int capacity);
+hipError_t launch_tiny_step(const TinyStepArgs& a, KvDtype kv, hipStream_t stream);
+
 // ------------------------------------------------------------- support ----
 hipError_t launch_rms_norm_rows(const float* in, const float* w, float eps, int rows, int cols, float* out,
                                 hipStream_t stream, bool final_norm = false);

@@ -31,6 +31,9 @@ struct DeviceModel {
   const float* inv_freq = nullptr;  // [d/2] RoPE frequencies, formula of decoder_layer.cpp:114
   mmr::GemvPlan plan_qkv, plan_o, plan_gu, plan_down, plan_lm;
   bool gemm_prefill = false;  // every projection's K suits the prefill GEMM
+  // Shapes below the GEMV / attention kernels' (the reference's toy model):
+  // every step is one launch of the one-workgroup kernel (tiny.hip).
+  bool tiny = false;
   std::size_t weight_bytes = 0;
 };
 

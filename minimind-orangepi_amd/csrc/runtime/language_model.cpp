@@ -48,6 +48,7 @@ struct DeviceState {
   float* attn = nullptr;
   float* act = nullptr;
   float* logits = nullptr;
+  mmr::TinyLayerPtrs* tiny_layers = nullptr;  // small-model path: per-layer weights and caches
   float* attn_part = nullptr;  // split partials: o [Hkv][splits][R][d], then (m, l) [Hkv][splits][R][2]
   float* lm_part_val = nullptr;  // per-block argmax partials of the head GEMV
   int* lm_part_idx = nullptr;
@@ -144,8 +145,15 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
   const auto errors = validate_config(config_);
   if (!errors.empty()) throw std::invalid_argument("invalid MiniMind config: " + errors.front());
   const auto dev_errors = validate_device_config(config_);
-  if (!dev_errors.empty()) throw std::invalid_argument("unsupported by the gfx950 runtime: " + dev_errors.front());
   const auto& c = config_;
+  // Shapes the GEMV / attention kernels do not take run through the
+  // one-workgroup step kernel when they fit it (the reference's toy model).
+  const bool tiny = !dev_errors.empty() && !c.use_moe &&
+                    mmr::tiny_step_supported(static_cast<int>(c.hidden_size), static_cast<int>(c.num_attention_heads),
+                                             static_cast<int>(c.num_key_value_heads), static_cast<int>(c.head_dim),
+                                             static_cast<int>(c.intermediate_size), static_cast<int>(c.vocab_size), 1);
+  if (!dev_errors.empty() && !tiny)
+    throw std::invalid_argument("unsupported by the gfx950 runtime: " + dev_errors.front());
   const int64_t H = c.hidden_size, V = c.vocab_size, D = c.head_dim, F = c.intermediate_size;
   const int64_t qs = c.num_attention_heads * D, kvs = c.num_key_value_heads * D;
   require_size(weights.embed_tokens, V * H, "embed_tokens");
@@ -157,6 +165,7 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
 
   auto dm = std::make_shared<DeviceModel>();
   dm->cfg = c;
+  dm->tiny = tiny;
   const bool share_head = weights.lm_head == weights.embed_tokens;
   const int64_t half_d = D / 2;
   Arena& ar = dm->arena;
@@ -182,6 +191,11 @@ LanguageModel::LanguageModel(MiniMindConfig config, DenseModelWeights weights) :
     dm->inv_freq = upload<float>(ar, inv.data(), inv.size());
   }
   dm->weight_bytes = wbytes;
+  if (tiny) {
+    check_hip(hipDeviceSynchronize(), "weight upload");
+    device_ = std::move(dm);
+    return;
+  }
   const LayerPlans lp = plan_layer(c);
   dm->plan_qkv = lp.qkv;
   dm->plan_o = lp.o;
@@ -207,9 +221,15 @@ DecoderState LanguageModel::make_state() const { return make_state(0, KvCacheDty
 
 DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const {
   const auto& c = config_;
-  if (capacity <= 0) capacity = c.max_position_embeddings;
-  if (capacity > c.max_position_embeddings)
-    throw std::invalid_argument("state capacity exceeds max_position_embeddings");
+  // A small model's step kernel evaluates RoPE at any position, as the
+  // reference CPU path does, so its states are bounded by the kernel's LDS
+  // (kTinyMaxContext) rather than by max_position_embeddings (16 for the toy).
+  const bool tiny = device_->tiny;
+  const int64_t limit = tiny ? mmr::kTinyMaxContext : c.max_position_embeddings;
+  if (capacity <= 0) capacity = limit;
+  if (capacity > limit)
+    throw std::invalid_argument(tiny ? "state capacity exceeds the small-model step kernel's 2048 positions"
+                                     : "state capacity exceeds max_position_embeddings");
   auto s = std::make_unique<DeviceState>();
   s->model = device_;
   s->kv = kv == KvCacheDtype::kFloat16 ? mmr::kKvF16 : mmr::kKvF32;
@@ -223,7 +243,7 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
   const int64_t F = c.intermediate_size, V = c.vocab_size;
   const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
-  s->cache_rows = mmr::attention_cache_rows(capacity, static_cast<int>(D));
+  s->cache_rows = tiny ? capacity : mmr::attention_cache_rows(capacity, static_cast<int>(D));
   const std::size_t cache_bytes = static_cast<std::size_t>(Hkv * s->cache_rows * D) * kv_elem;
   Arena& ar = s->arena;
   for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
@@ -231,7 +251,9 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     ar.plan(cache_bytes);
   }
   const std::size_t part_floats =
-      mmr::attention_partial_floats(static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(D), kMaxSplits);
+      tiny ? 0 : mmr::attention_partial_floats(static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(D), kMaxSplits);
+  const std::size_t tiny_bytes = tiny ? c.num_hidden_layers * sizeof(mmr::TinyLayerPtrs) : 0;
+  ar.plan(tiny_bytes);
   ar.plan((capacity + 1) * 4);
   ar.plan(4 * 4);  // pos, prompt_len, err, token_out
   ar.plan(H * 4);
@@ -291,6 +313,7 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->attn_part = ar.take<float>(part_floats);
   s->lm_part_val = ar.take<float>(device_->plan_lm.blocks);
   s->lm_part_idx = ar.take<int>(device_->plan_lm.blocks);
+  s->tiny_layers = tiny ? ar.take<mmr::TinyLayerPtrs>(static_cast<std::size_t>(c.num_hidden_layers)) : nullptr;
   if (C > 0) {
     s->pf_h = ar.take<float>(C * H);
     s->pf_x = ar.take<float>(C * H);
@@ -309,6 +332,24 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     s->pf_act_s.lo = ar.take<uint16_t>(C * F);
     s->pf_act_s.inv = ar.take<float>(C * ((F + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine));
     s->pf_act_s.chunk = mmr::kSplitChunkFine;
+  }
+  if (tiny) {
+    std::vector<mmr::TinyLayerPtrs> table(static_cast<std::size_t>(c.num_hidden_layers));
+    for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
+      const LayerDev& L = device_->layers[static_cast<std::size_t>(l)];
+      auto& t = table[static_cast<std::size_t>(l)];
+      t.input_norm = L.input_norm;
+      t.post_norm = L.post_norm;
+      t.q_norm = L.q_norm;
+      t.k_norm = L.k_norm;
+      t.qkv = L.qkv;
+      t.o = L.o;
+      t.gate_up = L.gate_up;
+      t.down = L.down;
+      t.kcache = s->kcache[static_cast<std::size_t>(l)];
+      t.vcache = s->vcache[static_cast<std::size_t>(l)];
+    }
+    check_hip(hipMemcpy(s->tiny_layers, table.data(), tiny_bytes, hipMemcpyHostToDevice), "hipMemcpy layer table");
   }
   check_hip(hipHostMalloc(reinterpret_cast<void**>(&s->staging), (capacity + 8) * sizeof(int32_t),
                           hipHostMallocDefault),
@@ -463,7 +504,41 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
   }
 }
 
+// The whole step of a small model in one launch (tiny.hip).
+void enqueue_tiny_step(const DeviceState& s) {
+  const DeviceModel& m = *s.model;
+  const auto& c = m.cfg;
+  mmr::TinyStepArgs a;
+  a.embed = m.embed;
+  a.lm_head = m.lm_head;
+  a.final_norm = m.final_norm;
+  a.layers = s.tiny_layers;
+  a.n_layers = static_cast<int>(c.num_hidden_layers);
+  a.inv_freq = m.inv_freq;
+  a.hidden = static_cast<int>(c.hidden_size);
+  a.hq = static_cast<int>(c.num_attention_heads);
+  a.hkv = static_cast<int>(c.num_key_value_heads);
+  a.d = static_cast<int>(c.head_dim);
+  a.f = static_cast<int>(c.intermediate_size);
+  a.vocab = static_cast<int>(c.vocab_size);
+  a.eps = c.rms_norm_eps;
+  a.rows = static_cast<int>(s.cache_rows);
+  a.capacity = static_cast<int>(s.capacity);
+  a.seq = s.seq;
+  a.pos = s.pos;
+  a.prompt_len = s.prompt_len;
+  a.seq_len = static_cast<int>(s.capacity + 1);
+  a.err = s.err;
+  a.token_out = s.token_out;
+  a.logits = s.logits;
+  check_hip(mmr::launch_tiny_step(a, s.kv, s.stream), "small-model step");
+}
+
 void enqueue_step_kernels(const DeviceState& s, int splits) {
+  if (s.model->tiny) {
+    enqueue_tiny_step(s);
+    return;
+  }
   for (size_t l = 0; l < s.model->layers.size(); ++l)
     for (int k = kQkv; k <= kDown; ++k) enqueue_kernel(s, k, l, splits, false);
   enqueue_kernel(s, kHead, 0, splits, false);
@@ -740,6 +815,7 @@ void LanguageModel::enqueue_prefill(DecoderState& state, const std::vector<int32
 
 void LanguageModel::enqueue_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const {
   DeviceState& s = *state.device;
+  if (device_->tiny) throw std::invalid_argument("a small model's step is one kernel: no per-kernel launches");
   const int64_t L = config_.num_hidden_layers;
   if (kernel < kQkv || kernel > kFinalize) throw std::invalid_argument("unknown step kernel");
   if (layer < 0 || layer >= L || count < 0) throw std::invalid_argument("layer / count out of range");
@@ -861,7 +937,8 @@ void LanguageModel::generate_stream(const std::vector<int32_t>& prompt_tokens, i
   if (max_new_tokens < 0) throw std::invalid_argument("max_new_tokens cannot be negative");
   const int64_t prompt_len = static_cast<int64_t>(prompt_tokens.size());
   const int64_t needed = prompt_len + std::max<int64_t>(max_new_tokens, 1) - 1;
-  if (needed > config_.max_position_embeddings) throw std::length_error("sequence exceeds max_position_embeddings");
+  const int64_t limit = device_->tiny ? mmr::kTinyMaxContext : config_.max_position_embeddings;
+  if (needed > limit) throw std::length_error("sequence exceeds max_position_embeddings");
   DecoderState state = make_state(std::max<int64_t>(needed, 1), KvCacheDtype::kFloat32);
   enqueue_prefill(state, prompt_tokens);
   // The prompt's last step predicts generated token 0 at seq[prompt_len].
@@ -894,6 +971,72 @@ std::vector<int32_t> LanguageModel::generate(const std::vector<int32_t>& prompt_
 int32_t argmax_token(const std::vector<float>& logits) {
   if (logits.empty()) throw std::invalid_argument("logits cannot be empty");
   return static_cast<int32_t>(std::distance(logits.begin(), std::max_element(logits.begin(), logits.end())));
+}
+
+std::pair<MiniMindConfig, DenseModelWeights> toy_model_weights() {
+  MiniMindConfig c;  // struct defaults (rms_norm_eps 1e-6), then the toy's shape
+  c.hidden_size = 4;
+  c.num_hidden_layers = 1;
+  c.use_moe = false;
+  c.vocab_size = 8;
+  c.bos_token_id = 1;
+  c.eos_token_id = 2;
+  c.num_attention_heads = 2;
+  c.num_key_value_heads = 1;
+  c.head_dim = 2;
+  c.intermediate_size = 8;
+  c.max_position_embeddings = 16;
+  c.rope_theta = 10000.0F;
+  c.tie_word_embeddings = false;
+  c.moe_intermediate_size = 8;
+  const int64_t H = c.hidden_size, V = c.vocab_size;
+  // rows x cols with ones on the leading diagonal
+  const auto eye = [](int64_t rows, int64_t cols) {
+    std::vector<float> m(static_cast<size_t>(rows * cols), 0.0F);
+    for (int64_t i = 0; i < std::min(rows, cols); ++i) m[static_cast<size_t>(i * cols + i)] = 1.0F;
+    return m;
+  };
+  DenseModelWeights w;
+  // Token 0 maps to zero; tokens 1..4 to the unit vectors e0..e3; tokens
+  // 5..7 to e_j + e_(j+1).  lm_head row 0 is zero, rows 1..4 are 0.2 e_j,
+  // rows 5..7 are 2 e_j + 0.1 e_(j+1): the tables of the reference toy.
+  w.embed_tokens.assign(static_cast<size_t>(V * H), 0.0F);
+  w.lm_head.assign(static_cast<size_t>(V * H), 0.0F);
+  for (int64_t t = 1; t < V; ++t) {
+    const int64_t j = t <= H ? t - 1 : t - H - 1;
+    float* e = &w.embed_tokens[static_cast<size_t>(t * H)];
+    float* o = &w.lm_head[static_cast<size_t>(t * H)];
+    if (t <= H) {
+      e[j] = 1.0F;
+      o[j] = 0.2F;
+    } else {
+      e[j] = 1.0F;
+      e[j + 1] = 1.0F;
+      o[j] = 2.0F;
+      o[j + 1] = 0.1F;
+    }
+  }
+  w.final_norm.assign(static_cast<size_t>(H), 1.0F);
+  DenseLayerWeights L;
+  const int64_t qs = c.num_attention_heads * c.head_dim, kvs = c.num_key_value_heads * c.head_dim;
+  L.input_norm.assign(static_cast<size_t>(H), 1.0F);
+  L.post_attention_norm.assign(static_cast<size_t>(H), 1.0F);
+  L.q_norm.assign(static_cast<size_t>(c.head_dim), 1.0F);
+  L.k_norm.assign(static_cast<size_t>(c.head_dim), 1.0F);
+  L.q_proj = eye(qs, H);
+  L.k_proj = eye(kvs, H);
+  L.v_proj = eye(kvs, H);
+  L.o_proj = eye(H, qs);
+  L.gate_proj = eye(c.intermediate_size, H);
+  L.up_proj = eye(c.intermediate_size, H);
+  L.down_proj = eye(H, c.intermediate_size);
+  w.layers.push_back(std::move(L));
+  return {c, std::move(w)};
+}
+
+LanguageModel make_toy_language_model() {
+  auto cw = toy_model_weights();
+  return LanguageModel(std::move(cw.first), std::move(cw.second));
 }
 
 bool has_runtime_language_model(const std::string& model_dir) {

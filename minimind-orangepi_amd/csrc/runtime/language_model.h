@@ -25,6 +25,7 @@
 #include <functional>
 #include <memory>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace minimind::model {
@@ -148,6 +149,13 @@ class LanguageModel {
 
 int32_t argmax_token(const std::vector<float>& logits);
 LanguageModel load_runtime_language_model(const std::string& model_dir);
+// The reference's built-in toy model (language_model.cpp:415-470): one layer,
+// hidden 4, 2 query / 1 KV heads of head_dim 2, FFN 8, vocab 8, 16
+// positions, identity projections and fixed embedding / lm_head tables.  The
+// CLI tools fall back to it when no model directory is given.  Its shapes run
+// on the small-model step kernel.
+std::pair<MiniMindConfig, DenseModelWeights> toy_model_weights();
+LanguageModel make_toy_language_model();
 bool has_runtime_language_model(const std::string& model_dir);
 
 }  // namespace minimind::model

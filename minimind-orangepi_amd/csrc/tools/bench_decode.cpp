@@ -1,7 +1,10 @@
 // bench_decode -- prefill/decode timing with the reference's flags and output
 // keys (bench/bench_decode.cpp:117-151):
 //   --model DIR --prompt TEXT --input-tokens 1,2 --tokens N --warmup W
-// decode_steps = tokens - 1 as in the reference.  The reference times
+// decode_steps = tokens - 1 as in the reference.  Without a runtime model
+// directory it times the reference's toy model (bench_decode.cpp:124-126).
+// --kv f16|f32 picks the KV cache dtype (default f16, the reference device
+// cache's).  The reference times
 // forward_next_token calls that each synchronise; --device-loop 1 instead
 // enqueues the steps back to back with the token fed forward on the device
 // and synchronises once (the runtime's throughput mode).
@@ -24,9 +27,9 @@ struct Timing {
 };
 
 Timing run(const LanguageModel& model, const std::vector<int32_t>& prompt, int64_t decode_tokens, bool device_loop,
-           std::vector<int32_t>& generated) {
+           KvCacheDtype kv, std::vector<int32_t>& generated) {
   const int64_t cap = static_cast<int64_t>(prompt.size()) + std::max<int64_t>(decode_tokens, 1);
-  DecoderState state = model.make_state(cap);
+  DecoderState state = model.make_state(cap, kv);
   Timing t;
   const auto p0 = std::chrono::steady_clock::now();
   int32_t next = model.prefill_next_token(prompt, state);
@@ -63,16 +66,20 @@ int main(int argc, char** argv) {
     const int64_t decode_tokens = mmr_cli::int_arg_value(argc, argv, "--tokens", 16);
     const int64_t warmup = mmr_cli::int_arg_value(argc, argv, "--warmup", 1);
     const bool device_loop = mmr_cli::int_arg_value(argc, argv, "--device-loop", 0) != 0;
-    if (model_dir.empty() || !has_runtime_language_model(model_dir)) {
-      std::cerr << "bench_decode: --model must name a runtime model directory\n";
+    const std::string kv_name = mmr_cli::arg_value(argc, argv, "--kv", "f16");
+    if (kv_name != "f16" && kv_name != "f32") {
+      std::cerr << "bench_decode: --kv must be f16 or f32\n";
       return 2;
     }
-    LanguageModel model = load_runtime_language_model(model_dir);
+    const KvCacheDtype kv = kv_name == "f16" ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32;
+    LanguageModel model = !model_dir.empty() && has_runtime_language_model(model_dir)
+                              ? load_runtime_language_model(model_dir)
+                              : make_toy_language_model();
     auto tokens = explicit_tokens.empty() ? std::vector<int32_t>{} : mmr_cli::parse_token_ids(explicit_tokens);
     if (tokens.empty()) tokens = mmr_cli::byte_prompt(prompt, model.config().vocab_size, model.config().bos_token_id);
     std::vector<int32_t> generated;
-    for (int64_t i = 0; i < warmup; ++i) (void)run(model, tokens, decode_tokens, device_loop, generated);
-    const Timing t = run(model, tokens, decode_tokens, device_loop, generated);
+    for (int64_t i = 0; i < warmup; ++i) (void)run(model, tokens, decode_tokens, device_loop, kv, generated);
+    const Timing t = run(model, tokens, decode_tokens, device_loop, kv, generated);
     const double dtps = t.decode_steps == 0 || t.decode_seconds == 0.0 ? 0.0 : t.decode_steps / t.decode_seconds;
     const double ptps = t.prefill_tokens == 0 || t.prefill_seconds == 0.0 ? 0.0 : t.prefill_tokens / t.prefill_seconds;
     std::cout << "prompt_tokens=" << tokens.size() << '\n';

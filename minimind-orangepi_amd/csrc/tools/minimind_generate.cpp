@@ -2,8 +2,8 @@
 // stdout protocol (src/csrc/tools/minimind_generate.cpp:77-111):
 //   --model DIR --prompt TEXT --tokens 1,2,3 --max-new-tokens N [--stream]
 // prints "prompt_tokens: ...", optional "token: N" lines, "generated_tokens: ...".
-// The reference falls back to a hidden-size-4 toy model without --model; the
-// gfx950 runtime has no CPU path, so --model is required here.
+// Without a runtime model directory it runs the reference's built-in toy model
+// (minimind_generate.cpp:84-86), on the GPU like any other model.
 #include "../runtime/language_model.h"
 #include "cli_args.h"
 
@@ -18,12 +18,9 @@ int main(int argc, char** argv) {
     const std::string model_dir = mmr_cli::arg_value(argc, argv, "--model", "");
     const int64_t max_new = mmr_cli::int_arg_value(argc, argv, "--max-new-tokens", 8);
     const bool stream = mmr_cli::has_arg(argc, argv, "--stream");
-    if (model_dir.empty() || !has_runtime_language_model(model_dir)) {
-      std::cerr << "minimind_generate: --model must name a directory with minimind_runtime_config.txt and "
-                   "weights.bin\n";
-      return 2;
-    }
-    LanguageModel model = load_runtime_language_model(model_dir);
+    LanguageModel model = !model_dir.empty() && has_runtime_language_model(model_dir)
+                              ? load_runtime_language_model(model_dir)
+                              : make_toy_language_model();
     auto tokens = explicit_tokens.empty() ? std::vector<int32_t>{} : mmr_cli::parse_token_ids(explicit_tokens);
     if (tokens.empty()) tokens = mmr_cli::byte_prompt(prompt, model.config().vocab_size, model.config().bos_token_id);
     for (int32_t t : tokens)

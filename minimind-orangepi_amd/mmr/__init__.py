@@ -140,6 +140,8 @@ _SIGS = {
     "mmr_model_config": ([VP, C.POINTER(Config)], C.c_int),
     "mmr_model_weight_bytes": ([VP, C.POINTER(U64)], C.c_int),
     "mmr_write_synthetic_model": ([C.c_char_p, C.POINTER(Config), U64, C.c_double, C.c_int], C.c_int),
+    "mmr_model_create_toy": ([C.POINTER(VP)], C.c_int),
+    "mmr_write_toy_model": ([C.c_char_p], C.c_int),
     "mmr_synthesize_normals": ([U64, U64, U64, C.c_double, C.c_int, VP], C.c_int),
     "mmr_synthesize_prompt": ([U64, I64, I64, VP], C.c_int),
     "mmr_state_create": ([VP, I64, C.c_int, C.POINTER(VP)], C.c_int),
@@ -587,6 +589,11 @@ def write_synthetic_model(model_dir, config: Config, seed: int, std: float = 0.0
     check(_lib.mmr_write_synthetic_model(str(model_dir).encode(), C.byref(config), seed, std, int(round_fp16)))
 
 
+def write_toy_model(model_dir) -> None:
+    """The toy model as a runtime directory (the oracle loads it from there)."""
+    check(_lib.mmr_write_toy_model(str(model_dir).encode()))
+
+
 def synthesize_normals(seed: int, first: int, count: int, std: float = 0.02, round_fp16: bool = False) -> np.ndarray:
     out = np.empty(count, np.float32)
     check(_lib.mmr_synthesize_normals(seed, first, count, std, int(round_fp16), _ptr(out)))
@@ -612,6 +619,13 @@ class Model:
     def load(cls, model_dir) -> "Model":
         h = VP()
         check(_lib.mmr_model_load(str(model_dir).encode(), C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def toy(cls) -> "Model":
+        """The reference's built-in toy model (make_toy_language_model)."""
+        h = VP()
+        check(_lib.mmr_model_create_toy(C.byref(h)))
         return cls(h.value)
 
     @classmethod

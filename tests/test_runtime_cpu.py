@@ -143,11 +143,13 @@ def test_fp16_codec_matches_numpy(mmr):
     np.testing.assert_array_equal(mmr.f16_to_f32(h), h.view(np.float16).astype(np.float32))
 
 
-def test_cli_tools_require_model(tmp_path):
-    for tool in ("bench_decode", "minimind_generate"):
-        exe = ROOT / "minimind-orangepi_amd" / "bin" / tool
-        proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
-        assert proc.returncode == 2 and "--model" in proc.stderr
+def test_cli_tools_reject_bad_flags_before_touching_a_device(tmp_path):
+    # argument errors are reported before any model (or GPU) is set up
+    bindir = ROOT / "minimind-orangepi_amd" / "bin"
+    proc = subprocess.run([str(bindir / "bench_decode"), "--kv", "f64"], capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 2 and "--kv" in proc.stderr
+    proc = subprocess.run([str(bindir / "check_prefill_consistency")], capture_output=True, text=True, timeout=60)
+    assert proc.returncode == 1 and "usage: check_prefill_consistency" in proc.stderr
 
 
 def test_op_argument_checks_need_no_device(mmr):
