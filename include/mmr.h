@@ -144,6 +144,9 @@ int mmr_rope_table_destroy(mmr_rope_table* table);
 int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, int kv_dtype, mmr_kv_cache** out);
 int mmr_kv_cache_destroy(mmr_kv_cache* cache);
 int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values);
+/* Shape of a cache (any output pointer may be NULL). */
+int mmr_kv_cache_info(const mmr_kv_cache* cache, int64_t* kv_heads, int64_t* head_dim, int64_t* capacity,
+                      int* kv_dtype);
 /* Rows allocated per KV head: capacity rounded up to the attention tile
  * (64 tokens, 32 for head_dim 128); keys/values are [kv_head][rows][head_dim]. */
 int mmr_kv_cache_rows(const mmr_kv_cache* cache, int64_t* rows);
@@ -193,6 +196,34 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
                                const mmr_rope_table* rope, const int32_t* position, mmr_kv_cache* cache,
                                int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out, void* workspace,
                                size_t workspace_bytes, int splits, int32_t* error, mmr_stream_t stream);
+
+/* ---- host-vector twins and availability probes: cube_matvec,
+ * cube_matmul, cube_matvec_argmax, cube_*_available (ascend_matmul.h:116-133,
+ * ascend_matmul.cpp:513-693) and custom_ops_available, custom_attention,
+ * custom_prefill_attention, custom_attention_cached (ascend_custom_ops.h:13,
+ * 33-55, ascend_custom_ops.cpp:333-530).  Every pointer is host memory; each
+ * call uploads, runs the device op, waits and copies back (so these
+ * allocate and synchronise, as the reference's do).  Matrices are fp32
+ * [rows][cols] rounded to fp16 on upload; inputs, outputs and the caches
+ * stay fp32 (the reference rounds them to fp16).  keys/values are in the
+ * reference layout [token][kv_head][head_dim]; key/value of the cached form
+ * are one token's [kv_head][head_dim], written at row tokens - 1.  The cache
+ * argument may be *cache == NULL (a new fp32 cache of at least 2048 tokens
+ * is created), a cache of another shape (replaced), or a cache too short
+ * (grown, rows kept; the reference starts an empty one).  The probes return
+ * 1 when a gfx950 device is visible, else 0. */
+int mmr_cube_matvec_available(void);
+int mmr_cube_matmul_available(void);
+int mmr_custom_ops_available(void);
+int mmr_cube_matvec(const float* matrix, int64_t rows, int64_t cols, const float* input, float* out);
+int mmr_cube_matmul(const float* matrix, int64_t rows, int64_t cols, const float* input, int64_t batch, float* out);
+int mmr_cube_matvec_argmax(const float* matrix, int64_t rows, int64_t cols, const float* input, int32_t* token);
+int mmr_custom_attention(const float* query, const float* keys, const float* values, int64_t tokens, int64_t q_heads,
+                         int64_t kv_heads, int64_t head_dim, float* out);
+int mmr_custom_prefill_attention(const float* query, const float* keys, const float* values, mmr_kv_cache** cache,
+                                 int64_t seq_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out);
+int mmr_custom_attention_cached(const float* query, const float* key, const float* value, mmr_kv_cache** cache,
+                                int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out);
 
 /* ---- one decoder layer: run_dense_decoder_layer_device (decoder_layer.h:50-80,
  * decoder_layer.cpp:617-659) and run_dense_decoder_layer (decoder_layer.cpp:312-407)

@@ -30,7 +30,8 @@ COMMON = ["-std=c++17", "-O3", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{ROOT
 # Packed FP32 (v_pk_*_f32) is disabled for all device code.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
-SOURCES = sorted(CSRC.glob("kernels/*.hip")) + sorted(CSRC.glob("runtime/*.cpp")) + [CSRC / "capi.cpp"]
+SOURCES = sorted(CSRC.glob("kernels/*.hip")) + sorted(CSRC.glob("runtime/*.cpp")) + [CSRC / "capi.cpp",
+                                                                                      CSRC / "host_ops.cpp"]
 TOOLS = {name: CSRC / "tools" / f"{name}.cpp"
          for name in ("bench_decode", "minimind_generate", "check_prefill_consistency")}
 

@@ -5,6 +5,7 @@
 #include "../../include/mmr.h"
 
 #include "kernels/kernels.h"
+#include "host_ops.h"
 #include "runtime/decoder_layer.h"
 #include "runtime/device.h"
 #include "runtime/language_model.h"
@@ -411,6 +412,17 @@ int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values) {
   });
 }
 
+int mmr_kv_cache_info(const mmr_kv_cache* cache, int64_t* kv_heads, int64_t* head_dim, int64_t* capacity,
+                      int* kv_dtype) {
+  return guarded([&] {
+    require(cache, "null argument");
+    if (kv_heads) *kv_heads = cache->kv_heads;
+    if (head_dim) *head_dim = cache->head_dim;
+    if (capacity) *capacity = cache->capacity;
+    if (kv_dtype) *kv_dtype = cache->dtype;
+  });
+}
+
 int mmr_kv_cache_rows(const mmr_kv_cache* cache, int64_t* rows) {
   return guarded([&] {
     require(cache && rows, "null argument");
@@ -638,6 +650,41 @@ int mmr_prefill_qkv_rows(const float* qkv, const float* q_norm, const float* k_n
     hip(mmr::launch_qkv_rows(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32, as_stream(stream)),
         "qkv rows launch");
   });
+}
+
+int mmr_cube_matvec_available(void) { return cube_matvec_available() ? 1 : 0; }
+int mmr_cube_matmul_available(void) { return cube_matmul_available() ? 1 : 0; }
+int mmr_custom_ops_available(void) { return custom_ops_available() ? 1 : 0; }
+
+int mmr_cube_matvec(const float* matrix, int64_t rows, int64_t cols, const float* input, float* out) {
+  return guarded([&] { host_matmul(matrix, rows, cols, input, 1, out); });
+}
+
+int mmr_cube_matmul(const float* matrix, int64_t rows, int64_t cols, const float* input, int64_t batch, float* out) {
+  return guarded([&] { host_matmul(matrix, rows, cols, input, batch, out); });
+}
+
+int mmr_cube_matvec_argmax(const float* matrix, int64_t rows, int64_t cols, const float* input, int32_t* token) {
+  return guarded([&] {
+    require(token, "null argument");
+    *token = host_matvec_argmax(matrix, rows, cols, input);
+  });
+}
+
+int mmr_custom_attention(const float* query, const float* keys, const float* values, int64_t tokens, int64_t q_heads,
+                         int64_t kv_heads, int64_t head_dim, float* out) {
+  return guarded([&] { host_attention(query, keys, values, tokens, q_heads, kv_heads, head_dim, out); });
+}
+
+int mmr_custom_prefill_attention(const float* query, const float* keys, const float* values, mmr_kv_cache** cache,
+                                 int64_t seq_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out) {
+  return guarded(
+      [&] { host_prefill_attention(query, keys, values, cache, seq_len, q_heads, kv_heads, head_dim, out); });
+}
+
+int mmr_custom_attention_cached(const float* query, const float* key, const float* value, mmr_kv_cache** cache,
+                                int64_t tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim, float* out) {
+  return guarded([&] { host_attention_cached(query, key, value, cache, tokens, q_heads, kv_heads, head_dim, out); });
 }
 
 int mmr_layer_weights_create(const mmr_config* config, const float* input_norm, const float* post_attention_norm,

@@ -113,6 +113,16 @@ _SIGS = {
     "mmr_kv_cache_destroy": ([VP], C.c_int),
     "mmr_kv_cache_data": ([VP, C.POINTER(VP), C.POINTER(VP)], C.c_int),
     "mmr_kv_cache_rows": ([VP, C.POINTER(I64)], C.c_int),
+    "mmr_kv_cache_info": ([VP, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64), C.POINTER(C.c_int)], C.c_int),
+    "mmr_cube_matvec_available": ([], C.c_int),
+    "mmr_cube_matmul_available": ([], C.c_int),
+    "mmr_custom_ops_available": ([], C.c_int),
+    "mmr_cube_matvec": ([VP, I64, I64, VP, VP], C.c_int),
+    "mmr_cube_matmul": ([VP, I64, I64, VP, I64, VP], C.c_int),
+    "mmr_cube_matvec_argmax": ([VP, I64, I64, VP, P_I32], C.c_int),
+    "mmr_custom_attention": ([VP, VP, VP, I64, I64, I64, I64, VP], C.c_int),
+    "mmr_custom_prefill_attention": ([VP, VP, VP, C.POINTER(VP), I64, I64, I64, I64, VP], C.c_int),
+    "mmr_custom_attention_cached": ([VP, VP, VP, C.POINTER(VP), I64, I64, I64, I64, VP], C.c_int),
     "mmr_decode_qkv_postprocess": ([VP, VP, VP, VP, I64, I64, I64, I64, I64, VP, F32, VP, VP], C.c_int),
     "mmr_attention_workspace_size": ([I64, I64, I64, C.c_int], SZ),
     "mmr_attention_from_cache": ([VP, VP, I64, I64, I64, I64, VP, VP, SZ, C.c_int, VP], C.c_int),
@@ -554,6 +564,92 @@ class LayerWeights:
             self.free()
         except Exception:
             pass
+
+
+# ------------------------------------------------- host-vector twins ----
+
+def cube_matvec_available() -> bool:
+    return bool(_lib.mmr_cube_matvec_available())
+
+
+def cube_matmul_available() -> bool:
+    return bool(_lib.mmr_cube_matmul_available())
+
+
+def custom_ops_available() -> bool:
+    return bool(_lib.mmr_custom_ops_available())
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def cube_matmul(matrix, inputs) -> np.ndarray:
+    """inputs [batch][cols] (or [cols]) @ matrix[rows][cols]^T through mmr_cube_matmul."""
+    w, x = _f32(matrix), _f32(inputs)
+    rows, cols = w.shape
+    batch = 1 if x.ndim == 1 else x.shape[0]
+    out = np.empty((batch, rows), np.float32)
+    check(_lib.mmr_cube_matmul(_ptr(w), rows, cols, _ptr(x), batch, _ptr(out)))
+    return out[0] if x.ndim == 1 else out
+
+
+def cube_matvec(matrix, x) -> np.ndarray:
+    w, v = _f32(matrix), _f32(x)
+    out = np.empty(w.shape[0], np.float32)
+    check(_lib.mmr_cube_matvec(_ptr(w), w.shape[0], w.shape[1], _ptr(v), _ptr(out)))
+    return out
+
+
+def cube_matvec_argmax(matrix, x) -> int:
+    w, v = _f32(matrix), _f32(x)
+    t = C.c_int32(0)
+    check(_lib.mmr_cube_matvec_argmax(_ptr(w), w.shape[0], w.shape[1], _ptr(v), C.byref(t)))
+    return int(t.value)
+
+
+def custom_attention(query, keys, values, tokens, q_heads, kv_heads, head_dim) -> np.ndarray:
+    q, k, v = _f32(query), _f32(keys), _f32(values)
+    out = np.empty(q_heads * head_dim, np.float32)
+    check(_lib.mmr_custom_attention(_ptr(q), _ptr(k), _ptr(v), tokens, q_heads, kv_heads, head_dim, _ptr(out)))
+    return out
+
+
+class HostAttentionCache:
+    """The cache handle the host-vector attention twins create, replace or grow."""
+
+    def __init__(self):
+        self.ptr = VP()
+
+    def info(self) -> tuple[int, int, int, int]:
+        a, b, c, d = C.c_int64(), C.c_int64(), C.c_int64(), C.c_int()
+        check(_lib.mmr_kv_cache_info(self.ptr, C.byref(a), C.byref(b), C.byref(c), C.byref(d)))
+        return a.value, b.value, c.value, d.value
+
+    def __del__(self):
+        try:
+            if self.ptr.value:
+                _lib.mmr_kv_cache_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+def custom_prefill_attention(query, keys, values, cache: HostAttentionCache, seq_len, q_heads, kv_heads,
+                             head_dim) -> np.ndarray:
+    q, k, v = _f32(query), _f32(keys), _f32(values)
+    out = np.empty(seq_len * q_heads * head_dim, np.float32)
+    check(_lib.mmr_custom_prefill_attention(_ptr(q), _ptr(k), _ptr(v), C.byref(cache.ptr), seq_len, q_heads,
+                                            kv_heads, head_dim, _ptr(out)))
+    return out
+
+
+def custom_attention_cached(query, key, value, cache: HostAttentionCache, tokens, q_heads, kv_heads,
+                            head_dim) -> np.ndarray:
+    q, k, v = _f32(query), _f32(key), _f32(value)
+    out = np.empty(q_heads * head_dim, np.float32)
+    check(_lib.mmr_custom_attention_cached(_ptr(q), _ptr(k), _ptr(v), C.byref(cache.ptr), tokens, q_heads,
+                                           kv_heads, head_dim, _ptr(out)))
+    return out
 
 
 # ---------------------------------------------------------------- model ----

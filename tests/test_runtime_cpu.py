@@ -152,6 +152,13 @@ def test_cli_tools_reject_bad_flags_before_touching_a_device(tmp_path):
     assert proc.returncode == 1 and "usage: check_prefill_consistency" in proc.stderr
 
 
+def test_availability_probes_without_a_device(mmr):
+    # this container has no GPU: the probes answer 0 instead of failing
+    assert mmr.device_count() == 0 or mmr.custom_ops_available()
+    if mmr.device_count() == 0:
+        assert not mmr.cube_matvec_available() and not mmr.cube_matmul_available() and not mmr.custom_ops_available()
+
+
 def test_op_argument_checks_need_no_device(mmr):
     # shape validation happens on the host before any launch
     with pytest.raises(mmr.InvalidArgument, match="multiple of 8"):
