@@ -287,21 +287,33 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
     gate_up: the GEMV (4096 x 768 fp16, RMSNorm prologue, SwiGLU epilogue, the
     step's launch plan: 32-lane groups, two rows per group) through the C ABI
     over a 16-copy weight rotation like the 16 layers of the step.
-    attention: the step's own attention kernel (q/k norm + RoPE + KV append +
-    attention partials) on the MiniMind2 decode state after the 512-token
-    prompt and 255 steps (768 keys, fp16 KV), cycling over the 16 layers'
-    caches (mmr_launch_step_kernel)."""
+    attention: the decode step's attention kernel (q/k norm + RoPE + KV append
+    + split partials, attention_head_kernel at 768 keys, 16 splits, fp16 KV)
+    through mmr_decode_attention_fused, cycling over 16 caches like the 16
+    layers of a step."""
     H, F, layers = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"], MINIMIND2["num_hidden_layers"]
     rng = np.random.default_rng(3)
     if kernel == "attention":
-        model = mmr.Model.synthetic(mmr.make_config(**MINIMIND2), 0, 0.02, True)
-        st = model.make_state(PROMPT_LEN + 264, mmr.KV_F16)
-        st.enqueue_prefill(mmr.synthesize_prompt(1, PROMPT_LEN, MINIMIND2["vocab_size"]))
-        st.enqueue_decode(255)
-        st.synchronize()
-        n_keys = st.position + 1
-        st.launch_step_kernel(mmr.KERNEL_ATTENTION, 0, launches)
-        stream = mmr.Stream(st.stream)
+        hq, hkv, d = MINIMIND2["num_attention_heads"], MINIMIND2["num_key_value_heads"], MINIMIND2["head_dim"]
+        n_keys = PROMPT_LEN + 256
+        caches = []
+        for _ in range(layers):
+            c = mmr.KvCache(hkv, d, n_keys, mmr.KV_F16)
+            c.upload(rng.standard_normal((hkv, c.rows, d)).astype(np.float16),
+                     rng.standard_normal((hkv, c.rows, d)).astype(np.float16))
+            caches.append(c)
+        rope = mmr.RopeTable(n_keys, d, MINIMIND2["rope_theta"])
+        qkv = mmr.DeviceArray.from_numpy(rng.standard_normal((hq + 2 * hkv) * d).astype(np.float32))
+        ones = mmr.DeviceArray.from_numpy(np.ones(d, np.float32))
+        pos = mmr.DeviceArray.from_numpy(np.array([n_keys - 1], np.int32))
+        err = mmr.DeviceArray(1, np.int32, zero=True)
+        splits = 16  # the decode step's split bucket at 768 keys (64-token tiles)
+        ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, splits), np.uint8)
+        out = mmr.DeviceArray(hq * d, np.float32)
+        stream = mmr.Stream()
+        for i in range(launches):
+            mmr.decode_attention_fused(qkv, ones, ones, MINIMIND2["rms_norm_eps"], rope, pos, caches[i % layers], hq,
+                                       hkv, d, out, ws, splits, err, stream=stream)
         stream.synchronize()
         alg = kernel_bytes(MINIMIND2, "attention", n_keys, 2)
     else:
