@@ -226,7 +226,8 @@ bool gemm_swiglu_supported(int m, int n, int k);
 // (the tiled path; the few-rows path reads fp32 A).
 bool gemm_presplit_supported(int m, int n, int k);
 // Whether the SwiGLU epilogue can write act pre-split (act_split) for this
-// shape: 64 x 128 tiles (a block holds 64 whole act columns of its rows) and
+// shape: unsplit tiles 64 wide or wider (64 x 128, 64 x 64 or 32 x 64: a block holds
+// whole 32-column act chunks of its rows) and
 // n a multiple of 64.
 bool gemm_swiglu_split_supported(int m, int n, int k);
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);

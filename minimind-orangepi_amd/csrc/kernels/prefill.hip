@@ -985,7 +985,7 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
                  (g.a_chunk == kSplitChunkFine && (g.swiglu || g.residual))))
     return hipErrorInvalidValue;
   if (!g.a_hi && !g.a) return hipErrorInvalidValue;
-  // act pre-split: the SwiGLU epilogue on 64 x 128 tiles, all three planes,
+  // act pre-split: the SwiGLU epilogue on unsplit 64 x 128, 64 x 64 or 32 x 64 tiles, all three planes,
   // 8-byte rows.
   if (g.act_split.hi && (!g.swiglu || !g.act_split.lo || !g.act_split.inv || g.ldc % 4 != 0 ||
                          !gemm_swiglu_split_supported(g.m, g.n, g.k)))

@@ -191,3 +191,32 @@ def test_gemm_prefill_on_used_state_and_fp16_cache(gpu, monkeypatch):
     n = tok.position + 1
     assert gem.read_sequence(0, n).tolist() == tok.read_sequence(0, n).tolist()
     assert rel_err(gem.read_logits(), tok.read_logits()) < 1e-4
+
+
+@pytest.mark.parametrize("prompt_len", [256, 512])
+def test_gemm_prefill_swiglu_presplit_tilings(gpu, monkeypatch, prompt_len):
+    # hidden 256 with FFN 1536 (gate_up n = 3072, k = 256): at 256 rows the
+    # tiling chooser gives 32 x 64 unsplit tiles, at 512 rows 64 x 64 from its
+    # block-target loop; both write the SwiGLU output pre-split for the down
+    # GEMM.  GEMM prefill against the same prompt fed token by token.
+    mmr = gpu
+    print(f"[case] prefill swiglu tiling rows={prompt_len}", flush=True)
+    cfg = mmr.make_config(hidden_size=256, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                          head_dim=64, intermediate_size=1536, vocab_size=512, max_position_embeddings=1024,
+                          rms_norm_eps=1e-5, rope_theta=1e6, tie_word_embeddings=0)
+    m = mmr.Model.synthetic(cfg, 13, 0.02, True)
+    rng = np.random.default_rng(prompt_len)
+    prompt = [int(t) for t in rng.integers(0, 512, prompt_len)]
+    monkeypatch.setenv("MMR_PREFILL_TOKENWISE", "1")
+    tok = m.make_state(prompt_len + 16)
+    monkeypatch.delenv("MMR_PREFILL_TOKENWISE")
+    gem = m.make_state(prompt_len + 16)
+    for st in (tok, gem):
+        st.enqueue_prefill(prompt)
+        st.synchronize()
+    assert rel_err(gem.read_logits(), tok.read_logits()) < 1e-4
+    for st in (tok, gem):
+        st.enqueue_decode(12)
+        st.synchronize()
+    n = prompt_len + 13
+    assert gem.read_sequence(0, n).tolist() == tok.read_sequence(0, n).tolist()
