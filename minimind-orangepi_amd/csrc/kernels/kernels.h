@@ -211,6 +211,9 @@ struct GemmArgs {
   const uint16_t* a_lo = nullptr;
   const float* a_inv = nullptr;
   int a_chunk = kSplitChunk;
+  // Keep the call on the register-staged kernel even where the direct-to-LDS
+  // one applies (both compute the full product; a comparison switch).
+  bool register_staged = false;
   // SwiGLU epilogue only: act as SplitPlanes instead of into c (c unused),
   // with kSplitChunkFine chunks (planes [m][ldc], inv [m][n / 2 / 32]);
   // needs the tiling gemm_swiglu_split_supported accepts.

@@ -212,15 +212,131 @@ struct GemmStage {
 // 175-182), the pair meeting through one lane exchange.
 constexpr int kGemmEpiStore = 0, kGemmEpiResidual = 1, kGemmEpiSwiGlu = 2;
 
+// Epilogue shared by the GEMM kernels: the block's accumulators (BM x BN, 2 x
+// 2 waves of 16 x 16 fragments; lane holds rows 4 (lane / 16) + {0..3} of
+// column lane % 16 of each fragment) go to C (store / + residual), or through
+// SwiGLU to act, optionally pre-split.  act_scratch: LDS the K loop no longer
+// uses, at least BM x (BN / 2 + 4) floats.
+template <int BM, int BN, int kEpi>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x4 (&acc)[BM / 32][BN / 32], float* out,
+                                              float* act_scratch, int m0, int n0, int tid) {
+  constexpr bool kResidual = kEpi == kGemmEpiResidual;
+  constexpr int TM = BM / 32, TN = BN / 32;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  // Output fragment: lane holds rows 4 * (lane / 16) + {0..3} of column
+  // lane % 16 of each 16 x 16 tile.  Residual loads are issued together
+  // (clamped indices), then the in-range elements are stored.
+  float res[TM][TN][4];
+  if constexpr (kResidual) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = min(n0 + wn * (BN / 2) + j * 16 + lane % 16, g.n - 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = min(m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r, g.m - 1);
+          res[i][j][r] = g.residual[static_cast<int64_t>(row) * g.ldc + col];
+        }
+      }
+  }
+  // SwiGLU: even lanes hold gate column 2i, their odd neighbours up column
+  // 2i + 1 (one DPP exchange).
+  auto swiglu_act = [](float v) {
+    const float u = dpp_move<dpp::kQuadXor1>(v);
+    return (v / (1.0f + expf(-v))) * u;
+  };
+  bool act_to_lds = false;
+  constexpr bool kActSplit = kEpi == kGemmEpiSwiGlu && (BN == 128 || BN == 64);  // whole 32-column act chunks
+  constexpr int kActLd = BN / 2 + 4;  // floats per row of the act tile in LDS
+  if constexpr (kActSplit) act_to_lds = g.act_split.hi != nullptr;
+  if (act_to_lds) {
+    // act tile for the pre-split writer below: [BM][BN / 2] (padded) over the
+    // W staging buffer, which the K loop no longer reads.  Rows past m hold
+    // values of clamped rows; the writer skips them.
+    float* act_s = act_scratch;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float act = swiglu_act(acc[i][j][r]);
+          if ((lane & 1) == 0)
+            act_s[(wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r) * kActLd + (wn * (BN / 2) + j * 16 + lane % 16) / 2] =
+                act;
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
+          const float v = acc[i][j][r];
+          if constexpr (kEpi == kGemmEpiSwiGlu) {
+            const float act = swiglu_act(v);
+            if ((lane & 1) == 0 && row < g.m && col < g.n) out[static_cast<int64_t>(row) * g.ldc + col / 2] = act;
+          } else if (row < g.m && col < g.n) {
+            out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
+          }
+        }
+      }
+  }
+  if constexpr (kActSplit) {
+    if (act_to_lds) {
+      // act pre-split per 32 columns (the down GEMM's A): thread = 4
+      // consecutive columns of one row, the 8 threads of a chunk reduce its
+      // max together, then write 8-byte runs of both planes.
+      __syncthreads();
+      const float* act_s = act_scratch;
+      const int nkc = g.n / 2 / kSplitChunkFine;
+#pragma unroll
+      for (int p = 0; p < BM * (BN / 2) / 4 / kGemmThreads; ++p) {
+        const int idx = tid + p * kGemmThreads;
+        const int r = idx / (BN / 8), c4 = idx % (BN / 8);
+        const int row = m0 + r, col = n0 / 2 + c4 * 4;
+        const bool ok = row < g.m && col < g.n / 2;
+        const float4 v = ok ? *reinterpret_cast<const float4*>(&act_s[r * kActLd + c4 * 4])
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float mx =
+            group_max<kSplitChunkFine / 4>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        int e = 0;
+        frexpf(mx, &e);  // e = 0 for a zero chunk
+        e = max(e, -100);
+        const float sc = ldexpf(1.0f, 15 - e);
+        const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+        f16x4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hi[j] = static_cast<_Float16>(x[j]);
+          lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(hi[j]));
+        }
+        if (ok) {
+          const int64_t off = static_cast<int64_t>(row) * g.ldc + col;
+          *reinterpret_cast<f16x4*>(g.act_split.hi + off) = hi;
+          *reinterpret_cast<f16x4*>(g.act_split.lo + off) = lo;
+          if (c4 % (kSplitChunkFine / 4) == 0)
+            g.act_split.inv[static_cast<int64_t>(row) * nkc + col / kSplitChunkFine] = ldexpf(1.0f, e - 15);
+        }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int kEpi, int kMode>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm_f16w_kernel(GemmArgs g) {
-  constexpr bool kResidual = kEpi == kGemmEpiResidual;
   constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 MFMA tiles per wave
   static_assert(GemmStage<BM, BN>::kA >= 1 && GemmStage<BM, BN>::kB >= 1, "tile too small for the block");
   __shared__ __align__(16) _Float16 Ah[BM][kGemmLDH];
   __shared__ __align__(16) _Float16 Al[BM][kGemmLDH];
   __shared__ __align__(16) _Float16 Bs[BN][kGemmLDH];
   __shared__ __align__(16) float inv_s[BM];
+  static_assert(BM * (BN / 2 + 4) * 4 <= BN * kGemmLDH * 2, "act tile exceeds the W buffer");
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = tid / kWave;
@@ -286,108 +402,177 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)
     __syncthreads();
   }
 
-  // Output fragment: lane holds rows 4 * (lane / 16) + {0..3} of column
-  // lane % 16 of each 16 x 16 tile.  Residual loads are issued together
-  // (clamped indices), then the in-range elements are stored.
-  float res[TM][TN][4];
-  if constexpr (kResidual) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = min(n0 + wn * (BN / 2) + j * 16 + lane % 16, g.n - 1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = min(m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r, g.m - 1);
-          res[i][j][r] = g.residual[static_cast<int64_t>(row) * g.ldc + col];
-        }
-      }
-  }
-  // SwiGLU: even lanes hold gate column 2i, their odd neighbours up column
-  // 2i + 1 (one DPP exchange).
-  auto swiglu_act = [](float v) {
-    const float u = dpp_move<dpp::kQuadXor1>(v);
-    return (v / (1.0f + expf(-v))) * u;
-  };
-  bool act_to_lds = false;
-  constexpr bool kActSplit = kEpi == kGemmEpiSwiGlu && (BN == 128 || BN == 64);  // whole 32-column act chunks
-  constexpr int kActLd = BN / 2 + 4;  // floats per row of the act tile in LDS
-  if constexpr (kActSplit) act_to_lds = g.act_split.hi != nullptr;
-  if (act_to_lds) {
-    // act tile for the pre-split writer below: [BM][BN / 2] (padded) over the
-    // W staging buffer, which the K loop no longer reads.  Rows past m hold
-    // values of clamped rows; the writer skips them.
-    float* act_s = reinterpret_cast<float*>(&Bs[0][0]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float act = swiglu_act(acc[i][j][r]);
-          if ((lane & 1) == 0)
-            act_s[(wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r) * kActLd + (wn * (BN / 2) + j * 16 + lane % 16) / 2] =
-                act;
-        }
+  gemm_epilogue<BM, BN, kEpi>(g, acc, out, reinterpret_cast<float*>(&Bs[0][0]), m0, n0, tid);
+}
+
+// ---- GEMM with direct global->LDS loads (pre-split A, K % 64 == 0) ----
+// The same product as gemm_f16w_kernel with A given as fp16 hi/lo planes,
+// but the tiles never pass through registers: every 16-byte piece of a K
+// tile goes from global memory straight into LDS (global_load_lds_dwordx4),
+// and three 64-wide K stages are in flight, so a block keeps up to two tiles
+// loading while it multiplies the third (the register-staged kernel has one).
+// The loads write 64 lanes x 16 bytes contiguously; the LDS image of a stage
+// is [rows][8 chunks of 8 halves] with chunk kc of row r at position
+// r * 8 + (kc ^ ((r >> 1) & 7)), so the matrix cores' fragment reads (16
+// lanes = 16 rows at one chunk) touch 16 distinct 16-byte bank groups.  The
+// row scales (one per row and 128 columns, or per 32 columns) come through
+// LDS the same way and are applied per stage, or per 32-k step.
+constexpr int kDmaBK = 64;      // K per stage
+constexpr int kDmaStages = 2;
+constexpr int kDmaRowChunks = kDmaBK / 8;
+
+__device__ __forceinline__ int dma_pos(int r, int kc) { return r * kDmaRowChunks + (kc ^ ((r >> 1) & 7)); }
+
+using lds_byte = __attribute__((address_space(3))) char;
+
+// One wave-wide direct load: lane l's `bytes` (16 or 4) at gsrc land in LDS
+// at wave_base + l * bytes.  M0 holds the wave's LDS base (a write of M0
+// needs one wait state before an LDS-direct load reads it: s_nop); the
+// instruction is issued from inline assembly so that the compiler, which does
+// not see the LDS write, inserts no wait for it: the kernel waits with
+// explicit vmcnt.
+template <int kBytes>
+__device__ __forceinline__ void dma_load(const void* gsrc, const void* wave_base) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_byte*)wave_base)));
+  if constexpr (kBytes == 16) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(m0) : "memory");
   } else {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
-          const float v = acc[i][j][r];
-          if constexpr (kEpi == kGemmEpiSwiGlu) {
-            const float act = swiglu_act(v);
-            if ((lane & 1) == 0 && row < g.m && col < g.n) out[static_cast<int64_t>(row) * g.ldc + col / 2] = act;
-          } else if (row < g.m && col < g.n) {
-            out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
-          }
-        }
-      }
+    static_assert(kBytes == 4, "16- or 4-byte loads");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dword %0, off" : : "v"(gsrc), "s"(m0) : "memory");
   }
-  if constexpr (kActSplit) {
-    if (act_to_lds) {
-      // act pre-split per 32 columns (the down GEMM's A): thread = 4
-      // consecutive columns of one row, the 8 threads of a chunk reduce its
-      // max together, then write 8-byte runs of both planes.
-      static_assert(BM * kActLd * 4 <= BN * kGemmLDH * 2, "act tile exceeds the W buffer");
-      __syncthreads();
-      const float* act_s = reinterpret_cast<const float*>(&Bs[0][0]);
-      const int nkc = g.n / 2 / kSplitChunkFine;
+}
+
+// Wait until at most kPending of this thread's vector-memory operations are
+// outstanding, then meet the other waves at a barrier.
+template <int kPending>
+__device__ __forceinline__ void dma_wait_barrier() {
+  static_assert(kPending >= 0 && kPending < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" : : "n"(kPending) : "memory");
+}
+
+template <int BM, int BN, int kEpi, int kGran, int kStages = kDmaStages>
+__global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
+  static_assert(kGran == kSplitChunk || kGran == kSplitChunkFine, "scale granularity");
+  constexpr int TM = BM / 32, TN = BN / 32;
+  constexpr int kScales = kGran >= kDmaBK ? 1 : kDmaBK / kGran;  // scale values per row per stage
+  constexpr int kAWaveLoads = BM * kDmaRowChunks / kWave / 4;  // per plane, per wave, per stage
+  constexpr int kBWaveLoads = BN * kDmaRowChunks / kWave / 4;
+  static_assert(kAWaveLoads >= 1 && kBWaveLoads >= 1 && BM <= kWave, "tile shape");
+  // Vector-memory operations one thread issues per stage (every wave the same).
+  constexpr int kStageOps = 2 * kAWaveLoads + kBWaveLoads + kScales;
+  static_assert(kStages >= 2, "at least double buffering");
+  __shared__ __align__(16) _Float16 Ah[kStages][BM * kDmaBK];
+  __shared__ __align__(16) _Float16 Al[kStages][BM * kDmaBK];
+  __shared__ __align__(16) _Float16 Bs[kStages][BN * kDmaBK];
+  // Scales per stage, each wave its own copy (uniform op counts): [wave][s][row]
+  __shared__ __align__(16) float Sc[kStages][4][kScales][kWave];
+  static_assert(BM * (BN / 2 + 4) * 4 <= kStages * BN * kDmaBK * 2, "act tile exceeds the W stages");
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int nk = g.k / kDmaBK;
+  const int per = (nk + static_cast<int>(gridDim.z) - 1) / static_cast<int>(gridDim.z);
+  const int kt0 = static_cast<int>(blockIdx.z) * per, kt1 = min(kt0 + per, nk);
+  float* out = g.c + static_cast<int64_t>(blockIdx.z) * g.split_stride;
+  const int nsc = (g.k + kGran - 1) / kGran;  // scales per row of a_inv
+
+  // Stage kt into buffer buf.  Rows past m (n) load a clamped row: in bounds,
+  // never stored.
+  auto issue = [&](int kt, int buf) {
+    const int k0 = kt * kDmaBK;
 #pragma unroll
-      for (int p = 0; p < BM * (BN / 2) / 4 / kGemmThreads; ++p) {
-        const int idx = tid + p * kGemmThreads;
-        const int r = idx / (BN / 8), c4 = idx % (BN / 8);
-        const int row = m0 + r, col = n0 / 2 + c4 * 4;
-        const bool ok = row < g.m && col < g.n / 2;
-        const float4 v = ok ? *reinterpret_cast<const float4*>(&act_s[r * kActLd + c4 * 4])
-                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const float mx =
-            group_max<kSplitChunkFine / 4>(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        int e = 0;
-        frexpf(mx, &e);  // e = 0 for a zero chunk
-        e = max(e, -100);
-        const float sc = ldexpf(1.0f, 15 - e);
-        const float x[4] = {v.x * sc, v.y * sc, v.z * sc, v.w * sc};
-        f16x4 hi, lo;
+    for (int j = 0; j < kAWaveLoads; ++j) {
+      const int i = wave + 4 * j;  // wave-wide load i fills chunks [64 i, 64 i + 64)
+      const int c = i * kWave + lane;
+      const int r = c / kDmaRowChunks, kc = (c % kDmaRowChunks) ^ ((r >> 1) & 7);
+      const int64_t off = static_cast<int64_t>(min(m0 + r, g.m - 1)) * g.lda + k0 + kc * 8;
+      dma_load<16>(g.a_hi + off, &Ah[buf][i * kWave * 8]);
+      dma_load<16>(g.a_lo + off, &Al[buf][i * kWave * 8]);
+    }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          hi[j] = static_cast<_Float16>(x[j]);
-          lo[j] = static_cast<_Float16>(x[j] - static_cast<float>(hi[j]));
+    for (int j = 0; j < kBWaveLoads; ++j) {
+      const int i = wave + 4 * j;
+      const int c = i * kWave + lane;
+      const int r = c / kDmaRowChunks, kc = (c % kDmaRowChunks) ^ ((r >> 1) & 7);
+      dma_load<16>(g.w + static_cast<int64_t>(min(n0 + r, g.n - 1)) * g.k + k0 + kc * 8, &Bs[buf][i * kWave * 8]);
+    }
+#pragma unroll
+    for (int sidx = 0; sidx < kScales; ++sidx) {
+      const int row = min(m0 + min(lane, BM - 1), g.m - 1);
+      dma_load<4>(g.a_inv + static_cast<int64_t>(row) * nsc + (k0 + sidx * kGran) / kGran, &Sc[buf][wave][sidx][0]);
+    }
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (kt0 < kt1) {  // a split past the end of K writes zeros
+    // Stages kt0 .. kt0 + kStages - 2 in flight before the first multiply
+    // (past the last K tile the last one is loaded again: in bounds, unused).
+#pragma unroll
+    for (int p = 0; p < kStages - 1; ++p) issue(min(kt0 + p, kt1 - 1), p);
+    for (int kt = kt0; kt < kt1; ++kt) {
+      const int it = kt - kt0, buf = it % kStages;
+      // Stage kt has landed (the kStages - 2 later ones may still be loading),
+      // and every wave is done with the buffer refilled next (read in
+      // iteration it - 1).
+      dma_wait_barrier<(kStages - 2) * kStageOps>();
+      issue(min(kt + kStages - 1, kt1 - 1), (it + kStages - 1) % kStages);
+      f32x4 part[TM][TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < kDmaBK / 32; ++ks) {
+        const int kc = ks * 4 + lane / 16;
+        f16x8 ah[TM], al[TM], bw[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int r = wm * (BM / 2) + i * 16 + lane % 16;
+          ah[i] = *reinterpret_cast<const f16x8*>(&Ah[buf][dma_pos(r, kc) * 8]);
+          al[i] = *reinterpret_cast<const f16x8*>(&Al[buf][dma_pos(r, kc) * 8]);
         }
-        if (ok) {
-          const int64_t off = static_cast<int64_t>(row) * g.ldc + col;
-          *reinterpret_cast<f16x4*>(g.act_split.hi + off) = hi;
-          *reinterpret_cast<f16x4*>(g.act_split.lo + off) = lo;
-          if (c4 % (kSplitChunkFine / 4) == 0)
-            g.act_split.inv[static_cast<int64_t>(row) * nkc + col / kSplitChunkFine] = ldexpf(1.0f, e - 15);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bw[j] = *reinterpret_cast<const f16x8*>(&Bs[buf][dma_pos(wn * (BN / 2) + j * 16 + lane % 16, kc) * 8]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], part[i][j], 0, 0, 0);
+            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], part[i][j], 0, 0, 0);
+          }
+        // Scale the finished k range by the rows' 1/s: every 32 k (fine
+        // scales) or once per stage.
+        if (kScales > 1 || ks == kDmaBK / 32 - 1) {
+          const int sidx = kScales > 1 ? ks : 0;
+#pragma unroll
+          for (int i = 0; i < TM; ++i) {
+            const float4 sv = *reinterpret_cast<const float4*>(&Sc[buf][wave][sidx][wm * (BM / 2) + i * 16 + 4 * (lane / 16)]);
+            const float sr[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(part[i][j][r], sr[r], acc[i][j][r]);
+              part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+          }
         }
       }
     }
   }
+  // Every load (the clamped re-loads of the last stage included) has landed
+  // and every wave is done with the stages before the epilogue reuses them.
+  dma_wait_barrier<0>();
+  gemm_epilogue<BM, BN, kEpi>(g, acc, out, reinterpret_cast<float*>(&Bs[0][0]), m0, n0, tid);
 }
 
 // Skinny GEMM for few rows of A (batched decode, m <= 16 * BT): one block per
@@ -878,6 +1063,45 @@ hipError_t launch_gemm_tile(const GemmArgs& g, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int kGran>
+void launch_gemm_dma_epi(const GemmArgs& g, hipStream_t s) {
+  const dim3 grid((g.n + BN - 1) / BN, (g.m + BM - 1) / BM, g.k_splits);
+  if (g.swiglu) {
+    gemm_dma_kernel<BM, BN, kGemmEpiSwiGlu, kGran><<<grid, kGemmThreads, 0, s>>>(g);
+  } else if (g.residual) {
+    gemm_dma_kernel<BM, BN, kGemmEpiResidual, kGran><<<grid, kGemmThreads, 0, s>>>(g);
+  } else {
+    gemm_dma_kernel<BM, BN, kGemmEpiStore, kGran><<<grid, kGemmThreads, 0, s>>>(g);
+  }
+}
+
+template <int BM, int BN>
+hipError_t launch_gemm_dma(const GemmArgs& g, hipStream_t s) {
+  if (g.a_chunk == kSplitChunk) {
+    launch_gemm_dma_epi<BM, BN, kSplitChunk>(g, s);
+  } else {
+    launch_gemm_dma_epi<BM, BN, kSplitChunkFine>(g, s);
+  }
+  return hipGetLastError();
+}
+
+// The direct-to-LDS kernel takes pre-split A with K a multiple of its stage.
+bool use_gemm_dma(const GemmArgs& g) {
+  return !g.register_staged && g.a_hi != nullptr && g.k % kDmaBK == 0 && g.lda % 8 == 0;
+}
+
+template <int BM, int BN>
+hipError_t launch_gemm_any(const GemmArgs& g, hipStream_t s) {
+  if (!use_gemm_dma(g)) return launch_gemm_tile<BM, BN>(g, s);
+  // The direct-to-LDS kernel runs 64 x 128 tiles as 64 x 64 (more blocks per
+  // CU measured faster: gate_up 16.5 -> 13.3 us).
+  if constexpr (BN == 128) {
+    return launch_gemm_dma<BM, 64>(g, s);
+  } else {
+    return launch_gemm_dma<BM, BN>(g, s);
+  }
+}
+
 template <typename KV>
 hipError_t launch_qkv_rows_kv(const QkvRowsArgs& a, hipStream_t s) {
   const dim3 grid(a.hq + a.hkv, (a.tokens + kQkvRowsTokens - 1) / kQkvRowsTokens);
@@ -926,36 +1150,29 @@ hipError_t launch_gemm_skinny(const GemmArgs& g, hipStream_t s) {
 namespace {
 bool use_skinny(int m, int k) { return m <= 32 && k % 32 == 0 && k >= 32 * kSkinnyWaves; }
 
-// Tiling of a launch_gemm call: 64 x 128 (below), else the largest tile whose
-// smallest split count reaches kGemmTargetBlocks blocks (1.5 per CU) while
-// every split keeps at least two K tiles; else the smallest tile with as many
-// splits as that allows.  Measured at M = 512: qkv 1152 x 768 15.3 -> 12.6 us (64 x 64, 3
-// splits), o 768 x 768 12.8 -> 9.8 us (32 x 64, 2), down 768 x 2048
-// 21.1 -> 18.8 us (64 x 64, 4), gate_up 4096 x 768 24.9 us unsplit.
+// Tiling of a launch_gemm call (tile and K split count); the consumers of the
+// split-K partials read the split count from gemm_k_splits.
 struct GemmTiling {
   int bm = 32, bn = 32, splits = 1;
 };
-constexpr int64_t kGemmTargetBlocks = 384;
+constexpr int64_t kGemmTargetBlocks = 768;
 
 GemmTiling choose_gemm_tiling(int m, int n, int k) {
   const int nk = (k + kGemmBK - 1) / kGemmBK;
   const int max_splits = std::max(1, std::min(8, nk / 2));
   // Unsplit: 64 x 128 when that gives every CU two blocks, else 64 x 64 when
-  // that does (A arrives pre-split, so the narrower tile costs only A
-  // re-reads, and the second block per CU hides the first's tile loads:
-  // gate_up at M = 512 19.6 -> 17.9 us).  Else the largest tile whose
-  // smallest split count reaches the target (down at M = 512: 64 x 64 with 4
-  // splits, as fast as 64 x 128 with 8 and half the partials to add).
+  // that does (gate_up at M = 512: 512 blocks, 13.3 us on the direct-to-LDS
+  // kernel, 16.7 register-staged; 64 x 128 measured 16.5).  Else 32 x 64
+  // tiles split along K until the launch reaches kGemmTargetBlocks (the
+  // direct-to-LDS kernel with two stages fits four such blocks per CU): at
+  // M = 512 down 768 x 2048 10.5 us with 4 splits (64 x 64 with 4: 11.4),
+  // QKV 6.3 us with 3, O 5.8-6.3 us with 2-4.
   const int64_t wide = static_cast<int64_t>((m + 63) / 64) * ((n + 127) / 128);
   if (wide >= 512) return {64, 128, 1};
   if (2 * wide >= 512) return {64, 64, 1};
-  const int tiles[3][2] = {{64, 64}, {32, 64}, {32, 32}};
-  for (const auto& t : tiles) {
-    const int64_t blocks = static_cast<int64_t>((m + t[0] - 1) / t[0]) * ((n + t[1] - 1) / t[1]);
-    const int64_t need = (kGemmTargetBlocks + blocks - 1) / blocks;
-    if (need <= max_splits) return {t[0], t[1], static_cast<int>(need)};
-  }
-  return {32, 32, max_splits};
+  const int64_t blocks = static_cast<int64_t>((m + 31) / 32) * ((n + 63) / 64);
+  const int64_t need = (kGemmTargetBlocks + blocks - 1) / blocks;
+  return {32, 64, static_cast<int>(std::min<int64_t>(std::max<int64_t>(need, 1), max_splits))};
 }
 }  // namespace
 
@@ -1001,20 +1218,20 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t s) {
   // Calls with the chooser's split count take its tile.
   const GemmTiling t = choose_gemm_tiling(g.m, g.n, g.k);
   if (g.k_splits == t.splits) {
-    if (t.bn == 128) return launch_gemm_tile<64, 128>(g, s);
-    if (t.bm == 64) return launch_gemm_tile<64, 64>(g, s);
-    if (t.bn == 64) return launch_gemm_tile<32, 64>(g, s);
-    return launch_gemm_tile<32, 32>(g, s);
+    if (t.bn == 128) return launch_gemm_any<64, 128>(g, s);
+    if (t.bm == 64) return launch_gemm_any<64, 64>(g, s);
+    if (t.bn == 64) return launch_gemm_any<32, 64>(g, s);
+    return launch_gemm_any<32, 32>(g, s);
   }
   // Otherwise the largest tile that still gives every CU a block (256 CUs,
   // counting the K splits), else the smallest tile.
   auto blocks = [&](int bm, int bn) {
     return static_cast<int64_t>((g.m + bm - 1) / bm) * ((g.n + bn - 1) / bn) * g.k_splits;
   };
-  if (blocks(64, 128) >= 256) return launch_gemm_tile<64, 128>(g, s);
-  if (blocks(64, 64) >= 256) return launch_gemm_tile<64, 64>(g, s);
-  if (blocks(32, 64) >= 256) return launch_gemm_tile<32, 64>(g, s);
-  return launch_gemm_tile<32, 32>(g, s);
+  if (blocks(64, 128) >= 256) return launch_gemm_any<64, 128>(g, s);
+  if (blocks(64, 64) >= 256) return launch_gemm_any<64, 64>(g, s);
+  if (blocks(32, 64) >= 256) return launch_gemm_any<32, 64>(g, s);
+  return launch_gemm_any<32, 32>(g, s);
 }
 
 hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream) {

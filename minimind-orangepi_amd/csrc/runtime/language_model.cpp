@@ -66,8 +66,10 @@ struct DeviceState {
   float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
   float* pf_attn = nullptr; // [chunk][Hq d]
   float* pf_part = nullptr; // split-K partials of one GEMM (QKV, O, gate_up or down): [splits][chunk][N]
+  int64_t pf_part_floats = 0;
   float* pf_act = nullptr;  // [chunk][F]
   bool prefill_tokenwise = false;  // prefill through the decode step instead of the GEMM path
+  bool gemm_register_staged = false;  // prefill GEMMs on the register-staged kernel only (comparison switch)
   hipStream_t stream = nullptr;
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;  // (attention splits, steps) -> captured steps
   bool use_graphs = true;
@@ -240,6 +242,8 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->combine_kernel = ck && ck[0] == '1';
   const char* pt = std::getenv("MMR_PREFILL_TOKENWISE");
   s->prefill_tokenwise = (pt && pt[0] == '1') || !device_->gemm_prefill;
+  const char* rs = std::getenv("MMR_GEMM_REGISTER_STAGED");
+  s->gemm_register_staged = rs && rs[0] == '1';
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
   const int64_t F = c.intermediate_size, V = c.vocab_size;
   const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
@@ -269,15 +273,16 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   if (const char* pc = std::getenv("MMR_PREFILL_CHUNK")) chunk = std::max<int64_t>(1, std::atoll(pc));
   s->pf_chunk = s->prefill_tokenwise ? 0 : std::min<int64_t>(capacity, chunk);
   const int64_t C = s->pf_chunk;
-  // Largest split-K partial set of a chunk (the split count depends on the
-  // row count only through the few-rows path, where it is 1).
+  // Largest split-K partial set of any chunk, over every row count up to C:
+  // fewer rows can take more K splits (the tiling targets a block count), so
+  // splits x rows is not largest at C.
   int64_t part_f = 0;
   if (C > 0) {
-    const int ci = static_cast<int>(C);
     const int64_t shapes[4][2] = {{qkv_w, H}, {H, Hq * D}, {2 * F, H}, {H, F}};
     for (const auto& sh : shapes)
-      part_f = std::max<int64_t>(
-          part_f, int64_t{mmr::gemm_k_splits(ci, static_cast<int>(sh[0]), static_cast<int>(sh[1]))} * C * sh[0]);
+      for (int r = 1; r <= static_cast<int>(C); ++r)
+        part_f = std::max<int64_t>(
+            part_f, int64_t{mmr::gemm_k_splits(r, static_cast<int>(sh[0]), static_cast<int>(sh[1]))} * r * sh[0]);
     ar.plan(C * H * 4);
     ar.plan(C * H * 4);
     ar.plan(C * Hq * D * 4);
@@ -320,6 +325,7 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
     s->pf_q = ar.take<float>(C * Hq * D);
     s->pf_attn = ar.take<float>(C * Hq * D);
     s->pf_part = ar.take<float>(part_f);
+    s->pf_part_floats = part_f;
     s->pf_act = ar.take<float>(C * F);
     s->pf_xs.hi = ar.take<uint16_t>(C * H);
     s->pf_xs.lo = ar.take<uint16_t>(C * H);
@@ -609,6 +615,9 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
     g.k = K;
     g.k_splits = std::min(mmr::gemm_k_splits(rows, N, K), max_splits);
     g.split_stride = static_cast<int64_t>(rows) * N;
+    g.register_staged = s.gemm_register_staged;
+    if (int64_t{g.k_splits} * g.split_stride > s.pf_part_floats)
+      throw std::logic_error("prefill split-K partials exceed their buffer");
     check_hip(mmr::launch_gemm(g, s.stream), "prefill gemm");
     return g.k_splits;
   };
@@ -673,6 +682,7 @@ void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
       g.n = 2 * F;
       g.k = H;
       g.swiglu = true;
+      g.register_staged = s.gemm_register_staged;
       check_hip(mmr::launch_gemm(g, s.stream), "prefill gate_up + SwiGLU");
     } else {
       const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H, kAnySplits);

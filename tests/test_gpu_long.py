@@ -32,7 +32,8 @@ from conftest import load_golden, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3          # logits vs the reference CPU path
-BATCH_TOL = 1e-4    # batched vs single-sequence GPU paths (same fp16 weights and KV)
+BATCH_TOL = 1e-4    # batched vs single-sequence GPU paths (same fp16 weights and KV); widened
+                    # per position to twice the measured prefill-vs-tokenwise logit gap
 
 
 def synth_model(mmr, g):
@@ -128,9 +129,20 @@ def test_minimind2_batch32_to_4096_positions(gpu):
             st.enqueue_prefill(got[:i].tolist())
             st.synchronize()
             lg = st.read_logits()
-            bound = BATCH_TOL * float(np.max(np.abs(lg)))
+            # The paths' own disagreement at this position: the same prefix fed
+            # token by token (GEMV projections, K/V rounded to fp16 one row at
+            # a time) against the GEMM prefill.  A flipped pair can differ by
+            # at most twice that in its margin.
+            st.reset()
+            for t in got[:i - 1].tolist():
+                st.forward_token(t)
+            noise = float(np.max(np.abs(st.forward_token(int(got[i - 1])) - lg)))
+            bound = max(BATCH_TOL * float(np.max(np.abs(lg))), 2.0 * noise)
             top2 = np.argsort(lg)[-2:]
-            assert set(top2.tolist()) == {int(got[i]), int(ref[i])} and abs(lg[got[i]] - lg[ref[i]]) <= bound, (
+            margin = abs(float(lg[got[i]] - lg[ref[i]]))
+            print(f"[tie] sequence {b} position {i}: margin {margin:.3g} bound {bound:.3g} (path noise {noise:.3g})",
+                  flush=True)
+            assert set(top2.tolist()) == {int(got[i]), int(ref[i])} and margin <= bound, (
                 f"sequence {b} position {i}: batch {got[i]} single {ref[i]} not a near-tie")
             ties += 1
             assert ties <= 8, "too many near-ties"

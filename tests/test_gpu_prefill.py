@@ -195,10 +195,11 @@ def test_gemm_prefill_on_used_state_and_fp16_cache(gpu, monkeypatch):
 
 @pytest.mark.parametrize("prompt_len", [256, 512])
 def test_gemm_prefill_swiglu_presplit_tilings(gpu, monkeypatch, prompt_len):
-    # hidden 256 with FFN 1536 (gate_up n = 3072, k = 256): at 256 rows the
-    # tiling chooser gives 32 x 64 unsplit tiles, at 512 rows 64 x 64 from its
-    # block-target loop; both write the SwiGLU output pre-split for the down
-    # GEMM.  GEMM prefill against the same prompt fed token by token.
+    # hidden 256 with FFN 1536 (gate_up n = 3072, k = 256): unsplit 32 x 64
+    # tiles at 256 and at 512 rows (the only K tile pair forbids splits),
+    # writing the SwiGLU output pre-split for the down GEMM (MiniMind2's
+    # gate_up covers the 64 x 64 tiles).  GEMM prefill against the same prompt
+    # fed token by token.
     mmr = gpu
     print(f"[case] prefill swiglu tiling rows={prompt_len}", flush=True)
     cfg = mmr.make_config(hidden_size=256, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
@@ -220,3 +221,47 @@ def test_gemm_prefill_swiglu_presplit_tilings(gpu, monkeypatch, prompt_len):
         st.synchronize()
     n = prompt_len + 13
     assert gem.read_sequence(0, n).tolist() == tok.read_sequence(0, n).tolist()
+
+
+@pytest.mark.parametrize("prompt_len", [333, 600])
+def test_minimind2_ragged_chunks_match_tokenwise(gpu, monkeypatch, prompt_len):
+    # MiniMind2 shapes at row counts below the 512-row chunk (333 alone; 600 =
+    # 512 + 88): fewer rows take more K splits, so the split-K partial sets
+    # of these chunks are larger than the full chunk's.  GEMM prefill against
+    # the same prompt fed token by token through the fp16 KV cache.
+    mmr = gpu
+    print(f"[case] MiniMind2 prefill rows={prompt_len}", flush=True)
+    g = load_golden("cfg3_short")
+    m = synth_model(mmr, g)
+    prompt = mmr.synthesize_prompt(11, prompt_len, 6400).tolist()
+    monkeypatch.setenv("MMR_PREFILL_TOKENWISE", "1")
+    tok = m.make_state(prompt_len + 8, mmr.KV_F16)
+    monkeypatch.delenv("MMR_PREFILL_TOKENWISE")
+    gem = m.make_state(prompt_len + 8, mmr.KV_F16)
+    for st in (tok, gem):
+        st.enqueue_prefill(prompt)
+        st.synchronize()
+    assert rel_err(gem.read_logits(), tok.read_logits()) < 1e-4
+    assert gem.read_sequence(prompt_len, 1).tolist() == tok.read_sequence(prompt_len, 1).tolist()
+
+
+def test_gemm_kernels_agree(gpu, monkeypatch):
+    # the direct-to-LDS GEMM (pre-split A, K % 64 == 0) against the
+    # register-staged one (MMR_GEMM_REGISTER_STAGED=1) on a MiniMind2 prefill
+    # of 512 tokens: same next token, logits within 1e-4 (the two add the
+    # same exact products in different groupings; through 16 layers and the
+    # fp16 KV cache's roundings that leaves ~5e-5, as against token-by-token)
+    mmr = gpu
+    g = load_golden("cfg3_short")
+    m = synth_model(mmr, g)
+    prompt = mmr.synthesize_prompt(5, 512, 6400).tolist()
+    dma = m.make_state(520, mmr.KV_F16)
+    monkeypatch.setenv("MMR_GEMM_REGISTER_STAGED", "1")
+    staged = m.make_state(520, mmr.KV_F16)
+    staged.enqueue_prefill(prompt)
+    staged.synchronize()
+    monkeypatch.delenv("MMR_GEMM_REGISTER_STAGED")
+    dma.enqueue_prefill(prompt)
+    dma.synchronize()
+    assert rel_err(dma.read_logits(), staged.read_logits()) < 1e-4
+    assert dma.read_sequence(512, 1).tolist() == staged.read_sequence(512, 1).tolist()
