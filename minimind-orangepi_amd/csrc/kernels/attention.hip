@@ -518,16 +518,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   // ---- 1. independent loads, issued before the position is known ----
   int p = -1;
   if constexpr (MODE == kAttnFused) p = a.pos[0];
-  uint4 kc[kPerThread], vc[kPerThread];
-  const int t_spec = split * TT;
-  const bool spec = t_spec + TT <= a.rows;
-  const int64_t t_load = kv_rows.row(spec ? t_spec : 0);
-#pragma unroll
-  for (int i = 0; i < kPerThread; ++i) {
-    const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
-    kc[i] = *reinterpret_cast<const uint4*>(kbase + t_load + c * CH);
-    vc[i] = *reinterpret_cast<const uint4*>(vbase + t_load + c * CH);
-  }
+  // The new token's q / k / v, the norm gains and the RoPE frequencies come
+  // first: vector loads complete in issue order, so the q norm and RoPE wait
+  // for these alone while the K/V tile below is still arriving.
   // Lane i < d/2 holds dims (i, i + d/2), the pair RoPE rotates together.
   const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
   const bool in_pair = lane < D / 2;
@@ -548,6 +541,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     kw0 = a.k_norm[d0];
     kw1 = a.k_norm[d1];
   }
+  uint4 kc[kPerThread], vc[kPerThread];
+  const int t_spec = split * TT;
+  const bool spec = t_spec + TT <= a.rows;
+  const int64_t t_load = kv_rows.row(spec ? t_spec : 0);
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+    kc[i] = *reinterpret_cast<const uint4*>(kbase + t_load + c * CH);
+    vc[i] = *reinterpret_cast<const uint4*>(vbase + t_load + c * CH);
+  }
 
   // ---- 2. extent of the context ----
   int n_keys;
@@ -566,6 +569,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   const int pv_pair = min(lane, kPairs - 1);
   const int tok = wave * kTokPerWave + lane / kLanesPerTok;  // scoring token within the tile
   const int share = lane % kLanesPerTok;  // which interleaved share of the dims
+  bool append_new = false;  // this lane writes dims (d0, d1) of cache row p at the end
 
   if (split < n_tiles) {
     // ---- 3. q (wave 0) and the new key/value (wave 1), in registers ----
@@ -587,20 +591,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     const bool owns_new = (MODE == kAttnFused) && ((p / TT) % S == split);
     if (owns_new && wave == 1) {
       wave_norm_rope_pair<D>(kx0, kx1, kw0, kw1, a.eps, rc, rs);
-      const KV k0 = from_float<KV>(kx0), k1 = from_float<KV>(kx1);
-      const KV v0 = from_float<KV>(vx0), v1 = from_float<KV>(vx1);
-      if (in_pair && r == 0) {
-        KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
-        KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
-        kdst[d0] = k0;
-        kdst[d1] = k1;
-        vdst[d0] = v0;
-        vdst[d1] = v1;
-      }
-      kx0 = to_float<KV>(k0);
-      kx1 = to_float<KV>(k1);
-      vx0 = to_float<KV>(v0);
-      vx1 = to_float<KV>(v1);
+      kx0 = to_float<KV>(from_float<KV>(kx0));
+      kx1 = to_float<KV>(from_float<KV>(kx1));
+      vx0 = to_float<KV>(from_float<KV>(vx0));
+      vx1 = to_float<KV>(from_float<KV>(vx1));
+      // The cache row is written at the end of the kernel: this block takes
+      // the new row from registers, the other blocks of the launch never read
+      // row p from the cache, and a store issued here would be waited for by
+      // the vector-memory waits of the staging below.
+      append_new = in_pair && r == 0;
     }
 
     const float sqrt_d = sqrtf(static_cast<float>(D));
@@ -716,6 +715,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     float* dst = a.part + attn_ml_offset(g, split, r, S, R, D, a.hkv);
     dst[0] = M;
     dst[1] = L;
+  }
+  // The new token's k / v (rounded to the cache dtype above), after every
+  // other memory operation of the block.
+  if (append_new) {
+    KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
+    KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
+    kdst[d0] = from_float<KV>(kx0);
+    kdst[d1] = from_float<KV>(kx1);
+    vdst[d0] = from_float<KV>(vx0);
+    vdst[d1] = from_float<KV>(vx1);
   }
 }
 
