@@ -242,11 +242,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x4 (&a
         }
       }
   }
-  // SwiGLU: even lanes hold gate column 2i, their odd neighbours up column
-  // 2i + 1 (one DPP exchange).
-  auto swiglu_act = [](float v) {
-    const float u = dpp_move<dpp::kQuadXor1>(v);
-    return (v / (1.0f + expf(-v))) * u;
+  // SwiGLU over lane pairs: lane 2c holds gate column 2c and lane 2c + 1 up
+  // column 2c + 1, of the same four rows 4 (lane / 16) + r.  One neighbour
+  // exchange per row, then the even lane forms act for rows r = 0, 1 and the
+  // odd lane for r = 2, 3: two SwiGLUs per lane and fragment, not four.
+  // Output k of this lane is row rsw[k] of the fragment.
+  const bool odd = (lane & 1) != 0;
+  const int rsw[2] = {odd ? 2 : 0, odd ? 3 : 1};
+  auto swiglu_pair = [&](const f32x4& v, float (&act)[2]) {
+    const float x0 = dpp_move<dpp::kQuadXor1>(v[0]), x1 = dpp_move<dpp::kQuadXor1>(v[1]);
+    const float x2 = dpp_move<dpp::kQuadXor1>(v[2]), x3 = dpp_move<dpp::kQuadXor1>(v[3]);
+    const float gate[2] = {odd ? x2 : v[0], odd ? x3 : v[1]};
+    const float up[2] = {odd ? v[2] : x0, odd ? v[3] : x1};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) act[k] = (gate[k] / (1.0f + expf(-gate[k]))) * up[k];
   };
   bool act_to_lds = false;
   constexpr bool kActSplit = kEpi == kGemmEpiSwiGlu && (BN == 128 || BN == 64);  // whole 32-column act chunks
@@ -260,29 +269,34 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x4 (&a
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j) {
+        float act[2];
+        swiglu_pair(acc[i][j], act);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float act = swiglu_act(acc[i][j][r]);
-          if ((lane & 1) == 0)
-            act_s[(wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r) * kActLd + (wn * (BN / 2) + j * 16 + lane % 16) / 2] =
-                act;
-        }
+        for (int k = 0; k < 2; ++k)
+          act_s[(wm * (BM / 2) + i * 16 + 4 * (lane / 16) + rsw[k]) * kActLd + (wn * (BN / 2) + j * 16 + lane % 16) / 2] =
+              act[k];
+      }
   } else {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn * (BN / 2) + j * 16 + lane % 16;
+        if constexpr (kEpi == kGemmEpiSwiGlu) {
+          float act[2];
+          swiglu_pair(acc[i][j], act);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
-          const float v = acc[i][j][r];
-          if constexpr (kEpi == kGemmEpiSwiGlu) {
-            const float act = swiglu_act(v);
-            if ((lane & 1) == 0 && row < g.m && col < g.n) out[static_cast<int64_t>(row) * g.ldc + col / 2] = act;
-          } else if (row < g.m && col < g.n) {
-            out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + v : v;
+          for (int k = 0; k < 2; ++k) {
+            const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + rsw[k];
+            if (row < g.m && col < g.n) out[static_cast<int64_t>(row) * g.ldc + col / 2] = act[k];
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = m0 + wm * (BM / 2) + i * 16 + 4 * (lane / 16) + r;
+            if (row < g.m && col < g.n)
+              out[static_cast<int64_t>(row) * g.ldc + col] = kResidual ? res[i][j][r] + acc[i][j][r] : acc[i][j][r];
           }
         }
       }
