@@ -762,8 +762,8 @@ __global__ __launch_bounds__(kWave* kQkvRowsTokens) void qkv_rows_kernel(QkvRows
 // conflict-free LDS words), so the probabilities never move between lanes;
 // only the per-query tile maximum needs the four 16-lane rows (two xor
 // shuffles).
-// Scores are dot / sqrt(d) (a division, as the reference), masked above the
-// query's position.  A wave may see tiles where a query has no key yet: its
+// Scores are dot / sqrt(d) in base-2 units (q pre-scaled by log2(e) / sqrt(d),
+// softmax by exp2), masked above the query's position.  A wave may see tiles where a query has no key yet: its
 // state stays (-inf, 0, 0) until one arrives.  At the end the waves' (m, l, O)
 // merge in LDS (log-sum-exp, wave order): the per-query wave weights and 1/L
 // are computed once, then each output is a dot product over the waves.
@@ -834,7 +834,12 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
   fetch(min(wave, n_tiles - 1), regs);  // unconditional; a wave with no tile never reads it
 
   // Q^T fragments: dims 16j + 4 kq + {0..3} of query qi (fp32), or dims
-  // 32j + 8 kq + {0..7} split into fp16 hi + lo (fp16 path).
+  // 32j + 8 kq + {0..7} split into fp16 hi + lo (fp16 path).  q is scaled
+  // once by log2(e) / sqrt(d): the scores come out in base-2 units, already
+  // divided by sqrt(d) (decoder_layer.cpp:213 divides each score), and the
+  // softmax takes exp2 (v_exp_f32) instead of expf.  The two forms differ by
+  // rounding only.
+  const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(D));
   float4 qf[kF16 ? 1 : DT];
   uint4 qh[kF16 ? D / 32 : 1], ql[kF16 ? D / 32 : 1];  // f16x8 bits
   const float* qsrc = a.query + static_cast<int64_t>(qrow) * a.query_stride + h * D;
@@ -843,7 +848,8 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
     for (int j = 0; j < D / 32; ++j) {
       const float4 x0 = *reinterpret_cast<const float4*>(qsrc + 32 * j + 8 * kq);
       const float4 x1 = *reinterpret_cast<const float4*>(qsrc + 32 * j + 8 * kq + 4);
-      const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+      const float x[8] = {x0.x * qscale, x0.y * qscale, x0.z * qscale, x0.w * qscale,
+                          x1.x * qscale, x1.y * qscale, x1.z * qscale, x1.w * qscale};
       f16x8 hv, lv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -855,14 +861,16 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < DT; ++j) qf[j] = *reinterpret_cast<const float4*>(qsrc + 16 * j + 4 * kq);
+    for (int j = 0; j < DT; ++j) {
+      const float4 x = *reinterpret_cast<const float4*>(qsrc + 16 * j + 4 * kq);
+      qf[j] = make_float4(x.x * qscale, x.y * qscale, x.z * qscale, x.w * qscale);
+    }
   }
 
   f32x4 ot[DT];  // O^T[d = 16 dt + 4 kq + i][query qi]
 #pragma unroll
   for (int j = 0; j < DT; ++j) ot[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = -INFINITY, l_part = 0.0f;
-  const float sqrt_d = sqrtf(static_cast<float>(D));
 
   auto step = [&](int tile, auto prefetch) {
     const int t0 = tile * KT;
@@ -923,15 +931,14 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int key = t0 + kt * 16 + 4 * kq + i;
-        const float sc = st[kt][i] / sqrt_d;  // decoder_layer.cpp:213
-        st[kt][i] = key <= qpos ? sc : -INFINITY;
+        st[kt][i] = key <= qpos ? st[kt][i] : -INFINITY;
         mx = fmaxf(mx, st[kt][i]);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
     // No key of this query seen yet (m_new = -inf): everything stays zero.
-    const float alpha = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+    const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     l_part *= alpha;
 #pragma unroll
     for (int j = 0; j < DT; ++j) ot[j] *= alpha;
@@ -939,7 +946,7 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
     for (int kt = 0; kt < KT / 16; ++kt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        st[kt][i] = st[kt][i] == -INFINITY ? 0.0f : expf(st[kt][i] - m_new);
+        st[kt][i] = st[kt][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st[kt][i] - m_new);
         l_part += st[kt][i];
       }
     m_run = m_new;
@@ -1011,7 +1018,7 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
 #pragma unroll
     for (int w = 0; w < kPrefillWaves; ++w) {
       const float mw = m_sh[w * kPrefillQueries + q];
-      e[w] = mw == -INFINITY ? 0.0f : expf(mw - M);
+      e[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
       L = fmaf(l_sh[w * kPrefillQueries + q], e[w], L);
     }
     const float inv = 1.0f / L;
