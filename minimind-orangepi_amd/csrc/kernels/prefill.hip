@@ -439,22 +439,28 @@ __device__ __forceinline__ int dma_pos(int r, int kc) { return r * kDmaRowChunks
 
 using lds_byte = __attribute__((address_space(3))) char;
 
-// One wave-wide direct load: lane l's `bytes` (16 or 4) at gsrc land in LDS
-// at wave_base + l * bytes.  M0 holds the wave's LDS base (a write of M0
-// needs one wait state before an LDS-direct load reads it: s_nop); the
-// instruction is issued from inline assembly so that the compiler, which does
-// not see the LDS write, inserts no wait for it: the kernel waits with
-// explicit vmcnt.
+// One wave-wide direct load: lane l's `bytes` (16 or 4) at sbase + voff land
+// in LDS at m0 + l * bytes.  sbase is a scalar (wave-uniform) address and
+// voff this lane's 32-bit byte offset (the scalar-base form of the global
+// load), m0 the wave's LDS destination; a write of M0 needs one wait state
+// before an LDS-direct load reads it (s_nop).  The instruction is issued from
+// inline assembly so that the compiler, which does not see the LDS write,
+// inserts no wait for it: the kernel waits with explicit vmcnt.
 template <int kBytes>
-__device__ __forceinline__ void dma_load(const void* gsrc, const void* wave_base) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_byte*)wave_base)));
+__device__ __forceinline__ void dma_load(const void* sbase, uint32_t voff, uint32_t m0) {
   if constexpr (kBytes == 16) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gsrc), "s"(m0) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(m0)
+                 : "memory");
   } else {
     static_assert(kBytes == 4, "16- or 4-byte loads");
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 1\n\tglobal_load_lds_dword %0, off" : : "v"(gsrc), "s"(m0) : "memory");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 1\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "s"(m0)
+                 : "memory");
   }
+}
+
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_byte*)p));
 }
 
 // Wait until at most kPending of this thread's vector-memory operations are
@@ -468,14 +474,12 @@ __device__ __forceinline__ void dma_wait_barrier() {
 template <int BM, int BN, int kEpi, int kGran, int kStages = kDmaStages>
 __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
   static_assert(kGran == kSplitChunk || kGran == kSplitChunkFine, "scale granularity");
+  static_assert(kStages == 2, "the K loop is unrolled over the two stage buffers");
   constexpr int TM = BM / 32, TN = BN / 32;
   constexpr int kScales = kGran >= kDmaBK ? 1 : kDmaBK / kGran;  // scale values per row per stage
   constexpr int kAWaveLoads = BM * kDmaRowChunks / kWave / 4;  // per plane, per wave, per stage
   constexpr int kBWaveLoads = BN * kDmaRowChunks / kWave / 4;
   static_assert(kAWaveLoads >= 1 && kBWaveLoads >= 1 && BM <= kWave, "tile shape");
-  // Vector-memory operations one thread issues per stage (every wave the same).
-  constexpr int kStageOps = 2 * kAWaveLoads + kBWaveLoads + kScales;
-  static_assert(kStages >= 2, "at least double buffering");
   __shared__ __align__(16) _Float16 Ah[kStages][BM * kDmaBK];
   __shared__ __align__(16) _Float16 Al[kStages][BM * kDmaBK];
   __shared__ __align__(16) _Float16 Bs[kStages][BN * kDmaBK];
@@ -485,7 +489,8 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  // Wave-uniform (an SGPR): the LDS destinations of the direct loads are scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wave / 2, wn = wave % 2;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int nk = g.k / kDmaBK;
@@ -494,31 +499,57 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
   float* out = g.c + static_cast<int64_t>(blockIdx.z) * g.split_stride;
   const int nsc = (g.k + kGran - 1) / kGran;  // scales per row of a_inv
 
-  // Stage kt into buffer buf.  Rows past m (n) load a clamped row: in bounds,
-  // never stored.
-  auto issue = [&](int kt, int buf) {
-    const int k0 = kt * kDmaBK;
+  // This lane's byte offsets for the direct loads and its LDS fragment
+  // offsets, the same for every stage: a stage only moves the scalar bases
+  // and alternates the buffer (a constant offset, the loop being unrolled
+  // over the two buffers).  Rows past m (n) load a clamped row: in bounds,
+  // never stored.  (launch_gemm keeps every offset below 2^32.)
+  uint32_t a_off[kAWaveLoads], b_off[kBWaveLoads];
+#pragma unroll
+  for (int j = 0; j < kAWaveLoads; ++j) {
+    const int c = (wave + 4 * j) * kWave + lane;  // wave-wide load wave + 4 j fills chunks [64 i, 64 i + 64)
+    const int r = c / kDmaRowChunks, kc = (c % kDmaRowChunks) ^ ((r >> 1) & 7);
+    a_off[j] = static_cast<uint32_t>((static_cast<int64_t>(min(m0 + r, g.m - 1)) * g.lda + kc * 8) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < kBWaveLoads; ++j) {
+    const int c = (wave + 4 * j) * kWave + lane;
+    const int r = c / kDmaRowChunks, kc = (c % kDmaRowChunks) ^ ((r >> 1) & 7);
+    b_off[j] = static_cast<uint32_t>((static_cast<int64_t>(min(n0 + r, g.n - 1)) * g.k + kc * 8) * 2);
+  }
+  const uint32_t s_off = static_cast<uint32_t>(static_cast<int64_t>(min(m0 + min(lane, BM - 1), g.m - 1)) * nsc * 4);
+  int a_rd[2][TM], b_rd[2][TN];  // [ks][fragment]: element offsets within a stage buffer
+#pragma unroll
+  for (int ks = 0; ks < kDmaBK / 32; ++ks) {
+    const int kc = ks * 4 + lane / 16;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a_rd[ks][i] = dma_pos(wm * (BM / 2) + i * 16 + lane % 16, kc) * 8;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b_rd[ks][j] = dma_pos(wn * (BN / 2) + j * 16 + lane % 16, kc) * 8;
+  }
+
+  // Stage kt into buffer buf.
+  auto issue = [&](int kt, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    const int64_t kb = static_cast<int64_t>(kt) * kDmaBK * 2;  // byte offset of the stage's first k
+    const char* ahb = reinterpret_cast<const char*>(g.a_hi) + kb;
+    const char* alb = reinterpret_cast<const char*>(g.a_lo) + kb;
+    const char* wb = reinterpret_cast<const char*>(g.w) + kb;
 #pragma unroll
     for (int j = 0; j < kAWaveLoads; ++j) {
-      const int i = wave + 4 * j;  // wave-wide load i fills chunks [64 i, 64 i + 64)
-      const int c = i * kWave + lane;
-      const int r = c / kDmaRowChunks, kc = (c % kDmaRowChunks) ^ ((r >> 1) & 7);
-      const int64_t off = static_cast<int64_t>(min(m0 + r, g.m - 1)) * g.lda + k0 + kc * 8;
-      dma_load<16>(g.a_hi + off, &Ah[buf][i * kWave * 8]);
-      dma_load<16>(g.a_lo + off, &Al[buf][i * kWave * 8]);
+      const int i = wave + 4 * j;
+      dma_load<16>(ahb, a_off[j], lds_address(&Ah[buf][i * kWave * 8]));
+      dma_load<16>(alb, a_off[j], lds_address(&Al[buf][i * kWave * 8]));
     }
 #pragma unroll
     for (int j = 0; j < kBWaveLoads; ++j) {
       const int i = wave + 4 * j;
-      const int c = i * kWave + lane;
-      const int r = c / kDmaRowChunks, kc = (c % kDmaRowChunks) ^ ((r >> 1) & 7);
-      dma_load<16>(g.w + static_cast<int64_t>(min(n0 + r, g.n - 1)) * g.k + k0 + kc * 8, &Bs[buf][i * kWave * 8]);
+      dma_load<16>(wb, b_off[j], lds_address(&Bs[buf][i * kWave * 8]));
     }
 #pragma unroll
-    for (int sidx = 0; sidx < kScales; ++sidx) {
-      const int row = min(m0 + min(lane, BM - 1), g.m - 1);
-      dma_load<4>(g.a_inv + static_cast<int64_t>(row) * nsc + (k0 + sidx * kGran) / kGran, &Sc[buf][wave][sidx][0]);
-    }
+    for (int sidx = 0; sidx < kScales; ++sidx)
+      dma_load<4>(reinterpret_cast<const char*>(g.a_inv) + ((kt * kDmaBK + sidx * kGran) / kGran) * 4, s_off,
+                  lds_address(&Sc[buf][wave][sidx][0]));
   };
 
   f32x4 acc[TM][TN];
@@ -527,60 +558,61 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  if (kt0 < kt1) {  // a split past the end of K writes zeros
-    // Stages kt0 .. kt0 + kStages - 2 in flight before the first multiply
-    // (past the last K tile the last one is loaded again: in bounds, unused).
+  // One K stage from buffer buf: wait for it, start the next one's loads
+  // (past the last stage the last is loaded again: in bounds, unused), then
+  // multiply.
+  auto stage = [&](int kt, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    // Stage kt has landed, and every wave is done with the other buffer
+    // (read in stage kt - 1).
+    dma_wait_barrier<0>();
+    issue(min(kt + 1, kt1 - 1), std::integral_constant<int, buf ^ 1>{});
+    f32x4 part[TM][TN];
 #pragma unroll
-    for (int p = 0; p < kStages - 1; ++p) issue(min(kt0 + p, kt1 - 1), p);
-    for (int kt = kt0; kt < kt1; ++kt) {
-      const int it = kt - kt0, buf = it % kStages;
-      // Stage kt has landed (the kStages - 2 later ones may still be loading),
-      // and every wave is done with the buffer refilled next (read in
-      // iteration it - 1).
-      dma_wait_barrier<(kStages - 2) * kStageOps>();
-      issue(min(kt + kStages - 1, kt1 - 1), (it + kStages - 1) % kStages);
-      f32x4 part[TM][TN];
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < kDmaBK / 32; ++ks) {
+      f16x8 ah[TM], al[TM], bw[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        ah[i] = *reinterpret_cast<const f16x8*>(&Ah[buf][a_rd[ks][i]]);
+        al[i] = *reinterpret_cast<const f16x8*>(&Al[buf][a_rd[ks][i]]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bw[j] = *reinterpret_cast<const f16x8*>(&Bs[buf][b_rd[ks][j]]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int ks = 0; ks < kDmaBK / 32; ++ks) {
-        const int kc = ks * 4 + lane / 16;
-        f16x8 ah[TM], al[TM], bw[TN];
+        for (int j = 0; j < TN; ++j) {
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], part[i][j], 0, 0, 0);
+          part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], part[i][j], 0, 0, 0);
+        }
+      // Scale the finished k range by the rows' 1/s: every 32 k (fine
+      // scales) or once per stage.
+      if (kScales > 1 || ks == kDmaBK / 32 - 1) {
+        const int sidx = kScales > 1 ? ks : 0;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-          const int r = wm * (BM / 2) + i * 16 + lane % 16;
-          ah[i] = *reinterpret_cast<const f16x8*>(&Ah[buf][dma_pos(r, kc) * 8]);
-          al[i] = *reinterpret_cast<const f16x8*>(&Al[buf][dma_pos(r, kc) * 8]);
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bw[j] = *reinterpret_cast<const f16x8*>(&Bs[buf][dma_pos(wn * (BN / 2) + j * 16 + lane % 16, kc) * 8]);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
+          const float4 sv = *reinterpret_cast<const float4*>(&Sc[buf][wave][sidx][wm * (BM / 2) + i * 16 + 4 * (lane / 16)]);
+          const float sr[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
-            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bw[j], part[i][j], 0, 0, 0);
-            part[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bw[j], part[i][j], 0, 0, 0);
-          }
-        // Scale the finished k range by the rows' 1/s: every 32 k (fine
-        // scales) or once per stage.
-        if (kScales > 1 || ks == kDmaBK / 32 - 1) {
-          const int sidx = kScales > 1 ? ks : 0;
 #pragma unroll
-          for (int i = 0; i < TM; ++i) {
-            const float4 sv = *reinterpret_cast<const float4*>(&Sc[buf][wave][sidx][wm * (BM / 2) + i * 16 + 4 * (lane / 16)]);
-            const float sr[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-#pragma unroll
-              for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(part[i][j][r], sr[r], acc[i][j][r]);
-              part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(part[i][j][r], sr[r], acc[i][j][r]);
+            part[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
           }
         }
       }
+    }
+  };
+
+  if (kt0 < kt1) {  // a split past the end of K writes zeros
+    issue(kt0, std::integral_constant<int, 0>{});
+    for (int kt = kt0; kt < kt1; kt += 2) {
+      stage(kt, std::integral_constant<int, 0>{});
+      if (kt + 1 < kt1) stage(kt + 1, std::integral_constant<int, 1>{});
     }
   }
   // Every load (the clamped re-loads of the last stage included) has landed
@@ -1108,7 +1140,11 @@ hipError_t launch_gemm_dma(const GemmArgs& g, hipStream_t s) {
 
 // The direct-to-LDS kernel takes pre-split A with K a multiple of its stage.
 bool use_gemm_dma(const GemmArgs& g) {
-  return !g.register_staged && g.a_hi != nullptr && g.k % kDmaBK == 0 && g.lda % 8 == 0;
+  // Its per-lane load offsets are 32-bit byte offsets from the operands' bases.
+  const int64_t a_bytes = static_cast<int64_t>(g.m) * g.lda * 2, w_bytes = static_cast<int64_t>(g.n) * g.k * 2;
+  const int64_t s_bytes = static_cast<int64_t>(g.m) * ((g.k + kSplitChunkFine - 1) / kSplitChunkFine) * 4;
+  return !g.register_staged && g.a_hi != nullptr && g.k % kDmaBK == 0 && g.lda % 8 == 0 && a_bytes < (int64_t{1} << 32) &&
+         w_bytes < (int64_t{1} << 32) && s_bytes < (int64_t{1} << 32);
 }
 
 template <int BM, int BN>
