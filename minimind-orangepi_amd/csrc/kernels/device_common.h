@@ -21,6 +21,17 @@ __device__ __forceinline__ void half8_to_float8(const uint4& u, float* f) {
   }
 }
 
+// a / b for 0 <= a < 2^20 and 1 <= b < 2^20, by a reciprocal multiply.  The
+// exact (a + 0.5) / b lies at least 0.5 / b from every integer.  v_rcp_f32 is
+// accurate to 1 ulp and the product adds half an ulp, a relative error below
+// 2^-22, i.e. an absolute error below (a + 0.5) / b * 2^-22 < 0.5 / b while
+// a + 0.5 < 2^21, so the truncation is exact.  (A runtime integer division is
+// a long instruction sequence; this is three instructions.)  The GEMV combine
+// prologue gives it element indices below 1024 and head indices below 16.
+__device__ __forceinline__ int small_quotient(int a, int b) {
+  return static_cast<int>((static_cast<float>(a) + 0.5f) * __builtin_amdgcn_rcpf(static_cast<float>(b)));
+}
+
 // Cross-lane reductions without an LDS round trip.  Inside a 16-lane row the
 // partners come from DPP permutations (GFX9 encodings): quad_perm [1,0,3,2]
 // and [2,3,0,1] pair lanes within a quad, row_half_mirror (lane i <-> 7 - i of

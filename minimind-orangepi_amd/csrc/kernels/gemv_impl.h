@@ -35,55 +35,60 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
   const int kchunks = k >> 3;
   const int row0 = (blockIdx.x * kGroups + group) * RPG;
 
-  // 1. Every load that does not depend on another is issued first: weights,
-  //    then residual / norm gain / x, so one memory latency covers them all.
+  // 1. Every load that does not depend on another goes out before any
+  //    arithmetic, so one memory latency covers them all, in this order: the
+  //    residual, the norm gains and the activations (x, or the attention
+  //    split partials), then the weights.  Vector loads complete in order, so
+  //    the prologue's arithmetic (RMSNorm, split merge) runs on the
+  //    activations while the weights still stream in.  (The embedding
+  //    prologue's row waits on two dependent scalar loads: its weights go
+  //    before it.)  Compiler barriers keep this order, which the compiler,
+  //    free to move these loads, would otherwise change (activations behind
+  //    the weights, the residual sunk to its use at the end).  No load is
+  //    guarded (a guard is a branch, with its own wait for the pointer it
+  //    loads through): rows past N read the last row and are not stored,
+  //    chunks past K read the last chunk and meet x = 0.
   uint4 wv[RPG][CPL];
+  auto load_weights = [&] {
+    asm volatile("" ::: "memory");
 #pragma unroll
-  for (int r = 0; r < RPG; ++r) {
-    const int row = row0 + r;
-    const uint4* wrow = reinterpret_cast<const uint4*>(a.w + static_cast<int64_t>(row) * k);
+    for (int r = 0; r < RPG; ++r) {
+      const int row = min(row0 + r, a.rows - 1);
+      const uint4* wrow = reinterpret_cast<const uint4*>(a.w + static_cast<int64_t>(row) * k);
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = lane + G * i;
-      if (row < a.rows && c < kchunks) {
-        wv[r][i] = wrow[c];
-      } else {
-        wv[r][i] = make_uint4(0u, 0u, 0u, 0u);
-      }
+      for (int i = 0; i < CPL; ++i) wv[r][i] = wrow[min(lane + G * i, kchunks - 1)];
     }
-  }
+    asm volatile("" ::: "memory");
+  };
   float res[RPG];
   if constexpr (EPI == kEpiResidual) {
 #pragma unroll
-    for (int r = 0; r < RPG; ++r) res[r] = (lane == 0 && row0 + r < a.rows) ? a.residual[row0 + r] : 0.0f;
+    for (int r = 0; r < RPG; ++r) res[r] = a.residual[min(row0 + r, a.rows - 1)];
   }
   float nw[CPL][8];
   if constexpr (PRO == kProRmsNorm || PRO == kProRmsNormFinal || PRO == kProEmbedRmsNorm) {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int c = lane + G * i;
-      if (c < kchunks) {
-        const float4* src = reinterpret_cast<const float4*>(a.norm_w + c * 8);
-        const float4 lo = src[0];
-        const float4 hi = src[1];
-        nw[i][0] = lo.x; nw[i][1] = lo.y; nw[i][2] = lo.z; nw[i][3] = lo.w;
-        nw[i][4] = hi.x; nw[i][5] = hi.y; nw[i][6] = hi.z; nw[i][7] = hi.w;
-      }
+      const float4* src = reinterpret_cast<const float4*>(a.norm_w + min(lane + G * i, kchunks - 1) * 8);
+      const float4 lo = src[0];
+      const float4 hi = src[1];
+      nw[i][0] = lo.x; nw[i][1] = lo.y; nw[i][2] = lo.z; nw[i][3] = lo.w;
+      nw[i][4] = hi.x; nw[i][5] = hi.y; nw[i][6] = hi.z; nw[i][7] = hi.w;
     }
   }
 
   // 2. x chunks owned by this lane (+ fused prologue).
   float xv[CPL][8];
   if constexpr (PRO == kProEmbedRmsNorm) {
+    load_weights();
     int token = a.seq[*a.pos];
     token = token < 0 ? 0 : (token >= a.vocab ? a.vocab - 1 : token);
     const uint4* erow = reinterpret_cast<const uint4*>(a.embed + static_cast<int64_t>(token) * k);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = lane + G * i;
-      if (c < kchunks) {
-        half8_to_float8(erow[c], xv[i]);
-      } else {
+      half8_to_float8(erow[min(c, kchunks - 1)], xv[i]);
+      if (c >= kchunks) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
       }
@@ -111,20 +116,28 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     __shared__ __align__(16) float s_l[kCombineMaxHeads][kCombineMaxSplits];
     const int S = a.splits, D = a.head_dim, R = a.hq / a.hkv;
     // Thread t owns x[4t, 4t + 4); its 16 float4 partial loads are
-    // unconditional (split index clamped) so they issue back to back.
+    // unconditional (split index clamped) so they issue back to back.  The
+    // offsets are attn_o_offset / attn_ml_offset written as a per-lane base
+    // plus a wave-uniform split term (scalar arithmetic), in 32 bits (the
+    // partial buffer of at most kCombineMaxSplits splits is small), and the
+    // lane's head and group come from small_quotient instead of divisions.
     const int t4 = min(static_cast<int>(threadIdx.x), k / 4 - 1);
-    const int head = (4 * t4) / D, dim = 4 * t4 - head * D;
+    const int head = small_quotient(4 * t4, D), dim = 4 * t4 - head * D;
+    const int g = small_quotient(head, R);
+    const int obase = ((g * S) * R + (head - g * R)) * D + dim;  // attn_o_offset(g, 0, head % R, S, R, D) + dim
     float4 ov[kCombineMaxSplits];
 #pragma unroll
     for (int s = 0; s < kCombineMaxSplits; ++s)
-      ov[s] = *reinterpret_cast<const float4*>(a.part + attn_o_offset(head / R, min(s, S - 1), head % R, S, R, D) + dim);
+      ov[s] = *reinterpret_cast<const float4*>(a.part + obase + min(s, S - 1) * (R * D));
     {
       // Lane (head, split) = (threadIdx / 16, threadIdx % 16): one 16-lane row
       // per head, so M_h is a row reduction.  Splits >= S get weight 0.
       const int wh = min(static_cast<int>(threadIdx.x) / kCombineMaxSplits, a.hq - 1);
       const int ws = static_cast<int>(threadIdx.x) % kCombineMaxSplits;
-      const float2 ml =
-          *reinterpret_cast<const float2*>(a.part + attn_ml_offset(wh / R, min(ws, S - 1), wh % R, S, R, D, a.hkv));
+      const int wg = small_quotient(wh, R);
+      const float2 ml = *reinterpret_cast<const float2*>(
+          a.part + a.hkv * S * R * D + ((wg * S + min(ws, S - 1)) * R + (wh - wg * R)) * 2);  // attn_ml_offset
+      load_weights();
       const bool live = ws < S;
       const float m = live ? ml.x : -INFINITY;
       const float M = group_max<kCombineMaxSplits>(m);
@@ -158,31 +171,31 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = lane + G * i;
-      if (c < kchunks) {
-        const float4 lo = *reinterpret_cast<const float4*>(&s_x[c * 8]);
-        const float4 hi = *reinterpret_cast<const float4*>(&s_x[c * 8 + 4]);
-        xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
-        xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
-      }
+      const int cc = min(c, kchunks - 1);
+      const float4 lo = *reinterpret_cast<const float4*>(&s_x[cc * 8]);
+      const float4 hi = *reinterpret_cast<const float4*>(&s_x[cc * 8 + 4]);
+      const bool in = c < kchunks;
+      xv[i][0] = in ? lo.x : 0.0f; xv[i][1] = in ? lo.y : 0.0f; xv[i][2] = in ? lo.z : 0.0f; xv[i][3] = in ? lo.w : 0.0f;
+      xv[i][4] = in ? hi.x : 0.0f; xv[i][5] = in ? hi.y : 0.0f; xv[i][6] = in ? hi.z : 0.0f; xv[i][7] = in ? hi.w : 0.0f;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = lane + G * i;
-      if (c < kchunks) {
-        const float4* src = reinterpret_cast<const float4*>(a.x + c * 8);
-        const float4 lo = src[0];
-        const float4 hi = src[1];
-        xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
-        xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
-      } else {
+      const float4* src = reinterpret_cast<const float4*>(a.x + min(c, kchunks - 1) * 8);
+      const float4 lo = src[0];
+      const float4 hi = src[1];
+      xv[i][0] = lo.x; xv[i][1] = lo.y; xv[i][2] = lo.z; xv[i][3] = lo.w;
+      xv[i][4] = hi.x; xv[i][5] = hi.y; xv[i][6] = hi.z; xv[i][7] = hi.w;
+    }
+    load_weights();
+    // Chunks past K meet x = 0 (after the weight loads are out: this reads x).
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+      if (lane + G * i >= kchunks) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
       }
-    }
   }
 
   if constexpr (PRO == kProRmsNorm || PRO == kProRmsNormFinal || PRO == kProEmbedRmsNorm) {
@@ -195,15 +208,12 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     const float scale = 1.0f / sqrtf(ss / static_cast<float>(k) + a.eps);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int c = lane + G * i;
-      if (c < kchunks) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if constexpr (PRO == kProRmsNormFinal) {
-            xv[i][e] = (xv[i][e] * scale) * nw[i][e];
-          } else {
-            xv[i][e] = xv[i][e] * (scale * nw[i][e]);
-          }
+      for (int e = 0; e < 8; ++e) {  // chunks past K: x = 0, stays 0
+        if constexpr (PRO == kProRmsNormFinal) {
+          xv[i][e] = (xv[i][e] * scale) * nw[i][e];
+        } else {
+          xv[i][e] = xv[i][e] * (scale * nw[i][e]);
         }
       }
     }
