@@ -528,6 +528,27 @@ def main() -> int:
             kernels[name]["splits_note"] = ("attention kernel only (one block per query head and split at this "
                                             "context); the split combine runs in the o-projection prologue")
         log(f"kernel {name:9s} {avg_us:8.3f} us  {kernels[name]['gbs']:8.1f} GB/s")
+    # The step's attention launch also carries 64 L2-warming blocks that load
+    # the layer's O, gate_up and down weights (bytes the next three kernels
+    # then read from L2).  The same kernel without them, on a state made with
+    # warming off at the same context:
+    c = MINIMIND2
+    warm_bytes = 2 * (c["hidden_size"] * c["num_attention_heads"] * c["head_dim"] +
+                      3 * c["hidden_size"] * c["intermediate_size"])
+    os.environ["MMR_L2_WARM_BLOCKS"] = "0"
+    cold = model.make_state(PROMPT_LEN + args.steps + 8, kv)
+    del os.environ["MMR_L2_WARM_BLOCKS"]
+    cold.enqueue_prefill(prompt)
+    cold.enqueue_decode(args.steps - 1)
+    cold.synchronize()
+    a = kernels["attention"]
+    a["avg_us_without_warm_blocks"] = round(cold.time_step_kernel(names.index("attention"), 0, args.kernel_reps), 3)
+    a["warm_bytes_per_launch"] = warm_bytes
+    a["warm_note"] = ("avg_us is the launch as the step runs it, with 64 extra blocks loading the layer's O, "
+                      "gate_up and down weights into the L2s of the XCDs that read them next; "
+                      "avg_us_without_warm_blocks is the attention work alone")
+    log(f"kernel attention without warming blocks {a['avg_us_without_warm_blocks']:.3f} us")
+    del cold
     per_step_us = sum(kernels[n]["avg_us"] for n in names[:5]) * MINIMIND2["num_hidden_layers"] + \
         kernels["lm_head"]["avg_us"] + kernels["finalize"]["avg_us"]
     step_bytes = sum(kernels[n]["bytes"] for n in names[:5]) * MINIMIND2["num_hidden_layers"] + \
@@ -597,7 +618,9 @@ def main() -> int:
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": tsrc if traffic is not None else None,
                 "bytes_per_launch": kernels[name]["bytes"], "avg_us": kernels[name]["avg_us"],
-                "us_per_step": kernels[name]["us_per_step"]}
+                "us_per_step": kernels[name]["us_per_step"],
+                **{k: kernels[name][k] for k in ("avg_us_without_warm_blocks", "warm_bytes_per_launch")
+                   if k in kernels[name]}}
 
     roofline = roofline_of(dom)
     roofline["secondary"] = {n: roofline_of(n) for n in ("gate_up", "attention", "lm_head") if n != dom}

@@ -488,6 +488,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
 
   const int R = a.hq / a.hkv;
   const int S = a.splits;
+  // Blocks past the S * hq head blocks: padding up to a multiple of kXcds,
+  // then the L2-warming blocks (their loads land in k_s, which they own).
+  static_assert(sizeof(k_s) >= kAttnThreads / kWave * kWave * 16, "a 1 KB landing zone per wave");
+  if (static_cast<int>(blockIdx.x) >= S * a.hq) {
+    const int first = (S * a.hq + kXcds - 1) / kXcds * kXcds;
+    if (MODE == kAttnFused && static_cast<int>(blockIdx.x) >= first)
+      l2_warm<kAttnThreads>(a.warm, static_cast<int>(blockIdx.x) - first, a.warm_blocks, &k_s[0][0]);
+    return;
+  }
   // Block -> (split, group, head): the R head-blocks of one (split, group)
   // unit take ids 8 apart, so the round-robin dispatch over the 8 XCDs puts
   // them on one XCD and their K/V tile is read from HBM into one L2.  (A
@@ -876,7 +885,12 @@ hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
     if (mode != kAttnFused) return hipErrorInvalidValue;
     attention_split_kernel<KV, D, kAttnFused, true><<<group_grid, block, 0, s>>>(a);
   } else if (static_cast<int64_t>(a.splits) * a.hq <= kHeadKernelMaxBlocks) {
-    const dim3 head_grid(a.splits * a.hq);
+    int blocks = a.splits * a.hq;
+    if (mode == kAttnFused && a.warm_blocks > 0) {
+      if (a.warm_blocks % kXcds != 0) return hipErrorInvalidValue;
+      blocks = (blocks + kXcds - 1) / kXcds * kXcds + a.warm_blocks;
+    }
+    const dim3 head_grid(blocks);
     if (mode == kAttnFused) {
       attention_head_kernel<KV, D, kAttnFused><<<head_grid, block, 0, s>>>(a);
     } else {

@@ -6,6 +6,8 @@
 
 #include <cstdint>
 
+#include "kernels.h"
+
 namespace mmr {
 
 constexpr int kWave = 64;  // CDNA wavefront width
@@ -121,6 +123,54 @@ __device__ __forceinline__ float from_float<float>(float v) {
 template <>
 __device__ __forceinline__ __half from_float<__half>(float v) {
   return __float2half_rn(v);
+}
+
+using lds_byte = __attribute__((address_space(3))) char;
+
+// One wave-wide direct load: lane l's `bytes` (16 or 4) at sbase + voff land
+// in LDS at m0 + l * bytes.  sbase is a scalar (wave-uniform) address and
+// voff this lane's 32-bit byte offset (the scalar-base form of the global
+// load), m0 the wave's LDS destination; a write of M0 needs one wait state
+// before an LDS-direct load reads it (s_nop).  The instruction is issued from
+// inline assembly so that the compiler, which does not see the LDS write,
+// inserts no wait for it: the kernel waits with explicit vmcnt.
+template <int kBytes>
+__device__ __forceinline__ void dma_load(const void* sbase, uint32_t voff, uint32_t m0) {
+  if constexpr (kBytes == 16) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(m0)
+                 : "memory");
+  } else {
+    static_assert(kBytes == 4, "16- or 4-byte loads");
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 1\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "s"(m0)
+                 : "memory");
+  }
+}
+
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_byte*)p));
+}
+
+// Warming block j of n (n a multiple of kXcds; the first warming block's id
+// is a multiple of kXcds, so j % kXcds is the XCD it runs on): loads the
+// slices of every region read by that region's blocks on the same XCD, with
+// direct-to-LDS loads that hold no registers, into the 1 KB per wave at lds
+// (the block's scratch, overwritten), and waits for them.
+template <int kThreads>
+__device__ void l2_warm(const L2Warm (&regions)[kL2WarmRegions], int j, int n, void* lds) {
+  const int xcd = j % kXcds, slot = j / kXcds, slots = n / kXcds;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_address(lds) + (threadIdx.x / kWave) * (kWave * 16));
+#pragma unroll
+  for (int r = 0; r < kL2WarmRegions; ++r) {
+    const L2Warm& g = regions[r];
+    if (g.base == nullptr) continue;
+    for (int b = xcd + kXcds * slot; b < g.blocks; b += kXcds * slots) {
+      const uint32_t lo = static_cast<uint32_t>(b) * g.block_bytes;
+      const uint32_t hi = min(lo + g.block_bytes, g.bytes);
+      for (uint32_t off = lo + threadIdx.x * 16; off < hi; off += kThreads * 16) dma_load<16>(g.base, off, m0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
 }
 
 }  // namespace mmr

@@ -13,6 +13,23 @@
 
 namespace mmr {
 
+// -------------------------------------------------------------- L2 warming ----
+// A later kernel's weight stream, described by the blocks that will read it:
+// block b of that kernel reads bytes [b * block_bytes, (b + 1) * block_bytes)
+// of base (the last block fewer).  The dispatcher deals a grid's blocks
+// round-robin over the 8 XCDs (block b on XCD b % 8), each XCD has its own L2,
+// and L2 contents outlive a kernel boundary; so blocks of an earlier kernel on
+// XCD x that load the slices of the later kernel's blocks b = x (mod 8) turn
+// that kernel's weight loads into L2 hits.
+constexpr int kXcds = 8;
+constexpr int kL2WarmRegions = 3;
+struct L2Warm {
+  const void* base = nullptr;  // nullptr: region unused
+  uint32_t bytes = 0;          // region size (byte offsets are 32-bit)
+  uint32_t block_bytes = 0;    // a multiple of 16
+  int blocks = 0;              // the reading kernel's grid
+};
+
 // ---------------------------------------------------------------- GEMV ----
 // y = W x with W fp16 row-major [rows][k] (weights streamed from HBM once),
 // x/y fp32, fp32 accumulation.
@@ -137,6 +154,12 @@ struct AttnArgs {
   // the page of sequence b's token t; rows = pages_per_seq * kKvPage.
   const int32_t* page_table = nullptr;
   int pages_per_seq = 0;
+  // Single-sequence fused launches on the per-head kernel: warm_blocks extra
+  // blocks (a multiple of kXcds, 0 = none), past the head blocks rounded up to
+  // a multiple of kXcds, load the warm regions into the XCDs' L2s while the
+  // head blocks run.  Other launch shapes ignore them.
+  L2Warm warm[kL2WarmRegions];
+  int warm_blocks = 0;
 };
 constexpr int kKvPage = 64;  // tokens per KV page (a multiple of every attention tile)
 

@@ -32,6 +32,13 @@
 
 namespace minimind::model {
 
+// L2 warming in the single-sequence step (the attention launch loads the
+// layer's O, gate_up and down weights for the XCDs that will read them):
+// 64 blocks measured best (48-80 within 1 us per step); regions above half
+// the 32 MB of L2 are not warmed.  MMR_L2_WARM_BLOCKS overrides the count.
+constexpr int kWarmBlocks = 64;
+constexpr int64_t kWarmMaxBytes = int64_t{16} << 20;
+
 struct DeviceState {
   std::shared_ptr<const DeviceModel> model;
   mmr::KvDtype kv = mmr::kKvF32;
@@ -74,6 +81,10 @@ struct DeviceState {
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;  // (attention splits, steps) -> captured steps
   bool use_graphs = true;
   bool combine_kernel = false;  // merge attention splits in a separate kernel, not the O prologue
+  // L2-warming blocks of the single-sequence attention launch (0 = none) and
+  // the GPU's CU count, which bounds head blocks + warming blocks.
+  int warm_blocks = kWarmBlocks;
+  int cus = 0;
 
   ~DeviceState() {
     if (stream) (void)hipStreamSynchronize(stream);
@@ -244,6 +255,13 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->prefill_tokenwise = (pt && pt[0] == '1') || !device_->gemm_prefill;
   const char* rs = std::getenv("MMR_GEMM_REGISTER_STAGED");
   s->gemm_register_staged = rs && rs[0] == '1';
+  if (const char* wb = std::getenv("MMR_L2_WARM_BLOCKS"))
+    s->warm_blocks = std::max(0, std::atoi(wb)) / mmr::kXcds * mmr::kXcds;
+  {
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "hipGetDevice");
+    check_hip(hipDeviceGetAttribute(&s->cus, hipDeviceAttributeMultiprocessorCount, dev), "CU count");
+  }
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
   const int64_t F = c.intermediate_size, V = c.vocab_size;
   const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
@@ -378,6 +396,22 @@ enum StepKernel : int { kQkv = 0, kAttention = 1, kOProj = 2, kGateUp = 3, kDown
 // One kernel (or, for kOProj with many splits, the combine + GEMV pair) of
 // the decode step; `bookkeeping` (finalize only) lets it write seq[pos + 1]
 // and advance the device position.
+// The bytes each block of a GEMV launch with plan p reads (W fp16 [rows][k],
+// rows in consecutive runs per block), as an L2-warming region; unused when
+// the region's byte offsets do not fit 32 bits.
+mmr::L2Warm gemv_warm_region(const __half* w, int rows, int k, const mmr::GemvPlan& p) {
+  mmr::L2Warm r;
+  const int64_t row_bytes = int64_t{k} * 2;
+  const int64_t bytes = rows * row_bytes;
+  const int64_t block_bytes = int64_t{mmr::kGemvBlock / p.lanes_per_row * p.rows_per_group} * row_bytes;
+  if (bytes + block_bytes >= (int64_t{1} << 32)) return r;
+  r.base = w;
+  r.bytes = static_cast<uint32_t>(bytes);
+  r.block_bytes = static_cast<uint32_t>(block_bytes);
+  r.blocks = p.blocks;
+  return r;
+}
+
 void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool bookkeeping) {
   const DeviceModel& m = *s.model;
   const auto& c = m.cfg;
@@ -426,6 +460,21 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       t.splits = splits;
       t.part = s.attn_part;
       t.err = s.err;
+      // While the head blocks run on part of the GPU, extra blocks load this
+      // layer's O, gate_up and down weights into the L2s of the XCDs whose
+      // blocks will read them; the warming blocks must not queue behind the
+      // head blocks, and the regions must fit the L2s with room to spare.
+      if (s.warm_blocks > 0 && int64_t{splits} * Hq + s.warm_blocks <= s.cus) {
+        t.warm[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
+        t.warm[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
+        t.warm[2] = gemv_warm_region(L.down, H, F, m.plan_down);
+        int64_t bytes = 0;
+        for (const auto& r : t.warm) bytes += r.bytes;
+        if (bytes <= kWarmMaxBytes)
+          t.warm_blocks = s.warm_blocks;
+        else
+          for (auto& r : t.warm) r = mmr::L2Warm{};
+      }
       check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "attention");
       return;
     }

@@ -169,6 +169,30 @@ def test_graph_replays_match_eager_launches(gpu, monkeypatch):
         tok_g = tok_e = int(np.argmax(lg))
 
 
+def test_l2_warming_blocks_leave_the_step_unchanged(gpu, monkeypatch):
+    # The attention launch's L2-warming blocks (on by default) only load the
+    # layer's O / gate_up / down weights: the decode with them equals the
+    # decode without, bit for bit, at configs[3]'s shape (16 splits x 8 heads
+    # + 64 warming blocks), and both equal the golden tokens.
+    mmr = gpu
+    print("[case] cfg3 512 + 256 kv=f16, warming on / off", flush=True)
+    g = load_golden("cfg3")
+    m = synth_model(mmr, g)
+    n = len(g["prompt"]) + g["max_new"]
+    warm = m.make_state(n, mmr.KV_F16)
+    monkeypatch.setenv("MMR_L2_WARM_BLOCKS", "0")
+    cold = m.make_state(n, mmr.KV_F16)
+    monkeypatch.delenv("MMR_L2_WARM_BLOCKS")
+    for st in (warm, cold):
+        st.enqueue_prefill(g["prompt"])
+        st.enqueue_decode(g["max_new"] - 1)
+        st.synchronize()
+    got = warm.read_sequence(len(g["prompt"]), g["max_new"])
+    np.testing.assert_array_equal(got, cold.read_sequence(len(g["prompt"]), g["max_new"]))
+    assert got.tolist() == g["generated"]
+    np.testing.assert_array_equal(warm.read_logits(), cold.read_logits())
+
+
 def test_state_reset_and_reuse(gpu):
     mmr = gpu
     g = load_golden("mini")
