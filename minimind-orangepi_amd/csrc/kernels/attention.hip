@@ -588,9 +588,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     }
     if (wave == 0) {
       if constexpr (MODE == kAttnFused) wave_norm_rope_pair<D>(qx0, qx1, qw0, qw1, a.eps, rc, rs);
+      // q staged times log2(e) / sqrt(d): the scores come out divided by
+      // sqrt(d) (decoder_layer.cpp:213) and in base-2 units for exp2.
+      const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(D));
       if (in_pair) {
-        q_s[d0] = qx0;
-        q_s[d1] = qx1;
+        q_s[d0] = qx0 * qscale;
+        q_s[d1] = qx1 * qscale;
       }
     }
     // The block owning tile p / TT places the new token's row in its stage;
@@ -611,7 +614,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
       append_new = in_pair && r == 0;
     }
 
-    const float sqrt_d = sqrtf(static_cast<float>(D));
     auto fetch_tile = [&](int tile) {
       const int t0 = tile * TT;
       const int rows = min(TT, n_keys - t0);
@@ -672,11 +674,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
       }
       dot = group_sum<kLanesPerTok>(dot);
       const bool live = tok < rows;
-      const float sc = live ? dot / sqrt_d : -INFINITY;  // decoder_layer.cpp:213 divides by sqrt(d)
-      // ---- the wave's online softmax (a wave may have no live token yet) ----
+      const float sc = live ? dot : -INFINITY;  // score / sqrt(d), times log2(e)
+      // ---- the wave's online softmax in base 2 (a wave may have no live
+      // token yet) ----
       const float m_new = fmaxf(m_run, group_max<kWave>(sc));
-      const float alpha = m_new == -INFINITY ? 1.0f : expf(m_run - m_new);
-      const float pv = live ? expf(sc - m_new) : 0.0f;
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      const float pv = live ? __builtin_amdgcn_exp2f(sc - m_new) : 0.0f;
       l_run = l_run * alpha + group_sum<kWave>(share == 0 ? pv : 0.0f);
       m_run = m_new;
       // ---- P.V over the wave's tokens ----
@@ -698,7 +701,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   }
 
   // ---- merge the waves' (m, l, o) in wave order; neutral when the split had
-  // no tile ----
+  // no tile.  m is in base-2 units until the store, which converts it to the
+  // natural-log units of the split partials. ----
   if (lane < kPairs) *reinterpret_cast<float2*>(&red_o[wave][2 * lane]) = pacc;
   if (lane == 0) {
     red_m[wave] = m_run;
@@ -710,7 +714,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w]);
   float e[kAttnWaves];
 #pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) e[w] = M == -INFINITY ? 0.0f : expf(red_m[w] - M);
+  for (int w = 0; w < kAttnWaves; ++w) e[w] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w] - M);
   for (int idx = threadIdx.x; idx < D; idx += kAttnThreads) {
     float o = 0.0f;
 #pragma unroll
@@ -722,7 +726,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
 #pragma unroll
     for (int w = 0; w < kAttnWaves; ++w) L = fmaf(e[w], red_l[w], L);
     float* dst = a.part + attn_ml_offset(g, split, r, S, R, D, a.hkv);
-    dst[0] = M;
+    dst[0] = M * 0.6931471805599453f;  // ln 2
     dst[1] = L;
   }
   // The new token's k / v (rounded to the cache dtype above), after every
