@@ -660,17 +660,32 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
       if constexpr (decltype(prefetch)::value) fetch_tile(tile + S);
       __syncthreads();
 
+      // Every LDS read of the tile step goes out before any arithmetic: the
+      // K and q shares for the scores, then the wave's V rows for P.V.  LDS
+      // returns in order, so the scores wait for K and q alone and the V rows
+      // arrive while the softmax runs (left to itself the compiler keeps two
+      // V reads in flight and waits on each).
+      float4 k4[kQuadsPerLane], q4[kQuadsPerLane];
+#pragma unroll
+      for (int c = 0; c < kQuadsPerLane; ++c) {
+        const int col = 4 * (c * kLanesPerTok + share);
+        k4[c] = *reinterpret_cast<const float4*>(&k_s[tok][col]);
+        q4[c] = *reinterpret_cast<const float4*>(&q_s[col]);
+      }
+      float2 vrow[kTokPerWave];
+#pragma unroll
+      for (int t = 0; t < kTokPerWave; ++t)
+        vrow[t] = *reinterpret_cast<const float2*>(&v_s[wave * kTokPerWave + t][2 * pv_pair]);
+      asm volatile("" : : : "memory");
+
       // ---- scores of the wave's tokens ----
       float dot = 0.0f;
 #pragma unroll
       for (int c = 0; c < kQuadsPerLane; ++c) {
-        const int col = 4 * (c * kLanesPerTok + share);
-        const float4 k4 = *reinterpret_cast<const float4*>(&k_s[tok][col]);
-        const float4 q4 = *reinterpret_cast<const float4*>(&q_s[col]);
-        dot = fmaf(q4.x, k4.x, dot);
-        dot = fmaf(q4.y, k4.y, dot);
-        dot = fmaf(q4.z, k4.z, dot);
-        dot = fmaf(q4.w, k4.w, dot);
+        dot = fmaf(q4[c].x, k4[c].x, dot);
+        dot = fmaf(q4[c].y, k4[c].y, dot);
+        dot = fmaf(q4[c].z, k4[c].z, dot);
+        dot = fmaf(q4[c].w, k4[c].w, dot);
       }
       dot = group_sum<kLanesPerTok>(dot);
       const bool live = tok < rows;
@@ -687,9 +702,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
 #pragma unroll
       for (int t = 0; t < kTokPerWave; ++t) {
         const float pt = lane_value(pv, t * kLanesPerTok);
-        const float2 v = *reinterpret_cast<const float2*>(&v_s[wave * kTokPerWave + t][2 * pv_pair]);
-        acc.x = fmaf(pt, v.x, acc.x);
-        acc.y = fmaf(pt, v.y, acc.y);
+        acc.x = fmaf(pt, vrow[t].x, acc.x);
+        acc.y = fmaf(pt, vrow[t].y, acc.y);
       }
       pacc = acc;
       // The next tile's staging overwrites k_s / v_s: every wave must be done.
