@@ -494,7 +494,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   if (static_cast<int>(blockIdx.x) >= S * a.hq) {
     const int first = (S * a.hq + kXcds - 1) / kXcds * kXcds;
     if (MODE == kAttnFused && static_cast<int>(blockIdx.x) >= first)
-      l2_warm<kAttnThreads>(a.warm, static_cast<int>(blockIdx.x) - first, a.warm_blocks, &k_s[0][0]);
+      l2_warm<kAttnThreads>(a.warm, static_cast<int>(blockIdx.x) - first, &k_s[0][0]);
     return;
   }
   // Block -> (split, group, head): the R head-blocks of one (split, group)
@@ -904,9 +904,9 @@ hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
     attention_split_kernel<KV, D, kAttnFused, true><<<group_grid, block, 0, s>>>(a);
   } else if (static_cast<int64_t>(a.splits) * a.hq <= kHeadKernelMaxBlocks) {
     int blocks = a.splits * a.hq;
-    if (mode == kAttnFused && a.warm_blocks > 0) {
-      if (a.warm_blocks % kXcds != 0) return hipErrorInvalidValue;
-      blocks = (blocks + kXcds - 1) / kXcds * kXcds + a.warm_blocks;
+    if (mode == kAttnFused && a.warm.blocks > 0) {
+      if (a.warm.blocks % kXcds != 0) return hipErrorInvalidValue;
+      blocks = (blocks + kXcds - 1) / kXcds * kXcds + a.warm.blocks;
     }
     const dim3 head_grid(blocks);
     if (mode == kAttnFused) {

@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kHeadThreads) void batch_head_kernel(const float* p
 // 16x16x32 MFMA per plane covers the block; the products are exact and
 // accumulate in fp32, and the result is multiplied by 1 / s (exact).
 // Output: part[split][m][n], every element written exactly once.
-constexpr int kSplitRows = 64;
+constexpr int kSplitRows = kSplitKRows;
 constexpr int kSplitMaxKc = 256;
 constexpr int kSplitMaxM = 32;
 
@@ -398,10 +398,20 @@ constexpr int kResManyRows = 64;
 template <bool kFinal, bool kSplit, int kResThreads>
 __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float* h, const float* part, int splits,
                                                                           int batch, int cols, const float* w,
-                                                                          float eps, float* x, SplitPlanes sp) {
+                                                                          float eps, float* x, SplitPlanes sp,
+                                                                          L2WarmSet warm) {
   constexpr int kResGroups = kResThreads / 256;
   __shared__ float4 red[kResGroups][kResChunkQuads];
   __shared__ float s_ss[kResThreads / kWave];
+  // Blocks past the rows: padding up to a multiple of kXcds, then the
+  // L2-warming blocks (their loads land in red, 1 KB per wave).
+  static_assert(sizeof(red) >= kResThreads / kWave * kWave * 16, "a 1 KB landing zone per wave");
+  if (static_cast<int>(blockIdx.x) >= batch) {
+    const int first = (batch + kXcds - 1) / kXcds * kXcds;
+    if (static_cast<int>(blockIdx.x) >= first)
+      l2_warm<kResThreads>(warm, static_cast<int>(blockIdx.x) - first, &red[0][0]);
+    return;
+  }
   const int b = blockIdx.x;
   const int nq = cols / 4;
   const int grp = threadIdx.x / 256, t = threadIdx.x % 256;
@@ -640,23 +650,26 @@ hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream) {
 
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,
                                       float eps, float* x, bool final_norm, hipStream_t stream,
-                                      const SplitPlanes* split) {
+                                      const SplitPlanes* split, const L2WarmSet* warm) {
   if (batch <= 0 || cols <= 0 || cols % 4 != 0 || splits < 0) return hipErrorInvalidValue;
   if (split && (!split->hi || !split->lo || !split->inv)) return hipErrorInvalidValue;
   if (!x && !split) return hipErrorInvalidValue;
+  if (warm && (warm->blocks < 0 || warm->blocks % kXcds != 0)) return hipErrorInvalidValue;
   const SplitPlanes sp = split ? *split : SplitPlanes{};
+  const L2WarmSet ws = warm ? *warm : L2WarmSet{};
+  const int grid = ws.blocks > 0 ? (batch + kXcds - 1) / kXcds * kXcds + ws.blocks : batch;
   auto run = [&](auto threads) {
     constexpr int T = decltype(threads)::value;
     if (final_norm) {
       if (split) {
-        batch_residual_norm_kernel<true, true, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+        batch_residual_norm_kernel<true, true, T><<<grid, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp, ws);
       } else {
-        batch_residual_norm_kernel<true, false, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+        batch_residual_norm_kernel<true, false, T><<<grid, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp, ws);
       }
     } else if (split) {
-      batch_residual_norm_kernel<false, true, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+      batch_residual_norm_kernel<false, true, T><<<grid, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp, ws);
     } else {
-      batch_residual_norm_kernel<false, false, T><<<batch, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp);
+      batch_residual_norm_kernel<false, false, T><<<grid, T, 0, stream>>>(h, part, splits, batch, cols, w, eps, x, sp, ws);
     }
   };
   if (batch >= kResManyRows) {

@@ -29,7 +29,8 @@ __device__ __forceinline__ void half8_to_float8(const uint4& u, float* f) {
 // 2^-22, i.e. an absolute error below (a + 0.5) / b * 2^-22 < 0.5 / b while
 // a + 0.5 < 2^21, so the truncation is exact.  (A runtime integer division is
 // a long instruction sequence; this is three instructions.)  The GEMV combine
-// prologue gives it element indices below 1024 and head indices below 16.
+// prologue gives it element indices below 1024 and head indices below 16,
+// l2_warm chunk indices below 2^16 (rows x 16-byte chunks of one block).
 __device__ __forceinline__ int small_quotient(int a, int b) {
   return static_cast<int>((static_cast<float>(a) + 0.5f) * __builtin_amdgcn_rcpf(static_cast<float>(b)));
 }
@@ -151,23 +152,36 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_byte*)p));
 }
 
-// Warming block j of n (n a multiple of kXcds; the first warming block's id
-// is a multiple of kXcds, so j % kXcds is the XCD it runs on): loads the
-// slices of every region read by that region's blocks on the same XCD, with
-// direct-to-LDS loads that hold no registers, into the 1 KB per wave at lds
-// (the block's scratch, overwritten), and waits for them.
+// Warming block j of set.blocks (the first warming block's id is a multiple
+// of kXcds, so j % kXcds is the XCD it runs on): loads what the reading
+// blocks of every region on the same XCD will read (the XCD's warming blocks
+// take every (set.blocks / kXcds)-th of those blocks), with direct-to-LDS
+// loads that hold no registers, into the 1 KB per wave at lds (the block's
+// scratch, overwritten), and waits for them.
 template <int kThreads>
-__device__ void l2_warm(const L2Warm (&regions)[kL2WarmRegions], int j, int n, void* lds) {
-  const int xcd = j % kXcds, slot = j / kXcds, slots = n / kXcds;
+__device__ void l2_warm(const L2WarmSet& set, int j, void* lds) {
+  const int xcd = j % kXcds, slot = j / kXcds, slots = set.blocks / kXcds;
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_address(lds) + (threadIdx.x / kWave) * (kWave * 16));
 #pragma unroll
   for (int r = 0; r < kL2WarmRegions; ++r) {
-    const L2Warm& g = regions[r];
+    const L2Warm& g = set.region[r];
     if (g.base == nullptr) continue;
-    for (int b = xcd + kXcds * slot; b < g.blocks; b += kXcds * slots) {
-      const uint32_t lo = static_cast<uint32_t>(b) * g.block_bytes;
-      const uint32_t hi = min(lo + g.block_bytes, g.bytes);
-      for (uint32_t off = lo + threadIdx.x * 16; off < hi; off += kThreads * 16) dma_load<16>(g.base, off, m0);
+    const int units = g.units_x * g.units_y;
+    const uint32_t seg_chunks = g.seg_bytes / 16;
+    for (int u = xcd + kXcds * slot; u < units; u += kXcds * slots) {
+      const int ux = u % g.units_x, uy = u / g.units_x;
+      const uint32_t lo = static_cast<uint32_t>(ux) * g.rows * g.row_bytes + static_cast<uint32_t>(uy) * g.seg_bytes;
+      if (g.seg_bytes == g.row_bytes) {  // whole rows: one contiguous run
+        const uint32_t hi = min(lo + static_cast<uint32_t>(g.rows) * g.row_bytes, g.bytes);
+        for (uint32_t off = lo + threadIdx.x * 16; off < hi; off += kThreads * 16) dma_load<16>(g.base, off, m0);
+      } else {  // one segment of each of the block's rows
+        const uint32_t chunks = static_cast<uint32_t>(g.rows) * seg_chunks;
+        for (uint32_t c = threadIdx.x; c < chunks; c += kThreads) {
+          const uint32_t row = static_cast<uint32_t>(small_quotient(static_cast<int>(c), static_cast<int>(seg_chunks)));
+          const uint32_t off = lo + row * g.row_bytes + (c - row * seg_chunks) * 16;
+          if (off < g.bytes) dma_load<16>(g.base, off, m0);
+        }
+      }
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" : : : "memory");

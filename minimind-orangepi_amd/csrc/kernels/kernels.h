@@ -14,20 +14,33 @@
 namespace mmr {
 
 // -------------------------------------------------------------- L2 warming ----
-// A later kernel's weight stream, described by the blocks that will read it:
-// block b of that kernel reads bytes [b * block_bytes, (b + 1) * block_bytes)
-// of base (the last block fewer).  The dispatcher deals a grid's blocks
-// round-robin over the 8 XCDs (block b on XCD b % 8), each XCD has its own L2,
-// and L2 contents outlive a kernel boundary; so blocks of an earlier kernel on
-// XCD x that load the slices of the later kernel's blocks b = x (mod 8) turn
-// that kernel's weight loads into L2 hits.
+// A later kernel's reads, described by the blocks that make them.  The
+// reading grid has units_x x units_y blocks (x fastest: block (x, y) has id
+// x + y * units_x); block (x, y) reads rows [x * rows, (x + 1) * rows) of a
+// row-major region (row_bytes apart), bytes [y * seg_bytes, (y + 1) *
+// seg_bytes) of each row (seg_bytes = row_bytes: whole rows), never past
+// `bytes`.  The dispatcher deals a grid's blocks round-robin over the 8 XCDs
+// (block id i on XCD i % 8), each XCD has its own L2, and L2 contents outlive
+// a kernel boundary; so blocks of an earlier kernel on XCD x that load what
+// the later kernel's blocks on XCD x will read turn those loads into L2 hits.
+// A GEMV block reads whole rows (units_y = 1); a split-K GEMM block one K
+// chunk of 64 rows.
 constexpr int kXcds = 8;
 constexpr int kL2WarmRegions = 3;
 struct L2Warm {
   const void* base = nullptr;  // nullptr: region unused
   uint32_t bytes = 0;          // region size (byte offsets are 32-bit)
-  uint32_t block_bytes = 0;    // a multiple of 16
-  int blocks = 0;              // the reading kernel's grid
+  uint32_t row_bytes = 0;      // multiple of 16
+  uint32_t seg_bytes = 0;      // multiple of 16, <= row_bytes
+  int rows = 0;                // rows per block
+  int units_x = 0, units_y = 1;
+};
+// Regions and the number of warming blocks that load them (a multiple of
+// kXcds; 0 = none).  A kernel that takes an L2WarmSet launches that many
+// extra blocks past its own grid (rounded up to a multiple of kXcds).
+struct L2WarmSet {
+  L2Warm region[kL2WarmRegions];
+  int blocks = 0;
 };
 
 // ---------------------------------------------------------------- GEMV ----
@@ -154,12 +167,10 @@ struct AttnArgs {
   // the page of sequence b's token t; rows = pages_per_seq * kKvPage.
   const int32_t* page_table = nullptr;
   int pages_per_seq = 0;
-  // Single-sequence fused launches on the per-head kernel: warm_blocks extra
-  // blocks (a multiple of kXcds, 0 = none), past the head blocks rounded up to
-  // a multiple of kXcds, load the warm regions into the XCDs' L2s while the
-  // head blocks run.  Other launch shapes ignore them.
-  L2Warm warm[kL2WarmRegions];
-  int warm_blocks = 0;
+  // Single-sequence fused launches on the per-head kernel: warming blocks past
+  // the head blocks load these regions into the XCDs' L2s while the head
+  // blocks run.  Other launch shapes ignore them.
+  L2WarmSet warm;
 };
 constexpr int kKvPage = 64;  // tokens per KV page (a multiple of every attention tile)
 
@@ -341,6 +352,8 @@ struct SplitKArgs {
   int64_t attn_part_stride = 0;
   int hq = 0, hkv = 0, d = 0;
 };
+// W rows per split-K block: the launch grid is (ceil(n / kSplitKRows), k / kc).
+constexpr int kSplitKRows = 64;
 // K chunk (a multiple of 32 that divides k, at most 256; 0 when k is not a
 // multiple of 32); splits = k / kc.
 int splitk_chunk(int n, int k);
@@ -353,9 +366,10 @@ bool splitk_combine_supported(int m, int kc, int attn_splits, int d);
 hipError_t launch_gemm_splitk(const SplitKArgs& g, hipStream_t stream);
 // h[b] += sum_s part[s][b] (splits may be 0), x[b] = RMSNorm(h[b]); x may be
 // null when `split` receives the normalised rows instead (or as well).
+// `warm`: warming blocks past the batch rows (see L2WarmSet).
 hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, int batch, int cols, const float* w,
                                       float eps, float* x, bool final_norm, hipStream_t stream,
-                                      const SplitPlanes* split = nullptr);
+                                      const SplitPlanes* split = nullptr, const L2WarmSet* warm = nullptr);
 // act[b][i] = silu(sum_s part[s][b][2i]) * sum_s part[s][b][2i + 1].
 hipError_t launch_batch_swiglu(const float* part, int splits, int batch, int f, float* act, hipStream_t stream);
 // out[b][i] = sum_s part[s][b][i].

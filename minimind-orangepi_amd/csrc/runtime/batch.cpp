@@ -36,6 +36,11 @@
 
 namespace minimind::model {
 
+// Warming blocks per residual + norm launch: 128 measured best (B = 32, 256 ->
+// 4096: 892.9 -> 885.3 us per step; 64: no gain; 192 / 256: 887.3 / 888.7).
+constexpr int kBatchWarmBlocks = 128;
+constexpr int64_t kBatchWarmMaxBytes = int64_t{16} << 20;  // half the 32 MB of L2
+
 struct BatchDeviceState {
   std::shared_ptr<const DeviceModel> model;
   mmr::KvDtype kv = mmr::kKvF16;
@@ -66,6 +71,10 @@ struct BatchDeviceState {
   hipStream_t stream = nullptr;
   std::map<int, hipGraphExec_t> graphs;
   bool use_graphs = true;
+  // L2-warming blocks of the residual + norm launches (0 = none): the one
+  // after the O projection loads gate_up and down, the one after down the
+  // next layer's qkv (after the last layer the lm_head's).
+  int warm_blocks = kBatchWarmBlocks;
 
   ~BatchDeviceState() {
     if (stream) (void)hipStreamSynchronize(stream);
@@ -198,6 +207,38 @@ int project_swiglu(const BatchDeviceState& s, const float* gu, int gu_parts, con
   return project(s, s.act, w, n, f, 0);
 }
 
+// The split-K launch of an n x k projection with chunk kc (grid
+// (ceil(n / kSplitKRows), k / kc): block (x, y) reads a kc-column chunk of 64
+// W rows) as an L2-warming region; unused for the dense fallback (kc = 0) or
+// byte offsets past 32 bits.
+mmr::L2Warm splitk_warm_region(const __half* w, int n, int k, int kc) {
+  mmr::L2Warm r;
+  const int64_t bytes = int64_t{n} * k * 2;
+  if (kc <= 0 || bytes + int64_t{k} * 2 * mmr::kSplitKRows >= (int64_t{1} << 32)) return r;
+  r.base = w;
+  r.bytes = static_cast<uint32_t>(bytes);
+  r.row_bytes = static_cast<uint32_t>(k * 2);
+  r.seg_bytes = static_cast<uint32_t>(kc * 2);
+  r.rows = mmr::kSplitKRows;
+  r.units_x = (n + mmr::kSplitKRows - 1) / mmr::kSplitKRows;
+  r.units_y = k / kc;
+  return r;
+}
+
+// A warming set over the given regions when they fit the byte budget.
+mmr::L2WarmSet warm_set(int blocks, std::initializer_list<mmr::L2Warm> regions) {
+  mmr::L2WarmSet w;
+  int64_t bytes = 0;
+  int i = 0;
+  for (const auto& r : regions) {
+    if (i == mmr::kL2WarmRegions) break;
+    w.region[i++] = r;
+    bytes += r.bytes;
+  }
+  w.blocks = bytes > 0 && bytes <= kBatchWarmMaxBytes ? blocks : 0;
+  return w;
+}
+
 void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
   const DeviceModel& m = *s.model;
   const auto& c = m.cfg;
@@ -208,9 +249,17 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
   const int B = static_cast<int>(s.batch);
   const int seq_stride = static_cast<int>(s.capacity + 1);
   const size_t L = m.layers.size();
+  // K chunks of the split-K projections (as project / project_swiglu choose them).
+  auto chunk = [&](int n, int k, int max_parts) { return B <= 32 ? proj_chunk(n, k, max_parts) : 0; };
+  const int kc_qkv = chunk(qkv_w, H, mmr::kAttnMaxQkvParts), kc_gu = chunk(2 * F, H, 0), kc_down = chunk(H, F, 0);
+  const int kc_lm = chunk(V, H, 0);
+  auto warm_qkv = [&](size_t l) {
+    return warm_set(s.warm_blocks, {splitk_warm_region(m.layers[l].qkv, qkv_w, H, kc_qkv)});
+  };
   check_hip(mmr::launch_batch_embed(m.embed, s.seq, seq_stride, s.pos, B, V, H, s.h, s.stream), "batch embed");
+  const mmr::L2WarmSet warm0 = warm_qkv(0);
   check_hip(mmr::launch_batch_residual_norm(s.h, nullptr, 0, B, H, m.layers[0].input_norm, c.rms_norm_eps, s.x, false,
-                                            s.stream),
+                                            s.stream, nullptr, &warm0),
             "batch input norm");
   for (size_t l = 0; l < L; ++l) {
     const LayerDev& Ld = m.layers[l];
@@ -241,15 +290,19 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
     t.pages_per_seq = static_cast<int>(s.pages_per_seq);
     check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "batch attention");
     const int o_parts = project_combine(s, splits, Ld.o, H, Hq, Hkv, D);
+    const mmr::L2WarmSet warm_mlp = warm_set(s.warm_blocks, {splitk_warm_region(Ld.gate_up, 2 * F, H, kc_gu),
+                                                             splitk_warm_region(Ld.down, H, F, kc_down)});
     check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, o_parts, B, H, Ld.post_norm, c.rms_norm_eps, s.x, false,
-                                              s.stream),
+                                              s.stream, nullptr, &warm_mlp),
               "batch residual + post norm");
     const int gu_parts = project(s, s.x, Ld.gate_up, 2 * F, H, 0, s.proj_gu);
     const int down_parts = project_swiglu(s, s.proj_gu, gu_parts, Ld.down, H, F);
     const bool last = l + 1 == L;
+    const mmr::L2WarmSet warm_next =
+        last ? warm_set(s.warm_blocks, {splitk_warm_region(m.lm_head, V, H, kc_lm)}) : warm_qkv(l + 1);
     check_hip(mmr::launch_batch_residual_norm(s.h, s.proj, down_parts, B, H,
                                               last ? m.final_norm : m.layers[l + 1].input_norm, c.rms_norm_eps, s.x,
-                                              last, s.stream),
+                                              last, s.stream, nullptr, &warm_next),
               "batch residual + norm");
   }
   const int lm_parts = project(s, s.x, m.lm_head, V, H, 0);
@@ -312,6 +365,8 @@ BatchState LanguageModel::make_batch_state(int64_t batch, int64_t capacity, KvCa
   s->batch = batch;
   s->capacity = capacity;
   s->pages_per_seq = (capacity + mmr::kKvPage - 1) / mmr::kKvPage;
+  if (const char* wb = std::getenv("MMR_L2_WARM_BLOCKS"))
+    s->warm_blocks = std::max(0, std::atoi(wb)) / mmr::kXcds * mmr::kXcds;
   const char* nog = std::getenv("MMR_NO_GRAPH");
   s->use_graphs = !(nog && nog[0] == '1');
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;

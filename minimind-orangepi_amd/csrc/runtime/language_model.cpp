@@ -403,12 +403,14 @@ mmr::L2Warm gemv_warm_region(const __half* w, int rows, int k, const mmr::GemvPl
   mmr::L2Warm r;
   const int64_t row_bytes = int64_t{k} * 2;
   const int64_t bytes = rows * row_bytes;
-  const int64_t block_bytes = int64_t{mmr::kGemvBlock / p.lanes_per_row * p.rows_per_group} * row_bytes;
-  if (bytes + block_bytes >= (int64_t{1} << 32)) return r;
+  const int rows_per_block = mmr::kGemvBlock / p.lanes_per_row * p.rows_per_group;
+  if (bytes + rows_per_block * row_bytes >= (int64_t{1} << 32)) return r;
   r.base = w;
   r.bytes = static_cast<uint32_t>(bytes);
-  r.block_bytes = static_cast<uint32_t>(block_bytes);
-  r.blocks = p.blocks;
+  r.row_bytes = static_cast<uint32_t>(row_bytes);
+  r.seg_bytes = r.row_bytes;
+  r.rows = rows_per_block;
+  r.units_x = p.blocks;
   return r;
 }
 
@@ -465,15 +467,15 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       // blocks will read them; the warming blocks must not queue behind the
       // head blocks, and the regions must fit the L2s with room to spare.
       if (s.warm_blocks > 0 && int64_t{splits} * Hq + s.warm_blocks <= s.cus) {
-        t.warm[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
-        t.warm[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
-        t.warm[2] = gemv_warm_region(L.down, H, F, m.plan_down);
+        t.warm.region[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
+        t.warm.region[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
+        t.warm.region[2] = gemv_warm_region(L.down, H, F, m.plan_down);
         int64_t bytes = 0;
-        for (const auto& r : t.warm) bytes += r.bytes;
+        for (const auto& r : t.warm.region) bytes += r.bytes;
         if (bytes <= kWarmMaxBytes)
-          t.warm_blocks = s.warm_blocks;
+          t.warm.blocks = s.warm_blocks;
         else
-          for (auto& r : t.warm) r = mmr::L2Warm{};
+          t.warm = mmr::L2WarmSet{};
       }
       check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "attention");
       return;
