@@ -528,7 +528,7 @@ def main() -> int:
             kernels[name]["splits_note"] = ("attention kernel only (one block per query head and split at this "
                                             "context); the split combine runs in the o-projection prologue")
         log(f"kernel {name:9s} {avg_us:8.3f} us  {kernels[name]['gbs']:8.1f} GB/s")
-    # The step's attention launch also carries 64 L2-warming blocks that load
+    # The step's attention launch also carries L2-warming blocks that load
     # the layer's O, gate_up and down weights (bytes the next three kernels
     # then read from L2).  The same kernel without them, on a state made with
     # warming off at the same context:
@@ -544,7 +544,7 @@ def main() -> int:
     a = kernels["attention"]
     a["avg_us_without_warm_blocks"] = round(cold.time_step_kernel(names.index("attention"), 0, args.kernel_reps), 3)
     a["warm_bytes_per_launch"] = warm_bytes
-    a["warm_note"] = ("avg_us is the launch as the step runs it, with 64 extra blocks loading the layer's O, "
+    a["warm_note"] = ("avg_us is the launch as the step runs it, with extra blocks on the idle CUs loading the layer's O, "
                       "gate_up and down weights into the L2s of the XCDs that read them next; "
                       "avg_us_without_warm_blocks is the attention work alone")
     log(f"kernel attention without warming blocks {a['avg_us_without_warm_blocks']:.3f} us")

@@ -33,10 +33,12 @@
 namespace minimind::model {
 
 // L2 warming in the single-sequence step (the attention launch loads the
-// layer's O, gate_up and down weights for the XCDs that will read them):
-// 64 blocks measured best (48-80 within 1 us per step); regions above half
-// the 32 MB of L2 are not warmed.  MMR_L2_WARM_BLOCKS overrides the count.
-constexpr int kWarmBlocks = 64;
+// layer's O, gate_up and down weights for the XCDs that will read them): the
+// warming blocks fill the CUs the head blocks leave idle, up to kWarmBlocks
+// (MiniMind2 at 768 keys, 128 head blocks: 96 or 128 warming blocks 255.2 us
+// per step, 64: 261.4, none: 263.5); regions above half the 32 MB of L2 are
+// not warmed.  MMR_L2_WARM_BLOCKS overrides the cap.
+constexpr int kWarmBlocks = 128;
 constexpr int64_t kWarmMaxBytes = int64_t{16} << 20;
 
 struct DeviceState {
@@ -462,18 +464,20 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       t.splits = splits;
       t.part = s.attn_part;
       t.err = s.err;
-      // While the head blocks run on part of the GPU, extra blocks load this
-      // layer's O, gate_up and down weights into the L2s of the XCDs whose
-      // blocks will read them; the warming blocks must not queue behind the
-      // head blocks, and the regions must fit the L2s with room to spare.
-      if (s.warm_blocks > 0 && int64_t{splits} * Hq + s.warm_blocks <= s.cus) {
+      // While the head blocks run on part of the GPU, extra blocks on the idle
+      // CUs load this layer's O, gate_up and down weights into the L2s of the
+      // XCDs whose blocks will read them; the regions must fit the L2s with
+      // room to spare.
+      const int idle = (s.cus - splits * Hq) / mmr::kXcds * mmr::kXcds;
+      const int warm_blocks = std::min(s.warm_blocks, idle);
+      if (warm_blocks > 0) {
         t.warm.region[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
         t.warm.region[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
         t.warm.region[2] = gemv_warm_region(L.down, H, F, m.plan_down);
         int64_t bytes = 0;
         for (const auto& r : t.warm.region) bytes += r.bytes;
         if (bytes <= kWarmMaxBytes)
-          t.warm.blocks = s.warm_blocks;
+          t.warm.blocks = warm_blocks;
         else
           t.warm = mmr::L2WarmSet{};
       }

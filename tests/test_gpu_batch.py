@@ -140,6 +140,32 @@ def test_batch_graph_replays_match_eager(gpu, monkeypatch):
         np.testing.assert_array_equal(graph.read_logits(b), eager.read_logits(b))
 
 
+def test_batch_l2_warming_leaves_the_step_unchanged(gpu, monkeypatch):
+    # The residual + norm launches' L2-warming blocks (on by default) only
+    # load the next GEMMs' weights: the batched decode with them equals the
+    # decode without, bit for bit, on MiniMind2's shapes (split-K GEMMs for
+    # qkv, gate_up, down and lm_head).
+    mmr = gpu
+    print("[case] batch cfg3 B=8, warming on / off", flush=True)
+    g = load_golden("cfg3")
+    m = synth_model(mmr, g)
+    rng = np.random.default_rng(21)
+    prompts = [[int(t) for t in rng.integers(0, g["config"]["vocab_size"], n)] for n in (40, 64, 17, 90, 8, 33, 71, 50)]
+    states = []
+    for warm in ("128", "0"):
+        monkeypatch.setenv("MMR_L2_WARM_BLOCKS", warm)
+        bs = m.make_batch_state(len(prompts), 160)
+        monkeypatch.delenv("MMR_L2_WARM_BLOCKS")
+        bs.prefill(prompts)
+        bs.decode(60)
+        bs.synchronize()
+        states.append(bs)
+    last = max(len(p) for p in prompts) + 60
+    for b in range(len(prompts)):
+        np.testing.assert_array_equal(states[0].read_sequence(b, 0, last + 1), states[1].read_sequence(b, 0, last + 1))
+        np.testing.assert_array_equal(states[0].read_logits(b), states[1].read_logits(b))
+
+
 def test_batch_error_behaviour(gpu):
     mmr = gpu
     g = load_golden("mini")

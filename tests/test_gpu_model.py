@@ -173,7 +173,7 @@ def test_l2_warming_blocks_leave_the_step_unchanged(gpu, monkeypatch):
     # The attention launch's L2-warming blocks (on by default) only load the
     # layer's O / gate_up / down weights: the decode with them equals the
     # decode without, bit for bit, at configs[3]'s shape (16 splits x 8 heads
-    # + 64 warming blocks), and both equal the golden tokens.
+    # + 128 warming blocks), and both equal the golden tokens.
     mmr = gpu
     print("[case] cfg3 512 + 256 kv=f16, warming on / off", flush=True)
     g = load_golden("cfg3")
