@@ -54,6 +54,7 @@ constexpr int kGemmLDH = kGemmBK + 8;  // halves per LDS row (16-byte aligned, c
 using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
+using i16x4 = short __attribute__((ext_vector_type(4)));
 
 // Per-thread staging registers of one K tile: BM x BK fp32 of A as float4s,
 // BN x BK fp16 of W as 8-half chunks; thread t takes chunks t, t + 256, ...
@@ -970,8 +971,15 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
         }
 #pragma unroll
         for (int j = 0; j < DT; ++j) {
-          const _Float16* vcol = &vh_s[(kt * 16 + 4 * kq) * LDH + 16 * j + qi];
-          const f16x4 va = {vcol[0], vcol[LDH], vcol[2 * LDH], vcol[3 * LDH]};
+          // A = V^T: lane (qi, kq) needs V[key 4 kq + i][dim 16 j + qi], i = 0..3,
+          // a column of the 4 x 16 block of V rows 4 kq .. 4 kq + 3, dims 16 j ..
+          // One transposing LDS read (ds_read_b64_tr_b16) delivers it: within a
+          // 16-lane group, lane i receives element i % 4 of the 8 bytes that lane
+          // 4 k + i / 4 addresses, for k = 0..3; so lane qi addresses row qi / 4,
+          // dims 4 (qi % 4) .. + 3 of the block.
+          const _Float16* vsrc = &vh_s[(kt * 16 + 4 * kq + qi / 4) * LDH + 16 * j + 4 * (qi % 4)];
+          const f16x4 va = __builtin_bit_cast(
+              f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(vsrc)));
           ot[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, ot[j], 0, 0, 0);
           ot[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, ot[j], 0, 0, 0);
         }
