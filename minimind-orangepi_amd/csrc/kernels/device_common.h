@@ -104,6 +104,41 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float best_v, int 
   return v > best_v || (v == best_v && i < best_i);
 }
 
+template <int kCtrl>
+__device__ __forceinline__ int dpp_move_int(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, kCtrl, 0xF, 0xF, false);
+}
+
+// (max, lowest index) over the 64 lanes of a wave with the DPP steps of
+// group_reduce, then the four rows' results in row order (v_readlane); every
+// lane ends with the result.  The pair order is associative and commutative,
+// so the steps cannot change it.  No LDS traffic: nothing waits on lgkmcnt.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  auto take = [&](float ov, int oi) {
+    if (argmax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  };
+  take(dpp_move<dpp::kQuadXor1>(v), dpp_move_int<dpp::kQuadXor1>(i));
+  take(dpp_move<dpp::kQuadXor2>(v), dpp_move_int<dpp::kQuadXor2>(i));
+  take(dpp_move<dpp::kRowHalfMirror>(v), dpp_move_int<dpp::kRowHalfMirror>(i));
+  take(dpp_move<dpp::kRowMirror>(v), dpp_move_int<dpp::kRowMirror>(i));
+  float bv = read_lane(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+  for (int row = 16; row < kWave; row += 16) {
+    const float rv = read_lane(v, row);
+    const int ri = __builtin_amdgcn_readlane(i, row);
+    if (argmax_better(rv, ri, bv, bi)) {
+      bv = rv;
+      bi = ri;
+    }
+  }
+  v = bv;
+  i = bi;
+}
+
 template <typename T>
 __device__ __forceinline__ float to_float(T v);
 template <>

@@ -34,6 +34,11 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
   const int k = a.k;
   const int kchunks = k >> 3;
   const int row0 = (blockIdx.x * kGroups + group) * RPG;
+  // kEpiArgmax position bookkeeping: read now, stored at the end.
+  int advance_from = 0;
+  if constexpr (EPI == kEpiArgmax) {
+    if (a.advance_pos != nullptr && blockIdx.x == 0) advance_from = *a.advance_pos;
+  }
 
   // 1. Every load that does not depend on another goes out before any
   //    arithmetic, so one memory latency covers them all, in this order: the
@@ -80,15 +85,78 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
   // 2. x chunks owned by this lane (+ fused prologue).
   float xv[CPL][8];
   if constexpr (PRO == kProEmbedRmsNorm) {
+    // The token at p = *pos: seq[p], or the argmax of the previous step's
+    // lm_head partials (every block reduces them).  pos and seq[p] are read
+    // through the scalar cache (no kernel writes them while this one runs,
+    // except seq_out[p], stored by block 0 only when no block reads seq[p]),
+    // so their dependent loads do not queue behind the vector loads.  The
+    // partial loads go out before the weights: vector loads complete in
+    // order, so the reduction waits for the partials alone.
+    using cint = __attribute__((address_space(4))) const int32_t;
+    const int p = *(cint*)a.pos;
+    constexpr int kPrevPer = kGemvMaxPrevParts / kGemvBlock;
+    const bool from_parts = a.prev_val != nullptr;
+    float pv[kPrevPer];
+    int pi[kPrevPer];
+    if (from_parts) {
+#pragma unroll
+      for (int i = 0; i < kPrevPer; ++i) {
+        const int j = min(static_cast<int>(threadIdx.x) + i * kGemvBlock, a.prev_parts - 1);
+        pv[i] = a.prev_val[j];
+        pi[i] = a.prev_idx[j];
+      }
+    }
     load_weights();
-    int token = a.seq[*a.pos];
+    int token;
+    if (from_parts) {
+      // (max, lowest index) is associative and commutative: the clamped
+      // duplicates and the reduction order cannot change the result.
+      float bv = pv[0];
+      int bi = pi[0];
+#pragma unroll
+      for (int i = 1; i < kPrevPer; ++i)
+        if (argmax_better(pv[i], pi[i], bv, bi)) {
+          bv = pv[i];
+          bi = pi[i];
+        }
+      wave_argmax(bv, bi);
+      __shared__ float s_bv[kGemvBlock / kWave];
+      __shared__ int s_bi[kGemvBlock / kWave];
+      if (threadIdx.x % kWave == 0) {
+        s_bv[threadIdx.x / kWave] = bv;
+        s_bi[threadIdx.x / kWave] = bi;
+      }
+      __syncthreads();
+      bv = s_bv[0];
+      bi = s_bi[0];
+#pragma unroll
+      for (int w = 1; w < kGemvBlock / kWave; ++w)
+        if (argmax_better(s_bv[w], s_bi[w], bv, bi)) {
+          bv = s_bv[w];
+          bi = s_bi[w];
+        }
+      const bool generated = p >= *(cint*)a.prompt_len;
+      if (generated) {
+        token = bi;
+        if (blockIdx.x == 0 && threadIdx.x == 0 && p < a.seq_len) a.seq_out[p] = bi;
+      } else {
+        token = ((cint*)a.seq)[p];
+      }
+    } else {
+      token = ((cint*)a.seq)[p];
+    }
     token = token < 0 ? 0 : (token >= a.vocab ? a.vocab - 1 : token);
     const uint4* erow = reinterpret_cast<const uint4*>(a.embed + static_cast<int64_t>(token) * k);
+    // Every chunk's load goes out before any is used (a use between them
+    // would wait for the first before the second is issued).
+    uint4 eraw[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) eraw[i] = erow[min(lane + G * i, kchunks - 1)];
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const int c = lane + G * i;
-      half8_to_float8(erow[min(c, kchunks - 1)], xv[i]);
-      if (c >= kchunks) {
+      half8_to_float8(eraw[i], xv[i]);
+      if (lane + G * i >= kchunks) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
       }
@@ -287,6 +355,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
         }
       a.part_val[blockIdx.x] = bv;
       a.part_idx[blockIdx.x] = bi;
+      if (a.advance_pos != nullptr && blockIdx.x == 0) *a.advance_pos = advance_from + 1;
     }
   }
 }

@@ -91,7 +91,23 @@ struct GemvArgs {
   // kEpiArgmax: one (value, index) pair per block
   float* part_val = nullptr;
   int* part_idx = nullptr;
+  // kProEmbedRmsNorm inside a replayed group of decode steps: when prev_val is
+  // set and *pos >= *prompt_len, the token is the argmax of the previous
+  // step's lm_head partials (prev_parts <= kGemvMaxPrevParts pairs, first
+  // index among equal maxima) instead of seq[*pos], and block 0 stores it to
+  // seq_out[*pos] (if *pos < seq_len; seq_out is seq): the argmax finalize's
+  // work, done where the token is consumed.
+  const float* prev_val = nullptr;
+  const int* prev_idx = nullptr;
+  int prev_parts = 0;
+  const int32_t* prompt_len = nullptr;
+  int32_t* seq_out = nullptr;
+  int seq_len = 0;
+  // kEpiArgmax: block 0 advances *advance_pos by one (the finalize's position
+  // bookkeeping, for a step whose finalize is folded into the next step).
+  int32_t* advance_pos = nullptr;
 };
+constexpr int kGemvMaxPrevParts = 2048;
 
 // Reduces the per-block argmax partials (first index among equal maxima),
 // writes the token, and optionally does the decode-step bookkeeping: the step

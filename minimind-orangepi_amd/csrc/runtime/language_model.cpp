@@ -416,7 +416,16 @@ mmr::L2Warm gemv_warm_region(const __half* w, int rows, int k, const mmr::GemvPl
   return r;
 }
 
-void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool bookkeeping) {
+// A step's place in a replayed group of steps: inside a group the argmax
+// finalize of every step but the last folds into the next step (its layer-0
+// qkv prologue reduces the lm_head partials; the lm_head launch advances the
+// position).
+struct StepLink {
+  bool token_from_partials = false;  // layer-0 qkv: token from the previous step's lm_head partials
+  bool advance_in_head = false;      // lm_head: advance the position (no finalize follows)
+};
+
+void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool bookkeeping, StepLink link = {}) {
   const DeviceModel& m = *s.model;
   const auto& c = m.cfg;
   const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
@@ -442,6 +451,14 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
         a.pos = s.pos;
         a.vocab = V;
         a.h_out = s.h;
+        if (link.token_from_partials) {
+          a.prev_val = s.lm_part_val;
+          a.prev_idx = s.lm_part_idx;
+          a.prev_parts = m.plan_lm.blocks;
+          a.prompt_len = s.prompt_len;
+          a.seq_out = s.seq;
+          a.seq_len = static_cast<int>(s.capacity + 1);
+        }
       }
       check_hip(mmr::launch_gemv(a, pro, mmr::kEpiStore, m.plan_qkv, s.stream), "qkv gemv");
       return;
@@ -542,6 +559,7 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       a.y = s.logits;
       a.part_val = s.lm_part_val;
       a.part_idx = s.lm_part_idx;
+      if (link.advance_in_head) a.advance_pos = s.pos;
       check_hip(mmr::launch_gemv(a, mmr::kProRmsNormFinal, mmr::kEpiArgmax, m.plan_lm, s.stream), "lm_head gemv");
       return;
     }
@@ -595,15 +613,25 @@ void enqueue_tiny_step(const DeviceState& s) {
   check_hip(mmr::launch_tiny_step(a, s.kv, s.stream), "small-model step");
 }
 
-void enqueue_step_kernels(const DeviceState& s, int splits) {
+// One decode step; first / last: its place in a replayed group of steps.  The
+// first step of a group reads its token from seq (the host may have written
+// it); inside the group the finalize folds into the next step's kernels.
+void enqueue_step_kernels(const DeviceState& s, int splits, bool first = true, bool last = true) {
   if (s.model->tiny) {
     enqueue_tiny_step(s);
     return;
   }
+  const bool fold = s.model->plan_lm.blocks <= mmr::kGemvMaxPrevParts;
   for (size_t l = 0; l < s.model->layers.size(); ++l)
-    for (int k = kQkv; k <= kDown; ++k) enqueue_kernel(s, k, l, splits, false);
-  enqueue_kernel(s, kHead, 0, splits, false);
-  enqueue_kernel(s, kFinalize, 0, splits, true);
+    for (int k = kQkv; k <= kDown; ++k) {
+      StepLink link;
+      link.token_from_partials = fold && !first && l == 0 && k == kQkv;
+      enqueue_kernel(s, k, l, splits, false, link);
+    }
+  StepLink head;
+  head.advance_in_head = fold && !last;
+  enqueue_kernel(s, kHead, 0, splits, false, head);
+  if (!head.advance_in_head) enqueue_kernel(s, kFinalize, 0, splits, true);
 }
 
 // One prefill chunk: prompt tokens at positions start .. start + n - 1 through
@@ -761,7 +789,7 @@ hipGraphExec_t capture_steps(DeviceState& s, int splits, int steps) {
   hipGraph_t graph = nullptr;
   check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   try {
-    for (int i = 0; i < steps; ++i) enqueue_step_kernels(s, splits);
+    for (int i = 0; i < steps; ++i) enqueue_step_kernels(s, splits, i == 0, i == steps - 1);
   } catch (...) {
     (void)hipStreamEndCapture(s.stream, &graph);
     if (graph) (void)hipGraphDestroy(graph);

@@ -169,6 +169,28 @@ def test_graph_replays_match_eager_launches(gpu, monkeypatch):
         tok_g = tok_e = int(np.argmax(lg))
 
 
+def test_grouped_steps_match_single_steps(gpu):
+    # enqueue_decode replays groups of 8 steps in which the argmax finalize of
+    # every step but the last folds into the next step (its layer-0 qkv
+    # prologue reduces the lm_head partials, the lm_head launch advances the
+    # position); 37 steps = 4 groups + 5 single steps.  Tokens and the last
+    # logits equal those of the same steps launched one at a time.
+    mmr = gpu
+    g = load_golden("mini")
+    m = synth_model(mmr, g)
+    prompt, n = g["prompt"], 37
+    grouped, single = m.make_state(200), m.make_state(200)
+    grouped.enqueue_prefill(prompt)
+    grouped.enqueue_decode(n)
+    grouped.synchronize()
+    toks = [single.prefill_next_token(prompt)]
+    for _ in range(n):
+        toks.append(single.forward_next_token(toks[-1]))
+    assert grouped.read_sequence(len(prompt), n + 1).tolist() == toks
+    assert grouped.position == single.position == len(prompt) + n
+    np.testing.assert_array_equal(grouped.read_logits(), single.read_logits())
+
+
 def test_l2_warming_blocks_leave_the_step_unchanged(gpu, monkeypatch):
     # The attention launch's L2-warming blocks (on by default) only load the
     # layer's O / gate_up / down weights: the decode with them equals the
