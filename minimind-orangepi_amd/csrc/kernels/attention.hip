@@ -525,25 +525,31 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   kv_rows.head_base = static_cast<int64_t>(g) * a.rows * D;
 
   // ---- 1. independent loads, issued before the position is known ----
+  // The position is read through the scalar cache (no kernel writes it while
+  // this one runs): its wait (lgkmcnt) never covers the vector loads below,
+  // which go out at once instead of behind one memory round trip.
   int p = -1;
-  if constexpr (MODE == kAttnFused) p = a.pos[0];
+  if constexpr (MODE == kAttnFused) p = *(const __attribute__((address_space(4))) int32_t*)a.pos;
   // The new token's q / k / v, the norm gains and the RoPE frequencies come
   // first: vector loads complete in issue order, so the q norm and RoPE wait
   // for these alone while the K/V tile below is still arriving.
   // Lane i < d/2 holds dims (i, i + d/2), the pair RoPE rotates together.
+  // Every lane loads (d0 is clamped, so in bounds): a guarded load is a
+  // branch, and the compiler waits for its data where the branches join.
+  // Lanes past d/2 are zeroed once the K/V tile loads are out.
   const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
   const bool in_pair = lane < D / 2;
   const float* qsrc = (MODE == kAttnFused ? a.qkv : a.q) + h * D;
-  float qx0 = in_pair ? qsrc[d0] : 0.0f, qx1 = in_pair ? qsrc[d1] : 0.0f;
+  float qx0 = qsrc[d0], qx1 = qsrc[d1];
   float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
   float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
   if constexpr (MODE == kAttnFused) {
     const float* kraw = a.qkv + a.hq * D + g * D;
     const float* vraw = kraw + a.hkv * D;
-    kx0 = in_pair ? kraw[d0] : 0.0f;
-    kx1 = in_pair ? kraw[d1] : 0.0f;
-    vx0 = in_pair ? vraw[d0] : 0.0f;
-    vx1 = in_pair ? vraw[d1] : 0.0f;
+    kx0 = kraw[d0];
+    kx1 = kraw[d1];
+    vx0 = vraw[d0];
+    vx1 = vraw[d1];
     inv_freq = a.inv_freq[d0];
     qw0 = a.q_norm[d0];
     qw1 = a.q_norm[d1];
@@ -560,6 +566,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     kc[i] = *reinterpret_cast<const uint4*>(kbase + t_load + c * CH);
     vc[i] = *reinterpret_cast<const uint4*>(vbase + t_load + c * CH);
   }
+  asm volatile("" ::: "memory");
+  if (!in_pair) qx0 = qx1 = kx0 = kx1 = vx0 = vx1 = 0.0f;
 
   // ---- 2. extent of the context ----
   int n_keys;
