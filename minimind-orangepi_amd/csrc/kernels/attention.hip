@@ -159,8 +159,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
 
   // ---- 1. independent loads, issued before the position is known ----
+  // The position is read through the scalar cache (no kernel writes it while
+  // this one runs), so no vector load waits behind its round trip.
   int p = -1;
-  if constexpr (MODE == kAttnFused) p = a.pos[b];
+  if constexpr (MODE == kAttnFused) p = ((const __attribute__((address_space(4))) int32_t*)a.pos)[b];
   uint4 kc[kPerThread], vc[kPerThread];
   const int t_spec = split * TT;
   const bool spec = t_spec + TT <= a.rows;
