@@ -34,11 +34,6 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
   const int k = a.k;
   const int kchunks = k >> 3;
   const int row0 = (blockIdx.x * kGroups + group) * RPG;
-  // kEpiArgmax position bookkeeping: read now, stored at the end.
-  int advance_from = 0;
-  if constexpr (EPI == kEpiArgmax) {
-    if (a.advance_pos != nullptr && blockIdx.x == 0) advance_from = *a.advance_pos;
-  }
 
   // 1. Every load that does not depend on another goes out before any
   //    arithmetic, so one memory latency covers them all, in this order: the
@@ -264,6 +259,17 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
       }
+  }
+
+  // kEpiArgmax position bookkeeping, read once every load of the block is out
+  // (a load under a branch is waited for where the branch joins), through the
+  // scalar cache (its wait never covers the vector loads; the only write to
+  // it in this kernel is block 0's own, at the end), and stored with the
+  // block's partial.
+  int advance_from = 0;
+  if constexpr (EPI == kEpiArgmax) {
+    if (a.advance_pos != nullptr && blockIdx.x == 0)
+      advance_from = *(const __attribute__((address_space(4))) int32_t*)a.advance_pos;
   }
 
   if constexpr (PRO == kProRmsNorm || PRO == kProRmsNormFinal || PRO == kProEmbedRmsNorm) {
