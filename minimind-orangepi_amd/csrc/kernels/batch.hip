@@ -377,9 +377,11 @@ __device__ inline T sum_parts4(const T* part4, int64_t sstride, int s0, int step
     T v[kPartLoads];
 #pragma unroll
     for (int u = 0; u < kPartLoads; ++u) v[u] = part4[min(base + step * u, splits - 1) * sstride];
+    // Indices past the last split (clamped above) add zero: a select, not a
+    // branch, which the compiler would turn into a reload of v[u] and a wait
+    // inside the branch.
 #pragma unroll
-    for (int u = 0; u < kPartLoads; ++u)
-      if (base + step * u < splits) acc = add4(acc, v[u]);
+    for (int u = 0; u < kPartLoads; ++u) acc = add4(acc, base + step * u < splits ? v[u] : T{});
   }
   return acc;
 }
@@ -394,6 +396,80 @@ __device__ inline T sum_parts4(const T* part4, int64_t sstride, int s0, int step
 // row), 256 for many (prefill: one group adds the splits in order).
 constexpr int kResChunkQuads = 256;
 constexpr int kResManyRows = 64;
+
+// The pre-split planes of one row's 4 normalised columns at quad q (thread
+// = 4 consecutive columns; the threads of a 128-column chunk reduce its
+// maximum together, so every thread of the block must call this).
+__device__ inline void write_split_quad(const float (&v)[4], bool live, int q, int64_t b, int cols, SplitPlanes sp) {
+  const int nchunks = (cols + kSplitChunk - 1) / kSplitChunk;
+  const float mx = group_max<kSplitChunk / 4>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  if (!live) return;
+  int e2 = 0;
+  frexpf(mx, &e2);  // e2 = 0 for a zero chunk
+  e2 = max(e2, -100);
+  const float sc = ldexpf(1.0f, 15 - e2);
+  uint16_t hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float xs = v[e] * sc;
+    const _Float16 hh = static_cast<_Float16>(xs);
+    const _Float16 ll = static_cast<_Float16>(xs - static_cast<float>(hh));
+    __builtin_memcpy(&hi[e], &hh, 2);
+    __builtin_memcpy(&lo[e], &ll, 2);
+  }
+  const int64_t off = b * cols + 4 * q;
+  *reinterpret_cast<uint2*>(sp.hi + off) = make_uint2(hi[0] | (uint32_t{hi[1]} << 16), hi[2] | (uint32_t{hi[3]} << 16));
+  *reinterpret_cast<uint2*>(sp.lo + off) = make_uint2(lo[0] | (uint32_t{lo[1]} << 16), lo[2] | (uint32_t{lo[3]} << 16));
+  if (q % (kSplitChunk / 4) == 0) sp.inv[b * nchunks + q / (kSplitChunk / 4)] = ldexpf(1.0f, e2 - 15);
+}
+
+// batch_residual_norm_kernel for a row of at most kResChunkQuads quads: every
+// load of the block goes out before any arithmetic (the split partials, the
+// row of h and the norm gains, indices clamped: a guarded load is waited for
+// where its branch joins), and group 0 keeps the updated row in registers
+// for both writers, so the row costs one memory round trip instead of three.
+// Same operations in the same order as the general path below.
+template <bool kFinal, bool kSplit, int kResThreads>
+__device__ inline void residual_norm_row(float4* h4, const float4* p4, int64_t sstride, int splits, int nq, int cols,
+                                         int b, const float* w, float eps, float* x, SplitPlanes sp,
+                                         float4 (&red)[kResThreads / 256][kResChunkQuads],
+                                         float (&s_ss)[kResThreads / kWave]) {
+  constexpr int kResGroups = kResThreads / 256;
+  const int grp = threadIdx.x / 256, t = threadIdx.x % 256;
+  const int qq = min(t, nq - 1);
+  const bool live = grp == 0 && t < nq;
+  const float4 hv = h4[qq];
+  const float4 wv = reinterpret_cast<const float4*>(w)[qq];
+  float4 ps = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (splits > 0) ps = sum_parts4(p4 + qq, sstride, grp, kResGroups, splits);
+  if (splits > 0) red[grp][t] = ps;
+  __syncthreads();
+  float4 v = hv;
+  if (splits > 0) {
+#pragma unroll
+    for (int g2 = 0; g2 < kResGroups; ++g2) v = add4(v, red[g2][t]);
+    if (live) h4[t] = v;
+  }
+  float ss = live ? v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w : 0.0f;
+  ss = group_sum<kWave>(ss);
+  if (threadIdx.x % kWave == 0) s_ss[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kResThreads / kWave; ++i) total += s_ss[i];
+  const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
+  const float hvv[4] = {v.x, v.y, v.z, v.w}, wvv[4] = {wv.x, wv.y, wv.z, wv.w};
+  float xv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) xv[e] = kFinal ? (hvv[e] * scale) * wvv[e] : hvv[e] * (scale * wvv[e]);
+  if (x && live) *reinterpret_cast<float4*>(x + static_cast<int64_t>(b) * cols + 4 * t) = make_float4(xv[0], xv[1], xv[2], xv[3]);
+  if constexpr (kSplit) {
+    float sv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sv[e] = live ? xv[e] : 0.0f;
+    write_split_quad(sv, live, t, b, cols, sp);
+  }
+}
 
 template <bool kFinal, bool kSplit, int kResThreads>
 __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float* h, const float* part, int splits,
@@ -418,6 +494,10 @@ __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float*
   float4* h4 = reinterpret_cast<float4*>(h + static_cast<int64_t>(b) * cols);
   const float4* p4 = reinterpret_cast<const float4*>(part) + static_cast<int64_t>(b) * nq;
   const int64_t sstride = static_cast<int64_t>(batch) * nq;
+  if (nq <= kResChunkQuads) {  // block-uniform
+    residual_norm_row<kFinal, kSplit, kResThreads>(h4, p4, sstride, splits, nq, cols, b, w, eps, x, sp, red, s_ss);
+    return;
+  }
   float ss = 0.0f;
   for (int c0 = 0; c0 < nq; c0 += kResChunkQuads) {  // block-uniform
     const int q = c0 + t;
@@ -655,6 +735,9 @@ hipError_t launch_batch_residual_norm(float* h, const float* part, int splits, i
   if (split && (!split->hi || !split->lo || !split->inv)) return hipErrorInvalidValue;
   if (!x && !split) return hipErrorInvalidValue;
   if (warm && (warm->blocks < 0 || warm->blocks % kXcds != 0)) return hipErrorInvalidValue;
+  // h, the gains and x are read and written as float4 rows.
+  auto aligned16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+  if (!aligned16(h) || !aligned16(w) || (x && !aligned16(x)) || (part && !aligned16(part))) return hipErrorInvalidValue;
   const SplitPlanes sp = split ? *split : SplitPlanes{};
   const L2WarmSet ws = warm ? *warm : L2WarmSet{};
   const int grid = ws.blocks > 0 ? (batch + kXcds - 1) / kXcds * kXcds + ws.blocks : batch;
