@@ -700,23 +700,33 @@ __global__ __launch_bounds__(kWave* kQkvRowsTokens) void qkv_rows_kernel(QkvRows
   const float* vsrc = row + a.hq * D + a.hkv * D + head * D;
   const float* w = is_q ? a.q_norm : a.k_norm;
   const int d0 = min(lane, D - 1), d1 = min(lane + kWave, D - 1);
-  // Sum of the projection's split partials at p[i] (clamped loads, all issued
-  // before the adds, added in split order).
-  auto part_sum = [&](const float* p, int i) {
-    float v[kQkvRowsMaxParts];
+  // The projection's split partials at p[i]: every load of the wave (the q or
+  // k row's partials, the V row's, the gains and the frequency) goes out
+  // before any add; the partials are then added in split order, the clamped
+  // duplicates past the last split as zeros (a select: a guarded add would be
+  // a branch, with a wait and a reload inside it).
+  using Parts = float[kQkvRowsMaxParts];
+  auto part_load = [&](const float* p, int i, Parts& v) {
 #pragma unroll
     for (int sp = 0; sp < kQkvRowsMaxParts; ++sp) v[sp] = p[min(sp, a.qkv_parts - 1) * a.qkv_part_stride + i];
+  };
+  auto part_add = [&](const Parts& v) {
     float x = v[0];
 #pragma unroll
-    for (int sp = 1; sp < kQkvRowsMaxParts; ++sp)
-      if (sp < a.qkv_parts) x += v[sp];
+    for (int sp = 1; sp < kQkvRowsMaxParts; ++sp) x += sp < a.qkv_parts ? v[sp] : 0.0f;
     return x;
   };
-  float x0 = part_sum(src, d0), x1 = part_sum(src, d1);
+  Parts px0, px1, pv0, pv1;
+  part_load(src, d0, px0);
+  part_load(src, d1, px1);
   // V rows of a KV head are loaded with the K rows (a query block's copy is unused).
-  const float v0 = part_sum(is_q ? src : vsrc, d0), v1 = part_sum(is_q ? src : vsrc, d1);
+  part_load(is_q ? src : vsrc, d0, pv0);
+  part_load(is_q ? src : vsrc, d1, pv1);
   const float w0 = w[d0], w1 = w[d1];
   const float f = a.inv_freq[min(lane, D / 2 - 1)];
+  asm volatile("" ::: "memory");
+  float x0 = part_add(px0), x1 = part_add(px1);
+  const float v0 = part_add(pv0), v1 = part_add(pv1);
   x0 = lane < D ? x0 : 0.0f;
   x1 = lane + kWave < D ? x1 : 0.0f;
   const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
