@@ -12,8 +12,12 @@
 //   down  GEMV  residual epilogue  (h += W_down act)
 //   head  GEMV  final RMSNorm prologue, per-block argmax partials, then the
 //               finalize kernel writes seq[pos + 1] and advances pos
-// Every kernel reads the position from device memory, so the step is captured
-// once into a hipGraph (per attention split count) and replayed per token.
+// Every kernel reads the position from device memory, so groups of 8 steps are
+// captured once into a hipGraph (per attention split count) and replayed;
+// inside a group the finalize runs after the last step only (the others fold
+// it into the lm_head launch and the next step's layer-0 prologue), and the
+// attention launch also warms the L2s with the layer's O, gate_up and down
+// weights.
 // Prompts run through the chunked prefill kernels (enqueue_prefill).
 #include "language_model.h"
 
