@@ -196,6 +196,7 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 template <int kThreads>
 __device__ void l2_warm(const L2WarmSet& set, int j, void* lds) {
   const int xcd = j % kXcds, slot = j / kXcds, slots = set.blocks / kXcds;
+  if (slots <= 0) return;  // the launchers pass a positive multiple of kXcds; the loops below need a stride
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_address(lds) + (threadIdx.x / kWave) * (kWave * 16));
 #pragma unroll
   for (int r = 0; r < kL2WarmRegions; ++r) {
