@@ -97,6 +97,11 @@ bool gemv_plan(int rows, int k, GemvEpilogue epi, int lanes_per_row, int rows_pe
 
 hipError_t launch_gemv(const GemvArgs& a, GemvPrologue pro, GemvEpilogue epi, const GemvPlan& p,
                        hipStream_t stream) {
+  // The embedding prologue's token from the previous step's argmax partials.
+  if (a.prev_val && (pro != kProEmbedRmsNorm || !a.prev_idx || !a.prompt_len || !a.seq_out || a.prev_parts < 1 ||
+                     a.prev_parts > kGemvMaxPrevParts))
+    return hipErrorInvalidValue;
+  if (a.advance_pos && epi != kEpiArgmax) return hipErrorInvalidValue;
   const int cpl = p.chunks_per_lane;
 #define MMR_GEMV_G(GV, RV)                                               \
   if (p.lanes_per_row == GV && p.rows_per_group == RV)                   \
