@@ -620,7 +620,10 @@ def main() -> int:
                 "bytes_per_launch": kernels[name]["bytes"], "avg_us": kernels[name]["avg_us"],
                 "us_per_step": kernels[name]["us_per_step"],
                 **{k: kernels[name][k] for k in ("avg_us_without_warm_blocks", "warm_bytes_per_launch")
-                   if k in kernels[name]}}
+                   if k in kernels[name]},
+                **({"traffic_scope": "the attention work alone (the --traffic-probe launch has no warming blocks); "
+                                     "the step's launch also fetches warm_bytes_per_launch"}
+                   if traffic is not None and "warm_bytes_per_launch" in kernels[name] else {})}
 
     roofline = roofline_of(dom)
     roofline["secondary"] = {n: roofline_of(n) for n in ("gate_up", "attention", "lm_head") if n != dom}
