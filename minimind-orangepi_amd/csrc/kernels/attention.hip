@@ -766,43 +766,30 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
 }
 
 // Log-sum-exp combine of the split partials: one block of 256 threads per
-// (query head, 32-dimension slice) (grid.y: sequence of a batch).  Thread t
-// holds the (m, l) of splits t, t + 256, ... (at most kCombineKernelMaxSplits
-// in all); block reductions give M = max m and L = sum_s l_s exp(m_s - M);
-// the weights exp(m_s - M) go to LDS, and eight groups of 32 threads (thread
-// = dimension) each sum e_s o_s over every eighth split.  The first eight o
-// values of every thread (sixteen above 64 splits) are loaded with the (m, l),
-// so one memory round trip serves up to 128 splits.  The groups' sums are added in group order.  Every
-// order is fixed, so the result is deterministic.  (The O-projection
-// prologue, kProAttnCombine, computes the same quantity for up to
-// kCombineMaxSplits splits.)
+// (query head, 16-dimension slice) (grid.y: sequence of a batch); sixteen
+// groups of 16 threads (thread = dimension), group j taking splits j, j + 16,
+// ...  Every thread loads the o values of its splits together with their
+// (m, l) pairs, so up to 16 * kRound splits cost one memory round trip: the
+// block's max M = max m (wave DPP max, then LDS), then each group sums
+// e_s o_s and e_s l_s with e_s = exp(m_s - M) in split order, and the groups'
+// sums meet in LDS and are added in group order.  Every order is fixed, so
+// the result is deterministic.  kMulti (more than 16 * kRound splits): M
+// first from every split's m (thread t: splits t, t + 256, ...), then rounds
+// of 16 * kRound splits.  (The O-projection prologue, kProAttnCombine,
+// computes the same quantity for up to kCombineMaxSplits splits.)
 constexpr int kCombineThreads = 256;
-constexpr int kCombineSlice = 32;                                   // dimensions per block
+constexpr int kCombineSlice = 16;                                   // dimensions per block
 constexpr int kCombineGroups = kCombineThreads / kCombineSlice;     // split groups
 constexpr int kCombineKernelMaxSplits = 4096;
-constexpr int kCombinePerThread = kCombineKernelMaxSplits / kCombineThreads;
+constexpr int kCombineMaxPerThread = kCombineKernelMaxSplits / kCombineThreads;
 
-// Sum over the block (all threads active) in a fixed order.
-template <typename Op>
-__device__ __forceinline__ float combine_block_reduce(float v, Op op, float* scratch) {
-  v = group_reduce<kWave>(v, op);
-  __syncthreads();  // scratch may still be read from a previous reduction
-  if (threadIdx.x % kWave == 0) scratch[threadIdx.x / kWave] = v;
-  __syncthreads();
-  float r = scratch[0];
-#pragma unroll
-  for (int w = 1; w < kCombineThreads / kWave; ++w) r = op(r, scratch[w]);
-  return r;
-}
-
-// kCombineUnroll: o loads in flight per thread (8, or 16 above 64 splits).
-template <int kCombineUnroll>
+template <int kRound, bool kMulti>
 __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(const float* part, int hq, int hkv, int d,
                                                                              int splits, int64_t part_stride,
                                                                              float* out) {
-  __shared__ float s_w[kCombineKernelMaxSplits];
   __shared__ float s_red[kCombineGroups][kCombineSlice];
-  __shared__ float s_scratch[kCombineThreads / kWave];
+  __shared__ float s_l[kCombineGroups];
+  __shared__ float s_m[kCombineThreads / kWave];
   const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
   const int qh = blockIdx.x / nslice, slice = blockIdx.x % nslice;
   part += static_cast<int64_t>(blockIdx.y) * part_stride;  // sequence of a batch
@@ -810,59 +797,63 @@ __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(cons
   const int R = hq / hkv;
   const int g = qh / R, h = qh % R;
   const int tid = threadIdx.x;
-  const int grp = tid / kCombineSlice, dim = slice * kCombineSlice + tid % kCombineSlice;
+  const int grp = tid / kCombineSlice, col = tid % kCombineSlice;
+  const int dim = slice * kCombineSlice + col;
   const int dd = min(dim, d - 1);
-  // This thread's first kCombineUnroll o values (clamped: in bounds, weighted
-  // only below `splits`), issued together with the (m, l) loads.
-  float v[kCombineUnroll];
+  // Loads of one round: o and (m, l) of splits base + grp + 16 u, indices
+  // clamped into range (the repeats are weighted 0), all issued together.
+  float v[kRound];
+  float2 ml[kRound];
+  auto load_round = [&](int base) {
 #pragma unroll
-  for (int u = 0; u < kCombineUnroll; ++u)
-    v[u] = part[attn_o_offset(g, min(grp + kCombineGroups * u, splits - 1), h, splits, R, d) + dd];
-  // Unconditional, clamped (m, l) loads: past `splits` they repeat the last
-  // split's (one cache line per wave), and no branch holds the loads back.
-  float2 ml[kCombinePerThread];
-#pragma unroll
-  for (int j = 0; j < kCombinePerThread; ++j) {
-    const int sp = min(tid + j * kCombineThreads, splits - 1);
-    ml[j] = *reinterpret_cast<const float2*>(part + attn_ml_offset(g, sp, h, splits, R, d, hkv));
-  }
+    for (int u = 0; u < kRound; ++u) {
+      const int sp = min(base + grp + kCombineGroups * u, splits - 1);
+      v[u] = part[attn_o_offset(g, sp, h, splits, R, d) + dd];
+      ml[u] = *reinterpret_cast<const float2*>(part + attn_ml_offset(g, sp, h, splits, R, d, hkv));
+    }
+  };
   float m_loc = -INFINITY;
+  if constexpr (kMulti) {
+    float mm[kCombineMaxPerThread];
 #pragma unroll
-  for (int j = 0; j < kCombinePerThread; ++j) m_loc = fmaxf(m_loc, ml[j].x);  // clamped repeats: max unchanged
-  const float M = combine_block_reduce(m_loc, OpMax{}, s_scratch);
-  float l_loc = 0.0f;
+    for (int j = 0; j < kCombineMaxPerThread; ++j)
+      mm[j] = part[attn_ml_offset(g, min(tid + j * kCombineThreads, splits - 1), h, splits, R, d, hkv)];
+    load_round(0);
 #pragma unroll
-  for (int j = 0; j < kCombinePerThread; ++j) {
-    const int sp = tid + j * kCombineThreads;
-    if (sp < splits) {
-      const float e = expf(ml[j].x - M);
-      s_w[sp] = e;
-      l_loc = fmaf(ml[j].y, e, l_loc);
+    for (int j = 0; j < kCombineMaxPerThread; ++j) m_loc = fmaxf(m_loc, mm[j]);  // clamped repeats: max unchanged
+  } else {
+    load_round(0);
+#pragma unroll
+    for (int u = 0; u < kRound; ++u) m_loc = fmaxf(m_loc, ml[u].x);
+  }
+  m_loc = group_max<kWave>(m_loc);
+  if (tid % kWave == 0) s_m[tid / kWave] = m_loc;
+  __syncthreads();
+  float M = s_m[0];
+#pragma unroll
+  for (int w = 1; w < kCombineThreads / kWave; ++w) M = fmaxf(M, s_m[w]);
+  float o = 0.0f, l = 0.0f;
+  for (int base = 0;;) {
+#pragma unroll
+    for (int u = 0; u < kRound; ++u) {
+      const float e = base + grp + kCombineGroups * u < splits ? expf(ml[u].x - M) : 0.0f;
+      o = fmaf(v[u], e, o);
+      l = fmaf(ml[u].y, e, l);
     }
+    base += kCombineGroups * kRound;
+    if (!kMulti || base >= splits) break;
+    load_round(base);
   }
-  const float L = combine_block_reduce(l_loc, OpSum{}, s_scratch);  // its barriers also publish s_w
-  float o = 0.0f;
-#pragma unroll
-  for (int u = 0; u < kCombineUnroll; ++u) {
-    const int sp = grp + kCombineGroups * u;
-    if (sp < splits) o = fmaf(v[u], s_w[sp], o);
-  }
-  for (int base = grp + kCombineGroups * kCombineUnroll; base < splits; base += kCombineGroups * kCombineUnroll) {
-#pragma unroll
-    for (int u = 0; u < kCombineUnroll; ++u)
-      v[u] = part[attn_o_offset(g, min(base + kCombineGroups * u, splits - 1), h, splits, R, d) + dd];
-#pragma unroll
-    for (int u = 0; u < kCombineUnroll; ++u) {
-      const int sp = base + kCombineGroups * u;
-      if (sp < splits) o = fmaf(v[u], s_w[sp], o);
-    }
-  }
-  s_red[grp][tid % kCombineSlice] = o;
+  s_red[grp][col] = o;
+  if (col == 0) s_l[grp] = l;
   __syncthreads();
   if (grp == 0 && dim < d) {
-    float x = s_red[0][tid];
+    float x = s_red[0][col], L = s_l[0];
 #pragma unroll
-    for (int gi = 1; gi < kCombineGroups; ++gi) x += s_red[gi][tid];
+    for (int gi = 1; gi < kCombineGroups; ++gi) {
+      x += s_red[gi][col];
+      L += s_l[gi];
+    }
     out[qh * d + dim] = x * (1.0f / L);
   }
 }
@@ -992,10 +983,16 @@ hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, i
     return hipErrorInvalidValue;
   const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
   const dim3 grid(hq * nslice, batch);
-  if (splits > 8 * kCombineGroups) {
-    attention_combine_kernel<16><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+  if (splits <= 8 * kCombineGroups) {
+    attention_combine_kernel<8, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+  } else if (splits <= 16 * kCombineGroups) {
+    attention_combine_kernel<16, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
+                                                                              out);
+  } else if (splits <= 32 * kCombineGroups) {
+    attention_combine_kernel<32, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
+                                                                              out);
   } else {
-    attention_combine_kernel<8><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+    attention_combine_kernel<16, true><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
   }
   return hipGetLastError();
 }
