@@ -172,8 +172,8 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     // every block (k = hq * head_dim <= 1024, splits <= 16, hq <= 16):
     //   M_h = max_s m[h][s],  e[h][s] = exp(m[h][s] - M_h),
     //   L_h = sum_s l[h][s] e[h][s],  x[h*d + i] = (sum_s o[h][s][i] e[h][s]) / L_h,
-    // both sums in split order: the same operations as
-    // attention_combine_kernel, so the two paths agree bit for bit.
+    // both sums in split order (attention_combine_kernel computes the same
+    // quantity, summing over groups of splits: the two agree to rounding).
     __shared__ __align__(16) float s_x[kCombineMaxDim];
     __shared__ __align__(16) float s_e[kCombineMaxHeads][kCombineMaxSplits];
     __shared__ __align__(16) float s_l[kCombineMaxHeads][kCombineMaxSplits];
