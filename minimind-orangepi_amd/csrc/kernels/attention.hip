@@ -254,14 +254,17 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     if constexpr (MODE == kAttnFused) {
       if (in_pair) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
     }
+    // q staged times log2(e) / sqrt(d): the scores come out divided by
+    // sqrt(d) (decoder_layer.cpp:213) and in base-2 units for exp2.
+    const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(D));
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int h = wave + j * kAttnWaves;
       if (h < R) {
         if constexpr (MODE == kAttnFused) wave_norm_rope_pair<D>(qx0[j], qx1[j], qw0, qw1, a.eps, rc, rs);
         if (in_pair) {
-          q_s[h][d0] = qx0[j];
-          q_s[h][d1] = qx1[j];
+          q_s[h][d0] = qx0[j] * qscale;
+          q_s[h][d1] = qx1[j] * qscale;
         }
       }
     }
@@ -288,7 +291,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
       vx1 = to_float<KV>(v1);
     }
 
-    const float sqrt_d = sqrtf(static_cast<float>(D));
     // Fetch tile `tile`'s K/V chunks into the registers (rows clamped into
     // the context, all loads issued before any is consumed).
     auto fetch_tile = [&](int tile, int page) {
@@ -356,24 +358,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
       for (int j = 0; j < 2; ++j) {
         const int h = wave + j * kAttnWaves;
         if (h >= R) break;
+        // Score in base-2 units, already divided by sqrt(d) (q is pre-scaled);
+        // four independent partial sums over the dims shorten the FMA chain.
         float s = -INFINITY;
         if (lane < rows) {
-          float dot = 0.0f;
+          float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int dd = 0; dd < D; dd += 4) {
             const float4 kv4 = *reinterpret_cast<const float4*>(&k_s[lane][dd]);
             const float4 q4 = *reinterpret_cast<const float4*>(&q_s[h][dd]);
-            dot = fmaf(q4.x, kv4.x, dot);
-            dot = fmaf(q4.y, kv4.y, dot);
-            dot = fmaf(q4.z, kv4.z, dot);
-            dot = fmaf(q4.w, kv4.w, dot);
+            dot[0] = fmaf(q4.x, kv4.x, dot[0]);
+            dot[1] = fmaf(q4.y, kv4.y, dot[1]);
+            dot[2] = fmaf(q4.z, kv4.z, dot[2]);
+            dot[3] = fmaf(q4.w, kv4.w, dot[3]);
           }
-          s = dot / sqrt_d;  // decoder_layer.cpp:213 divides by sqrt(d)
+          s = (dot[0] + dot[1]) + (dot[2] + dot[3]);
         }
         const float m_tile = group_max<kWave>(s);
         const float m_new = fmaxf(m_run[j], m_tile);
-        const float alpha = expf(m_run[j] - m_new);
-        const float pv = lane < rows ? expf(s - m_new) : 0.0f;
+        const float alpha = m_run[j] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[j] - m_new);
+        const float pv = lane < rows ? __builtin_amdgcn_exp2f(s - m_new) : 0.0f;
         l_run[j] = l_run[j] * alpha + group_sum<kWave>(pv);
         if (lane < TT) p_s[lane][h] = pv;
         if (lane == 0) alpha_s[h] = alpha;
@@ -439,7 +443,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     const int h = wave + j * kAttnWaves;
     if (h < R && lane == 0) {
       float* dst = part + attn_ml_offset(g, split, h, S, R, D, a.hkv);
-      dst[0] = m_run[j];
+      dst[0] = m_run[j] * 0.6931471805599453f;  // base-2 units -> natural log (ln 2)
       dst[1] = l_run[j];
     }
   }
