@@ -472,13 +472,19 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
 //  * P.V: one lane per dimension pair over the wave's tokens, the
 //    probabilities read out of the scoring lanes.
 // Writes the same (m, l, o[d]) split partials as attention_split_kernel.
-template <typename KV, int D, int MODE>
-__global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a) {
+// kHeads = 4 (1024 threads, one block per (split, group)): the group's four
+// heads share one staged tile, waves 4 j .. 4 j + 3 serving head j exactly as
+// a one-head block does; the long-context form, one staging per tile instead
+// of four while keeping the one-head block's short chain.
+template <typename KV, int D, int MODE, int kHeads>
+__global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(AttnArgs a) {
   constexpr int TT = attn_tile_tokens<D>();
   constexpr int LD = D + 4;
   constexpr int CH = 16 / static_cast<int>(sizeof(KV));
   constexpr int kChunks = TT * D / CH;
-  constexpr int kPerThread = (kChunks + kAttnThreads - 1) / kAttnThreads;
+  constexpr int kThreads = kAttnThreads * kHeads;
+  constexpr int kWaves = kThreads / kWave;  // kAttnWaves per head
+  constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
   constexpr int kPairs = D / 2;
   constexpr int kTokPerWave = TT / kAttnWaves;
   constexpr int kLanesPerTok = kWave / kTokPerWave;
@@ -486,45 +492,56 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   static_assert(TT % kAttnWaves == 0 && kWave % kTokPerWave == 0, "a wave holds whole tokens");
   static_assert((D / 4) % kLanesPerTok == 0, "the dims split evenly over a token's lanes");
   static_assert(D / 2 <= kWave, "a wave holds one head as d/2 RoPE pairs");
-  __shared__ __align__(16) float q_s[D];
+  __shared__ __align__(16) float q_s[kHeads][D];
   __shared__ __align__(16) float k_s[TT][LD];
   __shared__ __align__(16) float v_s[TT][LD];
-  __shared__ __align__(16) float red_o[kAttnWaves][D];
-  __shared__ float red_m[kAttnWaves], red_l[kAttnWaves];
+  __shared__ __align__(16) float red_o[kWaves][D];
+  __shared__ float red_m[kWaves], red_l[kWaves];
 
   const int R = a.hq / a.hkv;
   const int S = a.splits;
   // Blocks past the S * hq head blocks: padding up to a multiple of kXcds,
   // then the L2-warming blocks (their loads land in k_s, which they own).
-  static_assert(sizeof(k_s) >= kAttnThreads / kWave * kWave * 16, "a 1 KB landing zone per wave");
-  if (static_cast<int>(blockIdx.x) >= S * a.hq) {
-    const int first = (S * a.hq + kXcds - 1) / kXcds * kXcds;
-    if (MODE == kAttnFused && static_cast<int>(blockIdx.x) >= first)
-      l2_warm<kAttnThreads>(a.warm, static_cast<int>(blockIdx.x) - first, &k_s[0][0]);
-    return;
+  static_assert(kHeads > 1 || sizeof(k_s) >= kWaves * kWave * 16, "a 1 KB landing zone per wave");
+  if constexpr (kHeads == 1) {
+    if (static_cast<int>(blockIdx.x) >= S * a.hq) {
+      const int first = (S * a.hq + kXcds - 1) / kXcds * kXcds;
+      if (MODE == kAttnFused && static_cast<int>(blockIdx.x) >= first)
+        l2_warm<kAttnThreads>(a.warm, static_cast<int>(blockIdx.x) - first, &k_s[0][0]);
+      return;
+    }
   }
   // Block -> (split, group, head): the R head-blocks of one (split, group)
   // unit take ids 8 apart, so the round-robin dispatch over the 8 XCDs puts
   // them on one XCD and their K/V tile is read from HBM into one L2.  (A
   // last partial group of 8 units keeps its blocks together less tightly.)
-  const int units = S * a.hkv;
-  const int full = units / 8 * 8;
-  const int id = blockIdx.x;
+  // With kHeads = R, block (split, group) is one unit and its four waves
+  // 4 j .. 4 j + 3 serve head j of the group from the one staged tile.
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wq = kHeads == 1 ? wave : wave % kAttnWaves;  // the wave's token group of the tile
+  const int hb = kHeads == 1 ? 0 : wave / kAttnWaves;     // the wave's head within the block
   int unit, r;
-  if (id < full * R) {
-    const int w = id % (8 * R);
-    unit = id / (8 * R) * 8 + w % 8;
-    r = w / 8;
+  if constexpr (kHeads == 1) {
+    const int units = S * a.hkv;
+    const int full = units / 8 * 8;
+    const int id = blockIdx.x;
+    if (id < full * R) {
+      const int w = id % (8 * R);
+      unit = id / (8 * R) * 8 + w % 8;
+      r = w / 8;
+    } else {
+      const int tail = units - full, w = id - full * R;
+      unit = full + w % tail;
+      r = w / tail;
+    }
   } else {
-    const int tail = units - full, w = id - full * R;
-    unit = full + w % tail;
-    r = w / tail;
+    unit = blockIdx.x;
+    r = hb;
   }
   const int split = unit / a.hkv;
   const int g = unit % a.hkv;
   const int h = g * R + r;
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
   const KV* kbase = reinterpret_cast<const KV*>(a.kcache);
   const KV* vbase = reinterpret_cast<const KV*>(a.vcache);
   KvRows<D, false> kv_rows;
@@ -568,7 +585,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   const int64_t t_load = kv_rows.row(spec ? t_spec : 0);
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
-    const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+    const int c = min(static_cast<int>(threadIdx.x) + i * kThreads, kChunks - 1);
     kc[i] = *reinterpret_cast<const uint4*>(kbase + t_load + c * CH);
     vc[i] = *reinterpret_cast<const uint4*>(vbase + t_load + c * CH);
   }
@@ -590,7 +607,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
   float m_run = -INFINITY, l_run = 0.0f;
   float2 pacc = make_float2(0.0f, 0.0f);
   const int pv_pair = min(lane, kPairs - 1);
-  const int tok = wave * kTokPerWave + lane / kLanesPerTok;  // scoring token within the tile
+  const int tok = wq * kTokPerWave + lane / kLanesPerTok;  // scoring token within the tile
   const int share = lane % kLanesPerTok;  // which interleaved share of the dims
   bool append_new = false;  // this lane writes dims (d0, d1) of cache row p at the end
 
@@ -600,14 +617,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     if constexpr (MODE == kAttnFused) {
       if (in_pair) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
     }
-    if (wave == 0) {
+    if (wq == 0) {  // one wave per head
       if constexpr (MODE == kAttnFused) wave_norm_rope_pair<D>(qx0, qx1, qw0, qw1, a.eps, rc, rs);
       // q staged times log2(e) / sqrt(d): the scores come out divided by
       // sqrt(d) (decoder_layer.cpp:213) and in base-2 units for exp2.
       const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(D));
       if (in_pair) {
-        q_s[d0] = qx0 * qscale;
-        q_s[d1] = qx1 * qscale;
+        q_s[hb][d0] = qx0 * qscale;
+        q_s[hb][d1] = qx1 * qscale;
       }
     }
     // The block owning tile p / TT places the new token's row in its stage;
@@ -634,7 +651,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
       const int64_t tile_base = kv_rows.row(t0);
 #pragma unroll
       for (int i = 0; i < kPerThread; ++i) {
-        const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
+        const int c = min(static_cast<int>(threadIdx.x) + i * kThreads, kChunks - 1);
         const int r = min((c * CH) / D, rows - 1);
         const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
         kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
@@ -648,7 +665,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
       // Rows past the context are zero-filled (0 * stale LDS could be NaN).
 #pragma unroll
       for (int i = 0; i < kPerThread; ++i) {
-        const int c = threadIdx.x + i * kAttnThreads;
+        const int c = threadIdx.x + i * kThreads;
         const int r = (c * CH) / D;
         const int col = (c * CH) % D;
         if (c < kChunks && !(MODE == kAttnFused && t0 + r == p)) {
@@ -684,12 +701,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
       for (int c = 0; c < kQuadsPerLane; ++c) {
         const int col = 4 * (c * kLanesPerTok + share);
         k4[c] = *reinterpret_cast<const float4*>(&k_s[tok][col]);
-        q4[c] = *reinterpret_cast<const float4*>(&q_s[col]);
+        q4[c] = *reinterpret_cast<const float4*>(&q_s[hb][col]);
       }
       float2 vrow[kTokPerWave];
 #pragma unroll
       for (int t = 0; t < kTokPerWave; ++t)
-        vrow[t] = *reinterpret_cast<const float2*>(&v_s[wave * kTokPerWave + t][2 * pv_pair]);
+        vrow[t] = *reinterpret_cast<const float2*>(&v_s[wq * kTokPerWave + t][2 * pv_pair]);
       asm volatile("" : : : "memory");
 
       // ---- scores of the wave's tokens ----
@@ -737,25 +754,55 @@ __global__ __launch_bounds__(kAttnThreads) void attention_head_kernel(AttnArgs a
     red_l[wave] = l_run;
   }
   __syncthreads();
-  float M = red_m[0];
+  if constexpr (kHeads == 1) {
+    float M = red_m[0];
 #pragma unroll
-  for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w]);
-  float e[kAttnWaves];
+    for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w]);
+    float e[kAttnWaves];
 #pragma unroll
-  for (int w = 0; w < kAttnWaves; ++w) e[w] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w] - M);
-  for (int idx = threadIdx.x; idx < D; idx += kAttnThreads) {
-    float o = 0.0f;
+    for (int w = 0; w < kAttnWaves; ++w) e[w] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w] - M);
+    for (int idx = threadIdx.x; idx < D; idx += kAttnThreads) {
+      float o = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) o = fmaf(e[w], red_o[w][idx], o);
-    a.part[attn_o_offset(g, split, r, S, R, D) + idx] = o;
-  }
-  if (threadIdx.x == 0) {
-    float L = 0.0f;
+      for (int w = 0; w < kAttnWaves; ++w) o = fmaf(e[w], red_o[w][idx], o);
+      a.part[attn_o_offset(g, split, r, S, R, D) + idx] = o;
+    }
+    if (threadIdx.x == 0) {
+      float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) L = fmaf(e[w], red_l[w], L);
-    float* dst = a.part + attn_ml_offset(g, split, r, S, R, D, a.hkv);
-    dst[0] = M * 0.6931471805599453f;  // ln 2
-    dst[1] = L;
+      for (int w = 0; w < kAttnWaves; ++w) L = fmaf(e[w], red_l[w], L);
+      float* dst = a.part + attn_ml_offset(g, split, r, S, R, D, a.hkv);
+      dst[0] = M * 0.6931471805599453f;  // ln 2
+      dst[1] = L;
+    }
+  } else {
+    // Head j of the block: waves 4 j .. 4 j + 3.
+    for (int idx = threadIdx.x; idx < kHeads * D; idx += kThreads) {
+      const int j = idx / D, dim = idx - j * D;
+      float M = red_m[kAttnWaves * j];
+  #pragma unroll
+      for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[kAttnWaves * j + w]);
+      float o = 0.0f;
+  #pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) {
+        const float e = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[kAttnWaves * j + w] - M);
+        o = fmaf(e, red_o[kAttnWaves * j + w][dim], o);
+      }
+      a.part[attn_o_offset(g, split, r - hb + j, S, R, D) + dim] = o;
+    }
+    if (static_cast<int>(threadIdx.x) < kHeads) {
+      const int j = threadIdx.x;
+      float M = red_m[kAttnWaves * j];
+  #pragma unroll
+      for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[kAttnWaves * j + w]);
+      float L = 0.0f;
+  #pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w)
+        L = fmaf(M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[kAttnWaves * j + w] - M), red_l[kAttnWaves * j + w], L);
+      float* dst = a.part + attn_ml_offset(g, split, r - hb + j, S, R, D, a.hkv);
+      dst[0] = M * 0.6931471805599453f;  // ln 2
+      dst[1] = L;
+    }
   }
   // The new token's k / v (rounded to the cache dtype above), after every
   // other memory operation of the block.
@@ -900,6 +947,14 @@ __global__ __launch_bounds__(kWave) void qkv_postprocess_kernel(QkvPostArgs a) {
 // (split, group) serving every head of the group is faster.
 constexpr int kHeadKernelMaxBlocks = 512;
 
+// Query heads per KV group that the per-head kernel serves in one block
+// (four waves each) past kHeadKernelMaxBlocks head blocks, while the blocks
+// fit one round on the GPU (one 1024-thread block per CU): beyond, the block
+// holding the newest tile could wait for a second round, and the split
+// kernel (256-thread blocks, several per CU) runs.
+constexpr int kGroupBlockHeads = 4;
+constexpr int kGroupBlockMaxBlocks = 256;
+
 template <typename KV, int D>
 hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
   const dim3 block(kAttnThreads);
@@ -915,9 +970,18 @@ hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
     }
     const dim3 head_grid(blocks);
     if (mode == kAttnFused) {
-      attention_head_kernel<KV, D, kAttnFused><<<head_grid, block, 0, s>>>(a);
+      attention_head_kernel<KV, D, kAttnFused, 1><<<head_grid, block, 0, s>>>(a);
     } else {
-      attention_head_kernel<KV, D, kAttnFromCache><<<head_grid, block, 0, s>>>(a);
+      attention_head_kernel<KV, D, kAttnFromCache, 1><<<head_grid, block, 0, s>>>(a);
+    }
+  } else if (a.hq / a.hkv == kGroupBlockHeads && static_cast<int64_t>(a.splits) * a.hkv <= kGroupBlockMaxBlocks) {
+    // Long contexts, groups of four query heads: one 1024-thread block per
+    // (split, group) stages each tile once for the four heads.
+    const dim3 unit_grid(a.splits * a.hkv), group_block(kGroupBlockHeads * kAttnThreads);
+    if (mode == kAttnFused) {
+      attention_head_kernel<KV, D, kAttnFused, kGroupBlockHeads><<<unit_grid, group_block, 0, s>>>(a);
+    } else {
+      attention_head_kernel<KV, D, kAttnFromCache, kGroupBlockHeads><<<unit_grid, group_block, 0, s>>>(a);
     }
   } else if (mode == kAttnFused) {
     attention_split_kernel<KV, D, kAttnFused, false><<<group_grid, block, 0, s>>>(a);
