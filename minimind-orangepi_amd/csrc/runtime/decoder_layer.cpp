@@ -61,7 +61,10 @@ LayerPlans plan_layer(const MiniMindConfig& c) {
   const int qs = static_cast<int>(c.num_attention_heads * c.head_dim);
   const int qkv_rows = qs + 2 * static_cast<int>(c.num_key_value_heads * c.head_dim);
   LayerPlans p;
-  p.qkv = plan_or_throw(qkv_rows, H, mmr::kEpiStore, 0, "qkv_proj");
+  // qkv takes 32-lane groups too (K >= 384): 2.44 -> 2.29 us per launch and
+  // 249.7 -> 247.9 us per MiniMind2 step against the automatic 64; the O
+  // projection (same K) measured no better with 32, down and 16 lanes worse.
+  p.qkv = plan_or_throw(qkv_rows, H, mmr::kEpiStore, H / 8 >= 48 ? 32 : 0, "qkv_proj");
   p.o = plan_or_throw(H, qs, mmr::kEpiResidual, 0, "o_proj");
   // gate_up keeps 32-lane groups: 64 measured slower for this kernel alone
   // and within noise for the step.
