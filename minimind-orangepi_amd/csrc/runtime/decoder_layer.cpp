@@ -28,9 +28,10 @@ T* upload(Arena& arena, const void* host, std::size_t count) {
   return dst;
 }
 
-mmr::GemvPlan plan_or_throw(int rows, int k, mmr::GemvEpilogue epi, int lanes, const char* name) {
+mmr::GemvPlan plan_or_throw(int rows, int k, mmr::GemvEpilogue epi, int lanes, int rows_per_group,
+                            const char* name) {
   mmr::GemvPlan p;
-  if (!mmr::gemv_plan(rows, k, epi, lanes, 0, &p))
+  if (!mmr::gemv_plan(rows, k, epi, lanes, rows_per_group, &p))
     throw std::invalid_argument(std::string("unsupported GEMV shape for ") + name);
   return p;
 }
@@ -61,15 +62,18 @@ LayerPlans plan_layer(const MiniMindConfig& c) {
   const int qs = static_cast<int>(c.num_attention_heads * c.head_dim);
   const int qkv_rows = qs + 2 * static_cast<int>(c.num_key_value_heads * c.head_dim);
   LayerPlans p;
-  // qkv takes 32-lane groups too (K >= 384): 2.44 -> 2.29 us per launch and
-  // 249.7 -> 247.9 us per MiniMind2 step against the automatic 64; the O
-  // projection (same K) measured no better with 32, down and 16 lanes worse.
-  p.qkv = plan_or_throw(qkv_rows, H, mmr::kEpiStore, H / 8 >= 48 ? 32 : 0, "qkv_proj");
-  p.o = plan_or_throw(H, qs, mmr::kEpiResidual, 0, "o_proj");
+  // qkv from K = 768 up: 64-lane groups of two rows, 8 rows per block (144
+  // blocks for MiniMind2 instead of 288 with one row).  Same-box step A/Bs:
+  // 32-lane groups of one row (also 144 blocks) took the step from 249.7 to
+  // 247.9 us, and the two-row 64-lane groups from there 251.8 -> 251.0 us on
+  // another box.  O, down and gate_up measured slower with fewer, larger
+  // blocks or other lane widths.
+  p.qkv = plan_or_throw(qkv_rows, H, mmr::kEpiStore, 0, H / 8 >= 96 ? 2 : 0, "qkv_proj");
+  p.o = plan_or_throw(H, qs, mmr::kEpiResidual, 0, 0, "o_proj");
   // gate_up keeps 32-lane groups: 64 measured slower for this kernel alone
   // and within noise for the step.
-  p.gate_up = plan_or_throw(2 * F, H, mmr::kEpiSwiGlu, H / 8 >= 48 ? 32 : 0, "gate_up_proj");
-  p.down = plan_or_throw(H, F, mmr::kEpiResidual, 0, "down_proj");
+  p.gate_up = plan_or_throw(2 * F, H, mmr::kEpiSwiGlu, H / 8 >= 48 ? 32 : 0, 0, "gate_up_proj");
+  p.down = plan_or_throw(H, F, mmr::kEpiResidual, 0, 0, "down_proj");
   return p;
 }
 
