@@ -442,13 +442,20 @@ __device__ inline void residual_norm_row(float4* h4, const float4* p4, int64_t s
   const float4 wv = reinterpret_cast<const float4*>(w)[qq];
   float4 ps = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (splits > 0) ps = sum_parts4(p4 + qq, sstride, grp, kResGroups, splits);
-  if (splits > 0) red[grp][t] = ps;
-  __syncthreads();
   float4 v = hv;
-  if (splits > 0) {
+  if constexpr (kResGroups == 1) {  // the thread holds its column's whole sum: no LDS exchange
+    if (splits > 0) {
+      v = add4(v, ps);
+      if (live) h4[t] = v;
+    }
+  } else {
+    if (splits > 0) red[grp][t] = ps;
+    __syncthreads();
+    if (splits > 0) {
 #pragma unroll
-    for (int g2 = 0; g2 < kResGroups; ++g2) v = add4(v, red[g2][t]);
-    if (live) h4[t] = v;
+      for (int g2 = 0; g2 < kResGroups; ++g2) v = add4(v, red[g2][t]);
+      if (live) h4[t] = v;
+    }
   }
   float ss = live ? v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w : 0.0f;
   ss = group_sum<kWave>(ss);
