@@ -453,7 +453,8 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): batch-1 decode "
-              f"of a 104M-parameter model has no cross-GPU work; see DESIGN.md for how it would shard.",
+              f"of a 104M-parameter model has no cross-GPU work (it would shard by sequence: one weight replica "
+              f"and its own requests per GPU, no collective on the decode path).",
               file=sys.stderr)
         return 2
     if args.steps < 1 or args.steps + PROMPT_LEN > MINIMIND2["max_position_embeddings"]:
