@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
 #pragma unroll
       for (int sp = 0; sp < kCombine; ++sp) {
         if (sp < S) {
-          const float e = expf(ml[p][sp].x - M);
+          const float e = __builtin_amdgcn_exp2f((ml[p][sp].x - M) * 1.4426950408889634f);  // e^x = 2^(x log2 e)
           L = fmaf(ml[p][sp].y, e, L);
           o.x = fmaf(ov[p][sp].x, e, o.x);
           o.y = fmaf(ov[p][sp].y, e, o.y);
