@@ -177,6 +177,15 @@ using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 constexpr int kAPlain = 0, kASwiGlu = 1, kACombine4 = 2, kACombine8 = 3;
 constexpr int kSwiGluParts = 4;
 
+// silu(g) = g / (1 + e^-g) with e^-g as 2^(-g log2 e) on v_exp_f32 and the
+// quotient as a product with v_rcp_f32 (each within an ulp or two): the
+// batched down GEMM applies it to every staged element, where expf and an
+// IEEE divide cost some 30 instructions per element.  (The single-sequence
+// and prefill paths keep expf and the divide.)
+__device__ __forceinline__ float silu_fast(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
 template <int BT, int NB, int kAMode>
 __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   constexpr bool kSwiGlu = kAMode == kASwiGlu;
@@ -242,7 +251,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
       const int r = wave + 4 * (p * RPP + sub);
       float x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = (gs[j] / (1.0f + expf(-gs[j]))) * us[j];  // decoder_layer.cpp:175-182
+      for (int j = 0; j < 4; ++j) x[j] = silu_fast(gs[j]) * us[j];  // decoder_layer.cpp:175-182
       av[p] = (lane_on && r < g.m) ? make_float4(x[0], x[1], x[2], x[3]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
   } else if constexpr (kCombine > 0) {
@@ -584,8 +593,8 @@ __global__ void batch_swiglu_kernel(const float* part, int splits, int batch, in
   const float4 p = sum_parts4(reinterpret_cast<const float4*>(part) + static_cast<int64_t>(b) * f / 2 + i, sstride, 0, 1,
                               splits);
   float2 out;
-  out.x = (p.x / (1.0f + expf(-p.x))) * p.y;
-  out.y = (p.z / (1.0f + expf(-p.z))) * p.w;
+  out.x = silu_fast(p.x) * p.y;
+  out.y = silu_fast(p.z) * p.w;
   reinterpret_cast<float2*>(act + static_cast<int64_t>(b) * f)[i] = out;
 }
 
