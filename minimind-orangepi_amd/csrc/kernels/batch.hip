@@ -177,15 +177,6 @@ using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
 constexpr int kAPlain = 0, kASwiGlu = 1, kACombine4 = 2, kACombine8 = 3;
 constexpr int kSwiGluParts = 4;
 
-// silu(g) = g / (1 + e^-g) with e^-g as 2^(-g log2 e) on v_exp_f32 and the
-// quotient as a product with v_rcp_f32 (each within an ulp or two): the
-// batched down GEMM applies it to every staged element, where expf and an
-// IEEE divide cost some 30 instructions per element.  (The single-sequence
-// and prefill paths keep expf and the divide.)
-__device__ __forceinline__ float silu_fast(float g) {
-  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
-}
-
 template <int BT, int NB, int kAMode>
 __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   constexpr bool kSwiGlu = kAMode == kASwiGlu;

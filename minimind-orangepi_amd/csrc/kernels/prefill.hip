@@ -256,7 +256,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x4 (&a
     const float gate[2] = {odd ? x2 : v[0], odd ? x3 : v[1]};
     const float up[2] = {odd ? v[2] : x0, odd ? v[3] : x1};
 #pragma unroll
-    for (int k = 0; k < 2; ++k) act[k] = (gate[k] / (1.0f + expf(-gate[k]))) * up[k];
+    for (int k = 0; k < 2; ++k) act[k] = silu_fast(gate[k]) * up[k];
   };
   bool act_to_lds = false;
   constexpr bool kActSplit = kEpi == kGemmEpiSwiGlu && (BN == 128 || BN == 64);  // whole 32-column act chunks
