@@ -163,9 +163,8 @@ __device__ __forceinline__ __half from_float<__half>(float v) {
 
 // silu(g) = g / (1 + e^-g) with e^-g as 2^(-g log2 e) on v_exp_f32 and the
 // quotient as a product with v_rcp_f32 (each within an ulp or two): the
-// batched down GEMM and the prefill gate_up epilogue apply it to every
-// element, where expf and an IEEE divide cost some 30 instructions each.
-// (The single-sequence decode keeps expf and the divide.)
+// batched down GEMM, the prefill gate_up epilogue and the decode gate_up
+// GEMV apply it, where expf and an IEEE divide cost some 30 instructions.
 __device__ __forceinline__ float silu_fast(float g) {
   return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }

@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
         if (row + 1 < a.rows) {
           const float g = acc[2 * p];
           const float u = acc[2 * p + 1];
-          a.y[row / 2] = (g / (1.0f + expf(-g))) * u;
+          a.y[row / 2] = silu_fast(g) * u;
         }
       }
     }
