@@ -279,7 +279,9 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += xv[i][e] * xv[i][e];
     ss = group_sum<G>(ss);
-    const float scale = 1.0f / sqrtf(ss / static_cast<float>(k) + a.eps);
+    // 1 / sqrt as one v_rsq_f32 (about 1 ulp) instead of a correctly rounded
+    // sqrt and an IEEE divide on the prologue's critical path.
+    const float scale = __builtin_amdgcn_rsqf(ss / static_cast<float>(k) + a.eps);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
 #pragma unroll
