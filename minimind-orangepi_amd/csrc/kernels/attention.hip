@@ -64,7 +64,8 @@ template <int D>
 __device__ __forceinline__ void wave_norm_rope_pair(float& x0, float& x1, float w0, float w1, float eps, float c,
                                                     float s) {
   const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
-  const float scale = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + eps);  // v_rsq_f32, about 1 ulp
+  // v_rsq_f32 (about 1 ulp) of the mean as one fma with 1 / d (a constant)
+  const float scale = __builtin_amdgcn_rsqf(fmaf(ss, 1.0f / static_cast<float>(D), eps));
   const float first = x0 * (scale * w0);
   const float second = x1 * (scale * w1);
   x0 = first * c - second * s;

@@ -464,7 +464,7 @@ __device__ inline void residual_norm_row(float4* h4, const float4* p4, int64_t s
   float total = 0.0f;
 #pragma unroll
   for (int i = 0; i < kResThreads / kWave; ++i) total += s_ss[i];
-  const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
+  const float scale = __builtin_amdgcn_rsqf(total / static_cast<float>(cols) + eps);  // v_rsq_f32, about 1 ulp
   const float hvv[4] = {v.x, v.y, v.z, v.w}, wvv[4] = {wv.x, wv.y, wv.z, wv.w};
   float xv[4];
 #pragma unroll
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kResThreads) void batch_residual_norm_kernel(float*
   float total = 0.0f;
 #pragma unroll
   for (int i = 0; i < kResThreads / kWave; ++i) total += s_ss[i];
-  const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
+  const float scale = __builtin_amdgcn_rsqf(total / static_cast<float>(cols) + eps);  // v_rsq_f32, about 1 ulp
   float* hr = h + static_cast<int64_t>(b) * cols;
   if (x) {
     float* xr = x + static_cast<int64_t>(b) * cols;

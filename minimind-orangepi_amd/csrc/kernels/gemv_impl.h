@@ -60,6 +60,9 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     }
     asm volatile("" ::: "memory");
   };
+  // 1 / k for the RMSNorm mean, off the critical path (the mean is then one
+  // fma with the epsilon instead of an IEEE divide after the reduction).
+  const float inv_k = 1.0f / static_cast<float>(k);
   float res[RPG];
   if constexpr (EPI == kEpiResidual) {
 #pragma unroll
@@ -281,7 +284,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     ss = group_sum<G>(ss);
     // 1 / sqrt as one v_rsq_f32 (about 1 ulp) instead of a correctly rounded
     // sqrt and an IEEE divide on the prologue's critical path.
-    const float scale = __builtin_amdgcn_rsqf(ss / static_cast<float>(k) + a.eps);
+    const float scale = __builtin_amdgcn_rsqf(fmaf(ss, inv_k, a.eps));
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
 #pragma unroll

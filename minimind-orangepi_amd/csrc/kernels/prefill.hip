@@ -730,7 +730,7 @@ __global__ __launch_bounds__(kWave* kQkvRowsTokens) void qkv_rows_kernel(QkvRows
   x0 = lane < D ? x0 : 0.0f;
   x1 = lane + kWave < D ? x1 : 0.0f;
   const float ss = group_sum<kWave>(x0 * x0 + x1 * x1);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps);
+  const float scale = __builtin_amdgcn_rsqf(fmaf(ss, 1.0f / static_cast<float>(D), a.eps));  // v_rsq_f32, about 1 ulp
   if (lane < D) x_s[lane] = x0 * (scale * w0);
   if (lane + kWave < D) x_s[lane + kWave] = x1 * (scale * w1);
   const int pos = a.start + t;
