@@ -1,96 +1,131 @@
-// bench_decode -- prefill/decode timing with the reference's flags and output
-// keys (bench/bench_decode.cpp:117-151):
-//   --model DIR --prompt TEXT --input-tokens 1,2 --tokens N --warmup W
-// decode_steps = tokens - 1 as in the reference.  Without a runtime model
-// directory it times the reference's toy model (bench_decode.cpp:124-126).
-// --kv f16|f32 picks the KV cache dtype (default f16, the reference device
-// cache's).  The reference times
-// forward_next_token calls that each synchronise; --device-loop 1 instead
-// enqueues the steps back to back with the token fed forward on the device
-// and synchronises once (the runtime's throughput mode).
-#include "../runtime/language_model.h"
-#include "cli_args.h"
-
-#include <hip/hip_runtime.h>
+// bench_decode -- prefill and decode timing of one greedy run.
+//
+// Interface of the reference tool (bench/bench_decode.cpp:117-151):
+//   --model DIR  --prompt TEXT (default "hello")  --input-tokens 1,2
+//   --tokens N (default 16, ids collected)  --warmup W (default 1)
+// stdout: eight key=value lines, prompt_tokens, generated_tokens,
+// prefill_tokens, prefill_seconds, prefill_tokens_per_second, decode_steps,
+// decode_seconds, decode_tokens_per_second.  Timing semantics kept from the
+// reference: W untimed runs on fresh states, then one timed run on a fresh
+// state; the prefill clock covers prefill_next_token, the decode clock covers
+// the N-1 greedy steps that produce ids 2..N; decode_steps = N - 1; a rate is 0
+// when its count or time is 0.  Without a runtime model directory the toy model
+// runs (bench_decode.cpp:124-126).
+//
+// Added here:
+//   --kv f16|f32      KV cache dtype (default f16, the reference device cache's)
+//   --device-loop 1   enqueue the N-1 steps back to back with the token fed
+//                     forward on the device and one synchronisation at the end
+//                     (the runtime's throughput mode); 0 (default) makes one
+//                     synchronous forward_next_token call per step, as the
+//                     reference does.
+#include "tool_support.h"
 
 #include <algorithm>
 #include <chrono>
 #include <iostream>
+#include <sstream>
+#include <string>
+#include <utility>
 
 namespace {
 
-using namespace minimind::model;
+using minimind::model::DecoderState;
+using minimind::model::KvCacheDtype;
+using minimind::model::LanguageModel;
 
-struct Timing {
-  double prefill_seconds = 0, decode_seconds = 0;
-  int64_t prefill_tokens = 0, decode_steps = 0;
+template <class Work>
+double seconds_spent(Work&& work) {
+  const auto begin = std::chrono::steady_clock::now();
+  work();
+  return std::chrono::duration<double>(std::chrono::steady_clock::now() - begin).count();
+}
+
+double rate(double count, double seconds) { return count == 0.0 || seconds == 0.0 ? 0.0 : count / seconds; }
+
+// Counts print as integers, times and rates in the stream's default format.
+std::string as_text(int64_t count) { return std::to_string(count); }
+std::string as_text(double number) {
+  std::ostringstream out;
+  out << number;
+  return out.str();
+}
+
+struct Settings {
+  int64_t wanted = 16;  // ids to collect: the prefill's prediction plus wanted-1 steps
+  int64_t warmup = 1;
+  bool device_loop = false;
+  KvCacheDtype kv = KvCacheDtype::kFloat16;
 };
 
-Timing run(const LanguageModel& model, const std::vector<int32_t>& prompt, int64_t decode_tokens, bool device_loop,
-           KvCacheDtype kv, std::vector<int32_t>& generated) {
-  const int64_t cap = static_cast<int64_t>(prompt.size()) + std::max<int64_t>(decode_tokens, 1);
-  DecoderState state = model.make_state(cap, kv);
-  Timing t;
-  const auto p0 = std::chrono::steady_clock::now();
-  int32_t next = model.prefill_next_token(prompt, state);
-  const auto p1 = std::chrono::steady_clock::now();
-  generated.clear();
-  const auto d0 = std::chrono::steady_clock::now();
-  if (device_loop) {
-    if (decode_tokens > 1) model.enqueue_decode(state, decode_tokens - 1);
-    model.synchronize(state);
-    const auto d1 = std::chrono::steady_clock::now();
-    t.decode_seconds = std::chrono::duration<double>(d1 - d0).count();
-    generated = model.read_sequence(state, static_cast<int64_t>(prompt.size()), std::max<int64_t>(decode_tokens, 0));
+struct Measured {
+  std::vector<int32_t> ids;
+  double prefill_s = 0.0;
+  double decode_s = 0.0;
+};
+
+Measured measure_once(const LanguageModel& model, const std::vector<int32_t>& prompt, const Settings& s) {
+  const int64_t prompt_len = static_cast<int64_t>(prompt.size());
+  const int64_t steps = std::max<int64_t>(s.wanted - 1, 0);
+  DecoderState state = model.make_state(prompt_len + steps + 1, s.kv);
+  Measured m;
+  int32_t last = 0;
+  m.prefill_s = seconds_spent([&] { last = model.prefill_next_token(prompt, state); });
+  if (s.wanted <= 0) return m;
+  if (s.device_loop) {
+    m.decode_s = seconds_spent([&] {
+      if (steps > 0) model.enqueue_decode(state, steps);
+      model.synchronize(state);
+    });
+    m.ids = model.read_sequence(state, prompt_len, s.wanted);
   } else {
-    for (int64_t i = 0; i < decode_tokens; ++i) {
-      generated.push_back(next);
-      if (i + 1 < decode_tokens) next = model.forward_next_token(next, state);
-    }
-    const auto d1 = std::chrono::steady_clock::now();
-    t.decode_seconds = std::chrono::duration<double>(d1 - d0).count();
+    m.ids.reserve(static_cast<size_t>(s.wanted));
+    m.decode_s = seconds_spent([&] {
+      m.ids.push_back(last);
+      for (int64_t i = 0; i < steps; ++i) m.ids.push_back(last = model.forward_next_token(last, state));
+    });
   }
-  t.prefill_seconds = std::chrono::duration<double>(p1 - p0).count();
-  t.prefill_tokens = static_cast<int64_t>(prompt.size());
-  t.decode_steps = std::max<int64_t>(0, decode_tokens - 1);
-  return t;
+  return m;
+}
+
+int bench(const mmr_tools::Argv& args) {
+  Settings s;
+  const std::string kv = args.text("--kv", "f16");
+  if (kv != "f16" && kv != "f32") {
+    std::cerr << "bench_decode: --kv must be f16 or f32\n";
+    return 2;
+  }
+  s.kv = kv == "f16" ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32;
+  s.wanted = args.integer("--tokens", 16);
+  s.warmup = args.integer("--warmup", 1);
+  s.device_loop = args.integer("--device-loop", 0) != 0;
+
+  const LanguageModel model = mmr_tools::open_model(args.text("--model", ""));
+  const std::vector<int32_t> prompt = mmr_tools::prompt_ids(args, "--input-tokens", "hello", model.config(), false);
+  for (int64_t i = 0; i < s.warmup; ++i) (void)measure_once(model, prompt, s);
+  const Measured m = measure_once(model, prompt, s);
+
+  const int64_t prompt_len = static_cast<int64_t>(prompt.size());
+  const int64_t steps = std::max<int64_t>(s.wanted - 1, 0);
+  const std::pair<const char*, std::string> rows[] = {
+      {"prompt_tokens", as_text(prompt_len)},
+      {"generated_tokens", as_text(static_cast<int64_t>(m.ids.size()))},
+      {"prefill_tokens", as_text(prompt_len)},
+      {"prefill_seconds", as_text(m.prefill_s)},
+      {"prefill_tokens_per_second", as_text(rate(static_cast<double>(prompt_len), m.prefill_s))},
+      {"decode_steps", as_text(steps)},
+      {"decode_seconds", as_text(m.decode_s)},
+      {"decode_tokens_per_second", as_text(rate(static_cast<double>(steps), m.decode_s))},
+  };
+  for (const auto& [key, text] : rows) std::cout << key << '=' << text << '\n';
+  return 0;
 }
 
 }  // namespace
 
 int main(int argc, char** argv) {
   try {
-    const std::string model_dir = mmr_cli::arg_value(argc, argv, "--model", "");
-    const std::string prompt = mmr_cli::arg_value(argc, argv, "--prompt", "hello");
-    const std::string explicit_tokens = mmr_cli::arg_value(argc, argv, "--input-tokens", "");
-    const int64_t decode_tokens = mmr_cli::int_arg_value(argc, argv, "--tokens", 16);
-    const int64_t warmup = mmr_cli::int_arg_value(argc, argv, "--warmup", 1);
-    const bool device_loop = mmr_cli::int_arg_value(argc, argv, "--device-loop", 0) != 0;
-    const std::string kv_name = mmr_cli::arg_value(argc, argv, "--kv", "f16");
-    if (kv_name != "f16" && kv_name != "f32") {
-      std::cerr << "bench_decode: --kv must be f16 or f32\n";
-      return 2;
-    }
-    const KvCacheDtype kv = kv_name == "f16" ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32;
-    LanguageModel model = !model_dir.empty() && has_runtime_language_model(model_dir)
-                              ? load_runtime_language_model(model_dir)
-                              : make_toy_language_model();
-    auto tokens = explicit_tokens.empty() ? std::vector<int32_t>{} : mmr_cli::parse_token_ids(explicit_tokens);
-    if (tokens.empty()) tokens = mmr_cli::byte_prompt(prompt, model.config().vocab_size, model.config().bos_token_id);
-    std::vector<int32_t> generated;
-    for (int64_t i = 0; i < warmup; ++i) (void)run(model, tokens, decode_tokens, device_loop, kv, generated);
-    const Timing t = run(model, tokens, decode_tokens, device_loop, kv, generated);
-    const double dtps = t.decode_steps == 0 || t.decode_seconds == 0.0 ? 0.0 : t.decode_steps / t.decode_seconds;
-    const double ptps = t.prefill_tokens == 0 || t.prefill_seconds == 0.0 ? 0.0 : t.prefill_tokens / t.prefill_seconds;
-    std::cout << "prompt_tokens=" << tokens.size() << '\n';
-    std::cout << "generated_tokens=" << generated.size() << '\n';
-    std::cout << "prefill_tokens=" << t.prefill_tokens << '\n';
-    std::cout << "prefill_seconds=" << t.prefill_seconds << '\n';
-    std::cout << "prefill_tokens_per_second=" << ptps << '\n';
-    std::cout << "decode_steps=" << t.decode_steps << '\n';
-    std::cout << "decode_seconds=" << t.decode_seconds << '\n';
-    std::cout << "decode_tokens_per_second=" << dtps << '\n';
-    return 0;
+    return bench(mmr_tools::Argv(argc, argv));
   } catch (const std::exception& e) {
     std::cerr << "bench_decode: " << e.what() << '\n';
     return 1;

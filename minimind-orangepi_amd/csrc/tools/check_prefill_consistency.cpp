@@ -7,7 +7,7 @@
 // Prints "prefill consistency ok" and exits 0, or the first disagreement on
 // stderr and exits 1.
 #include "../runtime/language_model.h"
-#include "cli_args.h"
+#include "tool_support.h"
 
 #include <iostream>
 #include <string>
@@ -25,7 +25,7 @@ int main(int argc, char** argv) {
       std::cerr << "tokens must be positive\n";
       return 1;
     }
-    const std::string kv_name = mmr_cli::arg_value(argc, argv, "--kv", "f32");
+    const std::string kv_name = mmr_tools::Argv(argc, argv).text("--kv", "f32");
     const KvCacheDtype kv = kv_name == "f16" ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32;
     const LanguageModel model = load_runtime_language_model(argv[1]);
     std::vector<int32_t> prompt(static_cast<size_t>(n));

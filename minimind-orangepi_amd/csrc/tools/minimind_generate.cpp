@@ -1,46 +1,54 @@
-// minimind_generate -- greedy generation CLI with the reference's flags and
-// stdout protocol (src/csrc/tools/minimind_generate.cpp:77-111):
-//   --model DIR --prompt TEXT --tokens 1,2,3 --max-new-tokens N [--stream]
-// prints "prompt_tokens: ...", optional "token: N" lines, "generated_tokens: ...".
-// Without a runtime model directory it runs the reference's built-in toy model
-// (minimind_generate.cpp:84-86), on the GPU like any other model.
-#include "../runtime/language_model.h"
-#include "cli_args.h"
+// minimind_generate -- greedy generation from the command line.
+//
+// Interface of the reference tool (src/csrc/tools/minimind_generate.cpp:77-111):
+//   --model DIR  --prompt TEXT (default "MiniMind")  --tokens 1,2,3
+//   --max-new-tokens N (default 8)  --stream
+// stdout: "prompt_tokens: ...", with --stream one "token: N" line per id as it
+// is produced, then "generated_tokens: ...".  With no runtime model directory
+// the reference's built-in toy model runs, on the GPU like any other model.
+//
+// Every id goes through one sink that records it and, when streaming, echoes
+// it at once; the blocking and streaming modes differ only in that echo.
+#include "tool_support.h"
 
 #include <iostream>
-#include <stdexcept>
+
+namespace {
+
+class IdSink {
+ public:
+  IdSink(std::ostream& out, bool echo) : out_(out), echo_(echo) {}
+  void operator()(int32_t id) {
+    ids_.push_back(id);
+    if (echo_) out_ << "token: " << id << std::endl;  // one flushed line per id
+  }
+  const std::vector<int32_t>& ids() const { return ids_; }
+
+ private:
+  std::ostream& out_;
+  bool echo_;
+  std::vector<int32_t> ids_;
+};
+
+void generate_to(std::ostream& out, const mmr_tools::Argv& args) {
+  const minimind::model::LanguageModel model = mmr_tools::open_model(args.text("--model", ""));
+  const std::vector<int32_t> prompt = mmr_tools::prompt_ids(args, "--tokens", "MiniMind", model.config(), true);
+  const int64_t budget = args.integer("--max-new-tokens", 8);
+  const bool streaming = args.has("--stream");
+
+  mmr_tools::write_id_line(out, "prompt_tokens", prompt);
+  if (streaming) out.flush();  // the prompt line reaches a reader before the first id
+  IdSink sink(out, streaming);
+  model.generate_stream(prompt, budget, [&sink](int32_t id) { sink(id); });
+  mmr_tools::write_id_line(out, "generated_tokens", sink.ids());
+  out.flush();
+}
+
+}  // namespace
 
 int main(int argc, char** argv) {
-  using namespace minimind::model;
   try {
-    const std::string prompt = mmr_cli::arg_value(argc, argv, "--prompt", "MiniMind");
-    const std::string explicit_tokens = mmr_cli::arg_value(argc, argv, "--tokens", "");
-    const std::string model_dir = mmr_cli::arg_value(argc, argv, "--model", "");
-    const int64_t max_new = mmr_cli::int_arg_value(argc, argv, "--max-new-tokens", 8);
-    const bool stream = mmr_cli::has_arg(argc, argv, "--stream");
-    LanguageModel model = !model_dir.empty() && has_runtime_language_model(model_dir)
-                              ? load_runtime_language_model(model_dir)
-                              : make_toy_language_model();
-    auto tokens = explicit_tokens.empty() ? std::vector<int32_t>{} : mmr_cli::parse_token_ids(explicit_tokens);
-    if (tokens.empty()) tokens = mmr_cli::byte_prompt(prompt, model.config().vocab_size, model.config().bos_token_id);
-    for (int32_t t : tokens)
-      if (t < 0 || t >= model.config().vocab_size) throw std::out_of_range("input token id is out of vocabulary range");
-    std::cout << "prompt_tokens:";
-    for (int32_t t : tokens) std::cout << ' ' << t;
-    std::cout << '\n';
-    std::vector<int32_t> generated;
-    if (stream) {
-      std::cout << std::flush;
-      model.generate_stream(tokens, max_new, [&generated](int32_t t) {
-        generated.push_back(t);
-        std::cout << "token: " << t << '\n' << std::flush;
-      });
-    } else {
-      generated = model.generate(tokens, max_new);
-    }
-    std::cout << "generated_tokens:";
-    for (int32_t t : generated) std::cout << ' ' << t;
-    std::cout << '\n' << std::flush;
+    generate_to(std::cout, mmr_tools::Argv(argc, argv));
     return 0;
   } catch (const std::exception& e) {
     std::cerr << "minimind_generate: " << e.what() << '\n';
