@@ -91,6 +91,14 @@ int mmr_graph_destroy(void* graph);
  * (load_store 0: empty kernels; 1: each loads one float its predecessor
  * wrote and stores one), replayed `reps` times.  Synchronous. */
 int mmr_launch_floor_us(int kernels, int blocks, int load_store, int reps, float* us_per_kernel);
+/* Test aids with no counterpart in the reference (host arithmetic, no
+ * device needed): the K-split count the prefill / batched GEMM takes for an
+ * m x n x k product, and the floats of the prefill split-K partial buffer a
+ * state with prefill chunks of up to chunk_rows rows allocates (the largest
+ * splits x rows x n over the four projections and every row count
+ * 1..chunk_rows). */
+int mmr_gemm_k_splits(int64_t m, int64_t n, int64_t k, int* splits);
+int mmr_prefill_partial_floats(const mmr_config* config, int64_t chunk_rows, int64_t* floats);
 /* float_to_half / half_to_float (ascend_matmul.h:14-15), but IEEE
  * round-to-nearest-even instead of the reference's ties-away rounding. */
 int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n);
@@ -204,8 +212,10 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
  * 33-55, ascend_custom_ops.cpp:333-530).  Every pointer is host memory; each
  * call uploads, runs the device op, waits and copies back (so these
  * allocate and synchronise, as the reference's do).  Matrices are fp32
- * [rows][cols] rounded to fp16 on upload; inputs, outputs and the caches
- * stay fp32 (the reference rounds them to fp16).  keys/values are in the
+ * [rows][cols] rounded to fp16 on upload; inputs and outputs stay fp32 (the
+ * reference rounds them to fp16).  Caches the twins create are fp32; a
+ * caller's fp16 cache keeps its dtype (also when grown) and receives the rows
+ * rounded to fp16 (RNE).  keys/values are in the
  * reference layout [token][kv_head][head_dim]; key/value of the cached form
  * are one token's [kv_head][head_dim], written at row tokens - 1.  The cache
  * argument may be *cache == NULL (a new fp32 cache of at least 2048 tokens

@@ -49,23 +49,38 @@ std::vector<uint16_t> to_half(const float* v, std::size_t n) {
 }
 
 // Keys/values of tokens [first, first + count) from the reference layout
-// [token][kv_head][d] into the cache layout [kv_head][rows][d].
+// [token][kv_head][d] (fp32) into the cache layout [kv_head][rows][d], in the
+// cache's element type: an fp16 cache gets the rows rounded to fp16 (RNE),
+// the rounding the decode kernels apply when they append.
 void write_rows(mmr_kv_cache* cache, const float* keys, const float* values, int64_t first, int64_t count,
                 int64_t kv_heads, int64_t head_dim) {
   void *kp = nullptr, *vp = nullptr;
   int64_t rows = 0;
+  int dtype = MMR_KV_F32;
   ok(mmr_kv_cache_data(cache, &kp, &vp));
   ok(mmr_kv_cache_rows(cache, &rows));
-  const std::size_t pitch_src = static_cast<std::size_t>(kv_heads * head_dim) * 4;
-  const std::size_t width = static_cast<std::size_t>(head_dim) * 4;
+  ok(mmr_kv_cache_info(cache, nullptr, nullptr, nullptr, &dtype));
+  const std::size_t elem = dtype == MMR_KV_F16 ? 2 : 4;
+  const std::size_t n = static_cast<std::size_t>(count * kv_heads * head_dim);
+  std::vector<uint16_t> kh, vh;
+  const void* ksrc = keys;
+  const void* vsrc = values;
+  if (dtype == MMR_KV_F16) {
+    kh = to_half(keys, n);
+    vh = to_half(values, n);
+    ksrc = kh.data();
+    vsrc = vh.data();
+  }
+  const std::size_t pitch_src = static_cast<std::size_t>(kv_heads * head_dim) * elem;
+  const std::size_t width = static_cast<std::size_t>(head_dim) * elem;
   for (int64_t h = 0; h < kv_heads; ++h) {
-    const std::size_t dst = static_cast<std::size_t>((h * rows + first) * head_dim) * 4;
-    const std::size_t src = static_cast<std::size_t>(h * head_dim) * 4;
-    check_hip(hipMemcpy2D(static_cast<char*>(kp) + dst, width, reinterpret_cast<const char*>(keys) + src, pitch_src,
+    const std::size_t dst = static_cast<std::size_t>((h * rows + first) * head_dim) * elem;
+    const std::size_t src = static_cast<std::size_t>(h * head_dim) * elem;
+    check_hip(hipMemcpy2D(static_cast<char*>(kp) + dst, width, static_cast<const char*>(ksrc) + src, pitch_src,
                           width, static_cast<std::size_t>(count), hipMemcpyHostToDevice),
               "hipMemcpy2D keys");
-    check_hip(hipMemcpy2D(static_cast<char*>(vp) + dst, width, reinterpret_cast<const char*>(values) + src,
-                          pitch_src, width, static_cast<std::size_t>(count), hipMemcpyHostToDevice),
+    check_hip(hipMemcpy2D(static_cast<char*>(vp) + dst, width, static_cast<const char*>(vsrc) + src, pitch_src,
+                          width, static_cast<std::size_t>(count), hipMemcpyHostToDevice),
               "hipMemcpy2D values");
   }
 }

@@ -96,3 +96,28 @@ def test_cached_attention_grows_and_keeps_rows(gpu, oracle):
     out = mmr.custom_attention_cached(q, K[S], Vv[S], cache, S + 1, hq, hkv, d)
     assert cache.info()[2] >= S + 1
     assert rel_err(out, oracle.attention_step(q, K, Vv, S + 1, hq, hkv, d)) < 2e-3
+
+
+def test_cached_attention_forms_keep_a_callers_fp16_cache(gpu, oracle):
+    # A caller may hand the twins an fp16 cache (the reference's device cache
+    # dtype, ascend_custom_ops.cpp:126-139): rows are stored rounded to fp16,
+    # for every KV head, and the dtype survives growth.  The oracle sees the
+    # same fp16-rounded keys/values.
+    mmr = gpu
+    rng = np.random.default_rng(24)
+    hq, hkv, d, S = 8, 2, 64, 300
+    Q = rng.standard_normal((S, hq * d)).astype(np.float32)
+    K = rng.standard_normal((S + 2, hkv, d)).astype(np.float32)
+    Vv = rng.standard_normal((S + 2, hkv, d)).astype(np.float32)
+    Kh, Vh = (a.astype(np.float16).astype(np.float32) for a in (K, Vv))
+    cache = mmr.HostAttentionCache.create(hkv, d, S, mmr.KV_F16)
+    out = mmr.custom_prefill_attention(Q, K[:S], Vv[:S], cache, S, hq, hkv, d).reshape(S, hq * d)
+    for i in (0, 5, S - 1):
+        want = oracle.attention_step(Q[i], Kh[: i + 1], Vh[: i + 1], i + 1, hq, hkv, d)
+        assert rel_err(out[i], want) < 2e-3, i
+    q = rng.standard_normal(hq * d).astype(np.float32)
+    for t in (S + 1, S + 2):  # the second call outgrows the 300-row cache
+        got = mmr.custom_attention_cached(q, K[t - 1], Vv[t - 1], cache, t, hq, hkv, d)
+        assert rel_err(got, oracle.attention_step(q, Kh[:t], Vh[:t], t, hq, hkv, d)) < 2e-3, t
+    kvh, dd, cap, dtype = cache.info()
+    assert (kvh, dd, dtype) == (hkv, d, mmr.KV_F16) and cap >= S + 2
