@@ -8,9 +8,11 @@
 #include "host_ops.h"
 #include "runtime/decoder_layer.h"
 #include "runtime/device.h"
+#include "runtime/device_model.h"
 #include "runtime/language_model.h"
 
 #include <algorithm>
+#include <cstdint>
 #include <cmath>
 #include <cstring>
 #include <filesystem>
@@ -260,6 +262,20 @@ int mmr_launch_floor_us(int kernels, int blocks, int load_store, int reps, float
     require(us_per_kernel, "null us_per_kernel");
     require(kernels > 0 && kernels <= 4096 && blocks > 0 && blocks <= 65536 && reps > 0, "probe size out of range");
     hip(mmr::measure_launch_floor(kernels, blocks, load_store != 0, reps, us_per_kernel), "launch floor probe");
+  });
+}
+int mmr_gemm_k_splits(int64_t m, int64_t n, int64_t k, int* splits) {
+  return guarded([&] {
+    require(splits, "null splits");
+    require(m > 0 && n > 0 && k > 0 && m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX, "shape out of range");
+    *splits = mmr::gemm_k_splits(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k));
+  });
+}
+int mmr_prefill_partial_floats(const mmr_config* config, int64_t chunk_rows, int64_t* floats) {
+  return guarded([&] {
+    require(config && floats, "null argument");
+    require(chunk_rows >= 0, "chunk_rows must be non-negative");
+    *floats = minimind::model::prefill_partial_floats(to_cpp(*config), chunk_rows);
   });
 }
 int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n) {

@@ -174,19 +174,19 @@ using lds_byte = __attribute__((address_space(3))) char;
 // One wave-wide direct load: lane l's `bytes` (16 or 4) at sbase + voff land
 // in LDS at m0 + l * bytes.  sbase is a scalar (wave-uniform) address and
 // voff this lane's 32-bit byte offset (the scalar-base form of the global
-// load), m0 the wave's LDS destination; a write of M0 needs one wait state
-// before an LDS-direct load reads it (s_nop).  The instruction is issued from
-// inline assembly so that the compiler, which does not see the LDS write,
+// load), m0 the wave's LDS destination.  M0 is an input operand ("{m0}"): the
+// compiler writes it before the statement and knows what it holds after, so
+// no value of the compiler's own is lost in it.  A write of M0 needs one wait
+// state before an LDS-direct load reads it (s_nop).  The instruction is issued
+// from inline assembly so that the compiler, which does not see the LDS write,
 // inserts no wait for it: the kernel waits with explicit vmcnt.
 template <int kBytes>
 __device__ __forceinline__ void dma_load(const void* sbase, uint32_t voff, uint32_t m0) {
   if constexpr (kBytes == 16) {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "s"(m0)
-                 : "memory");
+    asm volatile("s_nop 1\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
   } else {
     static_assert(kBytes == 4, "16- or 4-byte loads");
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 1\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "s"(m0)
-                 : "memory");
+    asm volatile("s_nop 1\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
   }
 }
 

@@ -37,4 +37,11 @@ struct DeviceModel {
   std::size_t weight_bytes = 0;
 };
 
+// Floats of the prefill split-K partial buffer for chunks of up to
+// `chunk_rows` rows: the largest splits x rows x N over the four projections
+// (QKV, O, gate_up, down) and every row count 1..chunk_rows.  Fewer rows can
+// take more K splits (the GEMM tiling aims at a block count), so the product
+// is not largest at chunk_rows.  Host arithmetic only.
+int64_t prefill_partial_floats(const MiniMindConfig& cfg, int64_t chunk_rows);
+
 }  // namespace minimind::model

@@ -236,6 +236,19 @@ LanguageModel& LanguageModel::operator=(LanguageModel&&) noexcept = default;
 
 std::size_t LanguageModel::device_weight_bytes() const { return device_->weight_bytes; }
 
+int64_t prefill_partial_floats(const MiniMindConfig& c, int64_t chunk_rows) {
+  const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
+  const int64_t F = c.intermediate_size;
+  const int64_t shapes[4][2] = {{(Hq + 2 * Hkv) * D, H}, {H, Hq * D}, {2 * F, H}, {H, F}};  // {N, K}
+  int64_t most = 0;
+  for (const auto& nk : shapes)
+    for (int64_t r = 1; r <= chunk_rows; ++r) {
+      const int splits = mmr::gemm_k_splits(static_cast<int>(r), static_cast<int>(nk[0]), static_cast<int>(nk[1]));
+      most = std::max<int64_t>(most, int64_t{splits} * r * nk[0]);
+    }
+  return most;
+}
+
 DecoderState LanguageModel::make_state() const { return make_state(0, KvCacheDtype::kFloat32); }
 
 DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const {
@@ -292,21 +305,12 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   ar.plan(part_floats * 4);
   ar.plan(device_->plan_lm.blocks * 4);
   ar.plan(device_->plan_lm.blocks * 4);
-  const int64_t qkv_w = Hq * D + 2 * Hkv * D;
   int64_t chunk = kPrefillChunk;
   if (const char* pc = std::getenv("MMR_PREFILL_CHUNK")) chunk = std::max<int64_t>(1, std::atoll(pc));
   s->pf_chunk = s->prefill_tokenwise ? 0 : std::min<int64_t>(capacity, chunk);
   const int64_t C = s->pf_chunk;
-  // Largest split-K partial set of any chunk, over every row count up to C:
-  // fewer rows can take more K splits (the tiling targets a block count), so
-  // splits x rows is not largest at C.
-  int64_t part_f = 0;
+  const int64_t part_f = prefill_partial_floats(c, C);
   if (C > 0) {
-    const int64_t shapes[4][2] = {{qkv_w, H}, {H, Hq * D}, {2 * F, H}, {H, F}};
-    for (const auto& sh : shapes)
-      for (int r = 1; r <= static_cast<int>(C); ++r)
-        part_f = std::max<int64_t>(
-            part_f, int64_t{mmr::gemm_k_splits(r, static_cast<int>(sh[0]), static_cast<int>(sh[1]))} * r * sh[0]);
     ar.plan(C * H * 4);
     ar.plan(C * H * 4);
     ar.plan(C * Hq * D * 4);

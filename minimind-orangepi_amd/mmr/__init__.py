@@ -101,6 +101,8 @@ _SIGS = {
     "mmr_event_destroy": ([VP], C.c_int),
     "mmr_event_record": ([VP, VP], C.c_int),
     "mmr_event_elapsed_ms": ([VP, VP, P_F32], C.c_int),
+    "mmr_gemm_k_splits": ([I64, I64, I64, C.POINTER(C.c_int)], C.c_int),
+    "mmr_prefill_partial_floats": ([C.POINTER(Config), I64, C.POINTER(I64)], C.c_int),
     "mmr_f32_to_f16": ([VP, VP, SZ], C.c_int),
     "mmr_f16_to_f32": ([VP, VP, SZ], C.c_int),
     "mmr_matvec_f16": ([VP, I64, I64, VP, VP, VP, VP], C.c_int),
@@ -352,6 +354,20 @@ def synchronize() -> None:
 def _stream_handle(stream) -> int | None:
     """A Stream, a raw hipStream_t handle (int) or None (the null stream)."""
     return stream.handle if isinstance(stream, Stream) else stream
+
+
+def gemm_k_splits(m: int, n: int, k: int) -> int:
+    """K splits of the prefill / batched GEMM for an m x n x k product (host arithmetic)."""
+    out = C.c_int()
+    check(_lib.mmr_gemm_k_splits(m, n, k, C.byref(out)))
+    return out.value
+
+
+def prefill_partial_floats(cfg: Config, chunk_rows: int) -> int:
+    """Floats of the prefill split-K partial buffer of a state with chunk_rows-row chunks."""
+    out = C.c_int64()
+    check(_lib.mmr_prefill_partial_floats(C.byref(cfg), chunk_rows, C.byref(out)))
+    return out.value
 
 
 def f32_to_f16(a: np.ndarray) -> np.ndarray:
@@ -620,6 +636,13 @@ class HostAttentionCache:
 
     def __init__(self):
         self.ptr = VP()
+
+    @classmethod
+    def create(cls, kv_heads: int, head_dim: int, capacity: int, kv_dtype: int) -> "HostAttentionCache":
+        """A caller-made cache (e.g. fp16, the reference's device cache dtype)."""
+        c = cls()
+        check(_lib.mmr_kv_cache_create(kv_heads, head_dim, capacity, kv_dtype, C.byref(c.ptr)))
+        return c
 
     def info(self) -> tuple[int, int, int, int]:
         a, b, c, d = C.c_int64(), C.c_int64(), C.c_int64(), C.c_int()

@@ -21,7 +21,18 @@ logit tolerance of the comparison (2e-3 * max|logit| against the reference,
 1e-4 * max|logit| between the batched and single-sequence GPU paths).  After a
 certified near-tie against the single-sequence path the comparison resumes
 from the batch's choice; against the golden it ends there (the golden has no
-other branch).
+other branch), and the stop is printed.
+
+The batched-vs-single bound is fixed, never measured from either GPU path.
+Both paths read the same fp16 weights and fp16 KV and accumulate in fp32;
+they differ only in summation order (GEMV lane trees against the hi/lo-split
+MFMA dot products, whose split error is <= 2^-22 of sum |w a| per product,
+and attention split merges) and in the fp16 rounding of K/V elements that
+those ~1e-6 relative differences push across a rounding boundary.  The
+budget for all of it is 1e-4 of max|logit|, twenty times inside the 2e-3
+the reference comparison allows; a flipped pair needs a top-2 margin below
+the paths' logit difference, so a margin above the budget means a fault in
+one of the paths, not a tie.
 """
 from __future__ import annotations
 
@@ -32,8 +43,7 @@ from conftest import load_golden, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3          # logits vs the reference CPU path
-BATCH_TOL = 1e-4    # batched vs single-sequence GPU paths (same fp16 weights and KV); widened
-                    # per position to twice the measured prefill-vs-tokenwise logit gap
+BATCH_TOL = 1e-4    # batched vs single-sequence GPU paths (same fp16 weights and KV), fixed
 
 
 def synth_model(mmr, g):
@@ -105,9 +115,12 @@ def test_minimind2_batch32_to_4096_positions(gpu):
 
     # sequence 0 against the reference CPU path's golden continuation
     tol_ref = TOL * float(np.max(np.abs(g["logits"])))
-    n0 = golden_prefix_match(seqs[0][P:].tolist(), g, tol_ref)
-    print(f"[result] sequence 0: {n0} of {len(g['generated'])} tokens equal the reference", flush=True)
-    assert n0 >= 1024
+    n_gen = len(g["generated"])
+    n0 = golden_prefix_match(seqs[0][P:].tolist(), g, tol_ref)  # a mismatch must be a certified near-tie
+    print(f"[result] sequence 0: {n0} of {n_gen} tokens equal the reference", flush=True)
+    if n0 < n_gen:
+        print(f"[stop] sequence 0 stops at generated token {n0}: certified near-tie with the reference "
+              f"(margin {g['margin'][n0]:.3g} <= {tol_ref:.3g})", flush=True)
 
     # every sequence against its single-sequence decode
     st = m.make_state(total, mmr.KV_F16)
@@ -129,19 +142,10 @@ def test_minimind2_batch32_to_4096_positions(gpu):
             st.enqueue_prefill(got[:i].tolist())
             st.synchronize()
             lg = st.read_logits()
-            # The paths' own disagreement at this position: the same prefix fed
-            # token by token (GEMV projections, K/V rounded to fp16 one row at
-            # a time) against the GEMM prefill.  A flipped pair can differ by
-            # at most twice that in its margin.
-            st.reset()
-            for t in got[:i - 1].tolist():
-                st.forward_token(t)
-            noise = float(np.max(np.abs(st.forward_token(int(got[i - 1])) - lg)))
-            bound = max(BATCH_TOL * float(np.max(np.abs(lg))), 2.0 * noise)
+            bound = BATCH_TOL * float(np.max(np.abs(lg)))
             top2 = np.argsort(lg)[-2:]
             margin = abs(float(lg[got[i]] - lg[ref[i]]))
-            print(f"[tie] sequence {b} position {i}: margin {margin:.3g} bound {bound:.3g} (path noise {noise:.3g})",
-                  flush=True)
+            print(f"[tie] sequence {b} position {i}: margin {margin:.3g} bound {bound:.3g}", flush=True)
             assert set(top2.tolist()) == {int(got[i]), int(ref[i])} and margin <= bound, (
                 f"sequence {b} position {i}: batch {got[i]} single {ref[i]} not a near-tie")
             ties += 1

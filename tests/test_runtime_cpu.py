@@ -168,3 +168,25 @@ def test_op_argument_checks_need_no_device(mmr):
     assert mmr.matvec_argmax_workspace_size(6400, 768) > 0
     assert mmr.matvec_argmax_workspace_size(6400, 770) == 0
     assert mmr.attention_workspace_size(8, 2, 96, 64) == 2 * 64 * 4 * 98 * 4
+
+
+@pytest.mark.parametrize("case", ["cfg3", "cfg0", "mini"])
+def test_prefill_partial_buffer_covers_every_chunk_row_count(mmr, case):
+    # The prefill GEMMs write split-K partials [splits][rows][N] into one
+    # buffer sized when the state is made.  A chunk of r <= C rows can take
+    # more K splits than a full chunk (the tiling aims at a block count), so
+    # the buffer must hold the largest splits x r x N over every r, not r = C.
+    cfg = mmr.make_config(**load_golden(case)["config"])
+    H, D, Hq, Hkv, F = (cfg.hidden_size, cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads,
+                        cfg.intermediate_size)
+    shapes = [((Hq + 2 * Hkv) * D, H), (H, Hq * D), (2 * F, H), (H, F)]  # (N, K): QKV, O, gate_up, down
+    for C in (512, 333, 100, 17, 1):
+        have = mmr.prefill_partial_floats(cfg, C)
+        need = {r: max(mmr.gemm_k_splits(r, n, k) * r * n for n, k in shapes) for r in range(1, C + 1)}
+        worst = max(need, key=need.get)
+        assert need[worst] <= have, (case, C, worst, need[worst], have)
+        assert have == need[worst]  # tight: nothing beyond the largest chunk's need
+        if case == "cfg3" and C == 512:
+            # the case the buffer once missed: a shorter chunk needs more than a full one
+            assert need[worst] > need[C] and worst < C
+    assert mmr.prefill_partial_floats(cfg, 0) == 0
