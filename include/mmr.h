@@ -146,18 +146,42 @@ int mmr_rope_table_create(int64_t max_positions, int64_t head_dim, float theta, 
 int mmr_rope_table_destroy(mmr_rope_table* table);
 
 /* ---- resident KV cache of one layer: CustomAttentionCache /
- * ensure_attention_cache (ascend_custom_ops.cpp:59-65,126-139).  Layout
- * [kv_head][capacity][head_dim]; capacity fixed at creation, never
- * reallocated (the reference regrows and discards contents). */
+ * ensure_attention_cache (ascend_custom_ops.cpp:59-65,126-139), which
+ * reallocates and drops its rows when a longer context arrives.  Here the
+ * cache holds 64-token pages [kv_head][64][head_dim] (fp16 or fp32) in
+ * segments that double: segment 0 = positions [0, 512), segment s >= 1 =
+ * [512 << (s - 1), 512 << s).  `capacity` bounds the positions; only the
+ * rows reserved so far are backed by device memory, and growing adds
+ * segments without moving a row.
+ *   create:  backs segment 0 (min(capacity, 512) positions);
+ *   reserve: backs positions [0, tokens) (allocates, synchronous; not for
+ *            stream capture; tokens > capacity -> MMR_ERR_LENGTH);
+ *   reset:   frees every segment past the first and marks the cache empty
+ *            for mmr_prefill_layer_forward (synchronises the device; do not
+ *            replay graphs recorded with the freed segments);
+ *   write / read: host rows [first, first + count), keys and values each
+ *            [kv_head][count][head_dim] in the cache dtype (fp16 bits or
+ *            fp32); write reserves what it writes, read needs backed rows.
+ * Op-level calls never allocate: a call touching unbacked rows fails with
+ * MMR_ERR_LENGTH; calls with a device-side position flag positions past the
+ * backed rows through *error.  Kernels recorded into a graph keep the
+ * segments backed when they were recorded. */
 int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, int kv_dtype, mmr_kv_cache** out);
 int mmr_kv_cache_destroy(mmr_kv_cache* cache);
-int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values);
+int mmr_kv_cache_reserve(mmr_kv_cache* cache, int64_t tokens);
+int mmr_kv_cache_reset(mmr_kv_cache* cache);
 /* Shape of a cache (any output pointer may be NULL). */
 int mmr_kv_cache_info(const mmr_kv_cache* cache, int64_t* kv_heads, int64_t* head_dim, int64_t* capacity,
                       int* kv_dtype);
-/* Rows allocated per KV head: capacity rounded up to the attention tile
- * (64 tokens, 32 for head_dim 128); keys/values are [kv_head][rows][head_dim]. */
-int mmr_kv_cache_rows(const mmr_kv_cache* cache, int64_t* rows);
+/* Backed positions (from 0) and the device bytes held (either may be NULL). */
+int mmr_kv_cache_backed(const mmr_kv_cache* cache, int64_t* tokens, uint64_t* device_bytes);
+/* Device pointers of segment `index` (NULL while unbacked): keys and values
+ * [pages][kv_head][64][head_dim] for positions first_token ..
+ * first_token + tokens - 1 (tokens = its backed, usable positions). */
+int mmr_kv_cache_segment(const mmr_kv_cache* cache, int index, void** keys, void** values, int64_t* first_token,
+                         int64_t* tokens);
+int mmr_kv_cache_write(mmr_kv_cache* cache, int64_t first, int64_t count, const void* keys, const void* values);
+int mmr_kv_cache_read(const mmr_kv_cache* cache, int64_t first, int64_t count, void* keys, void* values);
 
 /* ---- QKV post-process + KV append: device_decode_qkv_postprocess
  * (ascend_custom_ops.h:132-143, ascend_custom_ops.cpp:825-884).
@@ -247,10 +271,12 @@ int mmr_custom_attention_cached(const float* query, const float* key, const floa
  * attention runs over *position + 1 keys (the reference's cache.tokens after
  * its increment).  hidden/out [hidden_size] fp32 on the device (out may
  * alias hidden); the cache must match the layer (kv_heads, head_dim); splits
- * 0 = automatic from the cache capacity.  No allocation, no
+ * 0 = automatic from the cache's backed positions (which follow the context
+ * when the caller reserves as it goes).  No allocation, no
  * synchronisation: the call may be recorded into a hipGraph and replayed
  * with the position advanced in device memory.  *error (device int32) is
- * set to 1 when *position is outside the cache or max_position_embeddings. */
+ * set to 1 when *position is outside the backed rows or
+ * max_position_embeddings. */
 int mmr_layer_weights_create(const mmr_config* config, const float* input_norm, const float* post_attention_norm,
                              const float* q_norm, const float* k_norm, const float* q_proj, const float* k_proj,
                              const float* v_proj, const float* o_proj, const float* gate_proj, const float* up_proj,
@@ -261,6 +287,23 @@ size_t mmr_decoder_layer_workspace_size(const mmr_config* config, int splits);
 int mmr_decoder_layer_forward(const mmr_layer_weights* weights, mmr_kv_cache* cache, const float* hidden,
                               const int32_t* position, float* out, void* workspace, size_t workspace_bytes,
                               int splits, int32_t* error, mmr_stream_t stream);
+
+/* ---- one decoder layer over a prompt: run_dense_prefill_layer_device
+ * (decoder_layer.h:74-80, decoder_layer.cpp:661-734) and
+ * run_dense_prefill_layer (decoder_layer.cpp:409-527).
+ * out = layer(hidden_seq) for seq_len rows [seq_len][hidden_size] fp32 on the
+ * device (out may alias hidden_seq), on the fp16 matrix cores with fp32
+ * accumulation.  Row i's query and key rotate to position start_position + i;
+ * the keys and values go to cache rows 0 .. seq_len - 1 and row i attends
+ * rows 0 .. i.  The cache must be empty (no prefill-layer call since it was
+ * created or reset; else MMR_ERR_INVALID_ARGUMENT, as the reference throws)
+ * and backed for seq_len rows; afterwards it counts as holding seq_len rows.
+ * The workspace (mmr_prefill_layer_workspace_size bytes) holds every
+ * intermediate: no allocation, no synchronisation, graph-capturable. */
+size_t mmr_prefill_layer_workspace_size(const mmr_config* config, int64_t seq_len);
+int mmr_prefill_layer_forward(const mmr_layer_weights* weights, mmr_kv_cache* cache, const float* hidden_seq,
+                              int64_t start_position, int64_t seq_len, float* out, void* workspace,
+                              size_t workspace_bytes, mmr_stream_t stream);
 
 /* ---- prefill (run_dense_prefill_layer_device, decoder_layer.cpp:661-734) ----
  * Batched projection: device_matmul / device_matmul_add with batch = seq_len
@@ -323,6 +366,14 @@ int mmr_synthesize_prompt(uint64_t seed, int64_t count, int64_t vocab, int32_t* 
 int mmr_state_create(const mmr_model* model, int64_t capacity, int kv_dtype, mmr_state** out);
 int mmr_state_free(mmr_state* state);
 int mmr_state_position(const mmr_state* state, int64_t* position);
+/* KV positions the state has backed with device memory so far (its cache
+ * grows in doubling segments of 64-token pages as the context reaches them,
+ * 512 positions at creation) and the device bytes they hold; either may be
+ * NULL. */
+int mmr_state_kv_backed(const mmr_state* state, int64_t* tokens, uint64_t* device_bytes);
+/* Back KV positions [0, positions) now (at most the capacity), so decoding up
+ * to there allocates nothing (allocates; synchronous). */
+int mmr_state_reserve(const mmr_model* model, mmr_state* state, int64_t positions);
 int mmr_state_stream(const mmr_state* state, mmr_stream_t* stream);
 int mmr_state_reset(const mmr_model* model, mmr_state* state);
 

@@ -9,6 +9,8 @@
 #include "runtime/decoder_layer.h"
 #include "runtime/device.h"
 #include "runtime/device_model.h"
+#include "runtime/kv_store.h"
+#include "runtime/prefill_layer.h"
 #include "runtime/language_model.h"
 
 #include <algorithm>
@@ -40,9 +42,14 @@ struct mmr_rope_table {
   const float* data() const { return static_cast<const float*>(inv_freq.data()); }
 };
 struct mmr_kv_cache {
-  DeviceBuffer keys, values;
-  int64_t kv_heads = 0, head_dim = 0, capacity = 0, rows = 0;
+  minimind::model::KvStore store;  // one layer
   int dtype = MMR_KV_F32;
+  int64_t prefilled = 0;  // rows a prefill-layer call filled; 0 = empty (reset clears it)
+  int64_t kv_heads() const { return store.kv_heads(); }
+  int64_t head_dim() const { return store.head_dim(); }
+  int64_t capacity() const { return store.capacity(); }
+  int64_t usable() const { return std::min(store.capacity(), store.backed()); }  // backed positions
+  mmr::KvDtype kv() const { return dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32; }
 };
 struct mmr_layer_weights {
   std::shared_ptr<DeviceLayerWeights> w;
@@ -147,6 +154,13 @@ void check_attention_shape(int64_t hq, int64_t hkv, int64_t d) {
   require(mmr::attention_supported(static_cast<int>(hq), static_cast<int>(hkv), static_cast<int>(d)),
           "unsupported heads/head_dim: need Hq % Hkv == 0, Hq/Hkv <= 8, head_dim in {16,32,64,96,128}");
   require(hkv <= 64, "kv_heads must be <= 64");
+}
+
+// Rows [0, tokens) must be backed: op-level calls never allocate.
+void require_backed(const mmr_kv_cache* c, int64_t tokens) {
+  if (tokens > c->usable())
+    throw std::length_error("KV cache rows [0, " + std::to_string(tokens) + ") are not backed (" +
+                            std::to_string(c->usable()) + " are): call mmr_kv_cache_reserve first");
 }
 
 }  // namespace
@@ -399,19 +413,11 @@ int mmr_kv_cache_create(int64_t kv_heads, int64_t head_dim, int64_t capacity, in
     require(out, "null out");
     require(kv_heads > 0 && head_dim > 0 && capacity > 0, "dimensions must be positive");
     require(kv_dtype == MMR_KV_F16 || kv_dtype == MMR_KV_F32, "unknown kv dtype");
-    require(capacity < (int64_t{1} << 28), "capacity too large");
     require(head_dim <= 128, "head_dim must be <= 128");
     auto c = std::make_unique<mmr_kv_cache>();
-    c->rows = mmr::attention_cache_rows(capacity, static_cast<int>(head_dim));
-    const size_t bytes = static_cast<size_t>(kv_heads * head_dim * c->rows) * (kv_dtype == MMR_KV_F16 ? 2 : 4);
-    c->keys.reset(bytes);
-    c->values.reset(bytes);
-    hip(hipMemset(c->keys.data(), 0, bytes), "hipMemset");
-    hip(hipMemset(c->values.data(), 0, bytes), "hipMemset");
-    c->kv_heads = kv_heads;
-    c->head_dim = head_dim;
-    c->capacity = capacity;
     c->dtype = kv_dtype;
+    c->store = minimind::model::KvStore(1, kv_heads, head_dim, c->kv(), capacity);
+    c->store.reserve(std::min<int64_t>(capacity, mmr::kv_segment_tokens(0)));
     *out = c.release();
   });
 }
@@ -420,11 +426,19 @@ int mmr_kv_cache_destroy(mmr_kv_cache* cache) {
   return guarded([&] { delete cache; });
 }
 
-int mmr_kv_cache_data(const mmr_kv_cache* cache, void** keys, void** values) {
+int mmr_kv_cache_reserve(mmr_kv_cache* cache, int64_t tokens) {
   return guarded([&] {
-    require(cache && keys && values, "null argument");
-    *keys = cache->keys.data();
-    *values = cache->values.data();
+    require(cache, "null argument");
+    require(tokens >= 0, "tokens must be non-negative");
+    cache->store.reserve(tokens);
+  });
+}
+
+int mmr_kv_cache_reset(mmr_kv_cache* cache) {
+  return guarded([&] {
+    require(cache, "null argument");
+    cache->store.release_tail();
+    cache->prefilled = 0;
   });
 }
 
@@ -432,17 +446,49 @@ int mmr_kv_cache_info(const mmr_kv_cache* cache, int64_t* kv_heads, int64_t* hea
                       int* kv_dtype) {
   return guarded([&] {
     require(cache, "null argument");
-    if (kv_heads) *kv_heads = cache->kv_heads;
-    if (head_dim) *head_dim = cache->head_dim;
-    if (capacity) *capacity = cache->capacity;
+    if (kv_heads) *kv_heads = cache->kv_heads();
+    if (head_dim) *head_dim = cache->head_dim();
+    if (capacity) *capacity = cache->capacity();
     if (kv_dtype) *kv_dtype = cache->dtype;
   });
 }
 
-int mmr_kv_cache_rows(const mmr_kv_cache* cache, int64_t* rows) {
+int mmr_kv_cache_backed(const mmr_kv_cache* cache, int64_t* tokens, uint64_t* device_bytes) {
   return guarded([&] {
-    require(cache && rows, "null argument");
-    *rows = cache->rows;
+    require(cache, "null argument");
+    if (tokens) *tokens = cache->usable();
+    if (device_bytes) *device_bytes = cache->store.device_bytes();
+  });
+}
+
+int mmr_kv_cache_segment(const mmr_kv_cache* cache, int index, void** keys, void** values, int64_t* first_token,
+                         int64_t* tokens) {
+  return guarded([&] {
+    require(cache && keys && values && first_token && tokens, "null argument");
+    require(index >= 0 && index < mmr::kKvSegments, "segment index out of range");
+    const mmr::KvSeg& sg = cache->store.layer(0).s[index];
+    *keys = sg.k;
+    *values = sg.v;
+    *first_token = mmr::kv_segment_first(index);
+    *tokens = sg.k ? std::max<int64_t>(0, std::min<int64_t>(mmr::kv_segment_tokens(index),
+                                                            cache->usable() - *first_token))
+                   : 0;
+  });
+}
+
+int mmr_kv_cache_write(mmr_kv_cache* cache, int64_t first, int64_t count, const void* keys, const void* values) {
+  return guarded([&] {
+    require(cache && keys && values, "null argument");
+    require(first >= 0 && count >= 0 && first + count <= cache->capacity(), "rows outside the cache capacity");
+    cache->store.write_rows(0, first, count, keys, values);
+  });
+}
+
+int mmr_kv_cache_read(const mmr_kv_cache* cache, int64_t first, int64_t count, void* keys, void* values) {
+  return guarded([&] {
+    require(cache && keys && values, "null argument");
+    require(first >= 0 && count >= 0 && first + count <= cache->usable(), "rows outside the backed cache");
+    cache->store.read_rows(0, first, count, keys, values);
   });
 }
 
@@ -452,9 +498,10 @@ int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const floa
   return guarded([&] {
     require(qkv && q_norm && k_norm && cache && rope && query, "null argument");
     check_attention_shape(q_heads, kv_heads, head_dim);
-    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(cache->kv_heads() == kv_heads && cache->head_dim() == head_dim, "cache shape mismatch");
     require(rope->head_dim == head_dim, "rope table head_dim mismatch");
-    require(tokens >= 1 && tokens <= cache->capacity, "tokens must be in [1, capacity]");
+    require(tokens >= 1 && tokens <= cache->capacity(), "tokens must be in [1, capacity]");
+    require_backed(cache, tokens);
     require(position >= 0 && position < rope->max_positions, "position outside the rope table");
     mmr::QkvPostArgs a;
     a.qkv = qkv;
@@ -464,15 +511,12 @@ int mmr_decode_qkv_postprocess(const float* qkv, const float* q_norm, const floa
     a.inv_freq = rope->data();
     a.position = static_cast<int>(position);
     a.index = static_cast<int>(tokens - 1);
-    a.kcache = cache->keys.data();
-    a.vcache = cache->values.data();
-    a.rows = static_cast<int>(cache->rows);
+    a.seg = cache->store.layer(0);
     a.hq = static_cast<int>(q_heads);
     a.hkv = static_cast<int>(kv_heads);
     a.d = static_cast<int>(head_dim);
     a.query_out = query;
-    hip(mmr::launch_qkv_postprocess(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32, as_stream(stream)),
-        "qkv postprocess launch");
+    hip(mmr::launch_qkv_postprocess(a, cache->kv(), as_stream(stream)), "qkv postprocess launch");
   });
 }
 
@@ -492,18 +536,15 @@ void enqueue_attention_from_cache(const float* query, const mmr_kv_cache* cache,
   mmr::AttnArgs a;
   a.q = query;
   a.tokens = static_cast<int>(tokens);
-  a.kcache = cache->keys.data();
-  a.vcache = cache->values.data();
-  a.capacity = static_cast<int>(cache->capacity);
-  a.rows = static_cast<int>(cache->rows);
+  a.seg = cache->store.layer(0);
+  a.capacity = static_cast<int>(cache->usable());
+  a.rows = static_cast<int>(cache->store.backed());
   a.hq = static_cast<int>(q_heads);
   a.hkv = static_cast<int>(kv_heads);
   a.d = static_cast<int>(head_dim);
   a.splits = splits;
   a.part = part;
-  hip(mmr::launch_attention(a, mmr::kAttnFromCache, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
-                            as_stream(stream)),
-      "attention launch");
+  hip(mmr::launch_attention(a, mmr::kAttnFromCache, cache->kv(), as_stream(stream)), "attention launch");
   hip(mmr::launch_attention_combine(a.part, a.hq, a.hkv, a.d, splits, out, as_stream(stream)),
       "attention combine launch");
 }
@@ -512,8 +553,9 @@ void check_attention_from_cache(const float* query, const mmr_kv_cache* cache, i
                                 int64_t kv_heads, int64_t head_dim, const float* out, int* splits) {
   require(query && cache && out, "null argument");
   check_attention_shape(q_heads, kv_heads, head_dim);
-  require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
-  require(tokens >= 1 && tokens <= cache->capacity, "tokens must be in [1, capacity]");
+  require(cache->kv_heads() == kv_heads && cache->head_dim() == head_dim, "cache shape mismatch");
+  require(tokens >= 1 && tokens <= cache->capacity(), "tokens must be in [1, capacity]");
+  require_backed(cache, tokens);
   if (*splits <= 0) *splits = auto_splits(tokens, head_dim);
   require(*splits <= 4096, "splits too large");
 }
@@ -584,9 +626,10 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
   return guarded([&] {
     require(qkv && q_norm && k_norm && rope && position && cache && out && workspace && error, "null argument");
     check_attention_shape(q_heads, kv_heads, head_dim);
-    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(cache->kv_heads() == kv_heads && cache->head_dim() == head_dim, "cache shape mismatch");
     require(rope->head_dim == head_dim, "rope table head_dim mismatch");
-    if (splits <= 0) splits = auto_splits(cache->capacity, head_dim);
+    // The device position is unknown here: size the splits for the backed rows.
+    if (splits <= 0) splits = auto_splits(cache->usable(), head_dim);
     require(splits <= 4096, "splits too large");
     require(workspace_bytes >= attention_ws_bytes(q_heads, kv_heads, head_dim, splits), "workspace too small");
     mmr::AttnArgs a;
@@ -596,19 +639,16 @@ int mmr_decode_attention_fused(const float* qkv, const float* q_norm, const floa
     a.eps = eps;
     a.inv_freq = rope->data();
     a.pos = position;
-    a.kcache = cache->keys.data();
-    a.vcache = cache->values.data();
-    a.capacity = static_cast<int>(std::min(cache->capacity, rope->max_positions));
-    a.rows = static_cast<int>(cache->rows);
+    a.seg = cache->store.layer(0);
+    a.capacity = static_cast<int>(std::min(cache->usable(), rope->max_positions));
+    a.rows = static_cast<int>(cache->store.backed());
     a.hq = static_cast<int>(q_heads);
     a.hkv = static_cast<int>(kv_heads);
     a.d = static_cast<int>(head_dim);
     a.splits = splits;
     a.part = static_cast<float*>(workspace);
     a.err = error;
-    hip(mmr::launch_attention(a, mmr::kAttnFused, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
-                              as_stream(stream)),
-        "fused attention launch");
+    hip(mmr::launch_attention(a, mmr::kAttnFused, cache->kv(), as_stream(stream)), "fused attention launch");
     hip(mmr::launch_attention_combine(a.part, a.hq, a.hkv, a.d, splits, out, as_stream(stream)),
         "attention combine launch");
   });
@@ -641,10 +681,11 @@ int mmr_prefill_qkv_rows(const float* qkv, const float* q_norm, const float* k_n
   return guarded([&] {
     require(qkv && q_norm && k_norm && rope && cache && query, "null argument");
     check_attention_shape(q_heads, kv_heads, head_dim);
-    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(cache->kv_heads() == kv_heads && cache->head_dim() == head_dim, "cache shape mismatch");
     require(rope->head_dim == head_dim, "rope table head_dim mismatch");
     require(seq_len >= 1 && start_position >= 0, "seq_len must be positive and start_position non-negative");
-    require(start_position + seq_len <= cache->capacity, "prompt exceeds the cache capacity");
+    require(start_position + seq_len <= cache->capacity(), "prompt exceeds the cache capacity");
+    require_backed(cache, start_position + seq_len);
     require(start_position + seq_len <= rope->max_positions, "positions outside the rope table");
     mmr::QkvRowsArgs a;
     a.qkv = qkv;
@@ -654,17 +695,15 @@ int mmr_prefill_qkv_rows(const float* qkv, const float* q_norm, const float* k_n
     a.eps = eps;
     a.inv_freq = rope->data();
     a.start = static_cast<int>(start_position);
+    a.row0 = static_cast<int>(start_position);
     a.tokens = static_cast<int>(seq_len);
-    a.kcache = cache->keys.data();
-    a.vcache = cache->values.data();
-    a.rows = static_cast<int>(cache->rows);
+    a.seg = cache->store.layer(0);
     a.hq = static_cast<int>(q_heads);
     a.hkv = static_cast<int>(kv_heads);
     a.d = static_cast<int>(head_dim);
     a.query = query;
     a.query_stride = static_cast<int>(q_heads * head_dim);
-    hip(mmr::launch_qkv_rows(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32, as_stream(stream)),
-        "qkv rows launch");
+    hip(mmr::launch_qkv_rows(a, cache->kv(), as_stream(stream)), "qkv rows launch");
   });
 }
 
@@ -764,24 +803,74 @@ int mmr_decoder_layer_forward(const mmr_layer_weights* weights, mmr_kv_cache* ca
   return guarded([&] {
     require(weights && weights->w && cache && hidden && position && out && workspace && error, "null argument");
     const MiniMindConfig& c = weights->w->cfg;
-    require(cache->kv_heads == c.num_key_value_heads && cache->head_dim == c.head_dim,
+    require(cache->kv_heads() == c.num_key_value_heads && cache->head_dim() == c.head_dim,
             "cache shape does not match the layer (kv_heads, head_dim)");
-    if (splits <= 0) splits = auto_splits(cache->capacity, c.head_dim);
+    // The device position is unknown here: size the splits for the backed
+    // rows, which follow the context when the cache is grown as it fills.
+    if (splits <= 0) splits = auto_splits(cache->usable(), c.head_dim);
     require(splits <= 4096, "splits too large");
     require(workspace_bytes >= decoder_layer_workspace_floats(c, splits) * 4, "workspace too small");
     DecoderLayerIo io;
     io.hidden = hidden;
     io.out = out;
     io.position = position;
-    io.kcache = cache->keys.data();
-    io.vcache = cache->values.data();
-    io.rows = static_cast<int>(cache->rows);
-    io.capacity = static_cast<int>(std::min(cache->capacity, c.max_position_embeddings));
-    io.kv = cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32;
+    io.seg = cache->store.layer(0);
+    io.rows = static_cast<int>(cache->store.backed());
+    io.capacity = static_cast<int>(std::min(cache->usable(), c.max_position_embeddings));
+    io.kv = cache->kv();
     io.splits = splits;
     io.workspace = static_cast<float*>(workspace);
     io.err = error;
     enqueue_decoder_layer(*weights->w, io, as_stream(stream));
+  });
+}
+
+size_t mmr_prefill_layer_workspace_size(const mmr_config* config, int64_t seq_len) {
+  if (!config || seq_len < 1 || seq_len > (int64_t{1} << 20)) return 0;
+  return prefill_scratch_bytes(to_cpp(*config), seq_len);
+}
+
+int mmr_prefill_layer_forward(const mmr_layer_weights* weights, mmr_kv_cache* cache, const float* hidden_seq,
+                              int64_t start_position, int64_t seq_len, float* out, void* workspace,
+                              size_t workspace_bytes, mmr_stream_t stream) {
+  return guarded([&] {
+    require(weights && weights->w && cache && hidden_seq && out && workspace, "null argument");
+    const MiniMindConfig& c = weights->w->cfg;
+    require(cache->kv_heads() == c.num_key_value_heads && cache->head_dim() == c.head_dim,
+            "cache shape does not match the layer (kv_heads, head_dim)");
+    // decoder_layer.cpp:416-418 / :669-671
+    require(cache->prefilled == 0, "prefill layer requires an empty KV cache");
+    require(seq_len >= 1 && seq_len <= (int64_t{1} << 20) && start_position >= 0,
+            "seq_len must be in [1, 2^20] and start_position non-negative");
+    require(start_position + seq_len <= c.max_position_embeddings, "positions exceed max_position_embeddings");
+    require(seq_len <= cache->capacity(), "prompt exceeds the cache capacity");
+    require_backed(cache, seq_len);
+    const int H = static_cast<int>(c.hidden_size), F = static_cast<int>(c.intermediate_size);
+    const int qs = static_cast<int>(c.num_attention_heads * c.head_dim);
+    const int qkv = static_cast<int>((c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim);
+    require(mmr::gemm_supported(1, qkv, H) && mmr::gemm_supported(1, H, qs) && mmr::gemm_supported(1, 2 * F, H) &&
+                mmr::gemm_supported(1, H, F),
+            "the prefill GEMMs need hidden_size, q_size and intermediate_size to be multiples of 8");
+    require(workspace_bytes >= prefill_scratch_bytes(c, seq_len), "workspace too small");
+    hipStream_t st = as_stream(stream);
+    const size_t bytes = static_cast<size_t>(seq_len * H) * sizeof(float);
+    if (out != hidden_seq) hip(hipMemcpyAsync(out, hidden_seq, bytes, hipMemcpyDeviceToDevice, st), "copy hidden_seq");
+    const PrefillScratch scratch = carve_prefill_scratch(c, seq_len, workspace);
+    const LayerDev& w = weights->w->w;
+    const int rows = static_cast<int>(seq_len);
+    enqueue_prefill_input_norm(c, scratch, rows, out, w.input_norm, st);
+    // Keys and values go to cache rows 0 .. seq_len - 1 and rotate to
+    // positions start_position + i (device_prefill_attention copies them to
+    // the front of the cache, ascend_custom_ops.cpp:796-803).
+    PrefillKv kv;
+    kv.seg = cache->store.layer(0);
+    kv.dtype = cache->kv();
+    kv.rope_start = static_cast<int>(start_position);
+    kv.row0 = 0;
+    // The norm after the last residual feeds no later layer here: it lands
+    // in the scratch unused.
+    enqueue_prefill_layer(c, w, weights->w->inv_freq, scratch, kv, rows, out, w.input_norm, false, st);
+    cache->prefilled = seq_len;  // cache.tokens = seq_len (decoder_layer.cpp:524, :733)
   });
 }
 
@@ -790,15 +879,14 @@ int mmr_prefill_attention(const float* query, const mmr_kv_cache* cache, int64_t
   return guarded([&] {
     require(query && cache && out, "null argument");
     check_attention_shape(q_heads, kv_heads, head_dim);
-    require(cache->kv_heads == kv_heads && cache->head_dim == head_dim, "cache shape mismatch");
+    require(cache->kv_heads() == kv_heads && cache->head_dim() == head_dim, "cache shape mismatch");
     require(seq_len >= 1 && start_position >= 0, "seq_len must be positive and start_position non-negative");
-    require(start_position + seq_len <= cache->capacity, "prompt exceeds the cache capacity");
+    require(start_position + seq_len <= cache->capacity(), "prompt exceeds the cache capacity");
+    require_backed(cache, start_position + seq_len);
     mmr::PrefillAttnArgs a;
     a.query = query;
     a.query_stride = static_cast<int>(q_heads * head_dim);
-    a.kcache = cache->keys.data();
-    a.vcache = cache->values.data();
-    a.rows = static_cast<int>(cache->rows);
+    a.seg = cache->store.layer(0);
     a.start = static_cast<int>(start_position);
     a.tokens = static_cast<int>(seq_len);
     a.hq = static_cast<int>(q_heads);
@@ -806,9 +894,7 @@ int mmr_prefill_attention(const float* query, const mmr_kv_cache* cache, int64_t
     a.d = static_cast<int>(head_dim);
     a.out = out;
     a.out_stride = static_cast<int>(q_heads * head_dim);
-    hip(mmr::launch_prefill_attention(a, cache->dtype == MMR_KV_F16 ? mmr::kKvF16 : mmr::kKvF32,
-                                      as_stream(stream)),
-        "prefill attention launch");
+    hip(mmr::launch_prefill_attention(a, cache->kv(), as_stream(stream)), "prefill attention launch");
   });
 }
 
@@ -975,6 +1061,21 @@ int mmr_state_position(const mmr_state* state, int64_t* position) {
   return guarded([&] {
     require(state && position, "null argument");
     *position = state->st.position;
+  });
+}
+
+int mmr_state_reserve(const mmr_model* model, mmr_state* state, int64_t positions) {
+  return guarded([&] {
+    require(model && state, "null argument");
+    model->lm->reserve_kv(state->st, positions);
+  });
+}
+
+int mmr_state_kv_backed(const mmr_state* state, int64_t* tokens, uint64_t* device_bytes) {
+  return guarded([&] {
+    require(state, "null argument");
+    if (tokens) *tokens = state->st.kv_backed();
+    if (device_bytes) *device_bytes = state->st.kv_device_bytes();
   });
 }
 

@@ -49,72 +49,54 @@ std::vector<uint16_t> to_half(const float* v, std::size_t n) {
 }
 
 // Keys/values of tokens [first, first + count) from the reference layout
-// [token][kv_head][d] (fp32) into the cache layout [kv_head][rows][d], in the
-// cache's element type: an fp16 cache gets the rows rounded to fp16 (RNE),
-// the rounding the decode kernels apply when they append.
+// [token][kv_head][d] (fp32) into the cache, as [kv_head][count][d] rows of
+// the cache's element type: an fp16 cache gets the rows rounded to fp16
+// (RNE), the rounding the decode kernels apply when they append.
 void write_rows(mmr_kv_cache* cache, const float* keys, const float* values, int64_t first, int64_t count,
                 int64_t kv_heads, int64_t head_dim) {
-  void *kp = nullptr, *vp = nullptr;
-  int64_t rows = 0;
   int dtype = MMR_KV_F32;
-  ok(mmr_kv_cache_data(cache, &kp, &vp));
-  ok(mmr_kv_cache_rows(cache, &rows));
   ok(mmr_kv_cache_info(cache, nullptr, nullptr, nullptr, &dtype));
-  const std::size_t elem = dtype == MMR_KV_F16 ? 2 : 4;
   const std::size_t n = static_cast<std::size_t>(count * kv_heads * head_dim);
-  std::vector<uint16_t> kh, vh;
-  const void* ksrc = keys;
-  const void* vsrc = values;
+  std::vector<float> kf(n), vf(n);
+  for (int64_t t = 0; t < count; ++t)
+    for (int64_t h = 0; h < kv_heads; ++h)
+      for (int64_t d = 0; d < head_dim; ++d) {
+        const std::size_t src = static_cast<std::size_t>((t * kv_heads + h) * head_dim + d);
+        const std::size_t dst = static_cast<std::size_t>((h * count + t) * head_dim + d);
+        kf[dst] = keys[src];
+        vf[dst] = values[src];
+      }
   if (dtype == MMR_KV_F16) {
-    kh = to_half(keys, n);
-    vh = to_half(values, n);
-    ksrc = kh.data();
-    vsrc = vh.data();
-  }
-  const std::size_t pitch_src = static_cast<std::size_t>(kv_heads * head_dim) * elem;
-  const std::size_t width = static_cast<std::size_t>(head_dim) * elem;
-  for (int64_t h = 0; h < kv_heads; ++h) {
-    const std::size_t dst = static_cast<std::size_t>((h * rows + first) * head_dim) * elem;
-    const std::size_t src = static_cast<std::size_t>(h * head_dim) * elem;
-    check_hip(hipMemcpy2D(static_cast<char*>(kp) + dst, width, static_cast<const char*>(ksrc) + src, pitch_src,
-                          width, static_cast<std::size_t>(count), hipMemcpyHostToDevice),
-              "hipMemcpy2D keys");
-    check_hip(hipMemcpy2D(static_cast<char*>(vp) + dst, width, static_cast<const char*>(vsrc) + src, pitch_src,
-                          width, static_cast<std::size_t>(count), hipMemcpyHostToDevice),
-              "hipMemcpy2D values");
+    const auto kh = to_half(kf.data(), n), vh = to_half(vf.data(), n);
+    ok(mmr_kv_cache_write(cache, first, count, kh.data(), vh.data()));
+  } else {
+    ok(mmr_kv_cache_write(cache, first, count, kf.data(), vf.data()));
   }
 }
 
 // A cache of this shape holding at least `needed` tokens: created when
-// absent, replaced when its shape differs, grown (rows kept) when short.
+// absent, replaced when its shape differs, and when its capacity is short,
+// replaced by one of twice the capacity holding the same rows and dtype.
 void ensure_cache(mmr_kv_cache** cache, int64_t kv_heads, int64_t head_dim, int64_t needed) {
   int64_t kvh = 0, d = 0, cap = 0;
   int dtype = MMR_KV_F32;
   if (*cache != nullptr) ok(mmr_kv_cache_info(*cache, &kvh, &d, &cap, &dtype));
   if (*cache != nullptr && kvh == kv_heads && d == head_dim && cap >= needed) return;
-  mmr_kv_cache* fresh = nullptr;
   const bool keep = *cache != nullptr && kvh == kv_heads && d == head_dim;
+  mmr_kv_cache* fresh = nullptr;
   ok(mmr_kv_cache_create(kv_heads, head_dim, std::max(needed, keep ? 2 * cap : kMinCacheTokens),
                          keep ? dtype : MMR_KV_F32, &fresh));
-  if (keep) {  // per KV head, rows [0, old rows) move to the same rows of the new layout
-    void *old_k, *old_v, *new_k, *new_v;
-    int64_t old_rows = 0, new_rows = 0;
-    ok(mmr_kv_cache_data(*cache, &old_k, &old_v));
-    ok(mmr_kv_cache_data(fresh, &new_k, &new_v));
-    ok(mmr_kv_cache_rows(*cache, &old_rows));
-    ok(mmr_kv_cache_rows(fresh, &new_rows));
-    const std::size_t row_bytes = static_cast<std::size_t>(head_dim) * (dtype == MMR_KV_F16 ? 2 : 4);
-    const std::size_t src_pitch = row_bytes * static_cast<std::size_t>(old_rows);
-    const std::size_t dst_pitch = row_bytes * static_cast<std::size_t>(new_rows);
-    check_hip(hipMemcpy2D(new_k, dst_pitch, old_k, src_pitch, src_pitch, static_cast<std::size_t>(kv_heads),
-                          hipMemcpyDeviceToDevice),
-              "hipMemcpy2D grow keys");
-    check_hip(hipMemcpy2D(new_v, dst_pitch, old_v, src_pitch, src_pitch, static_cast<std::size_t>(kv_heads),
-                          hipMemcpyDeviceToDevice),
-              "hipMemcpy2D grow values");
+  std::unique_ptr<mmr_kv_cache, int (*)(mmr_kv_cache*)> guard(fresh, mmr_kv_cache_destroy);
+  if (keep) {  // rows [0, backed) move over through the host, in the cache layout and dtype
+    int64_t backed = 0;
+    ok(mmr_kv_cache_backed(*cache, &backed, nullptr));
+    const std::size_t bytes = static_cast<std::size_t>(backed * kv_heads * head_dim) * (dtype == MMR_KV_F16 ? 2 : 4);
+    std::vector<char> k(bytes), v(bytes);
+    ok(mmr_kv_cache_read(*cache, 0, backed, k.data(), v.data()));
+    ok(mmr_kv_cache_write(fresh, 0, backed, k.data(), v.data()));
   }
   if (*cache != nullptr) ok(mmr_kv_cache_destroy(*cache));
-  *cache = fresh;
+  *cache = guard.release();
 }
 
 // out = attention of `query` [q_heads][d] over the first `tokens` cache rows.

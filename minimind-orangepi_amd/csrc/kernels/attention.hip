@@ -7,9 +7,11 @@
 //  * the decode attention (reference K3 via device_attention_from_cache,
 //    ascend_custom_ops.cpp:886-916; CPU semantics decoder_layer.cpp:184-234).
 //
-// Layout: per layer the cache holds K and V as [kv_head][rows][head_dim]
-// (fp16 or fp32, rows = capacity rounded up to the tile size), so one KV
-// head's context is one contiguous stream.
+// Layout: per layer the cache holds K and V in 64-token pages
+// [kv_head][64][head_dim] (fp16 or fp32): a single sequence's pages sit in
+// segments that double in size (KvSegs, token -> row by arithmetic), a
+// batch's in one pool behind per-sequence page tables.  Every attention tile
+// is one contiguous run of one KV head's rows inside one page.
 //
 // attention_split_kernel, grid (splits, kv_heads), 256 threads.  Block
 // (s, g) owns KV head g and the 64-token tiles s, s + splits, ... (32-token
@@ -91,36 +93,82 @@ constexpr int attn_pv_groups() {
   return g;
 }
 
-// Element offset of token t's K (or V) row for KV head g: the contiguous
-// cache is [Hkv][rows][D]; the paged cache is [page][Hkv][kKvPage][D] with
-// this sequence's page table mapping t / kKvPage to a page.  A tile never
-// crosses a page (tiles are <= kKvPage tokens and aligned).
-template <int D, bool PAGED>
+// Token t's K and V rows for KV head g.  Single sequence: the segmented
+// cache, where page_of(t) is t's segment (arithmetic, no memory access) and
+// the row sits at a computed offset in that segment.  Batch: page pools
+// [page][Hkv][kKvPage][D] with this sequence's page table mapping t / kKvPage
+// to a page.  A tile never crosses a page (tiles are <= kKvPage tokens and
+// aligned), so one lookup serves a whole tile.
+template <typename KV, int D, bool PAGED>
 struct KvRows {
-  const int32_t* pages = nullptr;
-  int64_t head_base = 0;
-  int hkv = 0, g = 0, n_pages = 0;
-  // Page holding token t (its index clamped into the page table, so a
-  // lookahead past the context stays in range); 0 for the contiguous cache.
-  // The table is read-only here and the index uniform: read through the
-  // constant address space, the lookup is a scalar-cache load whose wait
-  // (lgkmcnt) never covers the vector K/V loads in flight.
+  const AttnArgs& a;
+  const int32_t* pages;
+  int g;
+  __device__ __forceinline__ KvRows(const AttnArgs& args, int b, int group)
+      : a(args), pages(args.page_table + static_cast<int64_t>(b) * args.pages_per_seq), g(group) {}
+  // Batch: the page holding token t (its index clamped into the page table,
+  // so a lookahead past the context stays in range).  The table is read-only
+  // here and the index uniform: read through the constant address space, the
+  // lookup is a scalar-cache load whose wait (lgkmcnt) never covers the vector
+  // K/V loads in flight.  Single sequence: t's segment.
   __device__ __forceinline__ int page_of(int t) const {
     if constexpr (PAGED) {
       using ConstTable = const __attribute__((address_space(4))) int32_t;
-      return ((ConstTable*)pages)[min(t / kKvPage, n_pages - 1)];
+      return ((ConstTable*)pages)[min(t / kKvPage, a.pages_per_seq - 1)];
     } else {
-      return 0;
+      return kv_segment(t);
     }
   }
-  __device__ __forceinline__ int64_t row_at(int page, int t) const {
+  __device__ __forceinline__ int64_t offset(int page, int t) const {
     if constexpr (PAGED) {
-      return ((static_cast<int64_t>(page) * hkv + g) * kKvPage + t % kKvPage) * D;
+      return ((static_cast<int64_t>(page) * a.hkv + g) * kKvPage + t % kKvPage) * D;
     } else {
-      return head_base + static_cast<int64_t>(t) * D;
+      return kv_segment_offset(page, t, g, a.hkv, D);
     }
   }
-  __device__ __forceinline__ int64_t row(int t) const { return row_at(page_of(t), t); }
+  __device__ __forceinline__ KV* k_at(int page, int t) const {
+    if constexpr (PAGED) {
+      return static_cast<KV*>(a.kcache) + offset(page, t);
+    } else {
+      return static_cast<KV*>(a.seg.s[page].k) + offset(page, t);
+    }
+  }
+  __device__ __forceinline__ KV* v_at(int page, int t) const {
+    if constexpr (PAGED) {
+      return static_cast<KV*>(a.vcache) + offset(page, t);
+    } else {
+      return static_cast<KV*>(a.seg.s[page].v) + offset(page, t);
+    }
+  }
+  // Rows of the block's speculative first tile at t_spec when `spec` (it is
+  // backed), else of token 0.  Single sequence: the tile's segment pointer is
+  // one kernel-argument load at a computed index, issued once the split is
+  // known (a scalar round trip after the first argument batch; measured
+  // against a cache with one contiguous run per head: +0.2 us per bare
+  // launch, no change in the MiniMind2 step at 768 keys, +2% at 4096).
+  // Selecting with masks keeps the K/V loads global loads (a pointer select
+  // made the compiler fall back to flat loads).
+  __device__ __forceinline__ void first_tile(int t_spec, bool spec, const KV*& k, const KV*& v) const {
+    if constexpr (PAGED) {
+      const int t = spec ? t_spec : 0;
+      const int pg = page_of(t);
+      k = k_at(pg, t);
+      v = v_at(pg, t);
+    } else {
+      const int sg = kv_segment(t_spec);
+      const KvSeg cand = a.seg.s[sg];
+      const KvSeg zero = a.seg.s[0];
+      // Selected with masks, not a branch: the compiler keeps both pointer
+      // loads unconditional instead of sinking them behind the `rows` test.
+      const uint64_t take = spec ? ~uint64_t{0} : uint64_t{0};
+      const uint64_t off = static_cast<uint64_t>(kv_segment_offset(sg, t_spec, g, a.hkv, D)) & take;  // token 0: g's run
+      const uint64_t off0 = static_cast<uint64_t>(kv_segment_offset(0, 0, g, a.hkv, D)) & ~take;
+      const uint64_t kb = (reinterpret_cast<uint64_t>(cand.k) & take) | (reinterpret_cast<uint64_t>(zero.k) & ~take);
+      const uint64_t vb = (reinterpret_cast<uint64_t>(cand.v) & take) | (reinterpret_cast<uint64_t>(zero.v) & ~take);
+      k = reinterpret_cast<const KV*>(kb) + (off | off0);
+      v = reinterpret_cast<const KV*>(vb) + (off | off0);
+    }
+  }
 };
 
 template <typename KV, int D, int MODE, bool PAGED>
@@ -148,14 +196,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   const int lane = threadIdx.x % kWave;
   const int R = a.hq / a.hkv;
   const int S = a.splits;
-  const KV* kbase = reinterpret_cast<const KV*>(a.kcache);
-  const KV* vbase = reinterpret_cast<const KV*>(a.vcache);
-  KvRows<D, PAGED> kv_rows;
-  kv_rows.pages = a.page_table + static_cast<int64_t>(b) * a.pages_per_seq;
-  kv_rows.head_base = static_cast<int64_t>(g) * a.rows * D;
-  kv_rows.hkv = a.hkv;
-  kv_rows.g = g;
-  kv_rows.n_pages = a.pages_per_seq;
+  const KvRows<KV, D, PAGED> kv_rows(a, b, g);
   float* part = a.part + static_cast<int64_t>(b) * a.part_stride;
   const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
 
@@ -167,13 +208,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   uint4 kc[kPerThread], vc[kPerThread];
   const int t_spec = split * TT;
   const bool spec = t_spec + TT <= a.rows;
-  const int64_t t_load = kv_rows.row(spec ? t_spec : 0);  // always in range; unused unless spec
+  const KV* kspec;
+  const KV* vspec;
+  kv_rows.first_tile(t_spec, spec, kspec, vspec);  // always backed; unused unless spec
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
     const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
-    const int64_t off = t_load + c * CH;
-    kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
-    vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+    kc[i] = *reinterpret_cast<const uint4*>(kspec + c * CH);
+    vc[i] = *reinterpret_cast<const uint4*>(vspec + c * CH);
   }
   // Page of the block's second tile, looked up one tile ahead of its fetch.
   int next_page = kv_rows.page_of((split + S) * TT);
@@ -279,8 +321,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
       const KV k0 = from_float<KV>(kx0), k1 = from_float<KV>(kx1);
       const KV v0 = from_float<KV>(vx0), v1 = from_float<KV>(vx1);
       if (in_pair) {
-        KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
-        KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
+        const int pp = kv_rows.page_of(p);
+        KV* kdst = kv_rows.k_at(pp, p);
+        KV* vdst = kv_rows.v_at(pp, p);
         kdst[d0] = k0;
         kdst[d1] = k1;
         vdst[d0] = v0;
@@ -297,14 +340,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
     auto fetch_tile = [&](int tile, int page) {
       const int t0 = tile * TT;
       const int rows = min(TT, n_keys - t0);
-      const int64_t tile_base = kv_rows.row_at(page, t0);
+      const KV* ktile = kv_rows.k_at(page, t0);
+      const KV* vtile = kv_rows.v_at(page, t0);
 #pragma unroll
       for (int i = 0; i < kPerThread; ++i) {
         const int c = min(static_cast<int>(threadIdx.x) + i * kAttnThreads, kChunks - 1);
         const int r = min((c * CH) / D, rows - 1);
-        const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
-        kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
-        vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+        const int64_t off = static_cast<int64_t>(r) * D + (c * CH) % D;
+        kc[i] = *reinterpret_cast<const uint4*>(ktile + off);
+        vc[i] = *reinterpret_cast<const uint4*>(vtile + off);
       }
     };
     // The first tile comes from the speculative registers when they hold it.
@@ -543,10 +587,7 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
   const int split = unit / a.hkv;
   const int g = unit % a.hkv;
   const int h = g * R + r;
-  const KV* kbase = reinterpret_cast<const KV*>(a.kcache);
-  const KV* vbase = reinterpret_cast<const KV*>(a.vcache);
-  KvRows<D, false> kv_rows;
-  kv_rows.head_base = static_cast<int64_t>(g) * a.rows * D;
+  const KvRows<KV, D, false> kv_rows(a, 0, g);
 
   // ---- 1. independent loads, issued before the position is known ----
   // The position is read through the scalar cache (no kernel writes it while
@@ -583,12 +624,14 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
   uint4 kc[kPerThread], vc[kPerThread];
   const int t_spec = split * TT;
   const bool spec = t_spec + TT <= a.rows;
-  const int64_t t_load = kv_rows.row(spec ? t_spec : 0);
+  const KV* kspec;
+  const KV* vspec;
+  kv_rows.first_tile(t_spec, spec, kspec, vspec);  // always backed; unused unless spec
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
     const int c = min(static_cast<int>(threadIdx.x) + i * kThreads, kChunks - 1);
-    kc[i] = *reinterpret_cast<const uint4*>(kbase + t_load + c * CH);
-    vc[i] = *reinterpret_cast<const uint4*>(vbase + t_load + c * CH);
+    kc[i] = *reinterpret_cast<const uint4*>(kspec + c * CH);
+    vc[i] = *reinterpret_cast<const uint4*>(vspec + c * CH);
   }
   asm volatile("" ::: "memory");
   if (!in_pair) qx0 = qx1 = kx0 = kx1 = vx0 = vx1 = 0.0f;
@@ -649,14 +692,16 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
     auto fetch_tile = [&](int tile) {
       const int t0 = tile * TT;
       const int rows = min(TT, n_keys - t0);
-      const int64_t tile_base = kv_rows.row(t0);
+      const int seg = kv_rows.page_of(t0);
+      const KV* ktile = kv_rows.k_at(seg, t0);
+      const KV* vtile = kv_rows.v_at(seg, t0);
 #pragma unroll
       for (int i = 0; i < kPerThread; ++i) {
         const int c = min(static_cast<int>(threadIdx.x) + i * kThreads, kChunks - 1);
         const int r = min((c * CH) / D, rows - 1);
-        const int64_t off = tile_base + static_cast<int64_t>(r) * D + (c * CH) % D;
-        kc[i] = *reinterpret_cast<const uint4*>(kbase + off);
-        vc[i] = *reinterpret_cast<const uint4*>(vbase + off);
+        const int64_t off = static_cast<int64_t>(r) * D + (c * CH) % D;
+        kc[i] = *reinterpret_cast<const uint4*>(ktile + off);
+        vc[i] = *reinterpret_cast<const uint4*>(vtile + off);
       }
     };
     if (!spec) fetch_tile(split);
@@ -808,8 +853,9 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
   // The new token's k / v (rounded to the cache dtype above), after every
   // other memory operation of the block.
   if (append_new) {
-    KV* kdst = reinterpret_cast<KV*>(a.kcache) + kv_rows.row(p);
-    KV* vdst = reinterpret_cast<KV*>(a.vcache) + kv_rows.row(p);
+    const int seg = kv_rows.page_of(p);
+    KV* kdst = kv_rows.k_at(seg, p);
+    KV* vdst = kv_rows.v_at(seg, p);
     kdst[d0] = from_float<KV>(kx0);
     kdst[d1] = from_float<KV>(kx1);
     vdst[d0] = from_float<KV>(vx0);
@@ -938,8 +984,10 @@ __global__ __launch_bounds__(kWave) void qkv_postprocess_kernel(QkvPostArgs a) {
     a.query_out[head * D + d1] = x1;
   } else {
     const float* vsrc = a.qkv + a.hq * D + a.hkv * D + head * D;
-    KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.rows + a.index) * D;
-    KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + a.index) * D;
+    const int seg = kv_segment(a.index);
+    const int64_t off = kv_segment_offset(seg, a.index, head, a.hkv, D);
+    KV* kdst = static_cast<KV*>(a.seg.s[seg].k) + off;
+    KV* vdst = static_cast<KV*>(a.seg.s[seg].v) + off;
     kdst[d0] = from_float<KV>(x0);
     kdst[d1] = from_float<KV>(x1);
     vdst[d0] = from_float<KV>(vsrc[d0]);
@@ -1030,11 +1078,6 @@ bool attention_supported(int hq, int hkv, int d) {
 }
 
 int attention_tile_tokens(int d) { return d <= 96 ? 64 : 32; }
-
-int64_t attention_cache_rows(int64_t capacity, int d) {
-  const int tile = attention_tile_tokens(d);
-  return (capacity + tile - 1) / tile * tile;
-}
 
 size_t attention_partial_floats(int hq, int hkv, int d, int splits) {
   return static_cast<size_t>(hkv) * splits * (hq / hkv) * (d + 2);

@@ -139,10 +139,50 @@ hipError_t launch_gemv(const GemvArgs& a, GemvPrologue pro, GemvEpilogue epi, co
                        hipStream_t stream);
 constexpr int kGemvBlock = 256;
 
+// ------------------------------------------------------------ KV pages ----
+// A KV page holds 64 tokens of one layer's keys (or values) for every KV head,
+// [Hkv][kKvPage][D]: one head's 64 rows are one contiguous run, and every
+// attention tile (64 or 32 tokens, aligned) lies inside one page.
+//
+// Single-sequence caches keep their pages in segments that double: segment 0
+// holds tokens [0, 512), segment s >= 1 tokens [512 << (s - 1), 512 << s).
+// A segment's pages are contiguous, so token t's row is found by arithmetic
+// (segment from t, then the page and row inside it), with no table read, and
+// a cache grows by adding segments without moving a row.  Kernels take the
+// segment base pointers as arguments (KvSegs).  The batch path maps pages of
+// one pool through per-sequence page tables instead (AttnArgs::page_table).
+constexpr int kKvPage = 64;      // tokens per KV page (a multiple of every attention tile)
+constexpr int kKvSegShift = 9;   // segment 0 holds 1 << 9 = 512 tokens (8 pages)
+constexpr int kKvSegments = 12;  // segments 0..11: up to 512 << 11 = 1,048,576 tokens
+struct KvSeg {
+  void* k = nullptr;  // [pages][Hkv][kKvPage][D], keys
+  void* v = nullptr;  // values, same layout (adjacent to k: one scalar load fetches both)
+};
+struct KvSegs {
+  KvSeg s[kKvSegments];  // unbacked segments are null
+};
+// Segment holding token t (clamped to the table, so a lookahead past the
+// last segment stays in range), its first token, and its size in tokens.
+__host__ __device__ constexpr int kv_segment(int t) {
+  const unsigned q = static_cast<unsigned>(t) >> kKvSegShift;
+  const int s = q == 0 ? 0 : 32 - __builtin_clz(q);
+  return s < kKvSegments ? s : kKvSegments - 1;
+}
+__host__ __device__ constexpr int kv_segment_first(int s) { return s == 0 ? 0 : 1 << (kKvSegShift + s - 1); }
+__host__ __device__ constexpr int kv_segment_tokens(int s) {
+  return s == 0 ? 1 << kKvSegShift : 1 << (kKvSegShift + s - 1);
+}
+// Element offset of token t's row for KV head g inside segment s (t in s).
+__host__ __device__ constexpr int64_t kv_segment_offset(int s, int t, int g, int hkv, int d) {
+  const int r = t - kv_segment_first(s);
+  return (static_cast<int64_t>(r / kKvPage) * hkv + g) * kKvPage * d + static_cast<int64_t>(r % kKvPage) * d;
+}
+
 // ----------------------------------------------------------- attention ----
-// GQA decode attention for one query token over a resident KV cache laid out
-// [kv_head][rows][head_dim], split along the context into `splits` tile sets
-// per KV head; the partials are merged by a log-sum-exp combine in the consumer.
+// GQA decode attention for one query token over a resident KV cache
+// (segmented pages, or a page pool with page tables for a batch), split along
+// the context into `splits` tile sets per KV head; the partials are merged by
+// a log-sum-exp combine in the consumer.
 enum AttnMode : int {
   kAttnFused = 0,     // q/k RMSNorm + RoPE from the raw projection, append k/v at
                       // index *pos, attend over *pos + 1 keys
@@ -160,10 +200,10 @@ struct AttnArgs {
   const int32_t* pos = nullptr;     // fused: index of the new token (device)
   const float* q = nullptr;         // from-cache: [Hq*D]
   int tokens = 0;                   // from-cache: cached keys
-  void* kcache = nullptr;           // [Hkv][rows][D]
+  void* kcache = nullptr;           // batch: page pools (see page_table)
   void* vcache = nullptr;
-  int capacity = 0;                 // usable positions
-  int rows = 0;                     // allocated rows per head (capacity rounded up to the tile)
+  int capacity = 0;                 // usable positions (all backed)
+  int rows = 0;                     // backed rows per sequence (a multiple of kKvPage)
   int hq = 0, hkv = 0, d = 0;
   int splits = 1;
   float* part = nullptr;            // o [Hkv][splits][R][D], then (m, l) [Hkv][splits][R][2]
@@ -178,7 +218,7 @@ struct AttnArgs {
   // (summed in order; 1 = a plain row).
   int qkv_parts = 1;
   int64_t qkv_part_stride = 0;
-  // Paged cache (fused mode): kcache / vcache are page pools
+  // Batch (fused mode): kcache / vcache are page pools
   // [page][Hkv][kKvPage][D]; page_table[b * pages_per_seq + t / kKvPage] is
   // the page of sequence b's token t; rows = pages_per_seq * kKvPage.
   const int32_t* page_table = nullptr;
@@ -187,14 +227,16 @@ struct AttnArgs {
   // the head blocks load these regions into the XCDs' L2s while the head
   // blocks run.  Other launch shapes ignore them.
   L2WarmSet warm;
+  // Single sequence: the cache's segments.  Last, so that the fields every
+  // block reads first share the leading kernel-argument cache lines (measured:
+  // the table placed after `tokens` cost 6 us per MiniMind2 step).
+  KvSegs seg;
 };
-constexpr int kKvPage = 64;  // tokens per KV page (a multiple of every attention tile)
 
 constexpr int kAttnMaxGroup = 8;  // Hq / Hkv supported
 constexpr int kAttnMaxQkvParts = 8;
 size_t attention_partial_floats(int hq, int hkv, int d, int splits);
 int attention_tile_tokens(int d);
-int64_t attention_cache_rows(int64_t capacity, int d);
 bool attention_supported(int hq, int hkv, int d);
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream);
 // Merge the split partials into out [Hq*D] (one block per query head).
@@ -210,10 +252,8 @@ struct QkvPostArgs {
   float eps = 0.0f;
   const float* inv_freq = nullptr;  // [D/2]
   int position = 0;
-  int index = 0;
-  void* kcache = nullptr;
-  void* vcache = nullptr;
-  int rows = 0;
+  int index = 0;  // cache row the key / value go to (backed)
+  KvSegs seg;
   int hq = 0, hkv = 0, d = 0;
   float* query_out = nullptr;
 };
@@ -287,7 +327,8 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // Rows of the fused qkv projection for tokens at positions start ..
 // start + tokens - 1: per-head q/k RMSNorm + RoPE, q -> query rows, k/v
-// written to the cache at their positions.
+// written to cache rows row0 .. row0 + tokens - 1 (row0 = start when cache
+// rows are positions).
 struct QkvRowsArgs {
   const float* qkv = nullptr;  // [tokens][qkv_stride]
   int qkv_stride = 0;
@@ -299,11 +340,10 @@ struct QkvRowsArgs {
   const float* k_norm = nullptr;
   float eps = 0.0f;
   const float* inv_freq = nullptr;  // [D/2]
-  int start = 0;
+  int start = 0;  // RoPE position of token 0
+  int row0 = 0;   // cache row of token 0
   int tokens = 0;
-  void* kcache = nullptr;
-  void* vcache = nullptr;
-  int rows = 0;  // cache rows per KV head
+  KvSegs seg;  // rows row0 .. row0 + tokens - 1 backed
   int hq = 0, hkv = 0, d = 0;
   float* query = nullptr;  // [tokens][query_stride]
   int query_stride = 0;
@@ -316,9 +356,7 @@ hipError_t launch_qkv_rows(const QkvRowsArgs& a, KvDtype kv, hipStream_t stream)
 struct PrefillAttnArgs {
   const float* query = nullptr;  // [tokens][query_stride], normalised + rotated
   int query_stride = 0;
-  const void* kcache = nullptr;
-  const void* vcache = nullptr;
-  int rows = 0;
+  KvSegs seg;  // rows 0 .. start + tokens - 1 backed
   int start = 0;
   int tokens = 0;
   int hq = 0, hkv = 0, d = 0;

@@ -749,8 +749,11 @@ __global__ __launch_bounds__(kWave* kQkvRowsTokens) void qkv_rows_kernel(QkvRows
     float* dst = a.query + static_cast<int64_t>(t) * a.query_stride + head * D;
     for (int i = lane; i < D; i += kWave) dst[i] = x_s[i];
   } else {
-    KV* kdst = reinterpret_cast<KV*>(a.kcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
-    KV* vdst = reinterpret_cast<KV*>(a.vcache) + (static_cast<int64_t>(head) * a.rows + pos) * D;
+    const int row = a.row0 + t;
+    const int seg = kv_segment(row);
+    const int64_t off = kv_segment_offset(seg, row, head, a.hkv, D);
+    KV* kdst = static_cast<KV*>(a.seg.s[seg].k) + off;
+    KV* vdst = static_cast<KV*>(a.seg.s[seg].v) + off;
     if (lane < D) {
       kdst[lane] = from_float<KV>(x_s[lane]);
       vdst[lane] = from_float<KV>(v0);
@@ -820,8 +823,6 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
   const int qi = lane % 16, kq = lane / 16;  // query column, k slot
   const int qrow = min(q0 + qi, a.tokens - 1);
   const int qpos = a.start + q0 + qi;
-  const KV* kbase = reinterpret_cast<const KV*>(a.kcache) + static_cast<int64_t>(g) * a.rows * D;
-  const KV* vbase = reinterpret_cast<const KV*>(a.vcache) + static_cast<int64_t>(g) * a.rows * D;
   float* k_s = stage[wave];            // [KT][LD]
   float* v_s = stage[wave] + KT * LD;  // [KT][LD]
   // fp16 cache (d % 32 == 0): K and V stay fp16 in the stage and both
@@ -836,15 +837,21 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_attention_kernel
   const int n_tiles = last_key / KT + 1;
   // chunk c: key c / kRowChunks, dims (c % kRowChunks) * CH ..: consecutive
   // lanes read consecutive 16 bytes of a row.
+  // A tile's 16 keys lie in one KV page (pages hold 64 aligned tokens), where
+  // one head's rows are contiguous: one segment lookup per tile.
   auto fetch = [&](int tile, Regs& r) {
     const int t0 = tile * KT;
+    const int seg = kv_segment(t0);
+    const int64_t tile_off = kv_segment_offset(seg, t0, g, a.hkv, D);
+    const KV* ktile = static_cast<const KV*>(a.seg.s[seg].k) + tile_off;
+    const KV* vtile = static_cast<const KV*>(a.seg.s[seg].v) + tile_off;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = min(lane + i * kWave, kChunks - 1);
       const int key = min(t0 + c / kRowChunks, last_key);  // rows past the last key are masked
-      const int64_t off = static_cast<int64_t>(key) * D + (c % kRowChunks) * CH;
-      r.k[i] = *reinterpret_cast<const uint4*>(kbase + off);
-      r.v[i] = *reinterpret_cast<const uint4*>(vbase + off);
+      const int64_t off = static_cast<int64_t>(key - t0) * D + (c % kRowChunks) * CH;
+      r.k[i] = *reinterpret_cast<const uint4*>(ktile + off);
+      r.v[i] = *reinterpret_cast<const uint4*>(vtile + off);
     }
   };
   Regs regs;

@@ -208,8 +208,7 @@ void enqueue_decoder_layer(const DeviceLayerWeights& W, const DecoderLayerIo& io
   t.eps = c.rms_norm_eps;
   t.inv_freq = W.inv_freq;
   t.pos = io.position;
-  t.kcache = io.kcache;
-  t.vcache = io.vcache;
+  t.seg = io.seg;
   t.capacity = io.capacity;
   t.rows = io.rows;
   t.hq = Hq;

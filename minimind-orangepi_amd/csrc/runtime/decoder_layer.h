@@ -63,10 +63,9 @@ struct DecoderLayerIo {
   const float* hidden = nullptr;      // [H] fp32
   float* out = nullptr;               // [H] fp32, may alias hidden
   const int32_t* position = nullptr;  // device int32: RoPE position and cache row of the new token
-  void* kcache = nullptr;             // [Hkv][rows][d]
-  void* vcache = nullptr;
-  int rows = 0;                       // cache rows per KV head
-  int capacity = 0;                   // usable positions (a position >= capacity sets *err)
+  mmr::KvSegs seg;                    // the layer's cache segments (KvStore::layer)
+  int rows = 0;                       // backed cache rows
+  int capacity = 0;                   // usable positions, all backed (a position >= capacity sets *err)
   mmr::KvDtype kv = mmr::kKvF32;
   int splits = 1;                     // attention context splits
   float* workspace = nullptr;         // decoder_layer_workspace_floats(cfg, splits) floats

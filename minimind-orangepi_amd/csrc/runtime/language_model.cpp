@@ -24,6 +24,8 @@
 #include "device.h"
 #include "decoder_layer.h"
 #include "device_model.h"
+#include "kv_store.h"
+#include "prefill_layer.h"
 #include "../kernels/kernels.h"
 
 #include <algorithm>
@@ -50,7 +52,11 @@ struct DeviceState {
   mmr::KvDtype kv = mmr::kKvF32;
   int64_t capacity = 0;
   Arena arena;
-  std::vector<void*> kcache, vcache;
+  // The KV cache: 64-token pages in doubling segments, backed as the context
+  // grows (ensure_backed); the small-model kernel keeps [Hkv][capacity][d]
+  // per layer in the arena instead (tiny_k / tiny_v).
+  KvStore kv_store;
+  std::vector<void*> tiny_k, tiny_v;
   int32_t* seq = nullptr;  // [capacity + 1]
   int32_t* pos = nullptr;
   int32_t* prompt_len = nullptr;
@@ -65,24 +71,12 @@ struct DeviceState {
   float* attn_part = nullptr;  // split partials: o [Hkv][splits][R][d], then (m, l) [Hkv][splits][R][2]
   float* lm_part_val = nullptr;  // per-block argmax partials of the head GEMV
   int* lm_part_idx = nullptr;
-  int64_t cache_rows = 0;        // capacity rounded up to the attention tile
   int32_t* staging = nullptr;        // pinned host [capacity + 8]
   // Prefill chunk buffers (rows = prompt tokens of one chunk, <= pf_chunk).
   int64_t pf_chunk = 0;
   float* pf_h = nullptr;    // [chunk][H] residual stream
-  float* pf_x = nullptr;    // [chunk][H] normalised rows
-  // GEMM inputs pre-split (hi / lo fp16 planes and power-of-two scales): the
-  // normalised rows (per 128 columns, written by the norm kernels instead of
-  // pf_x), the attention output (per 32, instead of pf_attn) and act (per 32,
-  // written by the gate_up epilogue instead of pf_act).
-  mmr::SplitPlanes pf_xs, pf_attn_s, pf_act_s;
-  float* pf_q = nullptr;    // [chunk][Hq d] normalised, rotated queries
-  float* pf_attn = nullptr; // [chunk][Hq d]
-  float* pf_part = nullptr; // split-K partials of one GEMM (QKV, O, gate_up or down): [splits][chunk][N]
-  int64_t pf_part_floats = 0;
-  float* pf_act = nullptr;  // [chunk][F]
+  PrefillScratch pf;        // the layer's scratch for pf_chunk rows
   bool prefill_tokenwise = false;  // prefill through the decode step instead of the GEMM path
-  bool gemm_register_staged = false;  // prefill GEMMs on the register-staged kernel only (comparison switch)
   hipStream_t stream = nullptr;
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;  // (attention splits, steps) -> captured steps
   bool use_graphs = true;
@@ -153,6 +147,17 @@ DecoderState::~DecoderState() = default;
 DecoderState::DecoderState(DecoderState&&) noexcept = default;
 DecoderState& DecoderState::operator=(DecoderState&&) noexcept = default;
 int64_t DecoderState::capacity() const { return device ? device->capacity : 0; }
+int64_t DecoderState::kv_backed() const {
+  if (!device) return 0;
+  return device->model->tiny ? device->capacity : std::min(device->capacity, device->kv_store.backed());
+}
+std::size_t DecoderState::kv_device_bytes() const {
+  if (!device) return 0;
+  if (!device->model->tiny) return device->kv_store.device_bytes();
+  const auto& c = device->model->cfg;
+  return static_cast<std::size_t>(2 * c.num_hidden_layers * c.num_key_value_heads * device->capacity * c.head_dim) *
+         (device->kv == mmr::kKvF16 ? 2 : 4);
+}
 KvCacheDtype DecoderState::kv_dtype() const {
   return device && device->kv == mmr::kKvF16 ? KvCacheDtype::kFloat16 : KvCacheDtype::kFloat32;
 }
@@ -273,7 +278,7 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   const char* pt = std::getenv("MMR_PREFILL_TOKENWISE");
   s->prefill_tokenwise = (pt && pt[0] == '1') || !device_->gemm_prefill;
   const char* rs = std::getenv("MMR_GEMM_REGISTER_STAGED");
-  s->gemm_register_staged = rs && rs[0] == '1';
+  s->pf.register_staged = rs && rs[0] == '1';
   if (const char* wb = std::getenv("MMR_L2_WARM_BLOCKS"))
     s->warm_blocks = std::max(0, std::atoi(wb)) / mmr::kXcds * mmr::kXcds;
   {
@@ -284,12 +289,12 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;
   const int64_t F = c.intermediate_size, V = c.vocab_size;
   const std::size_t kv_elem = s->kv == mmr::kKvF16 ? 2 : 4;
-  s->cache_rows = tiny ? capacity : mmr::attention_cache_rows(capacity, static_cast<int>(D));
-  const std::size_t cache_bytes = static_cast<std::size_t>(Hkv * s->cache_rows * D) * kv_elem;
+  // Small models: one [Hkv][capacity][d] block per layer for K and V.
+  const std::size_t tiny_cache_bytes = tiny ? static_cast<std::size_t>(Hkv * capacity * D) * kv_elem : 0;
   Arena& ar = s->arena;
-  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
-    ar.plan(cache_bytes);
-    ar.plan(cache_bytes);
+  for (int64_t l = 0; l < c.num_hidden_layers && tiny; ++l) {
+    ar.plan(tiny_cache_bytes);
+    ar.plan(tiny_cache_bytes);
   }
   const std::size_t part_floats =
       tiny ? 0 : mmr::attention_partial_floats(static_cast<int>(Hq), static_cast<int>(Hkv), static_cast<int>(D), kMaxSplits);
@@ -309,28 +314,21 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   if (const char* pc = std::getenv("MMR_PREFILL_CHUNK")) chunk = std::max<int64_t>(1, std::atoll(pc));
   s->pf_chunk = s->prefill_tokenwise ? 0 : std::min<int64_t>(capacity, chunk);
   const int64_t C = s->pf_chunk;
-  const int64_t part_f = prefill_partial_floats(c, C);
+  const std::size_t pf_bytes = C > 0 ? prefill_scratch_bytes(c, C) : 0;
   if (C > 0) {
     ar.plan(C * H * 4);
-    ar.plan(C * H * 4);
-    ar.plan(C * Hq * D * 4);
-    ar.plan(C * Hq * D * 4);
-    ar.plan(part_f * 4);
-    ar.plan(C * F * 4);
-    ar.plan(C * H * 2);
-    ar.plan(C * H * 2);
-    ar.plan(C * ((H + mmr::kSplitChunk - 1) / mmr::kSplitChunk) * 4);
-    ar.plan(C * Hq * D * 2);
-    ar.plan(C * Hq * D * 2);
-    ar.plan(C * ((Hq * D + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine) * 4);
-    ar.plan(C * F * 2);
-    ar.plan(C * F * 2);
-    ar.plan(C * ((F + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine) * 4);
+    ar.plan(pf_bytes);
   }
   ar.allocate();
-  for (int64_t l = 0; l < c.num_hidden_layers; ++l) {
-    s->kcache.push_back(ar.take<char>(cache_bytes));
-    s->vcache.push_back(ar.take<char>(cache_bytes));
+  for (int64_t l = 0; l < c.num_hidden_layers && tiny; ++l) {
+    s->tiny_k.push_back(ar.take<char>(tiny_cache_bytes));
+    s->tiny_v.push_back(ar.take<char>(tiny_cache_bytes));
+  }
+  if (!tiny) {
+    // Up front only the first segment (512 positions); later segments are
+    // added as the context reaches them.
+    s->kv_store = KvStore(c.num_hidden_layers, Hkv, D, s->kv, capacity);
+    s->kv_store.reserve(std::min<int64_t>(capacity, mmr::kv_segment_tokens(0)));
   }
   s->seq = ar.take<int32_t>(capacity + 1);
   int32_t* scalars = ar.take<int32_t>(4);
@@ -349,23 +347,9 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   s->tiny_layers = tiny ? ar.take<mmr::TinyLayerPtrs>(static_cast<std::size_t>(c.num_hidden_layers)) : nullptr;
   if (C > 0) {
     s->pf_h = ar.take<float>(C * H);
-    s->pf_x = ar.take<float>(C * H);
-    s->pf_q = ar.take<float>(C * Hq * D);
-    s->pf_attn = ar.take<float>(C * Hq * D);
-    s->pf_part = ar.take<float>(part_f);
-    s->pf_part_floats = part_f;
-    s->pf_act = ar.take<float>(C * F);
-    s->pf_xs.hi = ar.take<uint16_t>(C * H);
-    s->pf_xs.lo = ar.take<uint16_t>(C * H);
-    s->pf_xs.inv = ar.take<float>(C * ((H + mmr::kSplitChunk - 1) / mmr::kSplitChunk));
-    s->pf_attn_s.hi = ar.take<uint16_t>(C * Hq * D);
-    s->pf_attn_s.lo = ar.take<uint16_t>(C * Hq * D);
-    s->pf_attn_s.inv = ar.take<float>(C * ((Hq * D + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine));
-    s->pf_attn_s.chunk = mmr::kSplitChunkFine;
-    s->pf_act_s.hi = ar.take<uint16_t>(C * F);
-    s->pf_act_s.lo = ar.take<uint16_t>(C * F);
-    s->pf_act_s.inv = ar.take<float>(C * ((F + mmr::kSplitChunkFine - 1) / mmr::kSplitChunkFine));
-    s->pf_act_s.chunk = mmr::kSplitChunkFine;
+    const bool staged = s->pf.register_staged;
+    s->pf = carve_prefill_scratch(c, C, ar.take<char>(pf_bytes));
+    s->pf.register_staged = staged;
   }
   if (tiny) {
     std::vector<mmr::TinyLayerPtrs> table(static_cast<std::size_t>(c.num_hidden_layers));
@@ -380,8 +364,8 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
       t.o = L.o;
       t.gate_up = L.gate_up;
       t.down = L.down;
-      t.kcache = s->kcache[static_cast<std::size_t>(l)];
-      t.vcache = s->vcache[static_cast<std::size_t>(l)];
+      t.kcache = s->tiny_k[static_cast<std::size_t>(l)];
+      t.vcache = s->tiny_v[static_cast<std::size_t>(l)];
     }
     check_hip(hipMemcpy(s->tiny_layers, table.data(), tiny_bytes, hipMemcpyHostToDevice), "hipMemcpy layer table");
   }
@@ -479,10 +463,11 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       t.eps = c.rms_norm_eps;
       t.inv_freq = m.inv_freq;
       t.pos = s.pos;
-      t.kcache = s.kcache[l];
-      t.vcache = s.vcache[l];
-      t.capacity = static_cast<int>(s.capacity);
-      t.rows = static_cast<int>(s.cache_rows);
+      t.seg = s.kv_store.layer(static_cast<int64_t>(l));
+      // Positions past the backed rows are flagged, never read (the launcher
+      // backs every position a launch can reach before it captures or runs it).
+      t.capacity = static_cast<int>(std::min(s.capacity, s.kv_store.backed()));
+      t.rows = static_cast<int>(s.kv_store.backed());
       t.hq = Hq;
       t.hkv = Hkv;
       t.d = D;
@@ -609,7 +594,7 @@ void enqueue_tiny_step(const DeviceState& s) {
   a.f = static_cast<int>(c.intermediate_size);
   a.vocab = static_cast<int>(c.vocab_size);
   a.eps = c.rms_norm_eps;
-  a.rows = static_cast<int>(s.cache_rows);
+  a.rows = static_cast<int>(s.capacity);
   a.capacity = static_cast<int>(s.capacity);
   a.seq = s.seq;
   a.pos = s.pos;
@@ -651,143 +636,24 @@ void enqueue_step_kernels(const DeviceState& s, int splits, bool first = true, b
 void enqueue_prefill_chunk(const DeviceState& s, int64_t start, int64_t n) {
   const DeviceModel& m = *s.model;
   const auto& c = m.cfg;
-  const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
-  const int Hq = static_cast<int>(c.num_attention_heads), Hkv = static_cast<int>(c.num_key_value_heads);
-  const int F = static_cast<int>(c.intermediate_size), V = static_cast<int>(c.vocab_size);
-  const int qkv_w = (Hq + 2 * Hkv) * D;
   const int rows = static_cast<int>(n);
-  check_hip(mmr::launch_embedding_gather(m.embed, s.seq + start, rows, V, H, s.pf_h, s.err, s.stream),
+  check_hip(mmr::launch_embedding_gather(m.embed, s.seq + start, rows, static_cast<int>(c.vocab_size),
+                                         static_cast<int>(c.hidden_size), s.pf_h, s.err, s.stream),
             "prefill embedding");
-  // Split-K partial products into pf_part (at most max_splits; returns the
-  // split count, 1 = the dense product); the consumers add the partials:
-  // q/k norm + RoPE + KV write, residual add + RMSNorm, or SwiGLU.
-  // The normalised rows go to the QKV and gate_up GEMMs pre-split when the
-  // tiled path takes them (all but the few-rows path): the GEMM blocks then
-  // stage the planes instead of each splitting the same rows again.
-  const bool presplit = mmr::gemm_presplit_supported(rows, qkv_w, H) && mmr::gemm_presplit_supported(rows, 2 * F, H);
-  const mmr::SplitPlanes* xs = presplit ? &s.pf_xs : nullptr;
-  float* const xf = presplit ? nullptr : s.pf_x;  // fp32 normalised rows, when the GEMMs read those
-  // Likewise the attention output (written split by the attention kernel)
-  // for the O GEMM, and act (written split by the gate_up SwiGLU epilogue)
-  // for the down GEMM.
-  const bool attn_split = D % mmr::kSplitChunkFine == 0 && mmr::gemm_presplit_supported(rows, H, Hq * D);
-  const bool act_split = mmr::gemm_swiglu_split_supported(rows, 2 * F, H) && mmr::gemm_presplit_supported(rows, H, F);
-  auto use_planes = [](mmr::GemmArgs& g, const mmr::SplitPlanes& p) {
-    g.a = nullptr;
-    g.a_hi = p.hi;
-    g.a_lo = p.lo;
-    g.a_inv = p.inv;
-    g.a_chunk = p.chunk;
-  };
-  auto use_x = [&](mmr::GemmArgs& g) {
-    if (presplit) {
-      use_planes(g, s.pf_xs);
-    } else {
-      g.a = s.pf_x;
-    }
-  };
-  auto gemm_parts = [&](const float* a, int lda, const __half* w, int N, int K, int max_splits) {
-    mmr::GemmArgs g;
-    if (a == s.pf_x) {
-      use_x(g);
-    } else if (a == s.pf_attn && attn_split) {
-      use_planes(g, s.pf_attn_s);
-    } else if (a == s.pf_act && act_split) {
-      use_planes(g, s.pf_act_s);
-    } else {
-      g.a = a;
-    }
-    g.lda = lda;
-    g.w = w;
-    g.c = s.pf_part;
-    g.ldc = N;
-    g.m = rows;
-    g.n = N;
-    g.k = K;
-    g.k_splits = std::min(mmr::gemm_k_splits(rows, N, K), max_splits);
-    g.split_stride = static_cast<int64_t>(rows) * N;
-    g.register_staged = s.gemm_register_staged;
-    if (int64_t{g.k_splits} * g.split_stride > s.pf_part_floats)
-      throw std::logic_error("prefill split-K partials exceed their buffer");
-    check_hip(mmr::launch_gemm(g, s.stream), "prefill gemm");
-    return g.k_splits;
-  };
-  constexpr int kAnySplits = 1 << 30;
+  // Layer 0's input norm; every later layer's comes from the previous
+  // layer's residual consumer (after the last layer the final norm, whose
+  // rows are not used: the head normalises the last row itself).
+  enqueue_prefill_input_norm(c, s.pf, rows, s.pf_h, m.layers[0].input_norm, s.stream);
   const size_t L = m.layers.size();
-  // Layer 0's input norm; later layers get theirs from the previous layer's
-  // residual consumer.
-  check_hip(mmr::launch_batch_residual_norm(s.pf_h, nullptr, 0, rows, H, m.layers[0].input_norm, c.rms_norm_eps, xf,
-                                            false, s.stream, xs),
-            "prefill input norm");
   for (size_t l = 0; l < L; ++l) {
-    const LayerDev& Ld = m.layers[l];
-    const int sq = gemm_parts(s.pf_x, H, Ld.qkv, qkv_w, H, mmr::kQkvRowsMaxParts);
-    mmr::QkvRowsArgs q;
-    q.qkv = s.pf_part;
-    q.qkv_stride = qkv_w;
-    q.qkv_parts = sq;
-    q.qkv_part_stride = static_cast<int64_t>(rows) * qkv_w;
-    q.q_norm = Ld.q_norm;
-    q.k_norm = Ld.k_norm;
-    q.eps = c.rms_norm_eps;
-    q.inv_freq = m.inv_freq;
-    q.start = static_cast<int>(start);
-    q.tokens = rows;
-    q.kcache = s.kcache[l];
-    q.vcache = s.vcache[l];
-    q.rows = static_cast<int>(s.cache_rows);
-    q.hq = Hq;
-    q.hkv = Hkv;
-    q.d = D;
-    q.query = s.pf_q;
-    q.query_stride = Hq * D;
-    check_hip(mmr::launch_qkv_rows(q, s.kv, s.stream), "prefill qkv rows");
-    mmr::PrefillAttnArgs at;
-    at.query = s.pf_q;
-    at.query_stride = Hq * D;
-    at.kcache = s.kcache[l];
-    at.vcache = s.vcache[l];
-    at.rows = static_cast<int>(s.cache_rows);
-    at.start = static_cast<int>(start);
-    at.tokens = rows;
-    at.hq = Hq;
-    at.hkv = Hkv;
-    at.d = D;
-    at.out = attn_split ? nullptr : s.pf_attn;
-    at.out_stride = Hq * D;
-    if (attn_split) at.out_split = s.pf_attn_s;
-    check_hip(mmr::launch_prefill_attention(at, s.kv, s.stream), "prefill attention");
-    const int so = gemm_parts(s.pf_attn, Hq * D, Ld.o, H, Hq * D, kAnySplits);
-    check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, so, rows, H, Ld.post_norm, c.rms_norm_eps, xf,
-                                              false, s.stream, xs),
-              "prefill residual + post norm");
-    if (mmr::gemm_swiglu_supported(rows, 2 * F, H)) {  // SwiGLU in the gate_up epilogue
-      mmr::GemmArgs g;
-      use_x(g);
-      g.lda = H;
-      g.w = Ld.gate_up;
-      g.c = act_split ? nullptr : s.pf_act;
-      if (act_split) g.act_split = s.pf_act_s;
-      g.ldc = F;
-      g.m = rows;
-      g.n = 2 * F;
-      g.k = H;
-      g.swiglu = true;
-      g.register_staged = s.gemm_register_staged;
-      check_hip(mmr::launch_gemm(g, s.stream), "prefill gate_up + SwiGLU");
-    } else {
-      const int sg = gemm_parts(s.pf_x, H, Ld.gate_up, 2 * F, H, kAnySplits);
-      check_hip(mmr::launch_batch_swiglu(s.pf_part, sg, rows, F, s.pf_act, s.stream), "prefill swiglu");
-    }
-    const int sd = gemm_parts(s.pf_act, F, Ld.down, H, F, kAnySplits);
-    // The next layer's input norm (after the last layer: the final norm, whose
-    // rows are not used; the head normalises the last row itself).
+    PrefillKv kv;
+    kv.seg = s.kv_store.layer(static_cast<int64_t>(l));
+    kv.dtype = s.kv;
+    kv.rope_start = static_cast<int>(start);
+    kv.row0 = static_cast<int>(start);
     const bool last = l + 1 == L;
-    // The final norm's rows are not split (nothing multiplies them).
-    check_hip(mmr::launch_batch_residual_norm(s.pf_h, s.pf_part, sd, rows, H,
-                                              last ? m.final_norm : m.layers[l + 1].input_norm, c.rms_norm_eps,
-                                              last ? s.pf_x : xf, last, s.stream, last ? nullptr : xs),
-              "prefill residual + norm");
+    enqueue_prefill_layer(c, m.layers[l], m.inv_freq, s.pf, kv, rows, s.pf_h,
+                          last ? m.final_norm : m.layers[l + 1].input_norm, last, s.stream);
   }
 }
 
@@ -811,6 +677,22 @@ hipGraphExec_t capture_steps(DeviceState& s, int splits, int steps) {
   return exec;
 }
 
+// Back every position a decode launch with `splits` attention splits can
+// reach before it is captured or run: choose_splits gives that split count
+// to contexts up to some length (the last bucket to all of the capacity), and
+// a replayed graph keeps the segment table it was captured with.  Segments
+// are never freed while the state lives, so every captured graph stays valid.
+void ensure_backed_for_splits(DeviceState& s, int splits, int tile) {
+  if (s.model->tiny || s.kv_store.backed() >= s.capacity) return;
+  int64_t reach = s.capacity;
+  if (splits < kMaxSplits) {
+    int64_t tiles = 1;
+    while (tiles * tile < s.capacity && choose_splits((tiles + 1) * tile, tile) <= splits) ++tiles;
+    reach = std::min(s.capacity, tiles * tile);
+  }
+  if (s.kv_store.backed() < reach) s.kv_store.reserve(reach);
+}
+
 void check_token(const MiniMindConfig& c, int32_t token) {
   if (token < 0 || token >= c.vocab_size) throw std::out_of_range("token id out of vocabulary range");
 }
@@ -820,7 +702,9 @@ void check_token(const MiniMindConfig& c, int32_t token) {
 void LanguageModel::launch_step(DecoderState& state) const {
   DeviceState& s = *state.device;
   if (state.position >= s.capacity) throw std::length_error("KV cache capacity exhausted");
-  const int splits = choose_splits(state.position + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  const int tile = mmr::attention_tile_tokens(static_cast<int>(config_.head_dim));
+  const int splits = choose_splits(state.position + 1, tile);
+  ensure_backed_for_splits(s, splits, tile);
   if (s.use_graphs) {
     const auto key = std::make_pair(splits, 1);
     auto it = s.graphs.find(key);
@@ -863,6 +747,7 @@ void LanguageModel::enqueue_decode(DecoderState& state, int64_t n, int32_t first
     for (; i + kGraphSteps <= n; i += kGraphSteps) {
       const int splits = choose_splits(state.position + kGraphSteps, tile);
       if (splits > mmr::kCombineMaxSplits) break;
+      ensure_backed_for_splits(s, splits, tile);
       const auto key = std::make_pair(splits, kGraphSteps);
       auto it = s.graphs.find(key);
       if (it == s.graphs.end()) it = s.graphs.emplace(key, capture_steps(s, splits, kGraphSteps)).first;
@@ -892,6 +777,7 @@ void LanguageModel::enqueue_prefill(DecoderState& state, const std::vector<int32
     for (int64_t i = 0; i < n; ++i) launch_step(state);
     return;
   }
+  if (!device_->tiny) s.kv_store.reserve(state.position + n);  // the rows the chunks write
   // Chunked GEMM prefill; the head (final norm, lm_head, argmax) then runs on
   // the last prompt row with the device position at that row, so the
   // finalize kernel writes the prediction to seq[position + n] and advances
@@ -921,7 +807,9 @@ void LanguageModel::enqueue_kernel(DecoderState& state, int kernel, int64_t laye
   if (kernel < kQkv || kernel > kFinalize) throw std::invalid_argument("unknown step kernel");
   if (layer < 0 || layer >= L || count < 0) throw std::invalid_argument("layer / count out of range");
   if (kernel == kAttention && state.position >= s.capacity) throw std::length_error("KV cache capacity exhausted");
-  const int splits = choose_splits(state.position + 1, mmr::attention_tile_tokens(static_cast<int>(config_.head_dim)));
+  const int tile = mmr::attention_tile_tokens(static_cast<int>(config_.head_dim));
+  const int splits = choose_splits(state.position + 1, tile);
+  ensure_backed_for_splits(s, splits, tile);
   for (int64_t i = 0; i < count; ++i)
     ::minimind::model::enqueue_kernel(s, kernel, static_cast<size_t>((layer + i) % L), splits, false);
 }
@@ -939,6 +827,9 @@ double LanguageModel::time_kernel(DecoderState& state, int kernel, int64_t layer
   try {
     check_hip(hipEventCreate(&e0), "hipEventCreate");
     check_hip(hipEventCreate(&e1), "hipEventCreate");
+    // Any KV segment the launches need is allocated now, not under capture.
+    const int tile = mmr::attention_tile_tokens(static_cast<int>(config_.head_dim));
+    ensure_backed_for_splits(s, choose_splits(state.position + 1, tile), tile);
     if (s.use_graphs) {
       hipGraph_t graph = nullptr;
       check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
@@ -1002,6 +893,13 @@ void LanguageModel::reset_state(DecoderState& state) const {
   check_hip(hipMemsetAsync(s.pos, 0, 2 * sizeof(int32_t), s.stream), "hipMemsetAsync");
   check_hip(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
   state.position = 0;
+}
+
+void LanguageModel::reserve_kv(DecoderState& state, int64_t positions) const {
+  DeviceState& s = *state.device;
+  if (positions < 0) throw std::invalid_argument("positions cannot be negative");
+  if (positions > s.capacity) throw std::length_error("KV cache capacity exhausted");
+  if (!device_->tiny) s.kv_store.reserve(positions);
 }
 
 std::vector<float> LanguageModel::forward_token(int32_t token, DecoderState& state) const {

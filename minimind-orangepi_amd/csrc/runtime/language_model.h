@@ -12,8 +12,10 @@
 //    falling back silently;
 //  * weights live on the GPU as fp16 (round to nearest even at upload), norm
 //    gains and activations stay fp32;
-//  * the KV cache has a fixed capacity chosen in make_state and is never
-//    reallocated; exceeding it raises std::length_error;
+//  * the KV cache has a capacity chosen in make_state; exceeding it raises
+//    std::length_error.  Device memory backs it in 64-token pages grouped in
+//    doubling segments, added as the context reaches them (512 positions up
+//    front), never moved or reallocated;
 //  * one decode step is one hipGraph replay; the next token, the position and
 //    the token sequence stay in device memory between steps.
 #pragma once
@@ -21,6 +23,7 @@
 #include "config.h"
 #include "weights.h"
 
+#include <cstddef>
 #include <cstdint>
 #include <functional>
 #include <memory>
@@ -47,6 +50,10 @@ struct DecoderState {
 
   int64_t position = 0;  // tokens already in the cache (host mirror)
   int64_t capacity() const;
+  // KV positions backed by device memory so far (the cache grows in
+  // doubling segments as the context reaches them) and the bytes they hold.
+  int64_t kv_backed() const;
+  std::size_t kv_device_bytes() const;
   KvCacheDtype kv_dtype() const;
   void* stream() const;  // hipStream_t all work of this state runs on
   std::unique_ptr<DeviceState> device;
@@ -121,6 +128,10 @@ class LanguageModel {
   double time_kernel(DecoderState& state, int kernel, int64_t layer, int64_t count) const;
   // Reset position to 0 (the cache contents are overwritten as it refills).
   void reset_state(DecoderState& state) const;
+  // Back KV positions [0, positions) now (at most the capacity), so decoding
+  // up to there allocates nothing; otherwise segments are added as the
+  // context reaches them.
+  void reserve_kv(DecoderState& state, int64_t positions) const;
 
   // ---- batched decode (independent sequences in lockstep) ----
   BatchState make_batch_state(int64_t batch, int64_t capacity, KvCacheDtype kv = KvCacheDtype::kFloat16) const;

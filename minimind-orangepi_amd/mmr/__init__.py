@@ -113,8 +113,12 @@ _SIGS = {
     "mmr_rope_table_destroy": ([VP], C.c_int),
     "mmr_kv_cache_create": ([I64, I64, I64, C.c_int, C.POINTER(VP)], C.c_int),
     "mmr_kv_cache_destroy": ([VP], C.c_int),
-    "mmr_kv_cache_data": ([VP, C.POINTER(VP), C.POINTER(VP)], C.c_int),
-    "mmr_kv_cache_rows": ([VP, C.POINTER(I64)], C.c_int),
+    "mmr_kv_cache_reserve": ([VP, I64], C.c_int),
+    "mmr_kv_cache_reset": ([VP], C.c_int),
+    "mmr_kv_cache_backed": ([VP, C.POINTER(I64), C.POINTER(U64)], C.c_int),
+    "mmr_kv_cache_segment": ([VP, C.c_int, C.POINTER(VP), C.POINTER(VP), C.POINTER(I64), C.POINTER(I64)], C.c_int),
+    "mmr_kv_cache_write": ([VP, I64, I64, VP, VP], C.c_int),
+    "mmr_kv_cache_read": ([VP, I64, I64, VP, VP], C.c_int),
     "mmr_kv_cache_info": ([VP, C.POINTER(I64), C.POINTER(I64), C.POINTER(I64), C.POINTER(C.c_int)], C.c_int),
     "mmr_cube_matvec_available": ([], C.c_int),
     "mmr_cube_matmul_available": ([], C.c_int),
@@ -136,6 +140,8 @@ _SIGS = {
     "mmr_layer_weights_destroy": ([VP], C.c_int),
     "mmr_decoder_layer_workspace_size": ([C.POINTER(Config), C.c_int], SZ),
     "mmr_decoder_layer_forward": ([VP, VP, VP, VP, VP, VP, SZ, C.c_int, VP, VP], C.c_int),
+    "mmr_prefill_layer_workspace_size": ([C.POINTER(Config), I64], SZ),
+    "mmr_prefill_layer_forward": ([VP, VP, VP, I64, I64, VP, VP, SZ, VP], C.c_int),
     "mmr_matmul_f16": ([VP, I64, I64, VP, I64, VP, VP, VP], C.c_int),
     "mmr_prefill_qkv_rows": ([VP, VP, VP, F32, VP, VP, I64, I64, I64, I64, I64, VP, VP], C.c_int),
     "mmr_prefill_attention": ([VP, VP, I64, I64, I64, I64, I64, VP, VP], C.c_int),
@@ -159,6 +165,8 @@ _SIGS = {
     "mmr_state_create": ([VP, I64, C.c_int, C.POINTER(VP)], C.c_int),
     "mmr_state_free": ([VP], C.c_int),
     "mmr_state_position": ([VP, C.POINTER(I64)], C.c_int),
+    "mmr_state_kv_backed": ([VP, C.POINTER(I64), C.POINTER(U64)], C.c_int),
+    "mmr_state_reserve": ([VP, VP, I64], C.c_int),
     "mmr_state_stream": ([VP, C.POINTER(VP)], C.c_int),
     "mmr_state_reset": ([VP, VP], C.c_int),
     "mmr_forward_token": ([VP, VP, I32, VP], C.c_int),
@@ -428,40 +436,59 @@ class RopeTable:
 
 
 class KvCache:
-    def __init__(self, kv_heads: int, head_dim: int, capacity: int, kv_dtype: int = KV_F32):
+    """One layer's KV cache (mmr_kv_cache): 64-token pages in doubling
+    segments, backed on demand.  With reserve=True (the default) every
+    position up to `capacity` is backed at once; with reserve=False only the
+    first segment is, until reserve() / upload() back more."""
+
+    def __init__(self, kv_heads: int, head_dim: int, capacity: int, kv_dtype: int = KV_F32, reserve: bool = True):
         h = VP()
         check(_lib.mmr_kv_cache_create(kv_heads, head_dim, capacity, kv_dtype, C.byref(h)))
         self.handle = h.value
         self.kv_heads, self.head_dim, self.capacity, self.kv_dtype = kv_heads, head_dim, capacity, kv_dtype
         self.np_dtype = np.float16 if kv_dtype == KV_F16 else np.float32
-        rows = C.c_int64(0)
-        check(_lib.mmr_kv_cache_rows(self.handle, C.byref(rows)))
-        self.rows = int(rows.value)  # capacity rounded up to the attention tile
+        if reserve:
+            self.reserve(capacity)
 
-    def pointers(self) -> tuple[int, int]:
-        k, v = VP(), VP()
-        check(_lib.mmr_kv_cache_data(self.handle, C.byref(k), C.byref(v)))
-        return k.value, v.value
+    def reserve(self, tokens: int) -> None:
+        check(_lib.mmr_kv_cache_reserve(self.handle, tokens))
 
-    def _nbytes(self) -> int:
-        return self.kv_heads * self.rows * self.head_dim * np.dtype(self.np_dtype).itemsize
+    def reset(self) -> None:
+        check(_lib.mmr_kv_cache_reset(self.handle))
 
-    def upload(self, keys: np.ndarray, values: np.ndarray) -> None:
-        """keys/values shaped [kv_heads, rows, head_dim] (cache layout)."""
-        kp, vp = self.pointers()
-        for ptr, a in ((kp, keys), (vp, values)):
-            a = np.ascontiguousarray(a, dtype=self.np_dtype)
-            assert a.nbytes == self._nbytes()
-            check(_lib.mmr_memcpy_h2d(ptr, _ptr(a), a.nbytes))
+    @property
+    def rows(self) -> int:
+        """Backed positions (from 0)."""
+        n = C.c_int64(0)
+        check(_lib.mmr_kv_cache_backed(self.handle, C.byref(n), None))
+        return int(n.value)
 
-    def download(self) -> tuple[np.ndarray, np.ndarray]:
-        kp, vp = self.pointers()
-        out = []
-        for ptr in (kp, vp):
-            a = np.empty((self.kv_heads, self.rows, self.head_dim), self.np_dtype)
-            check(_lib.mmr_memcpy_d2h(_ptr(a), ptr, a.nbytes))
-            out.append(a)
-        return out[0], out[1]
+    @property
+    def device_bytes(self) -> int:
+        b = C.c_uint64(0)
+        check(_lib.mmr_kv_cache_backed(self.handle, None, C.byref(b)))
+        return int(b.value)
+
+    def segment(self, index: int) -> tuple[int, int, int, int]:
+        """(keys pointer, values pointer, first position, backed positions) of one segment."""
+        k, v, first, n = VP(), VP(), C.c_int64(0), C.c_int64(0)
+        check(_lib.mmr_kv_cache_segment(self.handle, index, C.byref(k), C.byref(v), C.byref(first), C.byref(n)))
+        return k.value or 0, v.value or 0, int(first.value), int(n.value)
+
+    def upload(self, keys: np.ndarray, values: np.ndarray, first: int = 0) -> None:
+        """keys/values [kv_heads, n, head_dim] -> rows first .. first + n - 1 (backed as needed)."""
+        k = np.ascontiguousarray(keys, dtype=self.np_dtype)
+        v = np.ascontiguousarray(values, dtype=self.np_dtype)
+        assert k.shape == v.shape and k.shape[0] == self.kv_heads and k.shape[2] == self.head_dim
+        check(_lib.mmr_kv_cache_write(self.handle, first, k.shape[1], _ptr(k), _ptr(v)))
+
+    def download(self, count: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+        """Rows 0 .. count - 1 (default: every backed row) as [kv_heads, count, head_dim]."""
+        n = self.rows if count is None else count
+        k = np.empty((self.kv_heads, n, self.head_dim), self.np_dtype)
+        v = np.empty_like(k)
+        check(_lib.mmr_kv_cache_read(self.handle, 0, n, _ptr(k), _ptr(v)))
+        return k, v
 
     def __del__(self):
         try:
@@ -569,6 +596,15 @@ class LayerWeights:
         """mmr_decoder_layer_forward: out = layer(hidden) at device position *position."""
         check(_lib.mmr_decoder_layer_forward(self.handle, cache.handle, hidden.ptr, position.ptr, out.ptr,
                                              workspace.ptr, workspace.nbytes, splits, error.ptr, _s(stream)))
+
+    def prefill_workspace_size(self, seq_len: int) -> int:
+        return int(_lib.mmr_prefill_layer_workspace_size(C.byref(self.config), seq_len))
+
+    def prefill(self, cache: "KvCache", hidden_seq: DeviceArray, start_position: int, seq_len: int,
+                out: DeviceArray, workspace: DeviceArray, stream=None) -> None:
+        """mmr_prefill_layer_forward: out = layer(hidden_seq) over seq_len rows of an empty cache."""
+        check(_lib.mmr_prefill_layer_forward(self.handle, cache.handle, hidden_seq.ptr, start_position, seq_len,
+                                             out.ptr, workspace.ptr, workspace.nbytes, _s(stream)))
 
     def free(self) -> None:
         if self.handle:
@@ -800,6 +836,16 @@ class State:
         p = C.c_int64(0)
         check(_lib.mmr_state_position(self.handle, C.byref(p)))
         return int(p.value)
+
+    def kv_backed(self) -> tuple[int, int]:
+        """(KV positions backed by device memory, the bytes they hold)."""
+        n, b = C.c_int64(0), C.c_uint64(0)
+        check(_lib.mmr_state_kv_backed(self.handle, C.byref(n), C.byref(b)))
+        return int(n.value), int(b.value)
+
+    def reserve(self, positions: int) -> None:
+        """Back KV positions [0, positions) now (mmr_state_reserve)."""
+        check(_lib.mmr_state_reserve(self.model.handle, self.handle, positions))
 
     @property
     def stream(self) -> int:

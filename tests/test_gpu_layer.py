@@ -150,3 +150,149 @@ def test_decoder_layer_errors(mini):
     bad = mmr.make_config(**{**c, "head_dim": 48})  # rejected before any array is read
     with pytest.raises(mmr.InvalidArgument, match="head_dim"):
         mmr.LayerWeights.create(bad, **{k: np.zeros(1, np.float32) for k in mmr.LayerWeights.NAMES})
+
+
+@pytest.fixture(scope="module")
+def mm2(gpu, oracle, tmp_path_factory):
+    # MiniMind2 (BASELINE configs[3] shape): hidden 768, 8 / 2 heads of 96,
+    # FFN 2048; the qkv GEMV's 2-row plan and the 16-split combine prologue
+    mmr = gpu
+    g = load_golden("cfg3")
+    d = tmp_path_factory.mktemp("layer_mm2")
+    mmr.write_synthetic_model(d, mmr.make_config(**g["config"]), g["seed"], g["std"], g["round_fp16"])
+    return mmr, oracle, g, d, mmr.Model.load(d), oracle.OracleModel(d)
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+@pytest.mark.parametrize("splits", [0, 16])
+def test_minimind2_decoder_layer_in_place(mm2, kv, splits):
+    # out aliasing hidden (include/mmr.h allows it): every residual GEMV reads
+    # residual[row] before it stores y[row], so the in-place call gives the
+    # same bits as the call with separate buffers; both match the oracle
+    mmr, oracle, g, d, model, ref = mm2
+    print(f"[case] MiniMind2 layer in place kv={kv} splits={splits}", flush=True)
+    c = g["config"]
+    H, D, Hkv = c["hidden_size"], c["head_dim"], c["num_key_value_heads"]
+    layer, steps = 5, 200
+    lw = mmr.LayerWeights.of_model(model, layer)
+    kvd = mmr.KV_F16 if kv == "f16" else mmr.KV_F32
+    ca, cb = mmr.KvCache(Hkv, D, 4096, kvd, reserve=False), mmr.KvCache(Hkv, D, 4096, kvd, reserve=False)
+    n_split = splits or 8  # automatic: one split per 64-token tile of the 512 backed rows
+    ws_a, ws_b = (mmr.DeviceArray(lw.workspace_size(n_split), np.uint8) for _ in range(2))
+    pos = mmr.DeviceArray(1, np.int32)
+    err = mmr.DeviceArray(1, np.int32, zero=True)
+    xa, xb, yb = (mmr.DeviceArray(H, np.float32) for _ in range(3))
+    st = ref.new_state()
+    rng = np.random.default_rng(15)
+    worst = 0.0
+    for p in range(steps):
+        h = rng.standard_normal(H).astype(np.float32)
+        xa.upload(h)
+        xb.upload(h)
+        pos.upload(np.array([p], np.int32))
+        lw.forward(ca, xa, pos, xa, ws_a, splits, err)  # in place
+        lw.forward(cb, xb, pos, yb, ws_b, splits, err)
+        got = xa.numpy()
+        np.testing.assert_array_equal(got, yb.numpy())
+        e = rel_err(got, st.decoder_layer(layer, h, p))
+        worst = max(worst, e)
+        assert e < TOL, (p, e)
+    assert int(err.numpy()[0]) == 0
+    print(f"[result] {steps} positions, worst layer-output error {worst:.2e}", flush=True)
+    np.testing.assert_array_equal(ca.download(steps)[0], cb.download(steps)[0])
+
+
+_PREFILL_REF = {}
+
+
+def prefill_reference(ref, layer, hs, start, h_next):
+    """The oracle's layer applied position by position from an empty cache:
+    row i at RoPE position start + i, cached at row i (the reference's
+    prefill layer semantics, decoder_layer.cpp:409-527); then one decode
+    step of h_next at position start + T on that cache."""
+    key = (layer, hs.shape[0], start, float(hs[0, 0]))
+    if key not in _PREFILL_REF:
+        st = ref.new_state()
+        outs = np.stack([st.decoder_layer(layer, hs[i], start + i) for i in range(hs.shape[0])])
+        cache = st.layer_cache(layer)
+        _PREFILL_REF[key] = (outs, cache, st.decoder_layer(layer, h_next, start + hs.shape[0]))
+    return _PREFILL_REF[key]
+
+
+@pytest.mark.parametrize("kv", ["f32", "f16"])
+@pytest.mark.parametrize("T", [1, 17, 512])
+def test_minimind2_prefill_layer_matches_oracle(mm2, kv, T):
+    # mmr_prefill_layer_forward (run_dense_prefill_layer_device,
+    # decoder_layer.cpp:661-734): T rows through one layer on the matrix cores
+    mmr, oracle, g, d, model, ref = mm2
+    print(f"[case] MiniMind2 prefill layer kv={kv} T={T}", flush=True)
+    c = g["config"]
+    H, D, Hkv = c["hidden_size"], c["head_dim"], c["num_key_value_heads"]
+    layer = 7
+    lw = mmr.LayerWeights.of_model(model, layer)
+    kvd = mmr.KV_F16 if kv == "f16" else mmr.KV_F32
+    hs = np.random.default_rng(100 + T).standard_normal((T, H)).astype(np.float32)
+    h1 = np.random.default_rng(7).standard_normal(H).astype(np.float32)
+    want, (rk, rv), want_next = prefill_reference(ref, layer, hs, 0, h1)
+    cache = mmr.KvCache(Hkv, D, T + 8, kvd)
+    x, y = mmr.DeviceArray.from_numpy(hs.reshape(-1)), mmr.DeviceArray(T * H, np.float32)
+    ws = mmr.DeviceArray(lw.prefill_workspace_size(T), np.uint8)
+    lw.prefill(cache, x, 0, T, y, ws)
+    got = y.numpy().reshape(T, H)
+    e = rel_err(got, want)
+    print(f"[result] prefill layer T={T} kv={kv}: error {e:.2e}", flush=True)
+    assert e < TOL
+    for i in (0, T // 2, T - 1):
+        assert rel_err(got[i], want[i]) < TOL, i
+    keys, values = cache.download(T)
+    gk, gv = keys.astype(np.float32), values.astype(np.float32)
+    rk, rv = rk.transpose(1, 0, 2), rv.transpose(1, 0, 2)
+    if kv == "f32":
+        assert rel_err(gk, rk) < 1e-5 and rel_err(gv, rv) < 1e-5
+    else:
+        assert rel_err(gk, rk.astype(np.float16).astype(np.float32)) < 2e-3
+        assert rel_err(gv, rv.astype(np.float16).astype(np.float32)) < 2e-3
+    # the cache now holds T rows: a second prefill is refused (decoder_layer.cpp:416-418)
+    with pytest.raises(mmr.InvalidArgument, match="empty KV cache"):
+        lw.prefill(cache, x, 0, T, y, ws)
+    # decode continues from the prefilled cache: position T attends rows 0..T
+    pos = mmr.DeviceArray.from_numpy(np.array([T], np.int32))
+    err = mmr.DeviceArray(1, np.int32, zero=True)
+    xd, yd = mmr.DeviceArray.from_numpy(h1), mmr.DeviceArray(H, np.float32)
+    dws = mmr.DeviceArray(lw.workspace_size(4), np.uint8)
+    lw.forward(cache, xd, pos, yd, dws, 4, err)
+    assert rel_err(yd.numpy(), want_next) < TOL
+    assert int(err.numpy()[0]) == 0
+
+
+def test_minimind2_prefill_layer_in_place_rope_offset_and_capture(mm2):
+    # start_position shifts only the rotation (rows still go to cache rows
+    # 0..T-1); out may alias hidden_seq; the call replays from a hipGraph
+    # after the cache is reset, with the same bits every replay
+    mmr, oracle, g, d, model, ref = mm2
+    c = g["config"]
+    H, D, Hkv = c["hidden_size"], c["head_dim"], c["num_key_value_heads"]
+    layer, T, start = 2, 40, 300
+    lw = mmr.LayerWeights.of_model(model, layer)
+    hs = np.random.default_rng(41).standard_normal((T, H)).astype(np.float32)
+    want, _, _ = prefill_reference(ref, layer, hs, start, np.zeros(H, np.float32))
+    cache = mmr.KvCache(Hkv, D, 64, mmr.KV_F16)
+    ws = mmr.DeviceArray(lw.prefill_workspace_size(T), np.uint8)
+    x = mmr.DeviceArray.from_numpy(hs.reshape(-1))
+    lw.prefill(cache, x, start, T, x, ws)  # in place
+    first = x.numpy().reshape(T, H)
+    assert rel_err(first, want) < TOL
+    stream = mmr.Stream()
+    cache.reset()
+    x.upload(hs.reshape(-1))
+    xin = mmr.DeviceArray.from_numpy(hs.reshape(-1))
+    with mmr.Graph(stream) as graph:
+        lw.prefill(cache, xin, start, T, x, ws, stream=stream)
+    for _ in range(3):
+        graph.launch()
+        stream.synchronize()
+        np.testing.assert_array_equal(x.numpy().reshape(T, H), first)
+    with pytest.raises(mmr.LengthError, match="not backed"):
+        short = mmr.KvCache(Hkv, D, 4096, mmr.KV_F16, reserve=False)  # 512 rows backed
+        lw.prefill(short, mmr.DeviceArray(600 * H, np.float32), 0, 600, mmr.DeviceArray(600 * H, np.float32),
+                   mmr.DeviceArray(lw.prefill_workspace_size(600), np.uint8))

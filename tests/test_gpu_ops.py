@@ -178,7 +178,7 @@ def test_qkv_postprocess_and_append(gpu, oracle, d):
     assert rel_err(keys[:, tokens - 1, :].reshape(-1), k_ref) < 1e-5
     np.testing.assert_array_equal(vals[:, tokens - 1, :].reshape(-1), qkv[(hq + hkv) * d:])
     assert not keys[:, tokens:, :].any() and not keys[:, : tokens - 1, :].any()
-    assert cache.rows % 32 == 0 and cache.rows >= 16
+    assert cache.rows == 16 and cache.device_bytes == 2 * hkv * 64 * d * 4  # one 64-token page of K and of V
 
 
 @pytest.mark.parametrize("d", [32, 64, 96, 128])
