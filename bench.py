@@ -16,10 +16,11 @@ decode step (one token); `value` is decode tok/s = steps / time of the steps,
 measured with HIP events on the decode stream between two device syncs.
 
 The same line carries
-  * roofline: the dominant kernel (gate_up GEMV + SwiGLU) launched alone
-    `--kernel-reps` times over the 16 layers' weights as one hipGraph chain
-    (eager launches with --no-graph), timed with HIP events on the stream it
-    runs on; achieved = algorithmic bytes / average time per launch;
+  * roofline: the kernel with the largest share of the step (decode
+    attention at these contexts; gate_up and lm_head under `secondary`)
+    launched alone `--kernel-reps` times over the 16 layers as one hipGraph
+    chain (eager launches with --no-graph), timed with HIP events on the
+    stream it runs on; achieved = algorithmic bytes / average time per launch;
   * kernels: the same measurement for every kernel of the step;
   * gemv_sweep / attention_sweep: BASELINE configs[1] GEMV shapes and
     configs[2] attention contexts alone through the C ABI, MALL-resident and
@@ -35,9 +36,9 @@ The same line carries
   * copy_probe: a device-to-device copy of --copy-probe-mib MiB (HIP's blit
     kernel), the achievable-bandwidth yardstick and the calibration dispatch
     of the FETCH_SIZE / WRITE_SIZE counter runs;
-  * roofline.traffic: L2-to-memory bytes per launch of the dominant kernel from
-    the committed counter summary (profiles/gemv_gate_up_minimind2_traffic.md),
-    null when that file is absent;
+  * roofline.traffic: L2-to-memory bytes per launch of the roofline kernel
+    from its committed counter summary (profiles/*_traffic.md, written from
+    `bench.py --traffic-probe` runs), null when that file is absent;
   * cpu_baseline: the reference's own CPU path (oracle/_ref/ref_driver, built
     from the unmodified reference sources) on a bounded sample on this host.
 
@@ -116,24 +117,25 @@ GEMV_SHAPES = [("qkv", 1152, 768), ("o", 768, 768), ("gate_up", 4096, 768), ("do
 
 
 def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
-    """BASELINE configs[1] shapes through the C ABI (mmr_matvec_f16 and
-    mmr_matvec_argmax_f16), each timed over rotated weight copies: `mall` keeps
-    the rotation at <= 160 MiB (resident in the 256 MB Infinity Cache), `hbm`
-    at >= 640 MiB (every launch streams from HBM).  GB/s = algorithmic bytes
-    (W fp16 + x fp32 + y fp32, or the int32 token for argmax) / mean launch time
-    of `reps` launches replayed as one hipGraph chain."""
+    """BASELINE configs[1] shapes with its input format (x fp16 [K] ~ N(0,1))
+    through the C ABI (mmr_matvec_f16x and mmr_matvec_argmax_f16x), each timed
+    over rotated weight copies: `mall` keeps the rotation at <= 160 MiB
+    (resident in the 256 MB Infinity Cache), `hbm` at >= 640 MiB (every launch
+    streams from HBM).  GB/s = algorithmic bytes (W fp16 + x fp16 + y fp32, or
+    the int32 token for argmax: the per-shape bytes of the configs[1] table) /
+    mean launch time of `reps` launches replayed as one hipGraph chain."""
     lib = mmr.lib()
     out = {}
     rng = np.random.default_rng(7)
     for name, n, k in GEMV_SHAPES:
-        x = mmr.DeviceArray.from_numpy(rng.standard_normal(k).astype(np.float32))
+        x = mmr.DeviceArray.from_numpy(rng.standard_normal(k).astype(np.float16).view(np.uint16))
         y = mmr.DeviceArray(n, np.float32)
         tok = mmr.DeviceArray(1, np.int32)
         ws_bytes = mmr.matvec_argmax_workspace_size(n, k)
         ws = mmr.DeviceArray(max(ws_bytes, 1), np.uint8)
         wbytes = n * k * 2
         argmax = name.endswith("argmax")
-        alg = wbytes + k * 4 + (4 if argmax else n * 4)
+        alg = wbytes + k * 2 + (4 if argmax else n * 4)
         res = {"rows": n, "cols": k, "bytes": alg}
         for label, budget in (("mall", 160 << 20), ("hbm", 640 << 20)):
             copies = max(2, budget // wbytes) if label == "mall" else max(2, -(-budget // wbytes))
@@ -142,10 +144,10 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
             def launch(i):
                 w = big.ptr + (i % copies) * wbytes
                 if argmax:
-                    mmr.check(lib.mmr_matvec_argmax_f16(w, n, k, x.ptr, None, 0.0, None, tok.ptr, ws.ptr, ws_bytes,
-                                                        stream.handle))
+                    mmr.check(lib.mmr_matvec_argmax_f16x(w, n, k, x.ptr, None, tok.ptr, ws.ptr, ws_bytes,
+                                                         stream.handle))
                 else:
-                    mmr.check(lib.mmr_matvec_f16(w, n, k, x.ptr, None, y.ptr, stream.handle))
+                    mmr.check(lib.mmr_matvec_f16x(w, n, k, x.ptr, None, y.ptr, stream.handle))
 
             for i in range(copies):
                 launch(i)
@@ -386,7 +388,7 @@ def host_cpu() -> dict:
     return {"cpu_model": model, "cores_available": avail, "cores_online": os.cpu_count()}
 
 
-def cpu_baseline(mmr, cfg, prompt, sample_steps: int) -> dict | None:
+def cpu_baseline(mmr, cfg, prompt, sample_steps: int, gpu_steps: int) -> dict | None:
     """The reference CPU path (oracle/_ref/ref_driver, the unmodified reference
     sources; single-threaded as shipped) at the GPU line's context: the same
     512-token prompt fed token by token (the reference's CPU prefill,
@@ -424,7 +426,7 @@ def cpu_baseline(mmr, cfg, prompt, sample_steps: int) -> dict | None:
         "prompt_tok_s": round(out["prefill_tokens"] / out["prefill_seconds"], 3),
         "sample": f"MiniMind2, the GPU line's weights and 512-token prompt, fed token by token "
                   f"({out['prefill_seconds']:.1f} s), then {n} greedy decode steps at positions {P}..{P + n} "
-                  f"(the GPU line decodes {P}..{P + 256}); reference CPU path, one thread pinned to one core",
+                  f"(the GPU line decodes {P}..{P + gpu_steps}); reference CPU path, one thread pinned to one core",
     }
 
 
@@ -631,7 +633,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(mmr, cfg, prompt, args.cpu_sample_steps)
+        cpu = cpu_baseline(mmr, cfg, prompt, args.cpu_sample_steps, args.steps)
 
     line = {
         "metric": METRIC,

@@ -125,6 +125,10 @@ int mmr_matvec_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x
 int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
                       int prologue, int epilogue, const float* residual, float* y, int lanes_per_row,
                       int rows_per_group, mmr_stream_t stream);
+/* BASELINE configs[1]'s input format: x fp16 [cols] on the device (widened
+ * exactly to fp32 in the kernel), otherwise as mmr_matvec_f16. */
+int mmr_matvec_f16x(const uint16_t* w, int64_t rows, int64_t cols, const uint16_t* x, const float* residual, float* y,
+                    mmr_stream_t stream);
 
 /* ---- lm_head matvec + argmax: device_matmul_argmax (ascend_matmul.h:108-109,
  *      ascend_matmul.cpp:467-502) / cube_matvec_argmax (ascend_matmul.h:127-130).
@@ -137,6 +141,9 @@ size_t mmr_matvec_argmax_workspace_size(int64_t rows, int64_t cols);
 int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
                           float* logits, int32_t* token_out, void* workspace, size_t workspace_bytes,
                           mmr_stream_t stream);
+/* The same with x fp16 [cols] (configs[1]'s lm_head + argmax shape), no norm. */
+int mmr_matvec_argmax_f16x(const uint16_t* w, int64_t rows, int64_t cols, const uint16_t* x, float* logits,
+                           int32_t* token_out, void* workspace, size_t workspace_bytes, mmr_stream_t stream);
 
 /* ---- RoPE table: cached_rope_table (ascend_custom_ops.cpp:93-123).  Holds
  * the fp32 frequencies inv_freq[i] = 1 / powf(theta, 2i / d) of the CPU

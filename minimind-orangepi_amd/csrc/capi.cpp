@@ -313,12 +313,14 @@ int mmr_matvec_f16(const uint16_t* w, int64_t rows, int64_t cols, const float* x
                            residual ? MMR_EPI_RESIDUAL : MMR_EPI_STORE, residual, y, 0, 0, stream);
 }
 
-int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
-                      int prologue, int epilogue, const float* residual, float* y, int lanes_per_row,
-                      int rows_per_group, mmr_stream_t stream) {
-  return guarded([&] {
+namespace {
+
+// The GEMV entry points with x in fp32 (x) or fp16 (xh); exactly one is set.
+void enqueue_matvec(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const uint16_t* xh,
+                    const float* norm_w, float eps, int prologue, int epilogue, const float* residual, float* y,
+                    int lanes_per_row, int rows_per_group, mmr_stream_t stream) {
     check_matvec_shape(rows, cols);
-    require(w && x && y, "null buffer");
+    require(w && (x || xh) && y, "null buffer");
     require(prologue >= MMR_PRO_PLAIN && prologue <= MMR_PRO_RMSNORM_FINAL, "unknown prologue");
     require(epilogue >= MMR_EPI_STORE && epilogue <= MMR_EPI_SWIGLU, "unknown epilogue");
     require(prologue == MMR_PRO_PLAIN || norm_w, "RMSNorm prologue needs norm_w");
@@ -333,6 +335,7 @@ int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float
     a.rows = static_cast<int>(rows);
     a.k = static_cast<int>(cols);
     a.x = x;
+    a.x_half = reinterpret_cast<const __half*>(xh);
     a.norm_w = norm_w;
     a.eps = eps;
     a.y = y;
@@ -340,6 +343,57 @@ int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float
     hip(mmr::launch_gemv(a, static_cast<mmr::GemvPrologue>(prologue), static_cast<mmr::GemvEpilogue>(epilogue), plan,
                          as_stream(stream)),
         "matvec launch");
+}
+
+void enqueue_matvec_argmax(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const uint16_t* xh,
+                           const float* norm_w, float eps, float* logits, int32_t* token_out, void* workspace,
+                           size_t workspace_bytes, mmr_stream_t stream) {
+  check_matvec_shape(rows, cols);
+  require(w && (x || xh) && token_out && workspace, "null buffer");
+  mmr::GemvPlan plan;
+  require(mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), mmr::kEpiArgmax, 0, 0, &plan),
+          "unsupported shape");
+  require(workspace_bytes >= argmax_ws_bytes(plan), "workspace too small");
+  char* ws = static_cast<char*>(workspace);
+  mmr::GemvArgs a;
+  a.w = reinterpret_cast<const __half*>(w);
+  a.rows = static_cast<int>(rows);
+  a.k = static_cast<int>(cols);
+  a.x = x;
+  a.x_half = reinterpret_cast<const __half*>(xh);
+  a.norm_w = norm_w;
+  a.eps = eps;
+  a.y = logits;
+  a.part_val = reinterpret_cast<float*>(ws);
+  a.part_idx = reinterpret_cast<int*>(ws + static_cast<size_t>(plan.blocks) * 4);
+  hip(mmr::launch_gemv(a, norm_w ? mmr::kProRmsNormFinal : mmr::kProPlain, mmr::kEpiArgmax, plan, as_stream(stream)),
+      "matvec argmax launch");
+  mmr::ArgmaxFinalizeArgs f;
+  f.part_val = a.part_val;
+  f.part_idx = a.part_idx;
+  f.parts = plan.blocks;
+  f.token_out = token_out;
+  hip(mmr::launch_argmax_finalize(f, as_stream(stream)), "argmax finalize launch");
+}
+
+}  // namespace
+
+int mmr_matvec_f16_ex(const uint16_t* w, int64_t rows, int64_t cols, const float* x, const float* norm_w, float eps,
+                      int prologue, int epilogue, const float* residual, float* y, int lanes_per_row,
+                      int rows_per_group, mmr_stream_t stream) {
+  return guarded([&] {
+    require(x, "null buffer");
+    enqueue_matvec(w, rows, cols, x, nullptr, norm_w, eps, prologue, epilogue, residual, y, lanes_per_row,
+                   rows_per_group, stream);
+  });
+}
+
+int mmr_matvec_f16x(const uint16_t* w, int64_t rows, int64_t cols, const uint16_t* x, const float* residual, float* y,
+                    mmr_stream_t stream) {
+  return guarded([&] {
+    require(x, "null buffer");
+    enqueue_matvec(w, rows, cols, nullptr, x, nullptr, 0.0f, MMR_PRO_PLAIN, residual ? MMR_EPI_RESIDUAL : MMR_EPI_STORE,
+                   residual, y, 0, 0, stream);
   });
 }
 
@@ -355,32 +409,18 @@ int mmr_matvec_argmax_f16(const uint16_t* w, int64_t rows, int64_t cols, const f
                           float* logits, int32_t* token_out, void* workspace, size_t workspace_bytes,
                           mmr_stream_t stream) {
   return guarded([&] {
-    check_matvec_shape(rows, cols);
-    require(w && x && token_out && workspace, "null buffer");
-    mmr::GemvPlan plan;
-    require(mmr::gemv_plan(static_cast<int>(rows), static_cast<int>(cols), mmr::kEpiArgmax, 0, 0, &plan),
-            "unsupported shape");
-    require(workspace_bytes >= argmax_ws_bytes(plan), "workspace too small");
-    char* ws = static_cast<char*>(workspace);
-    mmr::GemvArgs a;
-    a.w = reinterpret_cast<const __half*>(w);
-    a.rows = static_cast<int>(rows);
-    a.k = static_cast<int>(cols);
-    a.x = x;
-    a.norm_w = norm_w;
-    a.eps = eps;
-    a.y = logits;
-    a.part_val = reinterpret_cast<float*>(ws);
-    a.part_idx = reinterpret_cast<int*>(ws + static_cast<size_t>(plan.blocks) * 4);
-    hip(mmr::launch_gemv(a, norm_w ? mmr::kProRmsNormFinal : mmr::kProPlain, mmr::kEpiArgmax, plan,
-                         as_stream(stream)),
-        "matvec argmax launch");
-    mmr::ArgmaxFinalizeArgs f;
-    f.part_val = a.part_val;
-    f.part_idx = a.part_idx;
-    f.parts = plan.blocks;
-    f.token_out = token_out;
-    hip(mmr::launch_argmax_finalize(f, as_stream(stream)), "argmax finalize launch");
+    require(x, "null buffer");
+    enqueue_matvec_argmax(w, rows, cols, x, nullptr, norm_w, eps, logits, token_out, workspace, workspace_bytes,
+                          stream);
+  });
+}
+
+int mmr_matvec_argmax_f16x(const uint16_t* w, int64_t rows, int64_t cols, const uint16_t* x, float* logits,
+                           int32_t* token_out, void* workspace, size_t workspace_bytes, mmr_stream_t stream) {
+  return guarded([&] {
+    require(x, "null buffer");
+    enqueue_matvec_argmax(w, rows, cols, nullptr, x, nullptr, 0.0f, logits, token_out, workspace, workspace_bytes,
+                          stream);
   });
 }
 

@@ -244,6 +244,21 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
       xv[i][0] = in ? lo.x : 0.0f; xv[i][1] = in ? lo.y : 0.0f; xv[i][2] = in ? lo.z : 0.0f; xv[i][3] = in ? lo.w : 0.0f;
       xv[i][4] = in ? hi.x : 0.0f; xv[i][5] = in ? hi.y : 0.0f; xv[i][6] = in ? hi.z : 0.0f; xv[i][7] = in ? hi.w : 0.0f;
     }
+  } else if (a.x_half != nullptr) {
+    // fp16 x (BASELINE configs[1]'s input format): one 16-byte chunk per 8
+    // elements, widened exactly to fp32 after the weight loads are out.
+    uint4 xr[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) xr[i] = reinterpret_cast<const uint4*>(a.x_half)[min(lane + G * i, kchunks - 1)];
+    load_weights();
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) half8_to_float8(xr[i], xv[i]);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i)
+      if (lane + G * i >= kchunks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
+      }
   } else {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {

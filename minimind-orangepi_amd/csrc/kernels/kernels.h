@@ -74,6 +74,7 @@ struct GemvArgs {
   int rows = 0;
   int k = 0;
   const float* x = nullptr;
+  const __half* x_half = nullptr;  // instead of x: fp16 activations (plain and RMSNorm prologues)
   const float* norm_w = nullptr;
   float eps = 0.0f;
   // kProEmbedRmsNorm

@@ -107,6 +107,8 @@ _SIGS = {
     "mmr_f16_to_f32": ([VP, VP, SZ], C.c_int),
     "mmr_matvec_f16": ([VP, I64, I64, VP, VP, VP, VP], C.c_int),
     "mmr_matvec_f16_ex": ([VP, I64, I64, VP, VP, F32, C.c_int, C.c_int, VP, VP, C.c_int, C.c_int, VP], C.c_int),
+    "mmr_matvec_f16x": ([VP, I64, I64, VP, VP, VP, VP], C.c_int),
+    "mmr_matvec_argmax_f16x": ([VP, I64, I64, VP, VP, VP, VP, SZ, VP], C.c_int),
     "mmr_matvec_argmax_workspace_size": ([I64, I64], SZ),
     "mmr_matvec_argmax_f16": ([VP, I64, I64, VP, VP, F32, VP, VP, VP, SZ, VP], C.c_int),
     "mmr_rope_table_create": ([I64, I64, F32, C.POINTER(VP)], C.c_int),
@@ -409,6 +411,18 @@ def matvec_f16_ex(w, rows, cols, x, y, *, norm_w=None, eps=0.0, prologue=PRO_PLA
                   residual=None, lanes_per_row=0, rows_per_group=0, stream=None) -> None:
     check(_lib.mmr_matvec_f16_ex(w.ptr, rows, cols, x.ptr, norm_w.ptr if norm_w else None, eps, prologue, epilogue,
                                  residual.ptr if residual else None, y.ptr, lanes_per_row, rows_per_group, _s(stream)))
+
+
+def matvec_f16x(w: DeviceArray, rows: int, cols: int, x: DeviceArray, y: DeviceArray,
+                residual: DeviceArray | None = None, stream=None) -> None:
+    """mmr_matvec_f16x: x fp16 (uint16 bits) [cols]."""
+    check(_lib.mmr_matvec_f16x(w.ptr, rows, cols, x.ptr, residual.ptr if residual else None, y.ptr, _s(stream)))
+
+
+def matvec_argmax_f16x(w, rows, cols, x, token_out, workspace, *, logits=None, stream=None) -> None:
+    """mmr_matvec_argmax_f16x: x fp16 (uint16 bits) [cols]."""
+    check(_lib.mmr_matvec_argmax_f16x(w.ptr, rows, cols, x.ptr, logits.ptr if logits else None, token_out.ptr,
+                                      workspace.ptr, workspace.nbytes, _s(stream)))
 
 
 def matvec_argmax_workspace_size(rows: int, cols: int) -> int:

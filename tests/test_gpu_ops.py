@@ -38,6 +38,16 @@ def test_matvec_matches_oracle(gpu, oracle, rows, cols):
     mmr.matvec_f16(dw, rows, cols, dx, dy)
     ref = oracle.matvec(w32, x)
     assert rel_err(dy.numpy(), ref) < TOL
+    # configs[1]'s fp16 x: widened exactly, the same products and sums, the same bits
+    dxh = mmr.DeviceArray.from_numpy(x.astype(np.float16).view(np.uint16))
+    dyh = mmr.DeviceArray(rows, np.float32)
+    mmr.matvec_f16x(dw, rows, cols, dxh, dyh)
+    np.testing.assert_array_equal(dyh.numpy(), dy.numpy())
+    ws = mmr.DeviceArray(mmr.matvec_argmax_workspace_size(rows, cols), np.uint8)
+    tok, lg = mmr.DeviceArray(1, np.int32), mmr.DeviceArray(rows, np.float32)
+    mmr.matvec_argmax_f16x(dw, rows, cols, dxh, tok, ws, logits=lg)
+    np.testing.assert_array_equal(lg.numpy(), dy.numpy())
+    assert int(tok.numpy()[0]) == oracle.argmax(dy.numpy())
     # residual epilogue (device_matmul_add)
     res = rng.standard_normal(rows).astype(np.float32)
     dr = mmr.DeviceArray.from_numpy(res)
