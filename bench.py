@@ -106,11 +106,14 @@ KERNEL_LABELS = {
     "lm_head": "gemv lm_head (6400x768 fp16, final RMSNorm prologue, argmax partials)",
     "finalize": "argmax finalize",
 }
-# Committed FETCH_SIZE / WRITE_SIZE summaries (bench.py --traffic-probe) per kernel.
-TRAFFIC_FILES = {
-    "gate_up": "profiles/gemv_gate_up_minimind2_traffic.md",
-    "attention": "profiles/attention_minimind2_768keys_traffic.md",
-}
+# Committed FETCH_SIZE / WRITE_SIZE summary of every step kernel (from
+# `bench.py --traffic-probe N --traffic-kernel layer` at KERNEL_CONTEXT keys):
+# one `traffic_bytes_per_launch[<kernel>]: <bytes>` line per kernel.
+TRAFFIC_FILE = "profiles/decode_step_kernels_minimind2_768keys_traffic.md"
+
+# Context of the per-kernel timings, the roofline and the counter probes: the
+# end of configs[3]'s decode (512-token prompt + 256 steps), whatever --steps.
+KERNEL_CONTEXT = PROMPT_LEN + 256
 
 GEMV_SHAPES = [("qkv", 1152, 768), ("o", 768, 768), ("gate_up", 4096, 768), ("down", 768, 2048),
                ("lm_head_argmax", 6400, 768)]
@@ -280,6 +283,30 @@ def decode_context_sweep(mmr, model, kv, steps: int = 64) -> dict:
     return out
 
 
+def context_probe(mmr, context: int, steps: int, kv) -> int:
+    """Workload of the long-context kernel-trace profiles: MiniMind2 with the
+    bench's synthetic weights, a uniform prompt of `context` tokens (chunked
+    GEMM prefill), then `steps` decode steps.  With --no-graph every step's
+    kernels are launched one by one, which is what rocprofv3's kernel trace
+    can follow on this image."""
+    cfg = mmr.make_config(**MINIMIND2)
+    model = mmr.Model.synthetic(cfg, 0, 0.02, True)
+    prompt = mmr.synthesize_prompt(1, context, MINIMIND2["vocab_size"]).tolist()
+    st = model.make_state(context + steps + 8, kv)
+    st.enqueue_prefill(prompt)
+    st.synchronize()
+    ev = [mmr.Event() for _ in range(2)]
+    ev[0].record(st.stream)
+    st.enqueue_decode(steps)
+    ev[1].record(st.stream)
+    st.synchronize()
+    ms = ev[0].elapsed_ms(ev[1])
+    print(json.dumps({"context_probe": {"context": context, "steps": steps, "us_per_step": round(ms * 1e3 / steps, 1),
+                                        "launch_mode": "eager" if os.environ.get("MMR_NO_GRAPH") else "hipGraph"}}),
+          flush=True)
+    return 0
+
+
 def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
     """Workload of the FETCH_SIZE / WRITE_SIZE counter runs: one kernel of the
     decode step launched alone, eagerly (rocprofv3's counter collection is
@@ -295,9 +322,49 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
     layers of a step."""
     H, F, layers = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"], MINIMIND2["num_hidden_layers"]
     rng = np.random.default_rng(3)
-    if kernel == "attention":
+    if kernel == "layer":
+        # Every kernel of the decode step's layers as the step launches them,
+        # through mmr_decoder_layer_forward (qkv GEMV + RMSNorm, fused
+        # attention at KERNEL_CONTEXT keys over an fp16 cache with 16 splits,
+        # O GEMV with the split-combine prologue + residual, gate_up + SwiGLU,
+        # down + residual: the step's launch plans) over the 16 layers of a
+        # MiniMind2 model, one layer per call; then the lm_head GEMV with the
+        # final RMSNorm and argmax partials (+ finalize), 16 times.  The step's
+        # attention launch also carries L2-warming blocks; this one does not.
+        cfg = mmr.make_config(**MINIMIND2)
+        model = mmr.Model.synthetic(cfg, 0, 0.02, True)
+        hkv, d, V = MINIMIND2["num_key_value_heads"], MINIMIND2["head_dim"], MINIMIND2["vocab_size"]
+        n_keys = KERNEL_CONTEXT
+        splits = 16  # the decode step's split bucket at 768 keys
+        views = [mmr.LayerWeights.of_model(model, l) for l in range(layers)]
+        caches = []
+        for _ in range(layers):
+            c = mmr.KvCache(hkv, d, n_keys, mmr.KV_F16)
+            c.upload(rng.standard_normal((hkv, n_keys, d)).astype(np.float16),
+                     rng.standard_normal((hkv, n_keys, d)).astype(np.float16))
+            caches.append(c)
+        x = mmr.DeviceArray.from_numpy(rng.standard_normal(H).astype(np.float32))
+        y = mmr.DeviceArray(H, np.float32)
+        pos = mmr.DeviceArray.from_numpy(np.array([n_keys - 1], np.int32))
+        err = mmr.DeviceArray(1, np.int32, zero=True)
+        ws = mmr.DeviceArray(views[0].workspace_size(splits), np.uint8)
+        lm = mmr.DeviceArray.from_numpy(
+            (rng.standard_normal((V, H)) * 0.02).astype(np.float16).reshape(-1).view(np.uint16))
+        fnorm = mmr.DeviceArray.from_numpy(np.ones(H, np.float32))
+        tok = mmr.DeviceArray(1, np.int32)
+        lws = mmr.DeviceArray(mmr.matvec_argmax_workspace_size(V, H), np.uint8)
+        stream = mmr.Stream()
+        for i in range(launches):
+            views[i % layers].forward(caches[i % layers], x, pos, y, ws, splits, err, stream=stream)
+        for i in range(layers):
+            mmr.matvec_argmax_f16(lm, V, H, y, tok, lws, norm_w=fnorm, eps=MINIMIND2["rms_norm_eps"], stream=stream)
+        stream.synchronize()
+        assert int(err.numpy()[0]) == 0
+        alg = {name: kernel_bytes(MINIMIND2, name, n_keys, 2) for name in ("qkv", "attention", "o", "gate_up", "down",
+                                                                          "lm_head")}
+    elif kernel == "attention":
         hq, hkv, d = MINIMIND2["num_attention_heads"], MINIMIND2["num_key_value_heads"], MINIMIND2["head_dim"]
-        n_keys = PROMPT_LEN + 256
+        n_keys = KERNEL_CONTEXT
         caches = []
         for _ in range(layers):
             c = mmr.KvCache(hkv, d, n_keys, mmr.KV_F16)
@@ -449,7 +516,10 @@ def main() -> int:
     ap.add_argument("--batch-context", type=int, default=4096)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
                     help="run only the counter-run workload (kernel launches + one copy) and exit")
-    ap.add_argument("--traffic-kernel", choices=["attention", "gate_up"], default="attention")
+    ap.add_argument("--traffic-kernel", choices=["layer", "attention", "gate_up"], default="layer")
+    ap.add_argument("--context-probe", type=int, default=0, metavar="TOKENS",
+                    help="run only a prefill of TOKENS prompt tokens + --context-probe-steps decode steps and exit")
+    ap.add_argument("--context-probe-steps", type=int, default=24)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -469,6 +539,9 @@ def main() -> int:
 
     if args.traffic_probe > 0:
         return traffic_probe(mmr, args.traffic_probe, max(args.copy_probe_mib, 1), args.traffic_kernel)
+    if args.context_probe > 0:
+        return context_probe(mmr, args.context_probe, args.context_probe_steps,
+                             mmr.KV_F16 if args.kv == "f16" else mmr.KV_F32)
 
     if mmr.device_count() < 1:
         print("no HIP device visible", file=sys.stderr)
@@ -512,19 +585,21 @@ def main() -> int:
         parity = bool(generated[:n] == ref_tokens[:n])
         log(f"tokens vs reference CPU path: {'identical' if parity else 'DIFFERENT'} over {n} tokens")
 
-    # Per-kernel timing: each kernel launched alone, cycling over the 16 layers.
-    n_keys = PROMPT_LEN + args.steps
+    # Per-kernel timing: each kernel launched alone, cycling over the 16
+    # layers, at KERNEL_CONTEXT keys (the context of configs[3]'s last step and
+    # of the committed counter probes), whatever --steps.
+    n_keys = KERNEL_CONTEXT
     kv_bytes = 2 if kv == mmr.KV_F16 else 4
     kernels = {}
     names = ["qkv", "attention", "o", "gate_up", "down", "lm_head", "finalize"]
-    state.reset()
-    state.enqueue_prefill(prompt)
-    state.enqueue_decode(args.steps - 1)
-    state.synchronize()
+    kstate = model.make_state(KERNEL_CONTEXT + 8, kv)
+    kstate.enqueue_prefill(prompt)
+    kstate.enqueue_decode(KERNEL_CONTEXT - PROMPT_LEN - 1)
+    kstate.synchronize()
     for kid, name in enumerate(names):
         # kernel_reps launches as one hipGraph chain (eager with --no-graph),
         # timed with HIP events on the decode stream
-        avg_us = state.time_step_kernel(kid, 0, args.kernel_reps)
+        avg_us = kstate.time_step_kernel(kid, 0, args.kernel_reps)
         b = kernel_bytes(MINIMIND2, name, n_keys, kv_bytes)
         kernels[name] = {"avg_us": round(avg_us, 3), "bytes": b, "gbs": round(b / (avg_us * 1e-6) / 1e9, 1)}
         if name == "attention":
@@ -539,10 +614,10 @@ def main() -> int:
     warm_bytes = 2 * (c["hidden_size"] * c["num_attention_heads"] * c["head_dim"] +
                       3 * c["hidden_size"] * c["intermediate_size"])
     os.environ["MMR_L2_WARM_BLOCKS"] = "0"
-    cold = model.make_state(PROMPT_LEN + args.steps + 8, kv)
+    cold = model.make_state(KERNEL_CONTEXT + 8, kv)
     del os.environ["MMR_L2_WARM_BLOCKS"]
     cold.enqueue_prefill(prompt)
-    cold.enqueue_decode(args.steps - 1)
+    cold.enqueue_decode(KERNEL_CONTEXT - PROMPT_LEN - 1)
     cold.synchronize()
     a = kernels["attention"]
     a["avg_us_without_warm_blocks"] = round(cold.time_step_kernel(names.index("attention"), 0, args.kernel_reps), 3)
@@ -551,7 +626,7 @@ def main() -> int:
                       "gate_up and down weights into the L2s of the XCDs that read them next; "
                       "avg_us_without_warm_blocks is the attention work alone")
     log(f"kernel attention without warming blocks {a['avg_us_without_warm_blocks']:.3f} us")
-    del cold
+    del cold, kstate
     per_step_us = sum(kernels[n]["avg_us"] for n in names[:5]) * MINIMIND2["num_hidden_layers"] + \
         kernels["lm_head"]["avg_us"] + kernels["finalize"]["avg_us"]
     step_bytes = sum(kernels[n]["bytes"] for n in names[:5]) * MINIMIND2["num_hidden_layers"] + \
@@ -612,14 +687,16 @@ def main() -> int:
     def roofline_of(name: str) -> dict:
         """HBM roofline entry of one step kernel; traffic (L2-to-memory bytes
         per launch) from its committed counter summary, null without one."""
-        traffic, tsrc = None, TRAFFIC_FILES.get(name)
-        if tsrc and (ROOT / tsrc).exists():
-            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", (ROOT / tsrc).read_text())
+        traffic, tsrc = None, TRAFFIC_FILE
+        if (ROOT / tsrc).exists():
+            m = re.search(r"traffic_bytes_per_launch\[" + name + r"\]:\s*(\d+)", (ROOT / tsrc).read_text())
             traffic = int(m.group(1)) if m else None
         ach = kernels[name]["gbs"]
         return {"bound": "hbm", "kernel": KERNEL_LABELS[name], "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "traffic_source": tsrc if traffic is not None else None,
+                "traffic_over_algorithmic": round(traffic / kernels[name]["bytes"], 3) if traffic else None,
+                "context_keys": KERNEL_CONTEXT,
                 "bytes_per_launch": kernels[name]["bytes"], "avg_us": kernels[name]["avg_us"],
                 "us_per_step": kernels[name]["us_per_step"],
                 **{k: kernels[name][k] for k in ("avg_us_without_warm_blocks", "warm_bytes_per_launch")
@@ -629,7 +706,7 @@ def main() -> int:
                    if traffic is not None and "warm_bytes_per_launch" in kernels[name] else {})}
 
     roofline = roofline_of(dom)
-    roofline["secondary"] = {n: roofline_of(n) for n in ("gate_up", "attention", "lm_head") if n != dom}
+    roofline["secondary"] = {n: roofline_of(n) for n in names[:6] if n != dom}
 
     cpu = None
     if not args.no_cpu_baseline:
