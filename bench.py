@@ -317,7 +317,7 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
     step's launch plan: 32-lane groups, two rows per group) through the C ABI
     over a 16-copy weight rotation like the 16 layers of the step.
     attention: the decode step's attention kernel (q/k norm + RoPE + KV append
-    + split partials, attention_head_kernel at 768 keys, 16 splits, fp16 KV)
+    + split partials, attention_head_kernel at 768 keys, 12 splits, fp16 KV)
     through mmr_decode_attention_fused, cycling over 16 caches like the 16
     layers of a step."""
     H, F, layers = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"], MINIMIND2["num_hidden_layers"]
@@ -325,7 +325,7 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
     if kernel == "layer":
         # Every kernel of the decode step's layers as the step launches them,
         # through mmr_decoder_layer_forward (qkv GEMV + RMSNorm, fused
-        # attention at KERNEL_CONTEXT keys over an fp16 cache with 16 splits,
+        # attention at KERNEL_CONTEXT keys over an fp16 cache with 12 splits,
         # O GEMV with the split-combine prologue + residual, gate_up + SwiGLU,
         # down + residual: the step's launch plans) over the 16 layers of a
         # MiniMind2 model, one layer per call; then the lm_head GEMV with the
@@ -335,7 +335,7 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
         model = mmr.Model.synthetic(cfg, 0, 0.02, True)
         hkv, d, V = MINIMIND2["num_key_value_heads"], MINIMIND2["head_dim"], MINIMIND2["vocab_size"]
         n_keys = KERNEL_CONTEXT
-        splits = 16  # the decode step's split bucket at 768 keys
+        splits = 12  # the decode step's split count at 768 keys (12 tiles of 64)
         views = [mmr.LayerWeights.of_model(model, l) for l in range(layers)]
         caches = []
         for _ in range(layers):
@@ -376,7 +376,7 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
         ones = mmr.DeviceArray.from_numpy(np.ones(d, np.float32))
         pos = mmr.DeviceArray.from_numpy(np.array([n_keys - 1], np.int32))
         err = mmr.DeviceArray(1, np.int32, zero=True)
-        splits = 16  # the decode step's split bucket at 768 keys (64-token tiles)
+        splits = 12  # the decode step's split count at 768 keys (12 tiles of 64)
         ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, splits), np.uint8)
         out = mmr.DeviceArray(hq * d, np.float32)
         stream = mmr.Stream()

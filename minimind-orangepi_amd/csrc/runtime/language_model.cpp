@@ -96,9 +96,14 @@ struct DeviceState {
 
 namespace {
 
-// Attention split counts: the smallest bucket holding one tile per split is
-// used, so the step graph only changes at bucket boundaries.
-constexpr int kSplitBuckets[] = {8, 16, 32, 64, 128, 256, 512};
+// Attention split counts: the step graph is captured per split count, so the
+// count only changes at bucket boundaries, and one tile per split up to
+// kMaxSplits.  A split past the context's last tile still issues its
+// speculative first-tile load (the kernel reads the position after its loads
+// are out), so the buckets are kept close to the tile count: 8, 12, 16, then
+// multiples of 8 (of 16 past 128 tiles, of 32 past 256).  Measured with
+// FETCH_SIZE at 768 keys (12 tiles): 16 splits fetched 1.54x the K/V bytes,
+// 4 idle splits' loads being most of the excess.
 constexpr int kMaxSplits = 512;
 // Prompt tokens per prefill chunk (GEMM rows); longer prompts run in chunks.
 constexpr int64_t kPrefillChunk = 512;
@@ -119,9 +124,12 @@ constexpr int kGraphSteps = 8;
 
 int choose_splits(int64_t n_keys, int tile) {
   const int64_t n_tiles = (n_keys + tile - 1) / tile;
-  for (int s : kSplitBuckets)
-    if (s >= n_tiles || (n_tiles <= kPrologueTiles && s >= mmr::kCombineMaxSplits)) return s;
-  return kMaxSplits;
+  if (n_tiles <= 8) return 8;
+  if (n_tiles <= 12) return 12;
+  if (n_tiles <= kPrologueTiles) return mmr::kCombineMaxSplits;
+  if (n_tiles >= kMaxSplits) return kMaxSplits;
+  const int64_t step = n_tiles <= 128 ? 8 : (n_tiles <= 256 ? 16 : 32);
+  return static_cast<int>((n_tiles + step - 1) / step * step);
 }
 
 std::vector<uint16_t> to_half(const std::vector<float>& v) {

@@ -96,10 +96,10 @@ def test_state_backs_one_segment_and_grows_with_the_context(gpu, oracle, tmp_pat
     st.enqueue_prefill(prompt)
     st.synchronize()
     assert st.kv_backed() == (1024, seg_bytes(16))  # the prompt's 600 rows: segments 0 and 1
-    st.enqueue_decode(8)  # context 601..608: 10 tiles, the 16-split bucket, up to 24 tiles (1536)
+    st.enqueue_decode(8)  # context 601..608: 10 tiles, the 12-split bucket, up to 12 tiles (768)
     st.synchronize()
-    assert st.kv_backed() == (2048, seg_bytes(32))
-    st.enqueue_decode(1500)  # context past 2048 (33+ tiles): the 64-split bucket backs segment 3
+    assert st.kv_backed() == (1024, seg_bytes(16))
+    st.enqueue_decode(1500)  # context past 2048 (33+ tiles): the 40-split bucket reaches 2560, segment 3
     st.synchronize()
     assert st.kv_backed() == (4096, seg_bytes(64))
     got = st.read_sequence(600, 1509).tolist()
