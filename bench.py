@@ -119,14 +119,39 @@ GEMV_SHAPES = [("qkv", 1152, 768), ("o", 768, 768), ("gate_up", 4096, 768), ("do
                ("lm_head_argmax", 6400, 768)]
 
 
-def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
+def timed_chain(mmr, stream, ev, reps: int, launch, graph: bool) -> float:
+    """Mean us per launch of launch(0) .. launch(reps - 1): replayed as one
+    hipGraph chain (graph=True; host launch cost never paces them), or
+    launched one by one between the events (graph=False, what rocprofv3's
+    kernel trace can follow)."""
+    if graph:
+        with mmr.Graph(stream) as g:
+            for i in range(reps):
+                launch(i)
+        g.launch()
+        ev[0].record(stream)
+        g.launch()
+        ev[1].record(stream)
+        stream.synchronize()
+        g.free()
+    else:
+        ev[0].record(stream)
+        for i in range(reps):
+            launch(i)
+        ev[1].record(stream)
+        stream.synchronize()
+    return ev[0].elapsed_ms(ev[1]) * 1e3 / reps
+
+
+def gemv_sweep(mmr, stream, ev, reps: int = 256, graph: bool = True, labels=("mall", "hbm")) -> dict:
     """BASELINE configs[1] shapes with its input format (x fp16 [K] ~ N(0,1))
     through the C ABI (mmr_matvec_f16x and mmr_matvec_argmax_f16x), each timed
     over rotated weight copies: `mall` keeps the rotation at <= 160 MiB
     (resident in the 256 MB Infinity Cache), `hbm` at >= 640 MiB (every launch
     streams from HBM).  GB/s = algorithmic bytes (W fp16 + x fp16 + y fp32, or
     the int32 token for argmax: the per-shape bytes of the configs[1] table) /
-    mean launch time of `reps` launches replayed as one hipGraph chain."""
+    mean launch time of `reps` launches replayed as one hipGraph chain (eager
+    launches with graph=False: a host-paced rate, for the kernel trace)."""
     lib = mmr.lib()
     out = {}
     rng = np.random.default_rng(7)
@@ -140,7 +165,7 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
         argmax = name.endswith("argmax")
         alg = wbytes + k * 2 + (4 if argmax else n * 4)
         res = {"rows": n, "cols": k, "bytes": alg}
-        for label, budget in (("mall", 160 << 20), ("hbm", 640 << 20)):
+        for label, budget in [b for b in (("mall", 160 << 20), ("hbm", 640 << 20)) if b[0] in labels]:
             copies = max(2, budget // wbytes) if label == "mall" else max(2, -(-budget // wbytes))
             big = mmr.DeviceArray(copies * wbytes, np.uint8, zero=True)
 
@@ -154,22 +179,12 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
 
             for i in range(copies):
                 launch(i)
-            # the reps launches as one graph chain: host launch cost never paces them
-            with mmr.Graph(stream) as graph:
-                for i in range(reps):
-                    launch(i)
-            graph.launch()
-            ev[0].record(stream)
-            graph.launch()
-            ev[1].record(stream)
-            stream.synchronize()
-            graph.free()
-            us = ev[0].elapsed_ms(ev[1]) * 1e3 / reps
+            us = timed_chain(mmr, stream, ev, reps, launch, graph)
             res[label] = {"avg_us": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
                           "rotation_mib": round(copies * wbytes / 2**20, 1)}
             big.free()
-        log(f"gemv {name:15s} {n}x{k}: MALL {res['mall']['avg_us']:.3f} us {res['mall']['gbs']:.0f} GB/s | "
-            f"HBM {res['hbm']['avg_us']:.3f} us {res['hbm']['gbs']:.0f} GB/s")
+        log(f"gemv {name:15s} {n}x{k}: " + " | ".join(f"{lb} {res[lb]['avg_us']:.3f} us {res[lb]['gbs']:.0f} GB/s"
+                                                      for lb in labels))
         out[name] = res
     return out
 
@@ -177,7 +192,7 @@ def gemv_sweep(mmr, stream, ev, reps: int = 256) -> dict:
 ATTN_CONTEXTS = (128, 1024, 4096, 8192)
 
 
-def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
+def attention_sweep(mmr, stream, ev, reps: int = 200, graph: bool = True) -> dict:
     """decode attention over T cached tokens plus the new
     one (T + 1 keys), 8 q / 2 kv heads, d 96, fp16 K/V ~ N(0, 1), through the
     C ABI (mmr_attention_from_cache: attention kernel + log-sum-exp combine, split
@@ -208,17 +223,9 @@ def attention_sweep(mmr, stream, ev, reps: int = 200) -> dict:
                 caches.append(mmr.KvCache(hkv, d, n, mmr.KV_F16))  # zero-filled
             for i in range(copies):
                 mmr.attention_from_cache(q, caches[i], n, hq, hkv, d, o, ws, stream=stream)
-            # the reps calls as one graph chain: host launch cost never paces them
-            with mmr.Graph(stream) as graph:
-                for i in range(reps):
-                    mmr.attention_from_cache(q, caches[i % copies], n, hq, hkv, d, o, ws, stream=stream)
-            graph.launch()
-            ev[0].record(stream)
-            graph.launch()
-            ev[1].record(stream)
-            stream.synchronize()
-            graph.free()
-            us = ev[0].elapsed_ms(ev[1]) * 1e3 / reps
+            us = timed_chain(mmr, stream, ev, reps,
+                             lambda i: mmr.attention_from_cache(q, caches[i % copies], n, hq, hkv, d, o, ws,
+                                                                stream=stream), graph)
             res[label] = {"avg_us": round(us, 3), "gbs": round(alg / (us * 1e-6) / 1e9, 1),
                           "frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "caches": copies}
         log(f"attention T={T}: " + " | ".join(f"{k} {res[k]['avg_us']:.2f} us {res[k]['gbs']:.0f} GB/s"
@@ -520,6 +527,10 @@ def main() -> int:
     ap.add_argument("--context-probe", type=int, default=0, metavar="TOKENS",
                     help="run only a prefill of TOKENS prompt tokens + --context-probe-steps decode steps and exit")
     ap.add_argument("--context-probe-steps", type=int, default=24)
+    ap.add_argument("--batch-probe", action="store_true",
+                    help="run only the configs[4] batched decode (--batch, --batch-context), then exit")
+    ap.add_argument("--sweep-probe", action="store_true",
+                    help="run only the GEMV sweep (HBM rotation) and the attention sweep, then exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -539,6 +550,22 @@ def main() -> int:
 
     if args.traffic_probe > 0:
         return traffic_probe(mmr, args.traffic_probe, max(args.copy_probe_mib, 1), args.traffic_kernel)
+    if args.sweep_probe:
+        # configs[1] GEMV shapes over the HBM rotation and the configs[2]
+        # attention op, launched one by one (the kernel-trace workload)
+        stream = mmr.Stream()
+        ev = [mmr.Event() for _ in range(2)]
+        sweep = gemv_sweep(mmr, stream, ev, graph=not args.no_graph, labels=("hbm",))
+        attn = attention_sweep(mmr, stream, ev, graph=not args.no_graph)
+        print(json.dumps({"sweep_probe": {"launch_mode": "eager" if args.no_graph else "hipGraph",
+                                          "gemv_sweep": sweep, "attention_sweep": attn}}), flush=True)
+        return 0
+    if args.batch_probe:
+        # configs[4] alone: the batched leg of the default run (the kernel-trace workload with --no-graph)
+        model = mmr.Model.synthetic(mmr.make_config(**MINIMIND2), 0, 0.02, True)
+        res = batched_decode(mmr, model, max(args.batch, 1), 256, args.batch_context)
+        print(json.dumps({"batch_probe": res, "launch_mode": "eager" if args.no_graph else "hipGraph"}), flush=True)
+        return 0
     if args.context_probe > 0:
         return context_probe(mmr, args.context_probe, args.context_probe_steps,
                              mmr.KV_F16 if args.kv == "f16" else mmr.KV_F32)
@@ -677,8 +704,9 @@ def main() -> int:
     prefill_tok_s = PROMPT_LEN / (float(np.median(pf)) / 1e3)
     log(f"prefill: median of 8 runs {np.median(pf):.3f} ms -> {prefill_tok_s:.1f} tok/s")
 
-    sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev)
-    attn_sweep = None if args.no_attention_sweep else attention_sweep(mmr, mmr.Stream(stream), ev)
+    sweep = None if args.no_gemv_sweep else gemv_sweep(mmr, mmr.Stream(stream), ev, graph=not args.no_graph)
+    attn_sweep = None if args.no_attention_sweep else attention_sweep(mmr, mmr.Stream(stream), ev,
+                                                                      graph=not args.no_graph)
     ctx_sweep = None if args.no_context_sweep else decode_context_sweep(mmr, model, kv)
     other_kv = None if args.no_other_kv else other_kv_decode(mmr, model, prompt, args.steps,
                                                              "f32" if args.kv == "f16" else "f16")

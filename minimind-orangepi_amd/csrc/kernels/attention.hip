@@ -504,6 +504,354 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   }
 }
 
+// attention_mfma_kernel: attention_split_kernel's work (same grid, fused
+// prologue, KV append and split partials) with the scores and P.V on the fp16
+// matrix cores, for an fp16 cache and 64-token tiles (d = 32, 64, 96).  Wave w
+// of the block takes keys [16 w, 16 w + 16) of each of the block's tiles: it
+// stages them in its own LDS region as loaded (fp16, no conversion), so the
+// waves never wait for each other inside the tile loop, and keeps its own
+// online softmax; the waves merge at the end.  Per 16-key sub-tile:
+//  * S^T = K Q^T on v_mfma_f32_16x16x32_f16 with q split into fp16 hi + lo
+//    (two products): lane l holds S^T[key 4 (l / 16) + i][query l % 16], the
+//    queries being the group's R heads (columns past R hold zero q and are
+//    never written out);
+//  * O^T += V^T P^T on v_mfma_f32_16x16x16f16 with p split hi + lo: the lane
+//    already holds the P^T entries the B operand needs, and the V^T fragments
+//    come from one transposing LDS read (ds_read_b64_tr_b16) each.
+// The hi + lo splits make each product as exact as the fp32 path's; only the
+// order of the fp32 sums differs.  The split kernel stages every tile as fp32
+// and reads K once per head: the LDS traffic, not HBM, set its time on long
+// contexts.
+using f32x4 = float __attribute__((ext_vector_type(4)));
+using f16x8 = _Float16 __attribute__((ext_vector_type(8)));
+using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+using i16x4 = short __attribute__((ext_vector_type(4)));
+constexpr int kMfmaKeys = 16;  // keys per wave sub-tile: one matrix-core row block
+
+template <int D>
+constexpr bool attn_mfma_supported() {
+  return D % 32 == 0 && attn_tile_tokens<D>() == kAttnWaves * kMfmaKeys;
+}
+
+template <int D, int MODE, bool PAGED>
+__global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(AttnArgs a) {
+  using KV = __half;
+  constexpr int TT = attn_tile_tokens<D>();
+  static_assert(attn_mfma_supported<D>(), "one 16-key sub-tile per wave, 32-dim slices");
+  constexpr int CH = 8;  // halves per 16-byte chunk
+  constexpr int kRowChunks = D / CH;
+  constexpr int kChunks = kMfmaKeys * kRowChunks;  // chunks of a K (or V) sub-tile
+  constexpr int kPer = (kChunks + kWave - 1) / kWave;
+  constexpr int LDH = D + 8;  // fp16 stage row: 16-byte aligned, rows start on shifted banks
+  constexpr int DT = D / 16;  // 16-dimension output slices
+  __shared__ __align__(16) float q_s[kAttnMaxGroup][D];
+  __shared__ __align__(16) _Float16 stage[kAttnWaves][2][kMfmaKeys][LDH];
+  __shared__ __align__(16) _Float16 new_s[2][D];  // the new token's k and v, as appended
+  __shared__ float red_m[kAttnWaves][kAttnMaxGroup], red_l[kAttnWaves][kAttnMaxGroup];
+  __shared__ __align__(16) float red_o[kAttnWaves][kAttnMaxGroup][D];
+  static_assert(D / 2 <= kWave, "a wave holds one head as d/2 RoPE pairs");
+
+  const int split = blockIdx.x;
+  const int g = blockIdx.y;
+  const int b = blockIdx.z;  // sequence of a batch (0 for a single sequence)
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int qi = lane % 16, kq = lane / 16;  // MFMA column (query head) and k slot
+  const int R = a.hq / a.hkv;
+  const int S = a.splits;
+  const KvRows<KV, D, PAGED> kv_rows(a, b, g);
+  float* part = a.part + static_cast<int64_t>(b) * a.part_stride;
+  const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
+
+  // ---- 1. independent loads, issued before the position is known (as in
+  // attention_split_kernel): the wave's sub-tile of the block's first tile,
+  // the raw q/k/v, gains and RoPE frequencies ----
+  int p = -1;
+  if constexpr (MODE == kAttnFused) p = ((const __attribute__((address_space(4))) int32_t*)a.pos)[b];
+  uint4 kc[kPer], vc[kPer];
+  const int t_spec = split * TT;
+  const bool spec = t_spec + TT <= a.rows;
+  const KV* kspec;
+  const KV* vspec;
+  kv_rows.first_tile(t_spec, spec, kspec, vspec);  // a tile is one page's contiguous rows
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int c = min(lane + i * kWave, kChunks - 1);
+    const int off = (kMfmaKeys * wave + c / kRowChunks) * D + (c % kRowChunks) * CH;
+    kc[i] = *reinterpret_cast<const uint4*>(kspec + off);
+    vc[i] = *reinterpret_cast<const uint4*>(vspec + off);
+  }
+  int next_page = kv_rows.page_of((split + S) * TT);
+  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
+  const bool in_pair = lane < D / 2;
+  constexpr int kParts = PAGED ? kAttnMaxQkvParts : 1;
+  float qx0[2] = {0.0f, 0.0f}, qx1[2] = {0.0f, 0.0f};
+  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
+  float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+#pragma unroll
+  for (int pt = 0; pt < kParts; ++pt) {
+    const float* row = qkv_row + static_cast<int64_t>(min(pt, a.qkv_parts - 1)) * a.qkv_part_stride;
+    const float wgt = pt < a.qkv_parts ? 1.0f : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = min(wave + j * kAttnWaves, R - 1);
+      const float* src = (MODE == kAttnFused ? row : a.q) + (g * R + h) * D;
+      qx0[j] += wgt * src[d0];
+      qx1[j] += wgt * src[d1];
+    }
+    if constexpr (MODE == kAttnFused) {
+      const float* kraw = row + a.hq * D + g * D;
+      const float* vraw = kraw + a.hkv * D;
+      kx0 += wgt * kraw[d0];
+      vx0 += wgt * vraw[d0];
+      kx1 += wgt * kraw[d1];
+      vx1 += wgt * vraw[d1];
+    }
+  }
+  if constexpr (MODE == kAttnFused) {
+    inv_freq = a.inv_freq[d0];
+    qw0 = a.q_norm[d0];
+    qw1 = a.q_norm[d1];
+    kw0 = a.k_norm[d0];
+    kw1 = a.k_norm[d1];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    qx0[j] = in_pair ? qx0[j] : 0.0f;
+    qx1[j] = in_pair ? qx1[j] : 0.0f;
+  }
+  kx0 = in_pair ? kx0 : 0.0f;
+  vx0 = in_pair ? vx0 : 0.0f;
+  kx1 = in_pair ? kx1 : 0.0f;
+  vx1 = in_pair ? vx1 : 0.0f;
+
+  // ---- 2. extent of the context ----
+  int n_keys;
+  if constexpr (MODE == kAttnFused) {
+    const bool ok = p >= 0 && p < a.capacity;
+    if (!ok && threadIdx.x == 0 && split == 0 && g == 0) *a.err = 1;  // vector store, once per sequence
+    n_keys = ok ? p + 1 : 0;
+  } else {
+    n_keys = a.tokens < a.capacity ? a.tokens : a.capacity;
+  }
+  const int n_tiles = (n_keys + TT - 1) / TT;
+
+  float m_run = -INFINITY, l_part = 0.0f;  // column qi's running max (base 2) and the lane's share of its sum
+  f32x4 ot[DT];                            // O^T[dim 16 j + 4 kq + i][head qi]
+#pragma unroll
+  for (int j = 0; j < DT; ++j) ot[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (split < n_tiles) {
+    // ---- 3. q (a wave per head) into LDS, scaled by log2(e) / sqrt(d) (the
+    // scores come out divided by sqrt(d), decoder_layer.cpp:213, in base-2
+    // units for exp2); the block owning the new token's tile normalises and
+    // rotates its k, rounds k and v to fp16 and appends them to the cache ----
+    float rc = 1.0f, rs = 0.0f;
+    if constexpr (MODE == kAttnFused) {
+      if (in_pair) sincosf(static_cast<float>(p) * inv_freq, &rs, &rc);
+    }
+    const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(D));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = wave + j * kAttnWaves;
+      if (h < R) {
+        if constexpr (MODE == kAttnFused) wave_norm_rope_pair<D>(qx0[j], qx1[j], qw0, qw1, a.eps, rc, rs);
+        if (in_pair) {
+          q_s[h][d0] = qx0[j] * qscale;
+          q_s[h][d1] = qx1[j] * qscale;
+        }
+      }
+    }
+    const bool owns_new = (MODE == kAttnFused) && ((p / TT) % S == split);
+    if (owns_new && wave == kAttnWaves - 1) {
+      wave_norm_rope_pair<D>(kx0, kx1, kw0, kw1, a.eps, rc, rs);
+      const KV k0 = from_float<KV>(kx0), k1 = from_float<KV>(kx1);
+      const KV v0 = from_float<KV>(vx0), v1 = from_float<KV>(vx1);
+      if (in_pair) {
+        const int pp = kv_rows.page_of(p);
+        KV* kdst = kv_rows.k_at(pp, p);
+        KV* vdst = kv_rows.v_at(pp, p);
+        kdst[d0] = k0;
+        kdst[d1] = k1;
+        vdst[d0] = v0;
+        vdst[d1] = v1;
+        new_s[0][d0] = __builtin_bit_cast(_Float16, k0);
+        new_s[0][d1] = __builtin_bit_cast(_Float16, k1);
+        new_s[1][d0] = __builtin_bit_cast(_Float16, v0);
+        new_s[1][d1] = __builtin_bit_cast(_Float16, v1);
+      }
+    }
+    __syncthreads();  // q_s and new_s
+
+    // Q^T fragments (B operand): lane (qi, kq) holds dims 32 j + 8 kq .. + 7
+    // of head qi, split into fp16 hi + lo; zero for columns past R.
+    uint4 qh[D / 32], ql[D / 32];
+    {
+      const float* qrow = q_s[min(qi, R - 1)];
+      const float use = qi < R ? 1.0f : 0.0f;
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) {
+        const float4 x0 = *reinterpret_cast<const float4*>(qrow + 32 * j + 8 * kq);
+        const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * j + 8 * kq + 4);
+        const float x[8] = {x0.x * use, x0.y * use, x0.z * use, x0.w * use,
+                            x1.x * use, x1.y * use, x1.z * use, x1.w * use};
+        f16x8 hv, lv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          hv[e] = static_cast<_Float16>(x[e]);
+          lv[e] = static_cast<_Float16>(x[e] - static_cast<float>(hv[e]));
+        }
+        qh[j] = __builtin_bit_cast(uint4, hv);
+        ql[j] = __builtin_bit_cast(uint4, lv);
+      }
+    }
+
+    _Float16* kh = &stage[wave][0][0][0];
+    _Float16* vh = &stage[wave][1][0][0];
+    // The wave's 16 keys of tile `tile` into the registers (rows clamped into
+    // the context: keys past it are masked below).
+    auto fetch = [&](int tile, int page) {
+      const int t0 = tile * TT;
+      const int rows = min(TT, n_keys - t0);
+      const KV* ktile = kv_rows.k_at(page, t0);
+      const KV* vtile = kv_rows.v_at(page, t0);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = min(lane + i * kWave, kChunks - 1);
+        const int r = min(kMfmaKeys * wave + c / kRowChunks, rows - 1);
+        const int64_t off = static_cast<int64_t>(r) * D + (c % kRowChunks) * CH;
+        kc[i] = *reinterpret_cast<const uint4*>(ktile + off);
+        vc[i] = *reinterpret_cast<const uint4*>(vtile + off);
+      }
+    };
+    if (!spec) fetch(split, kv_rows.page_of(split * TT));
+
+    auto step = [&](int tile, auto prefetch) {
+      const int key0 = tile * TT + kMfmaKeys * wave;
+      int page_after = 0;
+      if constexpr (decltype(prefetch)::value) page_after = kv_rows.page_of((tile + 2 * S) * TT);
+      // Stage the sub-tile as loaded, rows past the context as zeros (the
+      // speculative first tile reads whole pages, whose unwritten rows may
+      // hold any bits, and P.V multiplies every row: 0 * NaN is NaN); the new
+      // token's row from new_s instead of the cache (written by this launch).
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int c = lane + i * kWave;
+        if (c < kChunks) {
+          const int r = c / kRowChunks, col = (c % kRowChunks) * CH;
+          const uint32_t keep = key0 + r < n_keys ? ~0u : 0u;
+          const uint4 k4 = kc[i], v4 = vc[i];
+          *reinterpret_cast<u32x4*>(&kh[r * LDH + col]) = u32x4{k4.x & keep, k4.y & keep, k4.z & keep, k4.w & keep};
+          *reinterpret_cast<u32x4*>(&vh[r * LDH + col]) = u32x4{v4.x & keep, v4.y & keep, v4.z & keep, v4.w & keep};
+        }
+      }
+      if (MODE == kAttnFused && p >= key0 && p < key0 + kMfmaKeys && lane < kRowChunks) {
+        const int r = p - key0;
+        *reinterpret_cast<uint4*>(&kh[r * LDH + lane * CH]) = *reinterpret_cast<const uint4*>(&new_s[0][lane * CH]);
+        *reinterpret_cast<uint4*>(&vh[r * LDH + lane * CH]) = *reinterpret_cast<const uint4*>(&new_s[1][lane * CH]);
+      }
+      // The registers are free: the next tile's loads overlap this one's work
+      // (a compile-time choice; a guarded load would be waited for where the
+      // branches join).
+      if constexpr (decltype(prefetch)::value) {
+        fetch(tile + S, next_page);
+        next_page = page_after;
+      }
+      // The stage is the wave's own and its LDS operations complete in order:
+      // waiting for the writes suffices before other lanes read them.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) {
+        const f16x8 kf = *reinterpret_cast<const f16x8*>(&kh[qi * LDH + 32 * j + 8 * kq]);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, __builtin_bit_cast(f16x8, qh[j]), st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, __builtin_bit_cast(f16x8, ql[j]), st, 0, 0, 0);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        st[i] = key0 + 4 * kq + i < n_keys ? st[i] : -INFINITY;
+        mx = fmaxf(mx, st[i]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      // No key of this column seen yet (m_new = -inf): everything stays zero.
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) ot[j] *= alpha;
+      f16x4 ph, pl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = st[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st[i] - m_new);
+        l_part += pv;
+        ph[i] = static_cast<_Float16>(pv);
+        pl[i] = static_cast<_Float16>(pv - static_cast<float>(ph[i]));
+      }
+      m_run = m_new;
+#pragma unroll
+      for (int j = 0; j < DT; ++j) {
+        // A = V^T: lane (qi, kq) needs V[key 4 kq + i][dim 16 j + qi], i =
+        // 0..3; the transposing read gives lane i of a 16-lane group element
+        // i % 4 of the 8 bytes lane 4 k + i / 4 addresses (k = 0..3), so lane
+        // qi addresses key 4 kq + qi / 4, dims 16 j + 4 (qi % 4) .. + 3.
+        const _Float16* vsrc = &vh[(4 * kq + qi / 4) * LDH + 16 * j + 4 * (qi % 4)];
+        const f16x4 va = __builtin_bit_cast(
+            f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(vsrc)));
+        ot[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, ot[j], 0, 0, 0);
+        ot[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, ot[j], 0, 0, 0);
+      }
+      // Reads of this stage finish before the next tile's writes (in-order LDS).
+    };
+    int tile = split;
+    for (; tile + S < n_tiles; tile += S) step(tile, std::true_type{});
+    if (tile < n_tiles) step(tile, std::false_type{});
+  }
+
+  // ---- 4. merge the waves: per head, M = max of the waves' m, then
+  // o = sum_w e_w o_w and l = sum_w e_w l_w with e_w = exp2(m_w - M), in wave
+  // order; neutral (-inf, 0, 0) when the split had no tile ----
+  float l = l_part + __shfl_xor(l_part, 16);
+  l += __shfl_xor(l, 32);
+  if (qi < R) {
+    if (kq == 0) {
+      red_m[wave][qi] = m_run;
+      red_l[wave][qi] = l;
+    }
+#pragma unroll
+    for (int j = 0; j < DT; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red_o[wave][qi][16 * j + 4 * kq + i] = ot[j][i];
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * D; idx += kAttnThreads) {
+    const int h = idx / D, dim = idx - (idx / D) * D;
+    float M = red_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w][h]);
+    float o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w)
+      o = fmaf(M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][h] - M), red_o[w][h][dim], o);
+    part[attn_o_offset(g, split, 0, S, R, D) + idx] = o;
+  }
+  if (static_cast<int>(threadIdx.x) < R) {
+    const int h = threadIdx.x;
+    float M = red_m[0][h];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w][h]);
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w)
+      L = fmaf(M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w][h] - M), red_l[w][h], L);
+    float* dst = part + attn_ml_offset(g, split, h, S, R, D, a.hkv);
+    dst[0] = M * 0.6931471805599453f;  // base-2 units -> natural log (ln 2)
+    dst[1] = L;
+  }
+}
+
 // attention_head_kernel, splits * hq blocks, 256 threads: the contiguous-cache
 // (single-sequence) variant.  Block (s, h) serves query head h of KV group
 // g = h / R over the tiles s, s + splits, ...  The R blocks of a group stage
@@ -1008,13 +1356,24 @@ constexpr int kHeadKernelMaxBlocks = 512;
 constexpr int kGroupBlockHeads = 4;
 constexpr int kGroupBlockMaxBlocks = 256;
 
+// The split-K launch: on the fp16 matrix cores where the cache is fp16 and
+// the tile is 64 keys, else the fp32 split kernel.
+template <typename KV, int D, int MODE, bool PAGED>
+void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if constexpr (std::is_same<KV, __half>::value && attn_mfma_supported<D>()) {
+    attention_mfma_kernel<D, MODE, PAGED><<<grid, kAttnThreads, 0, s>>>(a);
+  } else {
+    attention_split_kernel<KV, D, MODE, PAGED><<<grid, kAttnThreads, 0, s>>>(a);
+  }
+}
+
 template <typename KV, int D>
 hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
   const dim3 block(kAttnThreads);
   const dim3 group_grid(a.splits, a.hkv, a.batch);
   if (a.page_table) {
     if (mode != kAttnFused) return hipErrorInvalidValue;
-    attention_split_kernel<KV, D, kAttnFused, true><<<group_grid, block, 0, s>>>(a);
+    launch_split<KV, D, kAttnFused, true>(a, group_grid, s);
   } else if (static_cast<int64_t>(a.splits) * a.hq <= kHeadKernelMaxBlocks) {
     int blocks = a.splits * a.hq;
     if (mode == kAttnFused && a.warm.blocks > 0) {
@@ -1037,9 +1396,9 @@ hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
       attention_head_kernel<KV, D, kAttnFromCache, kGroupBlockHeads><<<unit_grid, group_block, 0, s>>>(a);
     }
   } else if (mode == kAttnFused) {
-    attention_split_kernel<KV, D, kAttnFused, false><<<group_grid, block, 0, s>>>(a);
+    launch_split<KV, D, kAttnFused, false>(a, group_grid, s);
   } else {
-    attention_split_kernel<KV, D, kAttnFromCache, false><<<group_grid, block, 0, s>>>(a);
+    launch_split<KV, D, kAttnFromCache, false>(a, group_grid, s);
   }
   return hipGetLastError();
 }

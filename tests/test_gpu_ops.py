@@ -191,13 +191,17 @@ def test_qkv_postprocess_and_append(gpu, oracle, d):
     assert cache.rows == 16 and cache.device_bytes == 2 * hkv * 64 * d * 4  # one 64-token page of K and of V
 
 
+@pytest.mark.parametrize("splits", [8, 129])
 @pytest.mark.parametrize("d", [32, 64, 96, 128])
 @pytest.mark.parametrize("kv", ["f16", "f32"])
-def test_fused_append_attention_matches_oracle(gpu, oracle, kv, d):
+def test_fused_append_attention_matches_oracle(gpu, oracle, kv, d, splits):
     # regression: the appended key must be the rotated one for every head_dim
     # (d = 64 once stored a half-rotated key: a missing barrier between RoPE
-    # and the rounding of the new key)
+    # and the rounding of the new key).  8 splits run the per-head kernel;
+    # 129 (more blocks than the per-head and per-group kernels take) the
+    # split-K kernel, on the fp16 matrix cores for an fp16 cache and d <= 96.
     mmr = gpu
+    print(f"[case] fused attention kv={kv} d={d} splits={splits}", flush=True)
     hq, hkv, eps, theta = 8, 2, 1e-5, 1e6
     rng = np.random.default_rng(21)
     np_kv = np.float16 if kv == "f16" else np.float32
@@ -207,7 +211,7 @@ def test_fused_append_attention_matches_oracle(gpu, oracle, kv, d):
     qn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     kn = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
     dqn, dkn = mmr.DeviceArray.from_numpy(qn), mmr.DeviceArray.from_numpy(kn)
-    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, 8), np.uint8)
+    ws = mmr.DeviceArray(mmr.attention_workspace_size(hq, hkv, d, splits), np.uint8)
     err = mmr.DeviceArray(1, np.int32, zero=True)
     pos_d = mmr.DeviceArray(1, np.int32)
     out = mmr.DeviceArray(hq * d, np.float32)
@@ -216,7 +220,7 @@ def test_fused_append_attention_matches_oracle(gpu, oracle, kv, d):
         qkv = rng.standard_normal((hq + 2 * hkv) * d).astype(np.float32)
         pos_d.upload(np.array([pos], np.int32))
         mmr.decode_attention_fused(mmr.DeviceArray.from_numpy(qkv), dqn, dkn, eps, rope, pos_d, cache, hq, hkv, d,
-                                   out, ws, 8, err)
+                                   out, ws, splits, err)
         q_ref, k_ref = oracle.qk_norm_rope(qkv[: hq * d], qkv[hq * d: (hq + hkv) * d], qn, kn, hq, hkv, d, pos,
                                            eps, theta)
         keys_ref.append(k_ref.astype(np_kv).astype(np.float32))
@@ -233,7 +237,7 @@ def test_fused_append_attention_matches_oracle(gpu, oracle, kv, d):
     assert int(err.numpy()[0]) == 0
     pos_d.upload(np.array([cap], np.int32))  # out of range: flagged, nothing written
     mmr.decode_attention_fused(mmr.DeviceArray.from_numpy(qkv), dqn, dkn, eps, rope, pos_d, cache, hq, hkv, d, out,
-                               ws, 8, err)
+                               ws, splits, err)
     assert int(err.numpy()[0]) == 1
 
 
