@@ -2,8 +2,10 @@
 """Decode throughput of the MiniMind2 gfx950 runtime.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 1] [--kv f16|f32] [--no-other-kv] [--no-cpu-baseline]
-                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--no-attention-sweep] [--no-context-sweep] [--batch 32]
-                    [--batch-context 4096] [--traffic-probe N]
+                    [--no-graph] [--copy-probe-mib 256] [--no-gemv-sweep] [--no-attention-sweep]
+                    [--no-context-sweep] [--batch 32] [--batch-context 4096] [--kernel-reps 320]
+    python bench.py --traffic-probe N [--traffic-kernel layer|attention|gate_up]   (counter-run workload)
+    python bench.py [--no-graph] --context-probe T | --sweep-probe | --batch-probe  (kernel-trace workloads)
 
 Workload: MiniMind2 dense (hidden 768, 16 layers, 8/2 heads, d 96, FFN 2048,
 vocab 6400), fp16 weights drawn N(0, 0.02) from seed 0, a 512-token uniform
@@ -17,10 +19,11 @@ measured with HIP events on the decode stream between two device syncs.
 
 The same line carries
   * roofline: the kernel with the largest share of the step (decode
-    attention at these contexts; gate_up and lm_head under `secondary`)
-    launched alone `--kernel-reps` times over the 16 layers as one hipGraph
-    chain (eager launches with --no-graph), timed with HIP events on the
-    stream it runs on; achieved = algorithmic bytes / average time per launch;
+    attention at 768 keys, KERNEL_CONTEXT; the other step kernels under
+    `secondary`) launched alone `--kernel-reps` times over the 16 layers as
+    one hipGraph chain (eager launches with --no-graph), timed with HIP events
+    on the stream it runs on; achieved = algorithmic bytes / average time per
+    launch;
   * kernels: the same measurement for every kernel of the step;
   * gemv_sweep / attention_sweep: BASELINE configs[1] GEMV shapes and
     configs[2] attention contexts alone through the C ABI, MALL-resident and
@@ -36,9 +39,10 @@ The same line carries
   * copy_probe: a device-to-device copy of --copy-probe-mib MiB (HIP's blit
     kernel), the achievable-bandwidth yardstick and the calibration dispatch
     of the FETCH_SIZE / WRITE_SIZE counter runs;
-  * roofline.traffic: L2-to-memory bytes per launch of the roofline kernel
-    from its committed counter summary (profiles/*_traffic.md, written from
-    `bench.py --traffic-probe` runs), null when that file is absent;
+  * roofline.traffic: L2-to-memory bytes per launch of each step kernel at
+    the same 768 keys, from the committed counter summary TRAFFIC_FILE
+    (written from `bench.py --traffic-probe 48 --traffic-kernel layer` runs),
+    null when that file is absent;
   * cpu_baseline: the reference's own CPU path (oracle/_ref/ref_driver, built
     from the unmodified reference sources) on a bounded sample on this host.
 
