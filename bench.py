@@ -373,6 +373,35 @@ def traffic_probe(mmr, launches: int, copy_mib: int, kernel: str) -> int:
         assert int(err.numpy()[0]) == 0
         alg = {name: kernel_bytes(MINIMIND2, name, n_keys, 2) for name in ("qkv", "attention", "o", "gate_up", "down",
                                                                           "lm_head")}
+    elif kernel == "prefill":
+        # One 512-token chunked prefill of MiniMind2 (the configs[3] prompt):
+        # the GEMMs, attention, q/k rows and residual + norm kernels of 16
+        # layers once each, then the head.
+        cfg = mmr.make_config(**MINIMIND2)
+        model = mmr.Model.synthetic(cfg, 0, 0.02, True)
+        st = model.make_state(PROMPT_LEN + 8, mmr.KV_F16)
+        st.enqueue_prefill(mmr.synthesize_prompt(1, PROMPT_LEN, MINIMIND2["vocab_size"]).tolist())
+        st.synchronize()
+        stream = mmr.Stream(st.stream)
+        H, Fi, V = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"], MINIMIND2["vocab_size"]
+        qkv_rows = (MINIMIND2["num_attention_heads"] + 2 * MINIMIND2["num_key_value_heads"]) * MINIMIND2["head_dim"]
+        alg = {"qkv_w": qkv_rows * H * 2, "o_w": H * H * 2, "gate_up_w": 2 * Fi * H * 2, "down_w": H * Fi * 2,
+               "note": "weight bytes per launch; activations per launch are listed in the profile"}
+    elif kernel == "batch":
+        # configs[4]'s batch of 32 sequences, one prompt token each, then 3
+        # decode steps: the batched step's split-K GEMMs (M = 32), paged
+        # attention and residual + norm kernels, 4 steps of 16 layers.
+        cfg = mmr.make_config(**MINIMIND2)
+        model = mmr.Model.synthetic(cfg, 0, 0.02, True)
+        bs = model.make_batch_state(32, 64, mmr.KV_F16)
+        bs.prefill([[1 + b] for b in range(32)])
+        bs.decode(3)
+        bs.synchronize()
+        stream = mmr.Stream(bs.stream)
+        H, Fi = MINIMIND2["hidden_size"], MINIMIND2["intermediate_size"]
+        qkv_rows = (MINIMIND2["num_attention_heads"] + 2 * MINIMIND2["num_key_value_heads"]) * MINIMIND2["head_dim"]
+        alg = {"qkv_w": qkv_rows * H * 2, "o_w": H * H * 2, "gate_up_w": 2 * Fi * H * 2, "down_w": H * Fi * 2,
+               "lm_head_w": MINIMIND2["vocab_size"] * H * 2}
     elif kernel == "attention":
         hq, hkv, d = MINIMIND2["num_attention_heads"], MINIMIND2["num_key_value_heads"], MINIMIND2["head_dim"]
         n_keys = KERNEL_CONTEXT
@@ -527,7 +556,7 @@ def main() -> int:
     ap.add_argument("--batch-context", type=int, default=4096)
     ap.add_argument("--traffic-probe", type=int, default=0, metavar="LAUNCHES",
                     help="run only the counter-run workload (kernel launches + one copy) and exit")
-    ap.add_argument("--traffic-kernel", choices=["layer", "attention", "gate_up"], default="layer")
+    ap.add_argument("--traffic-kernel", choices=["layer", "attention", "gate_up", "prefill", "batch"], default="layer")
     ap.add_argument("--context-probe", type=int, default=0, metavar="TOKENS",
                     help="run only a prefill of TOKENS prompt tokens + --context-probe-steps decode steps and exit")
     ap.add_argument("--context-probe-steps", type=int, default=24)

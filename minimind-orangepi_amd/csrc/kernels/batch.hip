@@ -195,8 +195,21 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   __shared__ float row_inv[BT * 16];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  const int n0 = blockIdx.x * kSplitRows + wave * 16;
-  const int k0 = blockIdx.y * KC;
+  // Block -> (W row block bx, K chunk by).  The blocks of one K chunk stage
+  // the same A rows (for SwiGLU and combine input, the same partials): with
+  // the chunk count a multiple of kXcds, XCD x (block b runs on XCD b mod
+  // kXcds) takes every row block of chunks x * (chunks / kXcds) .., so each
+  // chunk's A is fetched into one L2.
+  int bx = blockIdx.x, by = blockIdx.y;
+  if (gridDim.y % kXcds == 0) {
+    const int nx = static_cast<int>(gridDim.x);
+    const int b = static_cast<int>(blockIdx.x) + nx * static_cast<int>(blockIdx.y);
+    const int slot = b / kXcds;
+    by = (b % kXcds) * (static_cast<int>(gridDim.y) / kXcds) + slot / nx;
+    bx = slot % nx;
+  }
+  const int n0 = bx * kSplitRows + wave * 16;
+  const int k0 = by * KC;
   // W: NB x 8 halves per lane (rows past n clamp to the last row).
   const int wrow = min(n0 + lane % 16, g.n - 1);
   const __half* wsrc = g.w + static_cast<int64_t>(wrow) * g.k + k0 + 8 * (lane / 16);
@@ -349,7 +362,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
     const int m = bt * 16 + lane % 16;
     if (m >= g.m) continue;
     const float inv = row_inv[m];
-    float* dst = g.part + (static_cast<int64_t>(blockIdx.y) * g.m + m) * g.n + nb;
+    float* dst = g.part + (static_cast<int64_t>(by) * g.m + m) * g.n + nb;
     const float o[4] = {(acc_hi[bt][0] + acc_lo[bt][0]) * inv, (acc_hi[bt][1] + acc_lo[bt][1]) * inv,
                         (acc_hi[bt][2] + acc_lo[bt][2]) * inv, (acc_hi[bt][3] + acc_lo[bt][3]) * inv};
     if (vec) {
