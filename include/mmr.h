@@ -99,6 +99,11 @@ int mmr_launch_floor_us(int kernels, int blocks, int load_store, int reps, float
  * 1..chunk_rows). */
 int mmr_gemm_k_splits(int64_t m, int64_t n, int64_t k, int* splits);
 int mmr_prefill_partial_floats(const mmr_config* config, int64_t chunk_rows, int64_t* floats);
+/* Test aid, no reference counterpart: the (W row block, K chunk) that block
+ * `block` of a batched split-K GEMM launch with grid (row_blocks, chunks)
+ * computes (the blocks of one K chunk are placed on one XCD where chunks is a
+ * multiple of 8). */
+int mmr_splitk_block_tile(int block, int row_blocks, int chunks, int* row_block, int* chunk);
 /* float_to_half / half_to_float (ascend_matmul.h:14-15), but IEEE
  * round-to-nearest-even instead of the reference's ties-away rounding. */
 int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n);

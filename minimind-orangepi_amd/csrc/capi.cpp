@@ -285,6 +285,17 @@ int mmr_gemm_k_splits(int64_t m, int64_t n, int64_t k, int* splits) {
     *splits = mmr::gemm_k_splits(static_cast<int>(m), static_cast<int>(n), static_cast<int>(k));
   });
 }
+int mmr_splitk_block_tile(int block, int row_blocks, int chunks, int* row_block, int* chunk) {
+  return guarded([&] {
+    require(row_block && chunk, "null argument");
+    require(row_blocks > 0 && chunks > 0 && block >= 0 && static_cast<int64_t>(row_blocks) * chunks <= INT32_MAX &&
+                block < row_blocks * chunks,
+            "block out of range");
+    const mmr::SplitKTile t = mmr::splitk_block_tile(block, row_blocks, chunks);
+    *row_block = t.row_block;
+    *chunk = t.chunk;
+  });
+}
 int mmr_prefill_partial_floats(const mmr_config* config, int64_t chunk_rows, int64_t* floats) {
   return guarded([&] {
     require(config && floats, "null argument");

@@ -195,19 +195,11 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   __shared__ float row_inv[BT * 16];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  // Block -> (W row block bx, K chunk by).  The blocks of one K chunk stage
-  // the same A rows (for SwiGLU and combine input, the same partials): with
-  // the chunk count a multiple of kXcds, XCD x (block b runs on XCD b mod
-  // kXcds) takes every row block of chunks x * (chunks / kXcds) .., so each
-  // chunk's A is fetched into one L2.
-  int bx = blockIdx.x, by = blockIdx.y;
-  if (gridDim.y % kXcds == 0) {
-    const int nx = static_cast<int>(gridDim.x);
-    const int b = static_cast<int>(blockIdx.x) + nx * static_cast<int>(blockIdx.y);
-    const int slot = b / kXcds;
-    by = (b % kXcds) * (static_cast<int>(gridDim.y) / kXcds) + slot / nx;
-    bx = slot % nx;
-  }
+  // Block -> (W row block bx, K chunk by), the blocks of one K chunk on one
+  // XCD where the chunk count allows (splitk_block_tile).
+  const SplitKTile tile = splitk_block_tile(static_cast<int>(blockIdx.x + gridDim.x * blockIdx.y),
+                                            static_cast<int>(gridDim.x), static_cast<int>(gridDim.y));
+  const int bx = tile.row_block, by = tile.chunk;
   const int n0 = bx * kSplitRows + wave * 16;
   const int k0 = by * KC;
   // W: NB x 8 halves per lane (rows past n clamp to the last row).

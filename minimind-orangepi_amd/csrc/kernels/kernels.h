@@ -409,6 +409,21 @@ struct SplitKArgs {
 };
 // W rows per split-K block: the launch grid is (ceil(n / kSplitKRows), k / kc).
 constexpr int kSplitKRows = 64;
+// (W row block, K chunk) of split-K block `block` (linear id x + row_blocks y
+// of the grid (row_blocks, chunks)).  The blocks of one K chunk stage the same
+// A rows (or the same partials); block b runs on XCD b mod kXcds, so with the
+// chunk count a multiple of kXcds, XCD x takes every row block of chunks
+// x * chunks / kXcds .. and each chunk's A is fetched into one L2.  Otherwise
+// block b takes (b mod row_blocks, b / row_blocks).  Every pair is taken by
+// exactly one block.
+struct SplitKTile {
+  int row_block, chunk;
+};
+__host__ __device__ inline SplitKTile splitk_block_tile(int block, int row_blocks, int chunks) {
+  if (chunks % kXcds != 0) return SplitKTile{block % row_blocks, block / row_blocks};
+  const int slot = block / kXcds;
+  return SplitKTile{slot % row_blocks, (block % kXcds) * (chunks / kXcds) + slot / row_blocks};
+}
 // K chunk (a multiple of 32 that divides k, at most 256; 0 when k is not a
 // multiple of 32); splits = k / kc.
 int splitk_chunk(int n, int k);

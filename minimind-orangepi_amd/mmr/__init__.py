@@ -103,6 +103,7 @@ _SIGS = {
     "mmr_event_elapsed_ms": ([VP, VP, P_F32], C.c_int),
     "mmr_gemm_k_splits": ([I64, I64, I64, C.POINTER(C.c_int)], C.c_int),
     "mmr_prefill_partial_floats": ([C.POINTER(Config), I64, C.POINTER(I64)], C.c_int),
+    "mmr_splitk_block_tile": ([C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)], C.c_int),
     "mmr_f32_to_f16": ([VP, VP, SZ], C.c_int),
     "mmr_f16_to_f32": ([VP, VP, SZ], C.c_int),
     "mmr_matvec_f16": ([VP, I64, I64, VP, VP, VP, VP], C.c_int),
@@ -371,6 +372,13 @@ def gemm_k_splits(m: int, n: int, k: int) -> int:
     out = C.c_int()
     check(_lib.mmr_gemm_k_splits(m, n, k, C.byref(out)))
     return out.value
+
+
+def splitk_block_tile(block: int, row_blocks: int, chunks: int) -> tuple[int, int]:
+    """(W row block, K chunk) that block `block` of a batched split-K GEMM launch computes (host arithmetic)."""
+    rb, ch = C.c_int(), C.c_int()
+    check(_lib.mmr_splitk_block_tile(block, row_blocks, chunks, C.byref(rb), C.byref(ch)))
+    return rb.value, ch.value
 
 
 def prefill_partial_floats(cfg: Config, chunk_rows: int) -> int:

@@ -190,3 +190,21 @@ def test_prefill_partial_buffer_covers_every_chunk_row_count(mmr, case):
             # the case the buffer once missed: a shorter chunk needs more than a full one
             assert need[worst] > need[C] and worst < C
     assert mmr.prefill_partial_floats(cfg, 0) == 0
+
+
+def test_splitk_block_tiles_cover_the_grid_once(mmr):
+    # Every (W row block, K chunk) of a batched split-K launch is computed by
+    # exactly one block, whatever the grid; with the chunk count a multiple of
+    # 8, the blocks of one chunk share an XCD (block b runs on XCD b mod 8).
+    for row_blocks in (1, 3, 12, 18, 64, 100):
+        for chunks in (1, 2, 3, 8, 12, 16, 24, 40):
+            tiles = [mmr.splitk_block_tile(b, row_blocks, chunks) for b in range(row_blocks * chunks)]
+            assert sorted(tiles) == [(r, c) for r in range(row_blocks) for c in range(chunks)], (row_blocks, chunks)
+            if chunks % 8 == 0:
+                xcd_of_chunk = {}
+                for b, (_, c) in enumerate(tiles):
+                    assert xcd_of_chunk.setdefault(c, b % 8) == b % 8, (row_blocks, chunks, c)
+            else:
+                assert tiles == [(b % row_blocks, b // row_blocks) for b in range(row_blocks * chunks)]
+    with pytest.raises(mmr.MmrError):
+        mmr.splitk_block_tile(12 * 16, 12, 16)
