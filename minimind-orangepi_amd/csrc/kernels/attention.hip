@@ -1242,14 +1242,25 @@ constexpr int kCombineGroups = kCombineThreads / kCombineSlice;     // split gro
 constexpr int kCombineKernelMaxSplits = 4096;
 constexpr int kCombineMaxPerThread = kCombineKernelMaxSplits / kCombineThreads;
 
+// Blocks past the first multiple of kXcds at or above the merge blocks (one
+// sequence only) are L2-warming blocks for `warm` (see L2WarmSet).
 template <int kRound, bool kMulti>
 __global__ __launch_bounds__(kCombineThreads) void attention_combine_kernel(const float* part, int hq, int hkv, int d,
                                                                              int splits, int64_t part_stride,
-                                                                             float* out) {
+                                                                             float* out, L2WarmSet warm) {
   __shared__ float s_red[kCombineGroups][kCombineSlice];
   __shared__ float s_l[kCombineGroups];
   __shared__ float s_m[kCombineThreads / kWave];
+  __shared__ __align__(16) uint32_t s_warm[kCombineThreads / kWave][kWave * 4];  // l2_warm scratch, 1 KB per wave
   const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
+  if (warm.blocks > 0) {
+    const int first = (hq * nslice + kXcds - 1) / kXcds * kXcds;
+    if (static_cast<int>(blockIdx.x) >= first) {
+      l2_warm<kCombineThreads>(warm, static_cast<int>(blockIdx.x) - first, &s_warm[0][0]);
+      return;
+    }
+    if (static_cast<int>(blockIdx.x) >= hq * nslice) return;  // padding up to the first warming block
+  }
   const int qh = blockIdx.x / nslice, slice = blockIdx.x % nslice;
   part += static_cast<int64_t>(blockIdx.y) * part_stride;  // sequence of a batch
   out += static_cast<int64_t>(blockIdx.y) * hq * d;
@@ -1469,21 +1480,30 @@ hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStr
 }
 
 hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
-                                    hipStream_t stream, int batch, int64_t part_stride) {
+                                    hipStream_t stream, int batch, int64_t part_stride, const L2WarmSet* warm) {
   if (!attention_supported(hq, hkv, d) || d > 128 || splits <= 0 || splits > kCombineKernelMaxSplits || batch <= 0)
     return hipErrorInvalidValue;
   const int nslice = (d + kCombineSlice - 1) / kCombineSlice;
-  const dim3 grid(hq * nslice, batch);
+  L2WarmSet w;
+  int blocks = hq * nslice;
+  if (warm && warm->blocks > 0) {
+    if (batch != 1 || warm->blocks % kXcds != 0) return hipErrorInvalidValue;
+    w = *warm;
+    blocks = (blocks + kXcds - 1) / kXcds * kXcds + w.blocks;
+  }
+  const dim3 grid(blocks, batch);
   if (splits <= 8 * kCombineGroups) {
-    attention_combine_kernel<8, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+    attention_combine_kernel<8, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out,
+                                                                             w);
   } else if (splits <= 16 * kCombineGroups) {
     attention_combine_kernel<16, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
-                                                                              out);
+                                                                              out, w);
   } else if (splits <= 32 * kCombineGroups) {
     attention_combine_kernel<32, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
-                                                                              out);
+                                                                              out, w);
   } else {
-    attention_combine_kernel<16, true><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out);
+    attention_combine_kernel<16, true><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out,
+                                                                             w);
   }
   return hipGetLastError();
 }

@@ -240,9 +240,12 @@ size_t attention_partial_floats(int hq, int hkv, int d, int splits);
 int attention_tile_tokens(int d);
 bool attention_supported(int hq, int hkv, int d);
 hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStream_t stream);
-// Merge the split partials into out [Hq*D] (one block per query head).
+// Merge the split partials into out [Hq*D] (one block per query head and
+// 16-dimension slice).  `warm` (one sequence only): warming blocks past the
+// merge blocks (see L2WarmSet).
 hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, int splits, float* out,
-                                    hipStream_t stream, int batch = 1, int64_t part_stride = 0);
+                                    hipStream_t stream, int batch = 1, int64_t part_stride = 0,
+                                    const L2WarmSet* warm = nullptr);
 
 // qkv post-process as a standalone op (reference K2): per-head q/k RMSNorm +
 // RoPE at `position`, q -> query_out, k/v appended at cache index `index`.

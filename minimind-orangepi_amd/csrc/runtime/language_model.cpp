@@ -416,6 +416,36 @@ mmr::L2Warm gemv_warm_region(const __half* w, int rows, int k, const mmr::GemvPl
   return r;
 }
 
+// Whether the O-projection GEMV's prologue merges the attention splits (else
+// attention_combine_kernel runs first).
+bool prologue_combines(const DeviceState& s, int splits) {
+  const auto& c = s.model->cfg;
+  const int64_t Hq = c.num_attention_heads;
+  return !s.combine_kernel && splits <= mmr::kCombineMaxSplits && Hq <= mmr::kCombineMaxHeads &&
+         Hq * c.head_dim <= mmr::kCombineMaxDim;
+}
+
+// L2 warming of layer L's O, gate_up and down weights by up to s.warm_blocks
+// blocks on `idle_cus` CUs (rounded down to whole XCD rounds); none when the
+// regions would pass kWarmMaxBytes (they must fit the L2s with room to spare).
+mmr::L2WarmSet layer_warm_set(const DeviceState& s, const LayerDev& L, int idle_cus) {
+  const DeviceModel& m = *s.model;
+  const auto& c = m.cfg;
+  const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
+  const int Hq = static_cast<int>(c.num_attention_heads), F = static_cast<int>(c.intermediate_size);
+  mmr::L2WarmSet w;
+  const int blocks = std::min(s.warm_blocks, std::max(0, idle_cus) / mmr::kXcds * mmr::kXcds);
+  if (blocks <= 0) return w;
+  w.region[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
+  w.region[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
+  w.region[2] = gemv_warm_region(L.down, H, F, m.plan_down);
+  int64_t bytes = 0;
+  for (const auto& r : w.region) bytes += r.bytes;
+  if (bytes > kWarmMaxBytes) return mmr::L2WarmSet{};
+  w.blocks = blocks;
+  return w;
+}
+
 // A step's place in a replayed group of steps: inside a group the argmax
 // finalize of every step but the last folds into the next step (its layer-0
 // qkv prologue reduces the lm_head partials; the lm_head launch advances the
@@ -484,21 +514,9 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       t.err = s.err;
       // While the head blocks run on part of the GPU, extra blocks on the idle
       // CUs load this layer's O, gate_up and down weights into the L2s of the
-      // XCDs whose blocks will read them; the regions must fit the L2s with
-      // room to spare.
-      const int idle = (s.cus - splits * Hq) / mmr::kXcds * mmr::kXcds;
-      const int warm_blocks = std::min(s.warm_blocks, idle);
-      if (warm_blocks > 0) {
-        t.warm.region[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
-        t.warm.region[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
-        t.warm.region[2] = gemv_warm_region(L.down, H, F, m.plan_down);
-        int64_t bytes = 0;
-        for (const auto& r : t.warm.region) bytes += r.bytes;
-        if (bytes <= kWarmMaxBytes)
-          t.warm.blocks = warm_blocks;
-        else
-          t.warm = mmr::L2WarmSet{};
-      }
+      // XCDs whose blocks will read them.  (Past the prologue's splits the
+      // combine launch warms instead.)
+      if (prologue_combines(s, splits)) t.warm = layer_warm_set(s, L, s.cus - splits * Hq);
       check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "attention");
       return;
     }
@@ -510,8 +528,7 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       a.y = s.h;
       a.residual = s.h;
       mmr::GemvPrologue pro = mmr::kProPlain;
-      if (!s.combine_kernel && splits <= mmr::kCombineMaxSplits && Hq <= mmr::kCombineMaxHeads &&
-          Hq * D <= mmr::kCombineMaxDim) {
+      if (prologue_combines(s, splits)) {
         pro = mmr::kProAttnCombine;
         a.part = s.attn_part;
         a.splits = splits;
@@ -519,7 +536,9 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
         a.hkv = Hkv;
         a.head_dim = D;
       } else {
-        check_hip(mmr::launch_attention_combine(s.attn_part, Hq, Hkv, D, splits, s.attn, s.stream),
+        const int merge_blocks = Hq * ((D + 15) / 16);  // one per head and 16-dimension slice
+        const mmr::L2WarmSet warm = layer_warm_set(s, L, s.cus - merge_blocks);
+        check_hip(mmr::launch_attention_combine(s.attn_part, Hq, Hkv, D, splits, s.attn, s.stream, 1, 0, &warm),
                   "attention combine");
         a.x = s.attn;
       }

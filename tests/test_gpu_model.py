@@ -215,6 +215,29 @@ def test_l2_warming_blocks_leave_the_step_unchanged(gpu, monkeypatch):
     np.testing.assert_array_equal(warm.read_logits(), cold.read_logits())
 
 
+def test_l2_warming_in_the_combine_launch_leaves_the_step_unchanged(gpu, monkeypatch):
+    # Past 16 splits the split merge runs in its own launch, and that launch
+    # carries the warming blocks: at 2,048 + 24 keys (40 splits) the decode
+    # with them equals the decode without, bit for bit.
+    mmr = gpu
+    print("[case] cfg3 model, 2048-token prompt + 24 steps kv=f16, combine-launch warming on / off", flush=True)
+    g = load_golden("cfg3")
+    m = synth_model(mmr, g)
+    prompt = np.random.default_rng(11).integers(0, g["config"]["vocab_size"], 2048).tolist()
+    steps = 24
+    n = len(prompt) + steps
+    warm = m.make_state(n, mmr.KV_F16)
+    monkeypatch.setenv("MMR_L2_WARM_BLOCKS", "0")
+    cold = m.make_state(n, mmr.KV_F16)
+    monkeypatch.delenv("MMR_L2_WARM_BLOCKS")
+    for st in (warm, cold):
+        st.enqueue_prefill(prompt)
+        st.enqueue_decode(steps - 1)
+        st.synchronize()
+    np.testing.assert_array_equal(warm.read_sequence(len(prompt), steps), cold.read_sequence(len(prompt), steps))
+    np.testing.assert_array_equal(warm.read_logits(), cold.read_logits())
+
+
 def test_state_reset_and_reuse(gpu):
     mmr = gpu
     g = load_golden("mini")
