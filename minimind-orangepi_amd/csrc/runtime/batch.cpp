@@ -94,16 +94,19 @@ void* BatchState::stream() const { return device ? static_cast<void*>(device->st
 
 namespace {
 
-// Attention splits per sequence: about eight 64-token tiles per block (the
+// Attention splits per sequence: up to sixteen 64-token tiles per block (the
 // next tile is prefetched while one is computed, so long per-block loops are
-// cheap; at B = 32 and 4096 keys, 1 / 2 / 4 / 8 / 16 tiles per block measured
-// 1.24 / 1.11 / 1.00 / 0.97 / 1.03 ms per step), and raised while the context
-// has the tiles until the launch has about two blocks per CU (256 -> 512
-// blocks: 867.2 -> 860.7 us per step from 256 to 4096 positions at B = 32;
-// 1024: 975.0).
+// cheap), raised while the context has the tiles until the launch has about
+// one block per CU.  Fewer splits also leave fewer partials for the O
+// projection's staging to merge, and past 8 the separate combine kernel runs.
+// On the matrix-core attention at B = 32, 256 -> 4096 positions (aggregate
+// tok/s, p50 step; same box): 16 tiles / 256 blocks (4 splits from 257
+// positions on) 42.03k, 0.764 ms; 8 / 256 41.79k, 0.773; 8 / 512 (8 splits)
+// 41.24k, 0.774; 8 / 128 41.58k, 0.773; 16 / 128 40.96k, 0.787; 4 / 512 and
+// 8 / 1024 (16 splits, combine kernel) 38.8k / 37.5k, 0.869.
 constexpr int kBatchMaxSplits = 64;
-constexpr int kBatchTilesPerSplit = 8;
-constexpr int64_t kBatchAttnBlocks = 512;
+constexpr int kBatchTilesPerSplit = 16;
+constexpr int64_t kBatchAttnBlocks = 256;
 
 int batch_splits(int64_t n_keys, int tile, int64_t seq_heads) {
   const int64_t tiles = (n_keys + tile - 1) / tile;
