@@ -176,7 +176,7 @@ struct KvRows {
   }
 };
 
-template <typename KV, int D, int MODE, bool PAGED>
+template <typename KV, int D, int MODE, bool PAGED, int QP = 1>
 __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs a) {
   constexpr int TT = attn_tile_tokens<D>();
   constexpr int LD = D + 4;  // padded row: conflict-free 16-byte LDS reads
@@ -230,10 +230,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   // holds dims (i, i + d/2), the pair RoPE rotates together.
   const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
   const bool in_pair = lane < D / 2;
-  // The batched (paged) path may hand the projection over as up to
-  // kAttnMaxQkvParts split-K partials: every part's load is issued (part index
-  // clamped, parts past qkv_parts weighted 0) and the parts summed in order.
-  constexpr int kParts = PAGED ? kAttnMaxQkvParts : 1;
+  // The batched (paged) path may hand the projection over as up to QP
+  // split-K partials (QP = kAttnFewQkvParts or kAttnMaxQkvParts): every part's
+  // load is issued (part index clamped, parts past qkv_parts weighted 0) and
+  // the parts summed in order.
+  constexpr int kParts = PAGED ? QP : 1;
   float qx0[2] = {0.0f, 0.0f}, qx1[2] = {0.0f, 0.0f};
   float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
   float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
@@ -539,7 +540,7 @@ constexpr bool attn_mfma_supported() {
   return D % 32 == 0 && attn_tile_tokens<D>() == kAttnWaves * kMfmaKeys;
 }
 
-template <int D, int MODE, bool PAGED>
+template <int D, int MODE, bool PAGED, int QP = 1>
 __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(AttnArgs a) {
   using KV = __half;
   constexpr int TT = attn_tile_tokens<D>();
@@ -590,7 +591,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(AttnArgs a
   int next_page = kv_rows.page_of((split + S) * TT);
   const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
   const bool in_pair = lane < D / 2;
-  constexpr int kParts = PAGED ? kAttnMaxQkvParts : 1;
+  constexpr int kParts = PAGED ? QP : 1;  // QKV partials loaded, as in attention_split_kernel
   float qx0[2] = {0.0f, 0.0f}, qx1[2] = {0.0f, 0.0f};
   float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
   float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
@@ -1382,12 +1383,12 @@ constexpr int kGroupBlockMaxBlocks = 256;
 
 // The split-K launch: on the fp16 matrix cores where the cache is fp16 and
 // the tile is 64 keys, else the fp32 split kernel.
-template <typename KV, int D, int MODE, bool PAGED>
+template <typename KV, int D, int MODE, bool PAGED, int QP = 1>
 void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
   if constexpr (std::is_same<KV, __half>::value && attn_mfma_supported<D>()) {
-    attention_mfma_kernel<D, MODE, PAGED><<<grid, kAttnThreads, 0, s>>>(a);
+    attention_mfma_kernel<D, MODE, PAGED, QP><<<grid, kAttnThreads, 0, s>>>(a);
   } else {
-    attention_split_kernel<KV, D, MODE, PAGED><<<grid, kAttnThreads, 0, s>>>(a);
+    attention_split_kernel<KV, D, MODE, PAGED, QP><<<grid, kAttnThreads, 0, s>>>(a);
   }
 }
 
@@ -1397,7 +1398,12 @@ hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
   const dim3 group_grid(a.splits, a.hkv, a.batch);
   if (a.page_table) {
     if (mode != kAttnFused) return hipErrorInvalidValue;
-    launch_split<KV, D, kAttnFused, true>(a, group_grid, s);
+    // Each QKV partial is a load per q/k/v value in the prologue: few parts
+    // take the variant that issues only kAttnFewQkvParts of them.
+    if (a.qkv_parts <= kAttnFewQkvParts)
+      launch_split<KV, D, kAttnFused, true, kAttnFewQkvParts>(a, group_grid, s);
+    else
+      launch_split<KV, D, kAttnFused, true, kAttnMaxQkvParts>(a, group_grid, s);
   } else if (static_cast<int64_t>(a.splits) * a.hq <= kHeadKernelMaxBlocks) {
     int blocks = a.splits * a.hq;
     if (mode == kAttnFused && a.warm.blocks > 0) {

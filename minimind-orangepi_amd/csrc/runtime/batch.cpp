@@ -118,13 +118,22 @@ int batch_splits(int64_t n_keys, int tile, int64_t seq_heads) {
 
 // K chunk of a projection's split-K launch (0: dense fallback, k not a
 // multiple of 32); QKV partials are consumed by the attention prologue, which
-// takes at most kAttnMaxQkvParts of them.
+// takes at most qkv_max_parts(k) of them.
 int proj_chunk(int n, int k, int max_parts) {
   int kc = mmr::splitk_chunk(n, k);
   if (kc == 0 || max_parts <= 0 || k / kc <= max_parts) return kc;
   for (kc = 32; kc <= 256; kc += 32)  // the smallest chunk that tiles K in max_parts pieces
     if (k % kc == 0 && k / kc <= max_parts) return kc;
   return 0;
+}
+
+// Most QKV partials for a K of k: kAttnFewQkvParts where chunks of up to 256
+// columns tile K in that many (the attention prologue's lighter variant),
+// else kAttnMaxQkvParts.
+int qkv_max_parts(int k) {
+  for (int kc = 32; kc <= 256; kc += 32)
+    if (k % kc == 0 && k / kc <= mmr::kAttnFewQkvParts) return mmr::kAttnFewQkvParts;
+  return mmr::kAttnMaxQkvParts;
 }
 
 // out_parts[s][b][n] = partial products of x (batch rows, stride k) with W
@@ -256,7 +265,7 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
   const size_t L = m.layers.size();
   // K chunks of the split-K projections (as project / project_swiglu choose them).
   auto chunk = [&](int n, int k, int max_parts) { return B <= 32 ? proj_chunk(n, k, max_parts) : 0; };
-  const int kc_qkv = chunk(qkv_w, H, mmr::kAttnMaxQkvParts), kc_gu = chunk(2 * F, H, 0), kc_down = chunk(H, F, 0);
+  const int kc_qkv = chunk(qkv_w, H, qkv_max_parts(H)), kc_gu = chunk(2 * F, H, 0), kc_down = chunk(H, F, 0);
   const int kc_lm = chunk(V, H, 0);
   auto warm_qkv = [&](size_t l) {
     return warm_set(s.warm_blocks, {splitk_warm_region(m.layers[l].qkv, qkv_w, H, kc_qkv)});
@@ -268,7 +277,7 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
             "batch input norm");
   for (size_t l = 0; l < L; ++l) {
     const LayerDev& Ld = m.layers[l];
-    const int qkv_parts = project(s, s.x, Ld.qkv, qkv_w, H, mmr::kAttnMaxQkvParts);
+    const int qkv_parts = project(s, s.x, Ld.qkv, qkv_w, H, qkv_max_parts(H));
     mmr::AttnArgs t;
     t.qkv = s.proj;
     t.qkv_stride = qkv_w;
@@ -331,7 +340,7 @@ int64_t proj_floats(const MiniMindConfig& c, int64_t batch) {
   const int F = static_cast<int>(c.intermediate_size), V = static_cast<int>(c.vocab_size);
   const int qd = static_cast<int>(c.num_attention_heads) * D;
   const struct { int n, k, max_parts; } shapes[] = {
-      {qkv_w, H, mmr::kAttnMaxQkvParts}, {H, qd, 0}, {2 * F, H, 0}, {H, F, 0}, {V, H, 0}};
+      {qkv_w, H, qkv_max_parts(H)}, {H, qd, 0}, {2 * F, H, 0}, {H, F, 0}, {V, H, 0}};
   int64_t most = 0;
   for (const auto& sh : shapes) most = std::max(most, parts_floats(sh.n, sh.k, sh.max_parts, batch));
   return most;

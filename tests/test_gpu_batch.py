@@ -56,6 +56,30 @@ def test_batch_matches_single_sequences(gpu, kv):
         assert rel_err(bs.read_logits(b), ref_logits) < 1e-4, b
 
 
+def test_batch_wide_hidden_takes_eight_qkv_partials(gpu):
+    # hidden 1024: no chunk of up to 256 columns tiles K in three, so the QKV
+    # projection hands the attention eight split-K partials (the prologue's
+    # full variant; MiniMind2 and the mini model take the three-part one)
+    mmr = gpu
+    print("[case] batch hidden 1024, 16/2 heads of 64, 8 QKV partials", flush=True)
+    g = load_golden("mini")
+    m = synth_model(mmr, g, hidden_size=1024, num_attention_heads=16, num_key_value_heads=2, head_dim=64,
+                    intermediate_size=1024)
+    rng = np.random.default_rng(3)
+    lengths = [40, 9, 75]
+    prompts = [[int(t) for t in rng.integers(0, g["config"]["vocab_size"], n)] for n in lengths]
+    cap, steps = 200, 90
+    bs = m.make_batch_state(len(prompts), cap, mmr.KV_F16)
+    bs.prefill(prompts)
+    bs.decode(steps)
+    bs.synchronize()
+    last = max(lengths) + steps
+    for b, p in enumerate(prompts):
+        ref_seq, ref_logits = single_sequence(mmr, m, p, last, cap, mmr.KV_F16)
+        np.testing.assert_array_equal(bs.read_sequence(b, 0, last + 1), ref_seq, err_msg=f"sequence {b}")
+        assert rel_err(bs.read_logits(b), ref_logits) < 1e-4, b
+
+
 def test_batch_long_context_split_paths(gpu):
     # positions up to 1150: the attention split count per sequence steps
     # through 1, 2, 4, 8 and 16, so the O projection's staging merges 1-4 and
