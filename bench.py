@@ -673,9 +673,13 @@ def main() -> int:
     c = MINIMIND2
     warm_bytes = 2 * (c["hidden_size"] * c["num_attention_heads"] * c["head_dim"] +
                       3 * c["hidden_size"] * c["intermediate_size"])
+    caller_warm = os.environ.get("MMR_L2_WARM_BLOCKS")
     os.environ["MMR_L2_WARM_BLOCKS"] = "0"
     cold = model.make_state(KERNEL_CONTEXT + 8, kv)
-    del os.environ["MMR_L2_WARM_BLOCKS"]
+    if caller_warm is None:
+        del os.environ["MMR_L2_WARM_BLOCKS"]
+    else:
+        os.environ["MMR_L2_WARM_BLOCKS"] = caller_warm  # the caller's setting holds for the later legs
     cold.enqueue_prefill(prompt)
     cold.enqueue_decode(KERNEL_CONTEXT - PROMPT_LEN - 1)
     cold.synchronize()
