@@ -223,12 +223,14 @@ def test_gemm_prefill_swiglu_presplit_tilings(gpu, monkeypatch, prompt_len):
     assert gem.read_sequence(0, n).tolist() == tok.read_sequence(0, n).tolist()
 
 
-@pytest.mark.parametrize("prompt_len", [333, 600])
+@pytest.mark.parametrize("prompt_len", [333, 600, 1300])
 def test_minimind2_ragged_chunks_match_tokenwise(gpu, monkeypatch, prompt_len):
     # MiniMind2 shapes at row counts below the 512-row chunk (333 alone; 600 =
-    # 512 + 88): fewer rows take more K splits, so the split-K partial sets
-    # of these chunks are larger than the full chunk's.  GEMM prefill against
-    # the same prompt fed token by token through the fp16 KV cache.
+    # 512 + 88; 1300 = 2 x 512 + 276): fewer rows take more K splits, so the
+    # split-K partial sets of these chunks are larger than the full chunk's.
+    # GEMM prefill against the same prompt fed token by token through the
+    # fp16 KV cache (from 1,025 positions on, the token-by-token steps run 16
+    # attention splits over 17 or more tiles: blocks with two tiles).
     mmr = gpu
     print(f"[case] MiniMind2 prefill rows={prompt_len}", flush=True)
     g = load_golden("cfg3_short")
