@@ -108,18 +108,21 @@ template <typename KV, int D, bool PAGED>
 struct KvRows {
   const AttnArgs& a;
   const int32_t* pages;
-  int g;
-  __device__ __forceinline__ KvRows(const AttnArgs& args, int b, int group)
-      : a(args), pages(args.page_table + static_cast<int64_t>(b) * args.pages_per_seq), g(group) {}
+  int g, b;
+  __device__ __forceinline__ KvRows(const AttnArgs& args, int seq, int group)
+      : a(args), pages(args.page_table + static_cast<int64_t>(seq) * args.pages_per_seq), g(group), b(seq) {}
   // Batch: the page holding token t (its index clamped into the page table,
-  // so a lookahead past the context stays in range).  The table is read-only
-  // here and the index uniform: read through the constant address space, the
-  // lookup is a scalar-cache load whose wait (lgkmcnt) never covers the vector
-  // K/V loads in flight.  Single sequence: t's segment.
+  // so a lookahead past the context stays in range).  With page_interleave the
+  // table's own rule is applied without reading it; otherwise the table is
+  // read through the constant address space (read-only here, uniform index):
+  // a scalar-cache load whose wait (lgkmcnt) never covers the vector K/V
+  // loads in flight.  Single sequence: t's segment.
   __device__ __forceinline__ int page_of(int t) const {
     if constexpr (PAGED) {
+      const int idx = min(t / kKvPage, a.pages_per_seq - 1);
+      if (a.page_interleave > 0) return idx * a.page_interleave + b;
       using ConstTable = const __attribute__((address_space(4))) int32_t;
-      return ((ConstTable*)pages)[min(t / kKvPage, a.pages_per_seq - 1)];
+      return ((ConstTable*)pages)[idx];
     } else {
       return kv_segment(t);
     }

@@ -224,6 +224,11 @@ struct AttnArgs {
   // the page of sequence b's token t; rows = pages_per_seq * kKvPage.
   const int32_t* page_table = nullptr;
   int pages_per_seq = 0;
+  // > 0: the table holds page_table[b * pages_per_seq + i] = i *
+  // page_interleave + b for every entry, and the kernels apply that rule
+  // instead of reading it (one dependent memory access fewer before the
+  // first K/V load).
+  int page_interleave = 0;
   // Single-sequence fused launches on the per-head kernel: warming blocks past
   // the head blocks load these regions into the XCDs' L2s while the head
   // blocks run.  Other launch shapes ignore them.

@@ -302,6 +302,7 @@ void enqueue_batch_step_kernels(const BatchDeviceState& s, int splits) {
     t.batch = B;
     t.page_table = s.page_table;
     t.pages_per_seq = static_cast<int>(s.pages_per_seq);
+    t.page_interleave = B;  // the table's rule (set up in make_batch_state)
     check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "batch attention");
     const int o_parts = project_combine(s, splits, Ld.o, H, Hq, Hkv, D);
     const mmr::L2WarmSet warm_mlp = warm_set(s.warm_blocks, {splitk_warm_region(Ld.gate_up, 2 * F, H, kc_gu),
