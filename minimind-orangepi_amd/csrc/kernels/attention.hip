@@ -573,11 +573,47 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(AttnArgs a
   float* part = a.part + static_cast<int64_t>(b) * a.part_stride;
   const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
 
-  // ---- 1. independent loads, issued before the position is known (as in
-  // attention_split_kernel): the wave's sub-tile of the block's first tile,
-  // the raw q/k/v, gains and RoPE frequencies ----
+  // ---- 1. independent loads, issued before the position is known: the raw
+  // q/k/v (every QKV partial), gains and RoPE frequencies first, then the
+  // wave's sub-tile of the block's first tile.  Vector loads complete in
+  // issue order, so the q/k norm and RoPE wait for the first group alone
+  // while the K/V tile is still arriving (the partials are summed after the
+  // tile's loads are out) ----
   int p = -1;
   if constexpr (MODE == kAttnFused) p = ((const __attribute__((address_space(4))) int32_t*)a.pos)[b];
+  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
+  const bool in_pair = lane < D / 2;
+  constexpr int kParts = PAGED ? QP : 1;  // QKV partials loaded, as in attention_split_kernel
+  float rq0[kParts][2], rq1[kParts][2], rk0[kParts], rk1[kParts], rv0[kParts], rv1[kParts];
+#pragma unroll
+  for (int pt = 0; pt < kParts; ++pt) {
+    const float* row = qkv_row + static_cast<int64_t>(min(pt, a.qkv_parts - 1)) * a.qkv_part_stride;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = min(wave + j * kAttnWaves, R - 1);
+      const float* src = (MODE == kAttnFused ? row : a.q) + (g * R + h) * D;
+      rq0[pt][j] = src[d0];
+      rq1[pt][j] = src[d1];
+    }
+    rk0[pt] = rk1[pt] = rv0[pt] = rv1[pt] = 0.0f;
+    if constexpr (MODE == kAttnFused) {
+      const float* kraw = row + a.hq * D + g * D;
+      const float* vraw = kraw + a.hkv * D;
+      rk0[pt] = kraw[d0];
+      rv0[pt] = vraw[d0];
+      rk1[pt] = kraw[d1];
+      rv1[pt] = vraw[d1];
+    }
+  }
+  float inv_freq = 0.0f, qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+  if constexpr (MODE == kAttnFused) {
+    inv_freq = a.inv_freq[d0];
+    qw0 = a.q_norm[d0];
+    qw1 = a.q_norm[d1];
+    kw0 = a.k_norm[d0];
+    kw1 = a.k_norm[d1];
+  }
+  asm volatile("" ::: "memory");  // the loads above go out before the tile's
   uint4 kc[kPer], vc[kPer];
   const int t_spec = split * TT;
   const bool spec = t_spec + TT <= a.rows;
@@ -592,38 +628,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(AttnArgs a
     vc[i] = *reinterpret_cast<const uint4*>(vspec + off);
   }
   int next_page = kv_rows.page_of((split + S) * TT);
-  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
-  const bool in_pair = lane < D / 2;
-  constexpr int kParts = PAGED ? QP : 1;  // QKV partials loaded, as in attention_split_kernel
+  asm volatile("" ::: "memory");
+  // The partials summed in order (parts past qkv_parts weighted 0).
   float qx0[2] = {0.0f, 0.0f}, qx1[2] = {0.0f, 0.0f};
-  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
-  float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f;
 #pragma unroll
   for (int pt = 0; pt < kParts; ++pt) {
-    const float* row = qkv_row + static_cast<int64_t>(min(pt, a.qkv_parts - 1)) * a.qkv_part_stride;
     const float wgt = pt < a.qkv_parts ? 1.0f : 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int h = min(wave + j * kAttnWaves, R - 1);
-      const float* src = (MODE == kAttnFused ? row : a.q) + (g * R + h) * D;
-      qx0[j] += wgt * src[d0];
-      qx1[j] += wgt * src[d1];
+      qx0[j] += wgt * rq0[pt][j];
+      qx1[j] += wgt * rq1[pt][j];
     }
-    if constexpr (MODE == kAttnFused) {
-      const float* kraw = row + a.hq * D + g * D;
-      const float* vraw = kraw + a.hkv * D;
-      kx0 += wgt * kraw[d0];
-      vx0 += wgt * vraw[d0];
-      kx1 += wgt * kraw[d1];
-      vx1 += wgt * vraw[d1];
-    }
-  }
-  if constexpr (MODE == kAttnFused) {
-    inv_freq = a.inv_freq[d0];
-    qw0 = a.q_norm[d0];
-    qw1 = a.q_norm[d1];
-    kw0 = a.k_norm[d0];
-    kw1 = a.k_norm[d1];
+    kx0 += wgt * rk0[pt];
+    vx0 += wgt * rv0[pt];
+    kx1 += wgt * rk1[pt];
+    vx1 += wgt * rv1[pt];
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
