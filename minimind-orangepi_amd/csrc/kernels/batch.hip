@@ -202,12 +202,19 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
   const int bx = tile.row_block, by = tile.chunk;
   const int n0 = bx * kSplitRows + wave * 16;
   const int k0 = by * KC;
-  // W: NB x 8 halves per lane (rows past n clamp to the last row).
+  // W: NB x 8 halves per lane (rows past n clamp to the last row).  Issued
+  // right after the A operand's loads: vector loads complete in issue order,
+  // so the A staging below waits for its own (small) loads, not for the W
+  // stream behind them.
   const int wrow = min(n0 + lane % 16, g.n - 1);
   const __half* wsrc = g.w + static_cast<int64_t>(wrow) * g.k + k0 + 8 * (lane / 16);
   uint4 wv[NB];
+  auto load_w = [&] {
+    asm volatile("" ::: "memory");
 #pragma unroll
-  for (int i = 0; i < NB; ++i) wv[i] = *reinterpret_cast<const uint4*>(wsrc + 32 * i);
+    for (int i = 0; i < NB; ++i) wv[i] = *reinterpret_cast<const uint4*>(wsrc + 32 * i);
+    asm volatile("" ::: "memory");
+  };
   // A: pass p, lane -> row wave + 4 (p RPP + lane / QR), columns 4 (lane % QR) ..
   const int sub = lane / QR, q = lane % QR;
   const bool lane_on = lane < RPP * QR;
@@ -228,6 +235,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
         pv[p][s][1] = *reinterpret_cast<const float4*>(src + 4);
       }
     }
+    load_w();
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
       float gs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, us[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -272,6 +280,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
         ov[p][sp] = *reinterpret_cast<const float4*>(base + attn_o_offset(gq, sc, hr, S, R, g.d) + dd);
       }
     }
+    load_w();
 #pragma unroll
     for (int p = 0; p < kPasses; ++p) {
       float M = -INFINITY;
@@ -304,6 +313,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitKArgs g) {
       if (lane_on && r < g.m)
         av[p] = *reinterpret_cast<const float4*>(g.a + static_cast<int64_t>(r) * g.lda + k0 + 4 * q);
     }
+    load_w();
   }
 #pragma unroll
   for (int p = 0; p < kPasses; ++p) {
