@@ -208,11 +208,56 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   float* part = a.part + static_cast<int64_t>(b) * a.part_stride;
   const float* qkv_row = a.qkv + static_cast<int64_t>(b) * a.qkv_stride;
 
-  // ---- 1. independent loads, issued before the position is known ----
+  // ---- 1. independent loads, issued before the position is known: the raw
+  // q/k/v (every QKV partial), gains and RoPE frequencies first, then the
+  // block's first tile.  Vector loads complete in issue order, so the q/k
+  // norm and RoPE wait for the first group alone while the tile is still
+  // arriving (the partials are summed after the tile's loads are out) ----
   // The position is read through the scalar cache (no kernel writes it while
   // this one runs), so no vector load waits behind its round trip.
   int p = -1;
   if constexpr (MODE == kAttnFused) p = ((const __attribute__((address_space(4))) int32_t*)a.pos)[b];
+  // Loads are unconditional (indices clamped into range, values masked
+  // afterwards): a predicated load makes the compiler wait for it before the
+  // branch joins, which would serialise these round trips.  Lane i < d/2
+  // holds dims (i, i + d/2), the pair RoPE rotates together.
+  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
+  const bool in_pair = lane < D / 2;
+  // The batched (paged) path may hand the projection over as up to QP
+  // split-K partials (QP = kAttnFewQkvParts or kAttnMaxQkvParts): every part's
+  // load is issued (part index clamped, parts past qkv_parts weighted 0) and
+  // the parts summed in order.
+  constexpr int kParts = PAGED ? QP : 1;
+  float rq0[kParts][2], rq1[kParts][2], rk0[kParts], rk1[kParts], rv0[kParts], rv1[kParts];
+#pragma unroll
+  for (int pt = 0; pt < kParts; ++pt) {
+    const float* row = qkv_row + static_cast<int64_t>(min(pt, a.qkv_parts - 1)) * a.qkv_part_stride;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int h = min(wave + j * kAttnWaves, R - 1);
+      const float* src = (MODE == kAttnFused ? row : a.q) + (g * R + h) * D;
+      rq0[pt][j] = src[d0];
+      rq1[pt][j] = src[d1];
+    }
+    rk0[pt] = rk1[pt] = rv0[pt] = rv1[pt] = 0.0f;
+    if constexpr (MODE == kAttnFused) {
+      const float* kraw = row + a.hq * D + g * D;
+      const float* vraw = kraw + a.hkv * D;
+      rk0[pt] = kraw[d0];
+      rv0[pt] = vraw[d0];
+      rk1[pt] = kraw[d1];
+      rv1[pt] = vraw[d1];
+    }
+  }
+  float inv_freq = 0.0f, qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+  if constexpr (MODE == kAttnFused) {
+    inv_freq = a.inv_freq[d0];
+    qw0 = a.q_norm[d0];
+    qw1 = a.q_norm[d1];
+    kw0 = a.k_norm[d0];
+    kw1 = a.k_norm[d1];
+  }
+  asm volatile("" ::: "memory");  // the loads above go out before the tile's
   uint4 kc[kPerThread], vc[kPerThread];
   const int t_spec = split * TT;
   const bool spec = t_spec + TT <= a.rows;
@@ -227,46 +272,21 @@ __global__ __launch_bounds__(kAttnThreads) void attention_split_kernel(AttnArgs 
   }
   // Page of the block's second tile, looked up one tile ahead of its fetch.
   int next_page = kv_rows.page_of((split + S) * TT);
-  // Loads are unconditional (indices clamped into range, values masked
-  // afterwards): a predicated load makes the compiler wait for it before the
-  // branch joins, which would serialise these round trips.  Lane i < d/2
-  // holds dims (i, i + d/2), the pair RoPE rotates together.
-  const int d0 = min(lane, D / 2 - 1), d1 = d0 + D / 2;
-  const bool in_pair = lane < D / 2;
-  // The batched (paged) path may hand the projection over as up to QP
-  // split-K partials (QP = kAttnFewQkvParts or kAttnMaxQkvParts): every part's
-  // load is issued (part index clamped, parts past qkv_parts weighted 0) and
-  // the parts summed in order.
-  constexpr int kParts = PAGED ? QP : 1;
+  asm volatile("" ::: "memory");
   float qx0[2] = {0.0f, 0.0f}, qx1[2] = {0.0f, 0.0f};
-  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f, inv_freq = 0.0f;
-  float qw0 = 0.0f, qw1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f;
+  float kx0 = 0.0f, kx1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f;
 #pragma unroll
   for (int pt = 0; pt < kParts; ++pt) {
-    const float* row = qkv_row + static_cast<int64_t>(min(pt, a.qkv_parts - 1)) * a.qkv_part_stride;
     const float wgt = pt < a.qkv_parts ? 1.0f : 0.0f;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int h = min(wave + j * kAttnWaves, R - 1);
-      const float* src = (MODE == kAttnFused ? row : a.q) + (g * R + h) * D;
-      qx0[j] += wgt * src[d0];
-      qx1[j] += wgt * src[d1];
+      qx0[j] += wgt * rq0[pt][j];
+      qx1[j] += wgt * rq1[pt][j];
     }
-    if constexpr (MODE == kAttnFused) {
-      const float* kraw = row + a.hq * D + g * D;
-      const float* vraw = kraw + a.hkv * D;
-      kx0 += wgt * kraw[d0];
-      vx0 += wgt * vraw[d0];
-      kx1 += wgt * kraw[d1];
-      vx1 += wgt * vraw[d1];
-    }
-  }
-  if constexpr (MODE == kAttnFused) {
-    inv_freq = a.inv_freq[min(lane, D / 2 - 1)];
-    qw0 = a.q_norm[d0];
-    qw1 = a.q_norm[d1];
-    kw0 = a.k_norm[d0];
-    kw1 = a.k_norm[d1];
+    kx0 += wgt * rk0[pt];
+    vx0 += wgt * rv0[pt];
+    kx1 += wgt * rk1[pt];
+    vx1 += wgt * rv1[pt];
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
