@@ -191,18 +191,22 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs a) {
     const int head = small_quotient(4 * t4, D), dim = 4 * t4 - head * D;
     const int g = small_quotient(head, R);
     const int obase = ((g * S) * R + (head - g * R)) * D + dim;  // attn_o_offset(g, 0, head % R, S, R, D) + dim
+    // Lane (head, split) = (threadIdx / 16, threadIdx % 16): one 16-lane row
+    // per head, so M_h is a row reduction.  Splits >= S get weight 0.  The
+    // lane's (m, l) goes out first, then the o partials and the weights:
+    // vector loads complete in issue order, so the weights' exponents below
+    // wait for (m, l) alone.
+    const int wh = min(static_cast<int>(threadIdx.x) / kCombineMaxSplits, a.hq - 1);
+    const int ws = static_cast<int>(threadIdx.x) % kCombineMaxSplits;
+    const int wg = small_quotient(wh, R);
+    const float2 ml = *reinterpret_cast<const float2*>(
+        a.part + a.hkv * S * R * D + ((wg * S + min(ws, S - 1)) * R + (wh - wg * R)) * 2);  // attn_ml_offset
+    asm volatile("" ::: "memory");
     float4 ov[kCombineMaxSplits];
 #pragma unroll
     for (int s = 0; s < kCombineMaxSplits; ++s)
       ov[s] = *reinterpret_cast<const float4*>(a.part + obase + min(s, S - 1) * (R * D));
     {
-      // Lane (head, split) = (threadIdx / 16, threadIdx % 16): one 16-lane row
-      // per head, so M_h is a row reduction.  Splits >= S get weight 0.
-      const int wh = min(static_cast<int>(threadIdx.x) / kCombineMaxSplits, a.hq - 1);
-      const int ws = static_cast<int>(threadIdx.x) % kCombineMaxSplits;
-      const int wg = small_quotient(wh, R);
-      const float2 ml = *reinterpret_cast<const float2*>(
-          a.part + a.hkv * S * R * D + ((wg * S + min(ws, S - 1)) * R + (wh - wg * R)) * 2);  // attn_ml_offset
       load_weights();
       const bool live = ws < S;
       const float m = live ? ml.x : -INFINITY;
