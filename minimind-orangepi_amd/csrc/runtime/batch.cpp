@@ -36,9 +36,13 @@
 
 namespace minimind::model {
 
-// Warming blocks per residual + norm launch: 128 measured best (B = 32, 256 ->
-// 4096: 892.9 -> 885.3 us per step; 64: no gain; 192 / 256: 887.3 / 888.7).
-constexpr int kBatchWarmBlocks = 128;
+// Warming blocks per residual + norm launch (MMR_L2_WARM_BLOCKS sets them):
+// none by default.  Since the split-K GEMMs stage A while their W fragments
+// are still arriving, warming W costs more than it saves (B = 32, 256 -> 4096,
+// same box: none 47.05k tok/s, p50 step 0.678 ms; 64 / 128 / 224 blocks
+// 45.13k / 46.00k / 46.18k, 0.706 / 0.693 / 0.690 ms).  Before that change 128
+// blocks measured best (892.9 -> 885.3 us per step).
+constexpr int kBatchWarmBlocks = 0;
 constexpr int64_t kBatchWarmMaxBytes = int64_t{16} << 20;  // half the 32 MB of L2
 
 struct BatchDeviceState {

@@ -165,10 +165,10 @@ def test_batch_graph_replays_match_eager(gpu, monkeypatch):
 
 
 def test_batch_l2_warming_leaves_the_step_unchanged(gpu, monkeypatch):
-    # The residual + norm launches' L2-warming blocks (on by default) only
-    # load the next GEMMs' weights: the batched decode with them equals the
-    # decode without, bit for bit, on MiniMind2's shapes (split-K GEMMs for
-    # qkv, gate_up, down and lm_head).
+    # The residual + norm launches' L2-warming blocks (MMR_L2_WARM_BLOCKS; off
+    # by default in the batched step) only load the next GEMMs' weights: the
+    # batched decode with them equals the decode without, bit for bit, on
+    # MiniMind2's shapes (split-K GEMMs for qkv, gate_up, down and lm_head).
     mmr = gpu
     print("[case] batch cfg3 B=8, warming on / off", flush=True)
     g = load_golden("cfg3")
