@@ -43,8 +43,12 @@ namespace minimind::model {
 // warming blocks fill the CUs the head blocks leave idle, up to kWarmBlocks
 // (MiniMind2 at 768 keys, 128 head blocks: 96 or 128 warming blocks 255.2 us
 // per step, 64: 261.4, none: 263.5); regions above half the 32 MB of L2 are
-// not warmed.  MMR_L2_WARM_BLOCKS overrides the cap.
+// not warmed.  Past 16 attention splits the split-merge launch carries them
+// instead and takes every CU its 48 merge blocks leave idle (kMergeWarmBlocks:
+// at 8,192 / 4,096 keys 208 blocks 341.5 / 312.9 us per step against 343.9 /
+// 314.3 with 128, same box).  MMR_L2_WARM_BLOCKS overrides both caps.
 constexpr int kWarmBlocks = 128;
+constexpr int kMergeWarmBlocks = 1 << 20;  // no cap beyond the idle CUs
 constexpr int64_t kWarmMaxBytes = int64_t{16} << 20;
 
 struct DeviceState {
@@ -84,6 +88,7 @@ struct DeviceState {
   // L2-warming blocks of the single-sequence attention launch (0 = none) and
   // the GPU's CU count, which bounds head blocks + warming blocks.
   int warm_blocks = kWarmBlocks;
+  int merge_warm_blocks = kMergeWarmBlocks;  // the same for the split-merge launch
   int cus = 0;
 
   ~DeviceState() {
@@ -288,7 +293,7 @@ DecoderState LanguageModel::make_state(int64_t capacity, KvCacheDtype kv) const 
   const char* rs = std::getenv("MMR_GEMM_REGISTER_STAGED");
   s->pf.register_staged = rs && rs[0] == '1';
   if (const char* wb = std::getenv("MMR_L2_WARM_BLOCKS"))
-    s->warm_blocks = std::max(0, std::atoi(wb)) / mmr::kXcds * mmr::kXcds;
+    s->warm_blocks = s->merge_warm_blocks = std::max(0, std::atoi(wb)) / mmr::kXcds * mmr::kXcds;
   {
     int dev = 0;
     check_hip(hipGetDevice(&dev), "hipGetDevice");
@@ -425,16 +430,16 @@ bool prologue_combines(const DeviceState& s, int splits) {
          Hq * c.head_dim <= mmr::kCombineMaxDim;
 }
 
-// L2 warming of layer L's O, gate_up and down weights by up to s.warm_blocks
-// blocks on `idle_cus` CUs (rounded down to whole XCD rounds); none when the
-// regions would pass kWarmMaxBytes (they must fit the L2s with room to spare).
-mmr::L2WarmSet layer_warm_set(const DeviceState& s, const LayerDev& L, int idle_cus) {
+// L2 warming of layer L's O, gate_up and down weights by up to `cap` blocks
+// on `idle_cus` CUs (rounded down to whole XCD rounds); none when the regions
+// would pass kWarmMaxBytes (they must fit the L2s with room to spare).
+mmr::L2WarmSet layer_warm_set(const DeviceState& s, const LayerDev& L, int idle_cus, int cap) {
   const DeviceModel& m = *s.model;
   const auto& c = m.cfg;
   const int H = static_cast<int>(c.hidden_size), D = static_cast<int>(c.head_dim);
   const int Hq = static_cast<int>(c.num_attention_heads), F = static_cast<int>(c.intermediate_size);
   mmr::L2WarmSet w;
-  const int blocks = std::min(s.warm_blocks, std::max(0, idle_cus) / mmr::kXcds * mmr::kXcds);
+  const int blocks = std::min(cap, std::max(0, idle_cus) / mmr::kXcds * mmr::kXcds);
   if (blocks <= 0) return w;
   w.region[0] = gemv_warm_region(L.o, H, Hq * D, m.plan_o);
   w.region[1] = gemv_warm_region(L.gate_up, 2 * F, H, m.plan_gu);
@@ -516,7 +521,7 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
       // CUs load this layer's O, gate_up and down weights into the L2s of the
       // XCDs whose blocks will read them.  (Past the prologue's splits the
       // combine launch warms instead.)
-      if (prologue_combines(s, splits)) t.warm = layer_warm_set(s, L, s.cus - splits * Hq);
+      if (prologue_combines(s, splits)) t.warm = layer_warm_set(s, L, s.cus - splits * Hq, s.warm_blocks);
       check_hip(mmr::launch_attention(t, mmr::kAttnFused, s.kv, s.stream), "attention");
       return;
     }
@@ -537,7 +542,7 @@ void enqueue_kernel(const DeviceState& s, int kernel, size_t l, int splits, bool
         a.head_dim = D;
       } else {
         const int merge_blocks = Hq * ((D + 15) / 16);  // one per head and 16-dimension slice
-        const mmr::L2WarmSet warm = layer_warm_set(s, L, s.cus - merge_blocks);
+        const mmr::L2WarmSet warm = layer_warm_set(s, L, s.cus - merge_blocks, s.merge_warm_blocks);
         check_hip(mmr::launch_attention_combine(s.attn_part, Hq, Hkv, D, splits, s.attn, s.stream, 1, 0, &warm),
                   "attention combine");
         a.x = s.attn;
