@@ -534,14 +534,15 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // One K stage from buffer buf: wait for it, start the next one's loads
-  // (past the last stage the last is loaded again: in bounds, unused), then
-  // multiply.
+  // (none after the last stage: the direct loads are inline assembly, so the
+  // block-uniform branch adds no compiler wait, and the epilogue waits for no
+  // unused loads), then multiply.
   auto stage = [&](int kt, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     // Stage kt has landed, and every wave is done with the other buffer
     // (read in stage kt - 1).
     dma_wait_barrier<0>();
-    issue(min(kt + 1, kt1 - 1), std::integral_constant<int, buf ^ 1>{});
+    if (kt + 1 < kt1) issue(kt + 1, std::integral_constant<int, buf ^ 1>{});
     f32x4 part[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -590,8 +591,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_dma_kernel(GemmArgs g) {
       if (kt + 1 < kt1) stage(kt + 1, std::integral_constant<int, 1>{});
     }
   }
-  // Every load (the clamped re-loads of the last stage included) has landed
-  // and every wave is done with the stages before the epilogue reuses them.
+  // Every wave is done with the stages before the epilogue reuses them.
   dma_wait_barrier<0>();
   gemm_epilogue<BM, BN, kEpi>(g, acc, out, reinterpret_cast<float*>(&Bs[0][0]), m0, n0, tid);
 }
