@@ -1522,6 +1522,10 @@ hipError_t launch_attention(const AttnArgs& a, AttnMode mode, KvDtype kv, hipStr
   if (!attention_supported(a.hq, a.hkv, a.d) || a.splits <= 0 || a.batch <= 0) return hipErrorInvalidValue;
   if (a.qkv_parts < 1 || a.qkv_parts > (a.page_table ? kAttnMaxQkvParts : 1)) return hipErrorInvalidValue;
   if (!a.page_table && a.batch != 1) return hipErrorInvalidValue;  // the contiguous cache holds one sequence
+  // The interleave rule (page i of sequence b is i * page_interleave + b)
+  // needs a table it describes and one page per sequence per index.
+  if (a.page_interleave < 0 || (a.page_interleave > 0 && (!a.page_table || a.page_interleave < a.batch)))
+    return hipErrorInvalidValue;
   if (a.batch > 1 && (a.part_stride < static_cast<int64_t>(attention_partial_floats(a.hq, a.hkv, a.d, a.splits)) ||
                       (mode == kAttnFused && a.qkv_stride <= 0)))
     return hipErrorInvalidValue;
