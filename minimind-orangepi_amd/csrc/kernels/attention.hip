@@ -47,6 +47,20 @@ namespace {
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
+// Waves per query head in attention_head_kernel's one-head blocks: eight
+// (two per SIMD, half a tile's tokens each) where a tile's tokens and a
+// head's dims split evenly over them (each wave holds whole tokens, each
+// token's lanes whole quads of dims), else four.  Eight against four,
+// MiniMind2 at 768 keys: the launch without its warming blocks 3.76 -> 3.70
+// us, decode 4,026 -> 4,032 tok/s, 1,024 keys 274.3 -> 271.6 us per step.
+constexpr int kHeadWaves = 8;
+template <int D, int kHeads>
+constexpr int head_kernel_waves() {
+  constexpr int TT = attn_tile_tokens<D>();
+  constexpr bool fits = TT % kHeadWaves == 0 && kWave % (TT / kHeadWaves) == 0 &&
+                        (D / 4) % (kWave / (TT / kHeadWaves)) == 0;
+  return kHeads == 1 && fits ? kHeadWaves : kAttnWaves;
+}
 
 template <typename KV>
 __device__ __forceinline__ void chunk_to_float(const uint4& c, float* dst);
@@ -909,37 +923,39 @@ __global__ __launch_bounds__(kAttnThreads) void attention_mfma_kernel(AttnArgs a
   }
 }
 
-// attention_head_kernel, splits * hq blocks, 256 threads: the contiguous-cache
-// (single-sequence) variant.  Block (s, h) serves query head h of KV group
-// g = h / R over the tiles s, s + splits, ...  The R blocks of a group stage
-// the same K/V tile: a single-sequence step has few tiles, and four times the
-// blocks spreads the scores and P.V over four times the CUs.  Inside the
-// block, wave w owns tokens [w, w + 1) * TT / 4 of each tile with its own
-// online softmax; the waves' (m, l, o) merge at the end.
+// attention_head_kernel, splits * hq blocks of kHW = head_kernel_waves()
+// waves (512 threads for d 32-128): the contiguous-cache (single-sequence)
+// variant.  Block (s, h) serves query head h of KV group g = h / R over the
+// tiles s, s + splits, ...  The R blocks of a group stage the same K/V tile:
+// a single-sequence step has few tiles, and four times the blocks spreads the
+// scores and P.V over four times the CUs.  Inside the block, wave w owns
+// tokens [w, w + 1) * TT / kHW of each tile with its own online softmax; the
+// waves' (m, l, o) merge at the end.
 //  * scores: the kLanesPerTok adjacent lanes of a token each sum an
 //    interleaved share of the dims (16-byte columns c * kLanesPerTok + share),
 //    then add across the share with DPP;
 //  * P.V: one lane per dimension pair over the wave's tokens, the
 //    probabilities read out of the scoring lanes.
 // Writes the same (m, l, o[d]) split partials as attention_split_kernel.
-// kHeads = 4 (1024 threads, one block per (split, group)): the group's four
-// heads share one staged tile, waves 4 j .. 4 j + 3 serving head j exactly as
-// a one-head block does; the long-context form, one staging per tile instead
-// of four while keeping the one-head block's short chain.
+// kHeads = 4 (four waves per head, 1024 threads, one block per (split,
+// group)): the group's four heads share one staged tile, waves 4 j .. 4 j + 3
+// serving head j as a one-head block of four waves would; the long-context
+// form, one staging per tile instead of four while keeping a short chain.
 template <typename KV, int D, int MODE, int kHeads>
-__global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(AttnArgs a) {
+__global__ __launch_bounds__((head_kernel_waves<D, kHeads>() * kWave * kHeads)) void attention_head_kernel(AttnArgs a) {
   constexpr int TT = attn_tile_tokens<D>();
   constexpr int LD = D + 4;
   constexpr int CH = 16 / static_cast<int>(sizeof(KV));
   constexpr int kChunks = TT * D / CH;
-  constexpr int kThreads = kAttnThreads * kHeads;
-  constexpr int kWaves = kThreads / kWave;  // kAttnWaves per head
+  constexpr int kHW = head_kernel_waves<D, kHeads>();  // waves per head
+  constexpr int kThreads = kHW * kWave * kHeads;
+  constexpr int kWaves = kThreads / kWave;
   constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
   constexpr int kPairs = D / 2;
-  constexpr int kTokPerWave = TT / kAttnWaves;
+  constexpr int kTokPerWave = TT / kHW;
   constexpr int kLanesPerTok = kWave / kTokPerWave;
   constexpr int kQuadsPerLane = D / 4 / kLanesPerTok;
-  static_assert(TT % kAttnWaves == 0 && kWave % kTokPerWave == 0, "a wave holds whole tokens");
+  static_assert(TT % kHW == 0 && kWave % kTokPerWave == 0, "a wave holds whole tokens");
   static_assert((D / 4) % kLanesPerTok == 0, "the dims split evenly over a token's lanes");
   static_assert(D / 2 <= kWave, "a wave holds one head as d/2 RoPE pairs");
   __shared__ __align__(16) float q_s[kHeads][D];
@@ -957,7 +973,7 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
     if (static_cast<int>(blockIdx.x) >= S * a.hq) {
       const int first = (S * a.hq + kXcds - 1) / kXcds * kXcds;
       if (MODE == kAttnFused && static_cast<int>(blockIdx.x) >= first)
-        l2_warm<kAttnThreads>(a.warm, static_cast<int>(blockIdx.x) - first, &k_s[0][0]);
+        l2_warm<kThreads>(a.warm, static_cast<int>(blockIdx.x) - first, &k_s[0][0]);
       return;
     }
   }
@@ -969,8 +985,8 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
   // 4 j .. 4 j + 3 serve head j of the group from the one staged tile.
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const int wq = kHeads == 1 ? wave : wave % kAttnWaves;  // the wave's token group of the tile
-  const int hb = kHeads == 1 ? 0 : wave / kAttnWaves;     // the wave's head within the block
+  const int wq = kHeads == 1 ? wave : wave % kHW;  // the wave's token group of the tile
+  const int hb = kHeads == 1 ? 0 : wave / kHW;     // the wave's head within the block
   int unit, r;
   if constexpr (kHeads == 1) {
     const int units = S * a.hkv;
@@ -1208,20 +1224,20 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
   if constexpr (kHeads == 1) {
     float M = red_m[0];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w]);
-    float e[kAttnWaves];
+    for (int w = 1; w < kHW; ++w) M = fmaxf(M, red_m[w]);
+    float e[kHW];
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) e[w] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w] - M);
-    for (int idx = threadIdx.x; idx < D; idx += kAttnThreads) {
+    for (int w = 0; w < kHW; ++w) e[w] = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[w] - M);
+    for (int idx = threadIdx.x; idx < D; idx += kThreads) {
       float o = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) o = fmaf(e[w], red_o[w][idx], o);
+      for (int w = 0; w < kHW; ++w) o = fmaf(e[w], red_o[w][idx], o);
       a.part[attn_o_offset(g, split, r, S, R, D) + idx] = o;
     }
     if (threadIdx.x == 0) {
       float L = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) L = fmaf(e[w], red_l[w], L);
+      for (int w = 0; w < kHW; ++w) L = fmaf(e[w], red_l[w], L);
       float* dst = a.part + attn_ml_offset(g, split, r, S, R, D, a.hkv);
       dst[0] = M * 0.6931471805599453f;  // ln 2
       dst[1] = L;
@@ -1230,26 +1246,26 @@ __global__ __launch_bounds__(kAttnThreads * kHeads) void attention_head_kernel(A
     // Head j of the block: waves 4 j .. 4 j + 3.
     for (int idx = threadIdx.x; idx < kHeads * D; idx += kThreads) {
       const int j = idx / D, dim = idx - j * D;
-      float M = red_m[kAttnWaves * j];
+      float M = red_m[kHW * j];
   #pragma unroll
-      for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[kAttnWaves * j + w]);
+      for (int w = 1; w < kHW; ++w) M = fmaxf(M, red_m[kHW * j + w]);
       float o = 0.0f;
   #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) {
-        const float e = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[kAttnWaves * j + w] - M);
-        o = fmaf(e, red_o[kAttnWaves * j + w][dim], o);
+      for (int w = 0; w < kHW; ++w) {
+        const float e = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[kHW * j + w] - M);
+        o = fmaf(e, red_o[kHW * j + w][dim], o);
       }
       a.part[attn_o_offset(g, split, r - hb + j, S, R, D) + dim] = o;
     }
     if (static_cast<int>(threadIdx.x) < kHeads) {
       const int j = threadIdx.x;
-      float M = red_m[kAttnWaves * j];
+      float M = red_m[kHW * j];
   #pragma unroll
-      for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[kAttnWaves * j + w]);
+      for (int w = 1; w < kHW; ++w) M = fmaxf(M, red_m[kHW * j + w]);
       float L = 0.0f;
   #pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w)
-        L = fmaf(M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[kAttnWaves * j + w] - M), red_l[kAttnWaves * j + w], L);
+      for (int w = 0; w < kHW; ++w)
+        L = fmaf(M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(red_m[kHW * j + w] - M), red_l[kHW * j + w], L);
       float* dst = a.part + attn_ml_offset(g, split, r - hb + j, S, R, D, a.hkv);
       dst[0] = M * 0.6931471805599453f;  // ln 2
       dst[1] = L;
@@ -1437,7 +1453,6 @@ void launch_split(const AttnArgs& a, dim3 grid, hipStream_t s) {
 
 template <typename KV, int D>
 hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
-  const dim3 block(kAttnThreads);
   const dim3 group_grid(a.splits, a.hkv, a.batch);
   if (a.page_table) {
     if (mode != kAttnFused) return hipErrorInvalidValue;
@@ -1453,11 +1468,11 @@ hipError_t launch_attn_d(const AttnArgs& a, AttnMode mode, hipStream_t s) {
       if (a.warm.blocks % kXcds != 0) return hipErrorInvalidValue;
       blocks = (blocks + kXcds - 1) / kXcds * kXcds + a.warm.blocks;
     }
-    const dim3 head_grid(blocks);
+    const dim3 head_grid(blocks), head_block(head_kernel_waves<D, 1>() * kWave);
     if (mode == kAttnFused) {
-      attention_head_kernel<KV, D, kAttnFused, 1><<<head_grid, block, 0, s>>>(a);
+      attention_head_kernel<KV, D, kAttnFused, 1><<<head_grid, head_block, 0, s>>>(a);
     } else {
-      attention_head_kernel<KV, D, kAttnFromCache, 1><<<head_grid, block, 0, s>>>(a);
+      attention_head_kernel<KV, D, kAttnFromCache, 1><<<head_grid, head_block, 0, s>>>(a);
     }
   } else if (!(std::is_same<KV, __half>::value && attn_mfma_supported<D>()) && a.hq / a.hkv == kGroupBlockHeads &&
              static_cast<int64_t>(a.splits) * a.hkv <= kGroupBlockMaxBlocks) {
