@@ -1560,19 +1560,30 @@ hipError_t launch_attention_combine(const float* part, int hq, int hkv, int d, i
     blocks = (blocks + kXcds - 1) / kXcds * kXcds + w.blocks;
   }
   const dim3 grid(blocks, batch);
-  if (splits <= 8 * kCombineGroups) {
-    attention_combine_kernel<8, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out,
-                                                                             w);
-  } else if (splits <= 16 * kCombineGroups) {
-    attention_combine_kernel<16, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
-                                                                              out, w);
-  } else if (splits <= 32 * kCombineGroups) {
-    attention_combine_kernel<32, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride,
-                                                                              out, w);
-  } else {
-    attention_combine_kernel<16, true><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out,
-                                                                             w);
+  // Rounds of loads per thread: the smallest instantiated count that covers
+  // the splits, so few of a thread's loads are clamped repeats (weight 0).
+  const int rounds = (splits + kCombineGroups - 1) / kCombineGroups;
+#define MMR_COMBINE_ROUNDS(K)                                                                                      \
+  if (rounds <= K) {                                                                                               \
+    attention_combine_kernel<K, false><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, \
+                                                                             out, w);                              \
+    return hipGetLastError();                                                                                      \
   }
+  MMR_COMBINE_ROUNDS(2)
+  MMR_COMBINE_ROUNDS(4)
+  MMR_COMBINE_ROUNDS(6)
+  MMR_COMBINE_ROUNDS(8)
+  MMR_COMBINE_ROUNDS(10)
+  MMR_COMBINE_ROUNDS(12)
+  MMR_COMBINE_ROUNDS(14)
+  MMR_COMBINE_ROUNDS(16)
+  MMR_COMBINE_ROUNDS(20)
+  MMR_COMBINE_ROUNDS(24)
+  MMR_COMBINE_ROUNDS(28)
+  MMR_COMBINE_ROUNDS(32)
+#undef MMR_COMBINE_ROUNDS
+  attention_combine_kernel<16, true><<<grid, kCombineThreads, 0, stream>>>(part, hq, hkv, d, splits, part_stride, out,
+                                                                           w);
   return hipGetLastError();
 }
 
