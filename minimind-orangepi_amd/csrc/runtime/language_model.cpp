@@ -772,7 +772,8 @@ void LanguageModel::enqueue_decode(DecoderState& state, int64_t n, int32_t first
   // the split count of the group's last (longest) step: extra splits of the
   // earlier steps hold no tile and merge as neutral partials.  (At 4096 and
   // 8192 keys, with the separate combine kernel, grouped steps measured 1-3%
-  // slower than single-step graphs; at 512 and 1024 keys 1.5% faster.)
+  // slower than single-step graphs, 308 -> 318 and 346 -> 354 us per step in
+  // the latest same-box A/B; at 512 and 1024 keys 1.5% faster.)
   const int tile = mmr::attention_tile_tokens(static_cast<int>(config_.head_dim));
   int64_t i = 0;
   if (s.use_graphs) {
