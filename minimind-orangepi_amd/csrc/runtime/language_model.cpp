@@ -106,7 +106,9 @@ namespace {
 // kMaxSplits.  A split past the context's last tile still issues its
 // speculative first-tile load (the kernel reads the position after its loads
 // are out), so the buckets are kept close to the tile count: 8, 12, 16, then
-// multiples of 8 (of 16 past 128 tiles, of 32 past 256).  Measured with
+// multiples of 8 (of 32 past 256 tiles; 8 rather than 16 from 129 to 256
+// tiles took the step at 8,192 keys from 345.1 to 343.6 us, 136 splits
+// against 144, same box).  Measured with
 // FETCH_SIZE at 768 keys (12 tiles): 16 splits fetched 1.54x the K/V bytes,
 // 4 idle splits' loads being most of the excess.
 constexpr int kMaxSplits = 512;
@@ -133,7 +135,7 @@ int choose_splits(int64_t n_keys, int tile) {
   if (n_tiles <= 12) return 12;
   if (n_tiles <= kPrologueTiles) return mmr::kCombineMaxSplits;
   if (n_tiles >= kMaxSplits) return kMaxSplits;
-  const int64_t step = n_tiles <= 128 ? 8 : (n_tiles <= 256 ? 16 : 32);
+  const int64_t step = n_tiles <= 256 ? 8 : 32;
   return static_cast<int>((n_tiles + step - 1) / step * step);
 }
 
