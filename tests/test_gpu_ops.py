@@ -145,9 +145,10 @@ def test_attention_from_cache_matches_oracle(gpu, oracle, kv, tokens):
     mmr.attention_from_cache(dq, cache, tokens, hq, hkv, d, out, ws)
     got = out.numpy()
     assert rel_err(got, ref) < TOL
-    # any split count (up to the limit) gives the same result; 128 / 129, 256 / 257 and 512 / 513 sit on either
-    # side of the combine kernel's one-round variants (16 groups x 8, 16, 32 loads), 4096 is its multi-round one
-    for splits in (1, 3, 7, 65, 128, 129, 256, 257, 512, 513, 4096):
+    # any split count (up to the limit) gives the same result.  The combine kernel takes 16 groups x R loads per
+    # thread, R the smallest of 2, 4, ..., 16, 20, ..., 32 covering the splits: every R is reached here (32 / 33,
+    # 128 / 129, 256 / 257 and 512 / 513 on either side of a variant's limit), and 4096 takes the multi-round one
+    for splits in (1, 3, 7, 32, 33, 65, 100, 128, 129, 180, 200, 240, 256, 257, 300, 350, 400, 512, 513, 4096):
         mmr.attention_from_cache(dq, cache, tokens, hq, hkv, d, out, ws, splits=splits)
         assert rel_err(out.numpy(), got) < 1e-5
 
