@@ -104,6 +104,10 @@ int mmr_prefill_partial_floats(const mmr_config* config, int64_t chunk_rows, int
  * computes (the blocks of one K chunk are placed on one XCD where chunks is a
  * multiple of 8). */
 int mmr_splitk_block_tile(int block, int row_blocks, int chunks, int* row_block, int* chunk);
+/* Test aid, no reference counterpart (host arithmetic, no device needed): the
+ * attention split count a single-sequence decode step takes over n_keys keys
+ * (its replayed graph's bucket) for heads of head_dim dimensions. */
+int mmr_decode_attention_splits(int64_t n_keys, int64_t head_dim, int* splits);
 /* float_to_half / half_to_float (ascend_matmul.h:14-15), but IEEE
  * round-to-nearest-even instead of the reference's ties-away rounding. */
 int mmr_f32_to_f16(const float* src, uint16_t* dst, size_t n);

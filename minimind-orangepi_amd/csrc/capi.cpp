@@ -296,6 +296,16 @@ int mmr_splitk_block_tile(int block, int row_blocks, int chunks, int* row_block,
     *chunk = t.chunk;
   });
 }
+int mmr_decode_attention_splits(int64_t n_keys, int64_t head_dim, int* splits) {
+  return guarded([&] {
+    require(splits, "null splits");
+    require(n_keys > 0 && n_keys <= INT32_MAX, "n_keys out of range");
+    require(head_dim > 0 && head_dim <= 128 && mmr::attention_supported(1, 1, static_cast<int>(head_dim)),
+            "unsupported head_dim");
+    *splits = minimind::model::decode_attention_splits(
+        n_keys, mmr::attention_tile_tokens(static_cast<int>(head_dim)));
+  });
+}
 int mmr_prefill_partial_floats(const mmr_config* config, int64_t chunk_rows, int64_t* floats) {
   return guarded([&] {
     require(config && floats, "null argument");

@@ -44,4 +44,10 @@ struct DeviceModel {
 // is not largest at chunk_rows.  Host arithmetic only.
 int64_t prefill_partial_floats(const MiniMindConfig& cfg, int64_t chunk_rows);
 
+// Attention splits of a single-sequence decode step over n_keys keys with
+// `tile`-key tiles (the step graph's bucket).  Never decreases as n_keys
+// grows: the KV backing reserved before a graph is captured covers every
+// context its split count serves.  Host arithmetic only.
+int decode_attention_splits(int64_t n_keys, int tile);
+
 }  // namespace minimind::model

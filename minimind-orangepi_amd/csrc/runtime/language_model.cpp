@@ -106,11 +106,12 @@ namespace {
 // kMaxSplits.  A split past the context's last tile still issues its
 // speculative first-tile load (the kernel reads the position after its loads
 // are out), so the buckets are kept close to the tile count: 8, 12, 16, then
-// multiples of 8 (of 32 past 256 tiles; 8 rather than 16 from 129 to 256
-// tiles took the step at 8,192 keys from 345.1 to 343.6 us, 136 splits
-// against 144, same box).  Measured with
-// FETCH_SIZE at 768 keys (12 tiles): 16 splits fetched 1.54x the K/V bytes,
-// 4 idle splits' loads being most of the excess.
+// multiples of 8 (of 32 past 256 tiles).  Measured with FETCH_SIZE at 768
+// keys (12 tiles): 16 splits fetched 1.54x the K/V bytes, 4 idle splits'
+// loads being most of the excess.  Multiples of 8 rather than 16 from 129 to
+// 256 tiles took the step at 8,192 keys from 345.1 to 343.6 us (136 splits
+// against 144, same box).  The count never falls as the context grows
+// (decode_attention_splits).
 constexpr int kMaxSplits = 512;
 // Prompt tokens per prefill chunk (GEMM rows); longer prompts run in chunks.
 constexpr int64_t kPrefillChunk = 512;
@@ -255,6 +256,8 @@ LanguageModel::LanguageModel(LanguageModel&&) noexcept = default;
 LanguageModel& LanguageModel::operator=(LanguageModel&&) noexcept = default;
 
 std::size_t LanguageModel::device_weight_bytes() const { return device_->weight_bytes; }
+
+int decode_attention_splits(int64_t n_keys, int tile) { return choose_splits(n_keys, tile); }
 
 int64_t prefill_partial_floats(const MiniMindConfig& c, int64_t chunk_rows) {
   const int64_t H = c.hidden_size, D = c.head_dim, Hq = c.num_attention_heads, Hkv = c.num_key_value_heads;

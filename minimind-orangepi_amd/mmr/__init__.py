@@ -104,6 +104,7 @@ _SIGS = {
     "mmr_gemm_k_splits": ([I64, I64, I64, C.POINTER(C.c_int)], C.c_int),
     "mmr_prefill_partial_floats": ([C.POINTER(Config), I64, C.POINTER(I64)], C.c_int),
     "mmr_splitk_block_tile": ([C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)], C.c_int),
+    "mmr_decode_attention_splits": ([I64, I64, C.POINTER(C.c_int)], C.c_int),
     "mmr_f32_to_f16": ([VP, VP, SZ], C.c_int),
     "mmr_f16_to_f32": ([VP, VP, SZ], C.c_int),
     "mmr_matvec_f16": ([VP, I64, I64, VP, VP, VP, VP], C.c_int),
@@ -379,6 +380,13 @@ def splitk_block_tile(block: int, row_blocks: int, chunks: int) -> tuple[int, in
     rb, ch = C.c_int(), C.c_int()
     check(_lib.mmr_splitk_block_tile(block, row_blocks, chunks, C.byref(rb), C.byref(ch)))
     return rb.value, ch.value
+
+
+def decode_attention_splits(n_keys: int, head_dim: int) -> int:
+    """Attention splits of a single-sequence decode step over n_keys keys (host arithmetic)."""
+    out = C.c_int()
+    check(_lib.mmr_decode_attention_splits(n_keys, head_dim, C.byref(out)))
+    return out.value
 
 
 def prefill_partial_floats(cfg: Config, chunk_rows: int) -> int:

@@ -192,6 +192,37 @@ def test_prefill_partial_buffer_covers_every_chunk_row_count(mmr, case):
     assert mmr.prefill_partial_floats(cfg, 0) == 0
 
 
+@pytest.mark.parametrize("head_dim,tile", [(96, 64), (64, 64), (128, 32)])
+def test_decode_split_buckets(mmr, head_dim, tile):
+    # The decode step replays one graph per attention split count, and the KV
+    # backing reserved before a capture covers every context that count serves,
+    # so the count may never fall as the context grows.  Buckets: 8, 12, then 16
+    # (the O-projection prologue merges up to 16) up to 24 tiles; then one tile
+    # per split rounded up to a multiple of 8, of 32 past 256 tiles, capped at
+    # 512 (the attention kernels loop over the tiles past the cap).
+    prev = 0
+    for n_keys in range(1, 600 * tile, 7):
+        s = mmr.decode_attention_splits(n_keys, head_dim)
+        tiles = -(-n_keys // tile)
+        assert s >= prev, (n_keys, s, prev)
+        prev = s
+        if tiles <= 8:
+            assert s == 8
+        elif tiles <= 12:
+            assert s == 12
+        elif tiles <= 24:
+            assert s == 16
+        elif tiles >= 512:
+            assert s == 512
+        else:
+            step = 8 if tiles <= 256 else 32
+            assert s % step == 0 and tiles <= s < tiles + step, (n_keys, tiles, s)
+    assert mmr.decode_attention_splits(8193, 96) == 136  # 129 tiles of 64 keys
+    for bad in ((0, 96), (100, 48), (100, 256)):
+        with pytest.raises(mmr.InvalidArgument):
+            mmr.decode_attention_splits(*bad)
+
+
 def test_splitk_block_tiles_cover_the_grid_once(mmr):
     # Every (W row block, K chunk) of a batched split-K launch is computed by
     # exactly one block, whatever the grid; with the chunk count a multiple of
